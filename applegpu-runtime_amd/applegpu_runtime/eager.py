@@ -1,0 +1,161 @@
+"""Thin Python handle over the eager C ABI (`applegpu_eager_*`).
+
+The reference drives this ABI from its PrivateUse1 shim
+(backend_cpp/applegpu_backend.cpp): each aten kernel becomes one or a few
+eager calls that enqueue work on the device and return at once.  `EagerTensor`
+wraps an eager id; ops return new EagerTensors; `synchronize()` waits for the
+stream (`applegpu_eager_flush_and_wait`).
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_double, c_int64, c_uint32, c_uint64
+
+import numpy as np
+
+from ._native import lib, eager_error, DTYPE_CODES, CODE_DTYPES
+
+_ready = False
+
+
+def init():
+    global _ready
+    if not _ready:
+        if not lib.applegpu_eager_init():
+            raise RuntimeError(f"applegpu eager init failed: {eager_error()}")
+        _ready = True
+
+
+class EagerTensor:
+    __slots__ = ("id", "ptr")
+
+    def __init__(self, tid: int, ptr: int | None):
+        self.id = tid
+        self.ptr = ptr
+
+    @property
+    def shape(self):
+        dims = (c_uint64 * 8)()
+        nd = c_uint32()
+        if lib.applegpu_eager_shape(self.id, dims, ctypes.byref(nd)) != 0:
+            raise RuntimeError(eager_error())
+        return tuple(int(dims[i]) for i in range(nd.value))
+
+    @property
+    def dtype(self) -> str:
+        return CODE_DTYPES[lib.applegpu_eager_dtype(self.id)]
+
+    def numpy(self) -> np.ndarray:
+        dt = self.dtype
+        out = np.empty(self.shape, dtype=np.uint16 if dt == "bfloat16" else np.dtype("bool" if dt == "bool" else dt))
+        if lib.applegpu_eager_copy_to_host(self.id, out.ctypes.data, out.nbytes) != 0:
+            raise RuntimeError(eager_error())
+        if dt == "bfloat16":
+            out = (out.astype(np.uint32) << 16).view(np.float32)
+        return out
+
+    def copy_from(self, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        if lib.applegpu_eager_copy_from_host(self.id, arr.ctypes.data, arr.nbytes) != 0:
+            raise RuntimeError(eager_error())
+
+    def __del__(self):
+        try:
+            lib.applegpu_eager_free(self.id)
+        except Exception:
+            pass
+
+
+def _wrap(ptr, oid: c_uint64) -> EagerTensor:
+    if not ptr and oid.value == 0:
+        raise RuntimeError(eager_error())
+    return EagerTensor(oid.value, ptr)
+
+
+def empty(shape, dtype="float32") -> EagerTensor:
+    init()
+    dims = (c_uint64 * len(shape))(*shape)
+    oid = c_uint64()
+    p = lib.applegpu_eager_alloc(dims, len(shape), DTYPE_CODES[dtype], ctypes.byref(oid))
+    return _wrap(p, oid)
+
+
+def from_numpy(arr: np.ndarray) -> EagerTensor:
+    arr = np.ascontiguousarray(arr)
+    name = "bool" if arr.dtype == np.bool_ else arr.dtype.name
+    t = empty(arr.shape, name)
+    t.copy_from(arr)
+    return t
+
+
+def _call(fn, *args) -> EagerTensor:
+    oid = c_uint64()
+    p = fn(*args, ctypes.byref(oid))
+    if not p:
+        raise RuntimeError(eager_error())
+    return EagerTensor(oid.value, p)
+
+
+def add(a, b): return _call(lib.applegpu_eager_add, a.id, b.id)
+def sub(a, b): return _call(lib.applegpu_eager_sub, a.id, b.id)
+def mul(a, b): return _call(lib.applegpu_eager_mul, a.id, b.id)
+def div(a, b): return _call(lib.applegpu_eager_div, a.id, b.id)
+def relu(x): return _call(lib.applegpu_eager_relu, x.id)
+def neg(x): return _call(lib.applegpu_eager_neg, x.id)
+def matmul(a, b): return _call(lib.applegpu_eager_matmul, a.id, b.id)
+def matmul_ex(a, b, ta=False, tb=False): return _call(lib.applegpu_eager_matmul_ex, a.id, b.id, ta, tb)
+def threshold_backward(g, x, thr=0.0): return _call(lib.applegpu_eager_threshold_backward, g.id, x.id, thr)
+def scalar_mul(x, s): return _call(lib.applegpu_eager_scalar_mul, x.id, s)
+def mean_all(x): return _call(lib.applegpu_eager_mean_all, x.id)
+def sum_dim(x, dim, keepdim=False): return _call(lib.applegpu_eager_sum_dim, x.id, dim, keepdim)
+def embedding(w, idx): return _call(lib.applegpu_eager_embedding, w.id, idx.id)
+def layer_norm(x, g, b, eps=1e-5): return _call(lib.applegpu_eager_layer_norm, x.id, g.id, b.id, eps)
+def gelu(x): return _call(lib.applegpu_eager_gelu, x.id)
+def softmax(x): return _call(lib.applegpu_eager_softmax, x.id)
+def mse_loss(a, b): return _call(lib.applegpu_eager_mse_loss, a.id, b.id)
+def mse_loss_backward(g, a, b): return _call(lib.applegpu_eager_mse_loss_backward, g.id, a.id, b.id)
+
+
+def linear(x, w, b=None, act=0):
+    """act(x @ w^T + b); act 0 none, 1 relu, 2 gelu-tanh, 3 gelu-erf."""
+    return _call(lib.applegpu_eager_linear, x.id, w.id, b.id if b is not None else 0, act)
+
+
+def matmul_masked(a, b, ta, tb, mask):
+    """(op(a) @ op(b)) where mask > 0, else 0 (matmul + relu backward in one kernel)."""
+    return _call(lib.applegpu_eager_matmul_masked, a.id, b.id, ta, tb, mask.id)
+
+
+def create_view(base, shape, strides, offset=0):
+    n = len(shape)
+    sh = (c_uint64 * n)(*shape)
+    st = (c_uint64 * n)(*strides)
+    return _call(lib.applegpu_eager_create_view, base.id, sh, st, n, offset)
+
+
+def add_(self, other, alpha=1.0):
+    if lib.applegpu_eager_add_scaled_inplace(self.id, other.id, alpha) != 0:
+        raise RuntimeError(eager_error())
+
+
+def fill_(t, value):
+    if lib.applegpu_eager_fill(t.id, float(value)) != 0:
+        raise RuntimeError(eager_error())
+
+
+def op(name: str, tensors, f=(), i=(), nout=1):
+    """Any op of the Python surface, run eagerly (applegpu_eager_op)."""
+    n = len(tensors)
+    ins = (c_uint64 * n)(*[t.id for t in tensors])
+    fa = (c_double * len(f))(*f) if f else None
+    ia = (c_int64 * len(i))(*i) if i else None
+    out = (c_uint64 * nout)()
+    r = lib.applegpu_eager_op(name.encode(), ins, n, fa, len(f), ia, len(i), out, nout)
+    if r < 0:
+        raise RuntimeError(eager_error())
+    res = [EagerTensor(out[k], None) for k in range(r)]
+    return res[0] if nout == 1 else tuple(res)
+
+
+def synchronize():
+    lib.applegpu_eager_flush_and_wait()

@@ -1,0 +1,78 @@
+"""MLP training step on the eager C ABI.
+
+The reference trains `nn.Sequential(Linear, ReLU, ..., Linear)` with MSE and
+SGD through its PrivateUse1 shim (benchmarks/bench_mlp_cpp.py:29-52,
+python/tests/bench_comparison.py:11-38); autograd turns each step into these
+aten calls: addmm (Linear), relu, mse_loss, mse_loss_backward, mm for the
+weight and input gradients, threshold_backward (relu'), sum over the batch
+(bias grads) and add_(alpha=-lr) per parameter (backend_cpp/applegpu_backend.cpp:
+533-566, 584-620, 678-686, 801-895).  This module issues the same sequence
+through the eager C ABI, with the fusions the MI355X backend offers:
+
+  forward   h = relu(x W^T + b)        one GEMM, bias + relu in the epilogue
+  backward  dh = (g W) * (h > 0)        one GEMM, relu' mask in the epilogue
+            dW = g^T h                  one GEMM, transposed A read in place
+            db = sum(g, 0)              column reduction
+  SGD       p += -lr * grad             one axpy per parameter
+
+Parameters follow torch.nn.Linear's layout (W [out, in], b [out]).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .. import eager as E
+
+
+def torch_default_init(sizes, seed=42):
+    """Kaiming-uniform weights/biases as torch.nn.Linear initialises them, made
+    with torch's own generator so the CPU reference starts from the same bits."""
+    import torch
+    torch.manual_seed(seed)
+    params = []
+    for fin, fout in zip(sizes[:-1], sizes[1:]):
+        lin = torch.nn.Linear(fin, fout)
+        params.append((lin.weight.detach().numpy().copy(), lin.bias.detach().numpy().copy()))
+    return params
+
+
+class EagerMLP:
+    """Linear -> ReLU -> ... -> Linear trained with MSE + SGD on the device."""
+
+    def __init__(self, params_np):
+        E.init()
+        self.params = [(E.from_numpy(np.asarray(w, np.float32)), E.from_numpy(np.asarray(b, np.float32)))
+                       for w, b in params_np]
+        self._one = E.from_numpy(np.ones((1,), np.float32))
+
+    def forward(self, x):
+        acts = [x]
+        h = x
+        n = len(self.params)
+        for i, (w, b) in enumerate(self.params):
+            h = E.linear(h, w, b, act=1 if i < n - 1 else 0)
+            acts.append(h)
+        return h, acts
+
+    def train_step(self, x, y, lr=0.01):
+        """One forward + MSE + backward + SGD step; returns the loss tensor (on device)."""
+        out, acts = self.forward(x)
+        loss = E.mse_loss(out, y)
+        g = E.mse_loss_backward(self._one, out, y)
+        grads = [None] * len(self.params)
+        for i in range(len(self.params) - 1, -1, -1):
+            w, _ = self.params[i]
+            a_in = acts[i]
+            dw = E.matmul_ex(g, a_in, True, False)
+            db = E.sum_dim(g, 0, False)
+            grads[i] = (dw, db)
+            if i > 0:
+                # dL/d(input of layer i) masked by relu' of the previous layer's output
+                g = E.matmul_masked(g, w, False, False, acts[i])
+        for (w, b), (dw, db) in zip(self.params, grads):
+            E.add_(w, dw, -lr)
+            E.add_(b, db, -lr)
+        return loss
+
+    def numpy_params(self):
+        return [(w.numpy(), b.numpy()) for w, b in self.params]

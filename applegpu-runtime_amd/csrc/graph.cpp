@@ -1,0 +1,426 @@
+// Op table, eager/lazy op runner and the lazy graph executor.
+#include "graph.hpp"
+
+#include <cmath>
+#include <unordered_map>
+#include <unordered_set>
+
+#include "ops.hpp"
+
+namespace agpu {
+
+// ── meta mode ──────────────────────────────────────────────────────────────
+static thread_local bool t_meta = false;
+bool meta_mode() { return t_meta; }
+MetaScope::MetaScope() : prev(t_meta) { t_meta = true; }
+MetaScope::~MetaScope() { t_meta = prev; }
+
+// ── op table ───────────────────────────────────────────────────────────────
+// Names follow the Python surface of the reference (crates/python/src/lib.rs).
+enum Op : int {
+  OP_ADD, OP_SUB, OP_MUL, OP_DIV, OP_MIN, OP_MAX, OP_MOD, OP_AND, OP_OR, OP_XOR,
+  OP_LT, OP_GT, OP_LE, OP_GE, OP_EQ, OP_NE,
+  OP_NEG, OP_RELU, OP_EXP, OP_LOG, OP_SQRT, OP_ABS, OP_SIGN, OP_TANH, OP_SIN, OP_COS, OP_SIGMOID,
+  OP_GELU, OP_GELU_EXACT, OP_LOGICAL_NOT, OP_BITWISE_NOT,
+  OP_SCALAR_MUL, OP_POW, OP_CLAMP, OP_SHL, OP_SHR, OP_CAST, OP_QUANTIZE, OP_DEQUANTIZE,
+  OP_SOFTMAX, OP_LOG_SOFTMAX, OP_SOFTMAX_CAUSAL, OP_LAYER_NORM,
+  OP_SUM, OP_MEAN, OP_AMAX, OP_ARGMAX, OP_VAR, OP_STD,
+  OP_SUM_DIM, OP_MEAN_ALL, OP_MSE_LOSS, OP_MSE_LOSS_BACKWARD, OP_SOFTMAX_BACKWARD, OP_THRESHOLD_BACKWARD,
+  OP_EMBEDDING, OP_INDEX_SELECT, OP_GATHER, OP_CONCAT, OP_SLICE, OP_RESHAPE, OP_TRANSPOSE, OP_TRANSPOSE_DIMS,
+  OP_MATMUL, OP_MATMUL_EX, OP_LINEAR, OP_ADD_BIAS, OP_ATTENTION, OP_ATTENTION_CAUSAL,
+  OP_WHERE, OP_MASKED_FILL, OP_TRIU, OP_TRIL,
+  OP_QUANTIZE_PER_ROW, OP_DEQUANTIZE_PER_ROW, OP_LINEAR_INT8, OP_CONTIGUOUS, OP_FULL,
+  OP_COUNT
+};
+
+static const char* kNames[OP_COUNT] = {
+    "add", "sub", "mul", "div", "elem_min", "elem_max", "mod", "bitwise_and", "bitwise_or", "bitwise_xor",
+    "lt", "gt", "le", "ge", "eq", "ne",
+    "neg", "relu", "exp", "log", "sqrt", "abs", "sign", "tanh", "sin", "cos", "sigmoid",
+    "gelu", "gelu_exact", "logical_not", "bitwise_not",
+    "scalar_mul", "pow", "clamp", "shl", "shr", "cast", "quantize", "dequantize",
+    "softmax", "log_softmax", "softmax_causal", "layer_norm",
+    "sum", "mean", "amax", "argmax", "var", "std",
+    "sum_dim", "mean_all", "mse_loss", "mse_loss_backward", "softmax_backward", "threshold_backward",
+    "embedding", "index_select", "gather", "concat", "slice", "reshape", "transpose", "transpose_dims",
+    "matmul", "matmul_ex", "linear", "add_bias", "attention", "attention_causal",
+    "where", "masked_fill", "triu", "tril",
+    "quantize_per_row", "dequantize_per_row", "linear_int8", "contiguous", "full",
+};
+
+int op_code(const char* name) {
+  static std::unordered_map<std::string, int> m = [] {
+    std::unordered_map<std::string, int> r;
+    for (int i = 0; i < OP_COUNT; ++i) r[kNames[i]] = i;
+    r["mod_"] = OP_MOD;
+    r["eq_"] = OP_EQ;
+    r["ne_"] = OP_NE;
+    r["std_dev"] = OP_STD;
+    r["where_cond"] = OP_WHERE;
+    return r;
+  }();
+  auto it = m.find(name);
+  return it == m.end() ? -1 : it->second;
+}
+const char* op_name(int code) { return code >= 0 && code < OP_COUNT ? kNames[code] : "?"; }
+int op_outputs(int code) { return code == OP_QUANTIZE_PER_ROW ? 2 : 1; }
+
+static void need(const std::vector<TensorP>& in, size_t n, int code) {
+  if (in.size() != n) fail("%s expects %zu tensor inputs, got %zu", op_name(code), n, in.size());
+}
+static double fp(const std::vector<double>& f, size_t i, int code) {
+  if (i >= f.size()) fail("%s: missing float parameter %zu", op_name(code), i);
+  return f[i];
+}
+static int64_t ip(const std::vector<int64_t>& v, size_t i, int code) {
+  if (i >= v.size()) fail("%s: missing integer parameter %zu", op_name(code), i);
+  return v[i];
+}
+static DType dt_param(int64_t w) {
+  DType d;
+  if (!dtype_from_wire((int)w, &d)) fail("invalid dtype wire value: %lld", (long long)w);
+  return d;
+}
+
+std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std::vector<double>& f,
+                            const std::vector<int64_t>& iv) {
+  using namespace ops;
+  switch (code) {
+    case OP_ADD: case OP_SUB: case OP_MUL: case OP_DIV: case OP_MIN: case OP_MAX: case OP_MOD:
+    case OP_AND: case OP_OR: case OP_XOR: case OP_LT: case OP_GT: case OP_LE: case OP_GE: case OP_EQ:
+    case OP_NE:
+      need(in, 2, code);
+      return {binary(code - OP_ADD, in[0], in[1])};
+    case OP_NEG: return need(in, 1, code), std::vector<TensorP>{unary(k::kNeg, in[0])};
+    case OP_RELU: return need(in, 1, code), std::vector<TensorP>{unary(k::kRelu, in[0])};
+    case OP_EXP: return need(in, 1, code), std::vector<TensorP>{unary(k::kExp, in[0])};
+    case OP_LOG: return need(in, 1, code), std::vector<TensorP>{unary(k::kLog, in[0])};
+    case OP_SQRT: return need(in, 1, code), std::vector<TensorP>{unary(k::kSqrt, in[0])};
+    case OP_ABS: return need(in, 1, code), std::vector<TensorP>{unary(k::kAbs, in[0])};
+    case OP_SIGN: return need(in, 1, code), std::vector<TensorP>{unary(k::kSign, in[0])};
+    case OP_TANH: return need(in, 1, code), std::vector<TensorP>{unary(k::kTanh, in[0])};
+    case OP_SIN: return need(in, 1, code), std::vector<TensorP>{unary(k::kSin, in[0])};
+    case OP_COS: return need(in, 1, code), std::vector<TensorP>{unary(k::kCos, in[0])};
+    case OP_SIGMOID: return need(in, 1, code), std::vector<TensorP>{unary(k::kSigmoid, in[0])};
+    case OP_GELU: return need(in, 1, code), std::vector<TensorP>{unary(k::kGelu, in[0])};
+    case OP_GELU_EXACT: return need(in, 1, code), std::vector<TensorP>{unary(k::kGeluExact, in[0])};
+    case OP_LOGICAL_NOT: return need(in, 1, code), std::vector<TensorP>{unary(k::kLogicalNot, in[0])};
+    case OP_BITWISE_NOT: return need(in, 1, code), std::vector<TensorP>{unary(k::kBitNot, in[0])};
+    case OP_SCALAR_MUL: need(in, 1, code); return {unary(k::kScale, in[0], (float)fp(f, 0, code))};
+    case OP_POW: need(in, 1, code); return {unary(k::kPow, in[0], (float)fp(f, 0, code))};
+    case OP_CLAMP: need(in, 1, code); return {unary(k::kClamp, in[0], (float)fp(f, 0, code), (float)fp(f, 1, code))};
+    case OP_SHL: need(in, 1, code); return {unary(k::kShl, in[0], (float)ip(iv, 0, code))};
+    case OP_SHR: need(in, 1, code); return {unary(k::kShr, in[0], (float)ip(iv, 0, code))};
+    case OP_CAST: need(in, 1, code); return {cast(in[0], dt_param(ip(iv, 0, code)))};
+    case OP_QUANTIZE:
+      need(in, 1, code);
+      return {quantize(in[0], dt_param(ip(iv, 0, code)), (float)fp(f, 0, code), (int)ip(iv, 1, code))};
+    case OP_DEQUANTIZE:
+      need(in, 1, code);
+      return {dequantize(in[0], dt_param(ip(iv, 0, code)), (float)fp(f, 0, code), (int)ip(iv, 1, code))};
+    case OP_SOFTMAX: need(in, 1, code); return {softmax(in[0], k::kSoftmax)};
+    case OP_LOG_SOFTMAX: need(in, 1, code); return {softmax(in[0], k::kLogSoftmax)};
+    case OP_SOFTMAX_CAUSAL: need(in, 1, code); return {softmax(in[0], k::kSoftmaxCausal)};
+    case OP_LAYER_NORM:
+      need(in, 3, code);
+      return {layer_norm(in[0], in[1], in[2], f.empty() ? 1e-5f : (float)f[0])};
+    case OP_SUM: need(in, 1, code); return {row_reduce(k::kRSum, in[0])};
+    case OP_MEAN: need(in, 1, code); return {row_reduce(k::kRMean, in[0])};
+    case OP_AMAX: need(in, 1, code); return {row_reduce(k::kRAmax, in[0])};
+    case OP_ARGMAX: need(in, 1, code); return {row_reduce(k::kRArgmax, in[0])};
+    case OP_VAR: need(in, 1, code); return {row_reduce(k::kRVar, in[0], iv.empty() ? 1 : (int)iv[0])};
+    case OP_STD: {
+      need(in, 1, code);
+      TensorP v = row_reduce(k::kRVar, in[0], iv.empty() ? 1 : (int)iv[0]);
+      return {unary(k::kSqrt, v)};
+    }
+    case OP_SUM_DIM:
+      need(in, 1, code);
+      return {sum_dim(in[0], ip(iv, 0, code), iv.size() > 1 && iv[1] != 0)};
+    case OP_MEAN_ALL: need(in, 1, code); return {mean_all(in[0])};
+    case OP_MSE_LOSS: need(in, 2, code); return {mse_loss(in[0], in[1])};
+    case OP_MSE_LOSS_BACKWARD: need(in, 3, code); return {mse_loss_backward(in[0], in[1], in[2])};
+    case OP_SOFTMAX_BACKWARD: need(in, 2, code); return {softmax_backward(in[0], in[1])};
+    case OP_THRESHOLD_BACKWARD:
+      need(in, 2, code);
+      return {threshold_backward(in[0], in[1], f.empty() ? 0.f : (float)f[0])};
+    case OP_EMBEDDING: need(in, 2, code); return {embedding(in[0], in[1])};
+    case OP_INDEX_SELECT: need(in, 2, code); return {index_select(in[0], (int)ip(iv, 0, code), in[1])};
+    case OP_GATHER: need(in, 2, code); return {gather(in[0], (int)ip(iv, 0, code), in[1])};
+    case OP_CONCAT: need(in, 2, code); return {concat(in[0], in[1], (int)ip(iv, 0, code))};
+    case OP_SLICE:
+      need(in, 1, code);
+      return {slice(in[0], (int)ip(iv, 0, code), ip(iv, 1, code), ip(iv, 2, code))};
+    case OP_RESHAPE: need(in, 1, code); return {reshape(in[0], iv)};
+    case OP_TRANSPOSE:
+      need(in, 1, code);
+      if (in[0]->ndim < 2) fail("transpose requires at least 2D tensor, got %s", shape_str(in[0]->dims()).c_str());
+      return {transpose_dims(in[0], in[0]->ndim - 2, in[0]->ndim - 1)};
+    case OP_TRANSPOSE_DIMS: {
+      need(in, 1, code);
+      int d0 = (int)ip(iv, 0, code), d1 = (int)ip(iv, 1, code);
+      if (d0 == d1 && d0 >= 0 && d0 < in[0]->ndim) return {in[0]};
+      return {transpose_dims(in[0], d0, d1)};
+    }
+    case OP_MATMUL: need(in, 2, code); return {matmul(in[0], in[1])};
+    case OP_MATMUL_EX:
+      need(in, 2, code);
+      return {matmul(in[0], in[1], ip(iv, 0, code) != 0, ip(iv, 1, code) != 0)};
+    case OP_LINEAR: {
+      // y = act(x W^T + b), W in torch layout [out, in]
+      if (in.size() != 2 && in.size() != 3) fail("linear expects 2 or 3 inputs");
+      Epilogue e;
+      if (in.size() == 3) e.bias = in[2];
+      e.act = iv.empty() ? 0 : (int)iv[0];
+      return {matmul(in[0], in[1], false, true, &e)};
+    }
+    case OP_ADD_BIAS: need(in, 2, code); return {add_bias(in[0], in[1])};
+    case OP_ATTENTION: need(in, 3, code); return {attention(in[0], in[1], in[2], false)};
+    case OP_ATTENTION_CAUSAL: need(in, 3, code); return {attention(in[0], in[1], in[2], true)};
+    case OP_WHERE: need(in, 3, code); return {where(in[0], in[1], in[2])};
+    case OP_MASKED_FILL: need(in, 2, code); return {masked_fill(in[0], in[1], (float)fp(f, 0, code))};
+    case OP_TRIU: need(in, 1, code); return {tri(in[0], true, iv.empty() ? 0 : iv[0])};
+    case OP_TRIL: need(in, 1, code); return {tri(in[0], false, iv.empty() ? 0 : iv[0])};
+    case OP_QUANTIZE_PER_ROW: {
+      need(in, 1, code);
+      auto qs = quantize_per_row(in[0]);
+      return {qs.first, qs.second};
+    }
+    case OP_DEQUANTIZE_PER_ROW:
+      need(in, 2, code);
+      return {dequantize_per_row(in[0], in[1], iv.empty() ? DType::F32 : dt_param(iv[0]))};
+    case OP_LINEAR_INT8: need(in, 3, code); return {linear_int8(in[0], in[1], in[2])};
+    case OP_CONTIGUOUS: {
+      need(in, 1, code);
+      TensorP c = contiguous(in[0]);
+      if (c == in[0]) {
+        // always hand back a distinct tensor object sharing the storage
+        auto v = std::make_shared<Tensor>(*c);
+        v->node = nullptr;
+        v->ext_refs = 0;
+        c = v;
+      }
+      return {c};
+    }
+    case OP_FULL: {
+      if (!in.empty()) fail("full takes no tensor inputs");
+      DType dt = dt_param(ip(iv, 0, code));
+      std::vector<int64_t> dims(iv.begin() + 1, iv.end());
+      return {full(dt, dims, f.empty() ? 0.f : (float)f[0])};
+    }
+  }
+  fail("unknown op code %d", code);
+}
+
+// ── lazy recording ─────────────────────────────────────────────────────────
+std::vector<TensorP> record_op(int code, const std::vector<TensorP>& in, const std::vector<double>& f,
+                               const std::vector<int64_t>& iv) {
+  std::vector<TensorP> metas;
+  {
+    MetaScope ms;
+    metas = run_op(code, in, f, iv);
+  }
+  auto node = std::make_shared<Node>();
+  node->code = code;
+  node->in = in;
+  node->f = f;
+  node->iv = iv;
+  std::vector<TensorP> outs;
+  for (size_t i = 0; i < metas.size(); ++i) {
+    auto t = make_meta(metas[i]->dtype, metas[i]->dims());
+    if (metas.size() == 1) {
+      t->node = node;
+    } else {
+      // Multi-output ops: output i is a selector node on a shared producer.
+      auto sel = std::make_shared<Node>();
+      sel->code = -1 - (int)i;  // selector
+      sel->in = {};
+      sel->f = {};
+      sel->iv = {};
+      t->node = sel;
+    }
+    outs.push_back(t);
+  }
+  if (metas.size() > 1) {
+    // Producer is shared through a hidden tensor held by every selector.
+    auto prod = make_meta(metas[0]->dtype, metas[0]->dims());
+    prod->node = node;
+    for (auto& t : outs) {
+      t->node->in = {prod};
+      node->selectors.push_back(t);
+    }
+  }
+  return outs;
+}
+
+// ── eval ───────────────────────────────────────────────────────────────────
+static GraphStats g_stats;
+GraphStats graph_stats() { return g_stats; }
+
+namespace {
+
+struct Group {
+  Tensor* mm = nullptr;   // matmul node (absorbed)
+  TensorP a, b;           // matmul operands
+  TensorP bias;
+  int act = k::kActNone;
+  TensorP residual;
+  bool has_bias = false;
+};
+
+bool is_single_internal_use(const TensorP& t, const std::unordered_map<Tensor*, int>& uses) {
+  if (!t->pending() || t->ext_refs != 0) return false;
+  auto it = uses.find(t.get());
+  if (it == uses.end() || it->second != 1) return false;
+  // holders: the consumer's node input + the eval order list
+  return t.use_count() == 2 + 0;
+}
+
+void assign(const TensorP& dst, const TensorP& src) {
+  if (src->dtype != dst->dtype || src->ndim != dst->ndim)
+    fail("internal: lazy result %s/%s does not match the recorded %s/%s", shape_str(src->dims()).c_str(),
+         dtype_name(src->dtype), shape_str(dst->dims()).c_str(), dtype_name(dst->dtype));
+  for (int i = 0; i < src->ndim; ++i)
+    if (src->shape[i] != dst->shape[i]) fail("internal: lazy result shape mismatch");
+  if (dst->buf) {
+    // *_out ops preallocated the destination: copy into it.
+    TensorP d = std::make_shared<Tensor>(*dst);
+    d->node = nullptr;
+    d->ext_refs = 0;
+    d->set_contiguous_strides();
+    ops::copy_into(d, src);
+    dst->node.reset();
+    return;
+  }
+  dst->buf = src->buf;
+  dst->offset = src->offset;
+  for (int i = 0; i < src->ndim; ++i) dst->strides[i] = src->strides[i];
+  dst->node.reset();
+}
+
+}  // namespace
+
+void eval(const TensorP& root) {
+  if (!root->pending()) return;
+  // Post-order walk over pending ancestors (iterative).
+  std::vector<TensorP> order;
+  std::unordered_set<Tensor*> seen;
+  std::vector<std::pair<TensorP, size_t>> stack;
+  stack.push_back({root, 0});
+  seen.insert(root.get());
+  while (!stack.empty()) {
+    auto& top = stack.back();
+    Node* n = top.first->node.get();
+    if (top.second < n->in.size()) {
+      TensorP c = n->in[top.second++];
+      if (c->pending() && !seen.count(c.get())) {
+        seen.insert(c.get());
+        stack.push_back({c, 0});
+      }
+    } else {
+      order.push_back(top.first);
+      stack.pop_back();
+    }
+  }
+  g_stats.evals++;
+  g_stats.nodes += order.size();
+
+  // Uses inside this subgraph.
+  std::unordered_map<Tensor*, int> uses;
+  for (auto& t : order)
+    for (auto& c : t->node->in)
+      if (c->pending()) uses[c.get()]++;
+
+  // GEMM epilogue fusion: matmul -> [add_bias (2-D)] -> [gelu|gelu_exact|relu] -> [add residual].
+  std::unordered_map<Tensor*, Group> groups;  // keyed by the group's current final node
+  std::unordered_set<Tensor*> absorbed;
+  for (auto& t : order) {
+    Node* n = t->node.get();
+    if (n->code == OP_ADD_BIAS && t->ndim == 2) {
+      const TensorP& x = n->in[0];
+      if (x->pending() && x->node->code == OP_MATMUL && x->ndim == 2 && is_single_internal_use(x, uses) &&
+          n->in[1]->ndim == 1) {
+        Group g;
+        g.mm = x.get();
+        g.a = x->node->in[0];
+        g.b = x->node->in[1];
+        g.bias = n->in[1];
+        g.has_bias = true;
+        absorbed.insert(x.get());
+        groups[t.get()] = g;
+      }
+    } else if (n->code == OP_GELU || n->code == OP_GELU_EXACT || n->code == OP_RELU) {
+      const TensorP& x = n->in[0];
+      auto it = groups.find(x.get());
+      if (it != groups.end() && it->second.act == k::kActNone && !it->second.residual &&
+          is_single_internal_use(x, uses)) {
+        Group g = it->second;
+        g.act = n->code == OP_RELU ? k::kActRelu : n->code == OP_GELU ? k::kActGelu : k::kActGeluExact;
+        groups.erase(it);
+        absorbed.insert(x.get());
+        groups[t.get()] = g;
+      }
+    } else if (n->code == OP_ADD) {
+      for (int side = 0; side < 2; ++side) {
+        const TensorP& x = n->in[side];
+        const TensorP& other = n->in[1 - side];
+        auto it = groups.find(x.get());
+        if (it == groups.end() || it->second.residual || !is_single_internal_use(x, uses)) continue;
+        if (other->dims() != t->dims() || other.get() == x.get()) continue;
+        Group g = it->second;
+        g.residual = other;
+        groups.erase(it);
+        absorbed.insert(x.get());
+        groups[t.get()] = g;
+        break;
+      }
+    }
+  }
+
+  for (size_t i = 0; i < order.size(); ++i) {
+    TensorP t = order[i];
+    if (absorbed.count(t.get())) {
+      order[i].reset();
+      continue;
+    }
+    Node* n = t->node.get();
+    auto git = groups.find(t.get());
+    std::vector<TensorP> res;
+    if (git != groups.end()) {
+      const Group& g = git->second;
+      ops::Epilogue e;
+      e.bias = g.bias;
+      e.act = g.act;
+      e.residual = g.residual;
+      res = {ops::matmul(g.a, g.b, false, false, &e)};
+      g_stats.fused_gemm_epilogues++;
+      g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0);
+    } else if (n->code < 0) {
+      fail("internal: multi-output selector reached without its producer");
+    } else if (op_outputs(n->code) > 1) {
+      // producer of a multi-output op: run once and fill every live output
+      res = run_op(n->code, n->in, n->f, n->iv);
+      for (size_t j = 0; j < n->selectors.size(); ++j) {
+        TensorP s = n->selectors[j].lock();
+        if (!s || !s->pending()) continue;
+        int idx = -1 - s->node->code;
+        assign(s, res[idx]);
+      }
+      t->buf = res[0]->buf;
+      t->offset = res[0]->offset;
+      for (int d = 0; d < t->ndim; ++d) t->strides[d] = res[0]->strides[d];
+      t->node.reset();
+      order[i].reset();
+      continue;
+    } else if (n->code == OP_ATTENTION || n->code == OP_ATTENTION_CAUSAL) {
+      // Head-interleaved output: a following transpose(0,1)+reshape is free.
+      res = {ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true)};
+    } else {
+      res = run_op(n->code, n->in, n->f, n->iv);
+    }
+    assign(t, res[0]);
+    order[i].reset();
+  }
+}
+
+}  // namespace agpu

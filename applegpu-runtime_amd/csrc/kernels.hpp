@@ -1,0 +1,135 @@
+// Launchers for the gfx950 kernels.  Every launcher enqueues on the stream it
+// is given and returns immediately; shapes are checked by the caller (ops.cpp)
+// before anything is launched.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "core.hpp"
+
+namespace agpu {
+namespace k {
+
+// N-D strided operand for elementwise kernels (element strides; 0 = broadcast).
+struct ND {
+  int ndim = 0;
+  int64_t shape[kMaxDims] = {};
+  int64_t stride[kMaxDims] = {};
+};
+
+// ── elementwise ───────────────────────────────────────────────────────────
+enum Bin : int {
+  kAdd, kSub, kMul, kDiv, kMin, kMax, kMod, kAnd, kOr, kXor,
+  kLt, kGt, kLe, kGe, kEq, kNe,
+  kThresholdBwd,  // out = b > p0 ? a : 0   (a = grad, b = input)
+  kSoftmaxBwd,    // unused by the binary launcher (row kernel)
+};
+enum Un : int {
+  kNeg, kRelu, kExp, kLog, kSqrt, kAbs, kSign, kTanh, kSin, kCos, kSigmoid,
+  kGelu, kGeluExact, kScale, kPow, kClamp, kBitNot, kLogicalNot, kShl, kShr,
+  kCopy,          // also used for dtype casts (in != out dtype)
+  kQuantize,      // round-half-away(x / p0) + p1, clamped to the int8/uint8 range
+  kDequantize,    // (q - p1) * p0
+  kFill,          // out = p0
+};
+
+// out has contiguous shape `so`; a/b are read through their own strides.
+void binary(int op, DType in, DType out, const void* a, const ND& sa, const void* b,
+            const ND& sb, void* o, const ND& so, float p0, hipStream_t s);
+void unary(int op, DType in, DType out, const void* x, const ND& sx, void* o, const ND& so,
+           float p0, float p1, hipStream_t s);
+void where(DType cdt, DType dt, const void* c, const ND& sc, const void* x, const ND& sx,
+           const void* y, const ND& sy, void* o, const ND& so, hipStream_t s);
+// out = in, with rows/cols above (triu) or below (tril) `diag` zeroed, over
+// the last two dims of a contiguous tensor.
+void tri(DType dt, bool upper, int64_t diag, const void* x, void* o, int64_t batch, int64_t rows,
+         int64_t cols, hipStream_t s);
+// y[i] += alpha * x[i], x broadcast through `sx` onto the contiguous shape `sy`.
+void axpy(DType dt, void* y, const ND& sy, const void* x, const ND& sx, float alpha, hipStream_t s);
+// out[i] = in[i] + bias[(i / channel_stride) % channels]
+// (crates/core/src/kernel_templates.rs:747-762)
+void add_bias(DType dt, const void* in, const void* bias, void* out, int64_t numel,
+              int64_t channels, int64_t channel_stride, hipStream_t s);
+
+// ── row kernels (last dim, row stride `ld`, unit column stride) ───────────
+enum RowOp : int { kSoftmax, kLogSoftmax, kSoftmaxCausal };
+void softmax_rows(int op, DType dt, const void* x, int64_t ldx, void* y, int64_t ldy,
+                  int64_t rows, int64_t cols, int64_t causal_rows, hipStream_t s);
+void layer_norm(DType dt, const void* x, int64_t ldx, const void* gamma, const void* beta,
+                void* y, int64_t rows, int64_t cols, float eps, hipStream_t s);
+enum RedOp : int { kRSum, kRMean, kRAmax, kRArgmax, kRVar };
+void row_reduce(int op, DType in, DType out, const void* x, int64_t ldx, void* y, int64_t rows,
+                int64_t cols, int correction, hipStream_t s);
+// Softmax backward: dx = y * (dy - sum(dy * y)) per row.
+void softmax_backward(DType dt, const void* dy, const void* y, void* dx, int64_t rows,
+                      int64_t cols, hipStream_t s);
+// Symmetric per-row int8: scale[r] = absmax(row)/127, q = clamp(rint(x/scale)).
+void quantize_rows(DType in, const void* x, int8_t* q, float* scale, int64_t rows,
+                   int64_t cols, hipStream_t s);
+void dequantize_rows(DType out, const int8_t* q, const float* scale, void* y, int64_t rows,
+                     int64_t cols, hipStream_t s);
+
+// ── reductions ────────────────────────────────────────────────────────────
+// Contiguous x viewed as [outer, red, inner] -> y[outer, inner] = scale * sum.
+void sum_dim(DType dt, const void* x, void* y, int64_t outer, int64_t red, int64_t inner,
+             float scale, hipStream_t s);
+// Whole-tensor reductions into one element of dtype `dt` (`ws` >= 4 KB of
+// scratch): kind 0 = scale * sum(x), kind 1 = scale * sum((a-b)^2).
+size_t reduce_all_ws_bytes();
+void reduce_all(int kind, DType dt, const void* a, const void* b, int64_t n, float scale,
+                void* out, void* ws, hipStream_t s);
+// MSE backward: dx = (a - b) * (2/n) * g[0]   (g: one element of dtype dt)
+void mse_backward(DType dt, const void* a, const void* b, const void* g, void* dx, int64_t n,
+                  hipStream_t s);
+
+// ── indexing ──────────────────────────────────────────────────────────────
+void embedding(DType dt, const void* w, int64_t vocab, int64_t dim, DType idx_dt,
+               const void* idx, int64_t n, void* out, hipStream_t s);
+// Gathers along `dim` of a contiguous [outer, size, inner] tensor.
+// index_select: out[o, j, i] = x[o, idx[j], i]            (idx 1-D, length m)
+// gather:       out[o, j, i] = x[o, idx[o, j, i], i]      (idx shaped like out)
+void index_select(DType dt, const void* x, int64_t outer, int64_t size, int64_t inner,
+                  DType idx_dt, const void* idx, int64_t m, void* out, hipStream_t s);
+void gather(DType dt, const void* x, int64_t outer, int64_t size, int64_t inner, DType idx_dt,
+            const void* idx, int64_t m, void* out, hipStream_t s);
+
+// ── GEMM (MFMA) ───────────────────────────────────────────────────────────
+enum Act : int { kActNone = 0, kActRelu = 1, kActGelu = 2, kActGeluExact = 3 };
+struct Gemm {
+  DType dt = DType::F32;      // A, B, C, bias and residual share this dtype
+  int64_t M = 0, N = 0, K = 0, batch = 1;
+  const void* A = nullptr; int64_t a_sm = 0, a_sk = 0, a_sb = 0;   // A(m,k)
+  const void* B = nullptr; int64_t b_sk = 0, b_sn = 0, b_sb = 0;   // B(k,n)
+  void* C = nullptr; int64_t c_sm = 0, c_sb = 0;                    // C(m,n), unit n stride
+  // epilogue: v = alpha*acc (+ bias[n]) -> act -> (+ residual(m,n)) -> (mask(m,n) > 0 ? v : 0)
+  float alpha = 1.f;
+  const void* bias = nullptr;
+  int act = kActNone;
+  const void* residual = nullptr; int64_t r_sm = 0, r_sb = 0;
+  const void* mask = nullptr; int64_t k_sm = 0, k_sb = 0;
+  // int8 B with per-n fp32 scales (dequant fused into the operand load)
+  const float* b_scale = nullptr;
+  DType b_dt = DType::F32;
+};
+// Workspace bytes the launch needs (split-K partials); 0 when none.
+size_t gemm_workspace_bytes(const Gemm& g);
+void gemm(const Gemm& g, void* workspace, hipStream_t s);
+
+// ── fused attention ───────────────────────────────────────────────────────
+struct Attn {
+  DType dt = DType::F32;
+  int64_t B = 1, H = 1, Tq = 0, Tk = 0, D = 0;
+  const void* q = nullptr; int64_t q_sb = 0, q_sh = 0, q_st = 0;  // unit d stride
+  const void* k = nullptr; int64_t k_sb = 0, k_sh = 0, k_st = 0;
+  const void* v = nullptr; int64_t v_sb = 0, v_sh = 0, v_st = 0;
+  void* o = nullptr; int64_t o_sb = 0, o_sh = 0, o_st = 0;
+  bool causal = false;   // key j visible to query i iff j <= i (diagonal at (0,0))
+  float scale = 1.f;
+};
+bool attention_supported(const Attn& a);
+void attention(const Attn& a, hipStream_t s);
+
+}  // namespace k
+}  // namespace agpu

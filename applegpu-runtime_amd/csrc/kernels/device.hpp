@@ -1,0 +1,73 @@
+// Device-side helpers shared by the gfx950 kernels: element types, float
+// conversion, wavefront reductions and dtype dispatch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../kernels.hpp"
+
+namespace agpu {
+namespace dev {
+
+typedef _Float16 half_t;
+typedef __bf16 bf16_t;
+
+template <typename T> __device__ __forceinline__ float to_f(T x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x) { return (T)x; }
+template <> __device__ __forceinline__ bool from_f<bool>(float x) { return x != 0.f; }
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Launch geometry helpers
+inline unsigned blocks_for(int64_t n, int per_block) {
+  int64_t b = (n + per_block - 1) / per_block;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+
+}  // namespace dev
+}  // namespace agpu
+
+// Dispatch on a float dtype (f32/f16/bf16); `T` is bound inside the body.
+#define AGPU_FLOAT_SWITCH(dt, ...)                                              \
+  switch (dt) {                                                                 \
+    case ::agpu::DType::F32: { typedef float T; __VA_ARGS__; break; }          \
+    case ::agpu::DType::F16: { typedef ::agpu::dev::half_t T; __VA_ARGS__; break; } \
+    case ::agpu::DType::BF16: { typedef ::agpu::dev::bf16_t T; __VA_ARGS__; break; } \
+    default: ::agpu::fail("dtype %s not supported by this kernel", ::agpu::dtype_name(dt)); \
+  }
+
+// Dispatch on every dtype the kernels compute in (no f64 on this path).
+#define AGPU_ALL_SWITCH(dt, ...)                                                \
+  switch (dt) {                                                                 \
+    case ::agpu::DType::F32: { typedef float T; __VA_ARGS__; break; }          \
+    case ::agpu::DType::F16: { typedef ::agpu::dev::half_t T; __VA_ARGS__; break; } \
+    case ::agpu::DType::BF16: { typedef ::agpu::dev::bf16_t T; __VA_ARGS__; break; } \
+    case ::agpu::DType::I8: { typedef int8_t T; __VA_ARGS__; break; }          \
+    case ::agpu::DType::I16: { typedef int16_t T; __VA_ARGS__; break; }        \
+    case ::agpu::DType::I32: { typedef int32_t T; __VA_ARGS__; break; }        \
+    case ::agpu::DType::I64: { typedef int64_t T; __VA_ARGS__; break; }        \
+    case ::agpu::DType::U8: { typedef uint8_t T; __VA_ARGS__; break; }         \
+    case ::agpu::DType::U32: { typedef uint32_t T; __VA_ARGS__; break; }       \
+    case ::agpu::DType::Bool: { typedef bool T; __VA_ARGS__; break; }          \
+    default: ::agpu::fail("dtype %s not supported on this device path", ::agpu::dtype_name(dt)); \
+  }
+
+#define AGPU_INT_SWITCH(dt, ...)                                                \
+  switch (dt) {                                                                 \
+    case ::agpu::DType::I32: { typedef int32_t I; __VA_ARGS__; break; }        \
+    case ::agpu::DType::I64: { typedef int64_t I; __VA_ARGS__; break; }        \
+    default: ::agpu::fail("index dtype must be int32 or int64, got %s", ::agpu::dtype_name(dt)); \
+  }

@@ -1,0 +1,583 @@
+// Batched GEMM C(m,n) = epilogue(sum_k A(m,k) B(k,n)) for gfx950.
+//
+// Reference semantics: row-major batched matmul with fp32 accumulate
+// (crates/core/src/kernel_templates.rs:987-1072, crates/core/src/eager.rs:403-479),
+// transposed operands read in place (crates/core/src/eager.rs:485-560), and
+// Linear = x W^T + b (backend_cpp/applegpu_backend.cpp:584-620).
+//
+// fp32 path: v_mfma_f32_32x32x2_f32 (gfx950 has no xf32 MFMA; this keeps full
+// fp32 products).  256 threads = 4 wavefronts in a 2x2 grid, a BMxBNx16 tile
+// staged through LDS with register prefetch of the next K slice, operands
+// stored k-major in LDS ([k][m], [k][n]) so each MFMA operand read is 32
+// consecutive floats per half-wave whatever the global layout (row- or
+// column-major A and B are both loaded with 16-byte vector loads).  Skinny
+// problems split K across blocks into an fp32 workspace that a second kernel
+// reduces in a fixed order (deterministic) while applying the epilogue.
+// Block ids are remapped so that consecutive tiles land on the same XCD
+// (blocks are dealt round-robin over the 8 XCDs, each with its own L2), then
+// grouped 8 tile-rows at a time for L2 reuse of B.
+//
+// fp16/bf16 path: v_mfma_f32_32x32x16_{f16,bf16} with the same tiling and fp32
+// accumulation.
+#include "device.hpp"
+
+namespace agpu {
+namespace k {
+using namespace dev;
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct GArgs {
+  const void* A; const void* B; void* C;
+  int64_t M, N, K;
+  int64_t a_sm, a_sk, a_sb, b_sk, b_sn, b_sb, c_sm, c_sb;
+  int64_t batch;
+  int splits;
+  int64_t k_per_split;
+  float alpha;
+  const void* bias;
+  int act;
+  const void* res; int64_t r_sm, r_sb;
+  const void* mask; int64_t k_sm, k_sb;
+  float* ws;
+  int tiles_m, tiles_n;
+  bool vec_a, vec_b;
+  const float* b_scale;
+};
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
+  inner = fminf(fmaxf(inner, -10.f), 10.f);
+  return 0.5f * x * (1.f + tanhf(inner));
+}
+
+template <typename T>
+__device__ __forceinline__ void epilogue_store(const GArgs& p, int64_t b, int64_t row, int64_t col, float acc) {
+  float v = p.alpha * acc;
+  if (p.bias) v += to_f(((const T*)p.bias)[col]);
+  if (p.act == kActRelu) v = fmaxf(v, 0.f);
+  else if (p.act == kActGelu) v = gelu_tanh(v);
+  else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+  if (p.res) v += to_f(((const T*)p.res)[b * p.r_sb + row * p.r_sm + col]);
+  if (p.mask) v = to_f(((const T*)p.mask)[b * p.k_sb + row * p.k_sm + col]) > 0.f ? v : 0.f;
+  ((T*)p.C)[b * p.c_sb + row * p.c_sm + col] = from_f<T>(v);
+}
+
+// Tile scheduling: XCD-aware remap, then 8-row tile groups.
+__device__ __forceinline__ void tile_coords(const GArgs& p, int& tm, int& tn) {
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  const int GM = 8;
+  const int per_group = GM * p.tiles_n;
+  const int group = bid / per_group;
+  const int first_m = group * GM;
+  const int gsz = min(p.tiles_m - first_m, GM);
+  const int in_group = bid % per_group;
+  tm = first_m + in_group % gsz;
+  tn = in_group / gsz;
+}
+
+// ── fp32 MFMA kernel ──────────────────────────────────────────────────────
+// Loads a ROWSxBK (KCONT: k contiguous) or BKxROWS (!KCONT) fp32 tile slice
+// owned by this thread into registers.
+template <int ROWS, bool KCONT>
+struct TileF32 {
+  static constexpr int BK = 16;
+  static constexpr int FPT = ROWS * BK / 256;  // floats per thread
+  float v[FPT];
+
+  __device__ __forceinline__ void load(const float* __restrict__ base, int64_t s_row, int64_t s_k, int64_t r0,
+                                       int64_t rmax, int64_t k, int64_t kmax, bool vec) {
+    const int t = threadIdx.x;
+    if constexpr (KCONT) {
+      constexpr int TPR = BK / FPT;
+      const int r = t / TPR, kk = (t % TPR) * FPT;
+      const int64_t gr = r0 + r, gk = k + kk;
+      const float* src = base + gr * s_row + gk;
+      if (vec && gr < rmax && gk + FPT <= kmax) {
+#pragma unroll
+        for (int i = 0; i < FPT; i += 4) *(float4*)&v[i] = *(const float4*)(src + i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < FPT; ++i) v[i] = (gr < rmax && gk + i < kmax) ? src[i] : 0.f;
+      }
+    } else {
+      constexpr int TPK = ROWS / FPT;
+      const int kk = t / TPK, r = (t % TPK) * FPT;
+      const int64_t gr = r0 + r, gk = k + kk;
+      const float* src = base + gk * s_k + gr;
+      if (vec && gk < kmax && gr + FPT <= rmax) {
+#pragma unroll
+        for (int i = 0; i < FPT; i += 4) *(float4*)&v[i] = *(const float4*)(src + i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < FPT; ++i) v[i] = (gk < kmax && gr + i < rmax) ? src[i] : 0.f;
+      }
+    }
+  }
+
+  // LDS tile is [BK][ROWS] (rows contiguous).
+  __device__ __forceinline__ void store(float* __restrict__ lds) const {
+    const int t = threadIdx.x;
+    if constexpr (KCONT) {
+      constexpr int TPR = BK / FPT;
+      const int r = t / TPR, kk = (t % TPR) * FPT;
+#pragma unroll
+      for (int i = 0; i < FPT; ++i) lds[(kk + i) * ROWS + r] = v[i];
+    } else {
+      constexpr int TPK = ROWS / FPT;
+      const int kk = t / TPK, r = (t % TPK) * FPT;
+#pragma unroll
+      for (int i = 0; i < FPT; i += 4) *(float4*)&lds[kk * ROWS + r + i] = *(const float4*)&v[i];
+    }
+  }
+};
+
+template <int BM, int BN, bool AK, bool BKC>
+__global__ void __launch_bounds__(256) gemm_f32_mfma(GArgs p) {
+  constexpr int BK = 16;
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 blocks per wave
+  __shared__ __attribute__((aligned(16))) float As[2][BK * BM];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * BN];
+
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const int64_t z = blockIdx.y;
+  const int64_t b = z / p.splits;
+  const int split = (int)(z % p.splits);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t kbeg = (int64_t)split * p.k_per_split;
+  int64_t kend = kbeg + p.k_per_split;
+  if (kend > p.K) kend = p.K;
+
+  const float* A = (const float*)p.A + b * p.a_sb;
+  const float* B = (const float*)p.B + b * p.b_sb;
+  // For A, "rows" are m; for B, "rows" are n.
+  const int64_t a_srow = p.a_sm, a_sk = p.a_sk;
+  const int64_t b_srow = p.b_sn, b_sk = p.b_sk;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  TileF32<BM, AK> ta;
+  TileF32<BN, BKC> tb;
+  const int64_t nk = (kend - kbeg + BK - 1) / BK;
+  if (nk > 0) {
+    ta.load(A, a_srow, a_sk, m0, p.M, kbeg, kend, p.vec_a);
+    tb.load(B, b_srow, b_sk, n0, p.N, kbeg, kend, p.vec_b);
+    ta.store(As[0]);
+    tb.store(Bs[0]);
+  }
+  __syncthreads();
+
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = (int)(kt & 1);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      const int64_t kn = kbeg + (kt + 1) * BK;
+      ta.load(A, a_srow, a_sk, m0, p.M, kn, kend, p.vec_a);
+      tb.load(B, b_srow, b_sk, n0, p.N, kn, kend, p.vec_b);
+    }
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      const int krow = kk + (lane >> 5);
+      float av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[i] = as[krow * BM + wm + i * 32 + (lane & 31)];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[j] = bs[krow * BN + wn + j * 32 + (lane & 31)];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      ta.store(As[buf ^ 1]);
+      tb.store(Bs[buf ^ 1]);
+    }
+    __syncthreads();
+  }
+
+  // Output layout of a 32x32 block: lane l, register r ->
+  //   row = 8*(r/4) + 4*(l/32) + r%4, col = l%32.
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn + j * 32 + (lane & 31);
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= p.M) continue;
+        if (p.splits > 1)
+          p.ws[((int64_t)split * p.batch + b) * p.M * p.N + row * p.N + col] = acc[i][j][r];
+        else
+          epilogue_store<float>(p, b, row, col, acc[i][j][r]);
+      }
+    }
+}
+
+// ── 16-bit MFMA kernel (f16 / bf16 operands, fp32 accumulate) ─────────────
+// LDS tiles are [rows][BK] with k contiguous so one lane's 8 consecutive k
+// values are one 16-byte read; rows are padded by 8 elements.
+template <typename T, int ROWS, bool KCONT>
+struct Tile16 {
+  static constexpr int BK = 32;
+  static constexpr int EPT = ROWS * BK / 256;  // elements per thread (8 or 16)
+  static constexpr int LD = BK + 8;
+  T v[EPT];
+
+  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t s_row, int64_t s_k, int64_t r0,
+                                       int64_t rmax, int64_t k, int64_t kmax, bool vec) {
+    const int t = threadIdx.x;
+    if constexpr (KCONT) {
+      constexpr int TPR = BK / EPT;
+      const int r = t / TPR, kk = (t % TPR) * EPT;
+      const int64_t gr = r0 + r, gk = k + kk;
+      const T* src = base + gr * s_row + gk;
+      if (vec && gr < rmax && gk + EPT <= kmax) {
+#pragma unroll
+        for (int i = 0; i < EPT; i += 8) *(float4*)&v[i] = *(const float4*)(src + i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) v[i] = (gr < rmax && gk + i < kmax) ? src[i] : T(0);
+      }
+    } else {
+      constexpr int TPK = ROWS / EPT;
+      const int kk = t / TPK, r = (t % TPK) * EPT;
+      const int64_t gr = r0 + r, gk = k + kk;
+      const T* src = base + gk * s_k + gr;
+      if (vec && gk < kmax && gr + EPT <= rmax) {
+#pragma unroll
+        for (int i = 0; i < EPT; i += 8) *(float4*)&v[i] = *(const float4*)(src + i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) v[i] = (gk < kmax && gr + i < rmax) ? src[i] : T(0);
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(T* __restrict__ lds) const {
+    const int t = threadIdx.x;
+    if constexpr (KCONT) {
+      constexpr int TPR = BK / EPT;
+      const int r = t / TPR, kk = (t % TPR) * EPT;
+#pragma unroll
+      for (int i = 0; i < EPT; i += 8) *(float4*)&lds[r * LD + kk + i] = *(const float4*)&v[i];
+    } else {
+      constexpr int TPK = ROWS / EPT;
+      const int kk = t / TPK, r = (t % TPK) * EPT;
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) lds[(r + i) * LD + kk] = v[i];
+    }
+  }
+};
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<half_t> {
+  static __device__ __forceinline__ f32x16 run(const half_t* a, const half_t* b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)a, *(const f16x8*)b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<bf16_t> {
+  static __device__ __forceinline__ f32x16 run(const bf16_t* a, const bf16_t* b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)a, *(const bf16x8*)b, c, 0, 0, 0);
+  }
+};
+
+template <typename T, int BM, int BN, bool AK, bool BKC>
+__global__ void __launch_bounds__(256) gemm_16_mfma(GArgs p) {
+  constexpr int BK = 32;
+  constexpr int LD = BK + 8;
+  constexpr int TM = BM / 64, TN = BN / 64;
+  __shared__ __attribute__((aligned(16))) T As[2][BM * LD];
+  __shared__ __attribute__((aligned(16))) T Bs[2][BN * LD];
+
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const int64_t z = blockIdx.y;
+  const int64_t b = z / p.splits;
+  const int split = (int)(z % p.splits);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t kbeg = (int64_t)split * p.k_per_split;
+  int64_t kend = kbeg + p.k_per_split;
+  if (kend > p.K) kend = p.K;
+  const T* A = (const T*)p.A + b * p.a_sb;
+  const T* B = (const T*)p.B + b * p.b_sb;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  Tile16<T, BM, AK> ta;
+  Tile16<T, BN, BKC> tb;
+  const int64_t nk = (kend - kbeg + BK - 1) / BK;
+  if (nk > 0) {
+    ta.load(A, p.a_sm, p.a_sk, m0, p.M, kbeg, kend, p.vec_a);
+    tb.load(B, p.b_sn, p.b_sk, n0, p.N, kbeg, kend, p.vec_b);
+    ta.store(As[0]);
+    tb.store(Bs[0]);
+  }
+  __syncthreads();
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = (int)(kt & 1);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      const int64_t kn = kbeg + (kt + 1) * BK;
+      ta.load(A, p.a_sm, p.a_sk, m0, p.M, kn, kend, p.vec_a);
+      tb.load(B, p.b_sn, p.b_sk, n0, p.N, kn, kend, p.vec_b);
+    }
+    const T* as = As[buf];
+    const T* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      // lane l holds A[row = l%32][k = 8*(l/32) .. +8] (and likewise B[k][col])
+      const int ko = kk + 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = Mfma16<T>::run(&as[(wm + i * 32 + (lane & 31)) * LD + ko],
+                                     &bs[(wn + j * 32 + (lane & 31)) * LD + ko], acc[i][j]);
+    }
+    if (more) {
+      ta.store(As[buf ^ 1]);
+      tb.store(Bs[buf ^ 1]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t col = n0 + wn + j * 32 + (lane & 31);
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= p.M) continue;
+        if (p.splits > 1)
+          p.ws[((int64_t)split * p.batch + b) * p.M * p.N + row * p.N + col] = acc[i][j][r];
+        else
+          epilogue_store<T>(p, b, row, col, acc[i][j][r]);
+      }
+    }
+}
+
+// Split-K reduction in split order, then the epilogue.
+template <typename T>
+__global__ void __launch_bounds__(256) splitk_reduce(GArgs p) {
+  const int64_t total = p.batch * p.M * p.N;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    float s = 0.f;
+    for (int sp = 0; sp < p.splits; ++sp) s += p.ws[(int64_t)sp * total + i];
+    const int64_t col = i % p.N, row = (i / p.N) % p.M, b = i / (p.M * p.N);
+    epilogue_store<T>(p, b, row, col, s);
+  }
+}
+
+// Any strides, any float dtype, and int8 B with per-n scales: a plain tiled
+// kernel (16x16 threads, 4x4 outputs each) used for layouts the MFMA kernels
+// do not take.
+template <typename T, typename TB>
+__global__ void __launch_bounds__(256) gemm_generic(GArgs p) {
+  __shared__ float As[16][65];
+  __shared__ float Bs[16][65];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t b = blockIdx.z;
+  const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+  const T* A = (const T*)p.A + b * p.a_sb;
+  const TB* B = (const TB*)p.B + b * p.b_sb;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < p.K; k0 += 16) {
+    for (int e = threadIdx.x; e < 16 * 64; e += 256) {
+      int kk = e / 64, r = e % 64;
+      int64_t gm = m0 + r, gn = n0 + r, gk = k0 + kk;
+      As[kk][r] = (gm < p.M && gk < p.K) ? to_f(A[gm * p.a_sm + gk * p.a_sk]) : 0.f;
+      float bv = 0.f;
+      if (gn < p.N && gk < p.K) {
+        bv = (float)B[gk * p.b_sk + gn * p.b_sn];
+        if (p.b_scale) bv *= p.b_scale[gn];
+      }
+      Bs[kk][r] = bv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += As[kk][ty * 4 + i] * Bs[kk][tx * 4 + j];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      int64_t row = m0 + ty * 4 + i, col = n0 + tx * 4 + j;
+      if (row < p.M && col < p.N) epilogue_store<T>(p, b, row, col, acc[i][j]);
+    }
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+struct Plan {
+  int bm, bn, splits;
+  int64_t kps;
+  bool mfma;
+};
+
+Plan make_plan(const Gemm& g, int cus) {
+  Plan pl{};
+  const bool is16 = g.dt == DType::F16 || g.dt == DType::BF16;
+  const bool a_ok = g.a_sk == 1 || g.a_sm == 1;
+  const bool b_ok = g.b_sk == 1 || g.b_sn == 1;
+  pl.mfma = a_ok && b_ok && g.b_dt == g.dt && !g.b_scale && (g.dt == DType::F32 || is16);
+  pl.bm = g.M <= 64 ? 64 : 128;
+  pl.bn = g.N <= 64 ? 64 : 128;
+  const int BK = is16 ? 32 : 16;
+  int64_t tiles = ((g.M + pl.bm - 1) / pl.bm) * ((g.N + pl.bn - 1) / pl.bn) * g.batch;
+  int64_t nk = (g.K + BK - 1) / BK;
+  int splits = 1;
+  const int64_t target = 2LL * cus;
+  while (pl.mfma && tiles * splits < target && nk / (splits * 2) >= 8 && splits < 32 &&
+         g.batch * splits * 2 <= 65535)
+    splits *= 2;
+  pl.splits = splits;
+  pl.kps = ((nk + splits - 1) / splits) * BK;
+  return pl;
+}
+
+GArgs make_args(const Gemm& g, const Plan& pl) {
+  GArgs p{};
+  p.A = g.A; p.B = g.B; p.C = g.C;
+  p.M = g.M; p.N = g.N; p.K = g.K;
+  p.a_sm = g.a_sm; p.a_sk = g.a_sk; p.a_sb = g.a_sb;
+  p.b_sk = g.b_sk; p.b_sn = g.b_sn; p.b_sb = g.b_sb;
+  p.c_sm = g.c_sm; p.c_sb = g.c_sb;
+  p.batch = g.batch;
+  p.splits = pl.splits;
+  p.k_per_split = pl.kps;
+  p.alpha = g.alpha;
+  p.bias = g.bias;
+  p.act = g.act;
+  p.res = g.residual; p.r_sm = g.r_sm; p.r_sb = g.r_sb;
+  p.mask = g.mask; p.k_sm = g.k_sm; p.k_sb = g.k_sb;
+  p.tiles_m = (int)((g.M + pl.bm - 1) / pl.bm);
+  p.tiles_n = (int)((g.N + pl.bn - 1) / pl.bn);
+  p.b_scale = g.b_scale;
+  const size_t esz = dtype_size(g.dt);
+  const int vw = (int)(16 / esz);  // elements per 16-byte vector
+  // Vector loads need 16-byte aligned rows along the contiguous axis.
+  const int64_t a_lead = g.a_sk == 1 ? g.a_sm : g.a_sk;
+  const int64_t b_lead = g.b_sk == 1 ? g.b_sn : g.b_sk;
+  p.vec_a = al16(g.A) && (a_lead % vw == 0) && (g.a_sb % vw == 0);
+  p.vec_b = al16(g.B) && (b_lead % vw == 0) && (g.b_sb % vw == 0);
+  return p;
+}
+
+template <int BM, int BN>
+void launch_f32(const GArgs& p, bool ak, bool bk, dim3 grid, hipStream_t s) {
+  if (ak && bk) hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, true, true>), grid, dim3(256), 0, s, p);
+  else if (ak) hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, true, false>), grid, dim3(256), 0, s, p);
+  else if (bk) hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, false, true>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, false, false>), grid, dim3(256), 0, s, p);
+}
+
+template <typename T, int BM, int BN>
+void launch_16(const GArgs& p, bool ak, bool bk, dim3 grid, hipStream_t s) {
+  if (ak && bk) hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, true, true>), grid, dim3(256), 0, s, p);
+  else if (ak) hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, true, false>), grid, dim3(256), 0, s, p);
+  else if (bk) hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, false, true>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, false, false>), grid, dim3(256), 0, s, p);
+}
+
+int cu_count() {
+  static int cus = 0;
+  if (!cus) {
+    hipDeviceProp_t prop;
+    cus = hipGetDeviceProperties(&prop, 0) == hipSuccess ? prop.multiProcessorCount : 256;
+  }
+  return cus;
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(const Gemm& g) {
+  Plan pl = make_plan(g, cu_count());
+  if (pl.splits <= 1) return 0;
+  return (size_t)pl.splits * g.batch * g.M * g.N * sizeof(float);
+}
+
+void gemm(const Gemm& g, void* workspace, hipStream_t s) {
+  if (g.M == 0 || g.N == 0 || g.batch == 0) return;
+  Plan pl = make_plan(g, cu_count());
+  GArgs p = make_args(g, pl);
+  p.ws = (float*)workspace;
+  if (pl.splits > 1 && !workspace) fail("gemm: split-K workspace missing");
+  if (!pl.mfma) {
+    dim3 grid((unsigned)((g.N + 63) / 64), (unsigned)((g.M + 63) / 64), (unsigned)g.batch);
+    p.splits = 1;
+    if (g.b_scale) {
+      if (g.b_dt != DType::I8) fail("gemm: scaled B operand must be int8");
+      AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((gemm_generic<T, int8_t>), grid, dim3(256), 0, s, p));
+    } else {
+      AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((gemm_generic<T, T>), grid, dim3(256), 0, s, p));
+    }
+    check_launch("gemm_generic");
+    return;
+  }
+  if (g.batch * pl.splits > 65535) fail("gemm: batch %lld too large", (long long)g.batch);
+  const bool ak = g.a_sk == 1, bk = g.b_sk == 1;
+  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)(g.batch * pl.splits));
+  if (g.dt == DType::F32) {
+    if (pl.bm == 128 && pl.bn == 128) launch_f32<128, 128>(p, ak, bk, grid, s);
+    else if (pl.bm == 128) launch_f32<128, 64>(p, ak, bk, grid, s);
+    else if (pl.bn == 128) launch_f32<64, 128>(p, ak, bk, grid, s);
+    else launch_f32<64, 64>(p, ak, bk, grid, s);
+  } else if (g.dt == DType::F16) {
+    if (pl.bm == 128 && pl.bn == 128) launch_16<half_t, 128, 128>(p, ak, bk, grid, s);
+    else if (pl.bm == 128) launch_16<half_t, 128, 64>(p, ak, bk, grid, s);
+    else if (pl.bn == 128) launch_16<half_t, 64, 128>(p, ak, bk, grid, s);
+    else launch_16<half_t, 64, 64>(p, ak, bk, grid, s);
+  } else {
+    if (pl.bm == 128 && pl.bn == 128) launch_16<bf16_t, 128, 128>(p, ak, bk, grid, s);
+    else if (pl.bm == 128) launch_16<bf16_t, 128, 64>(p, ak, bk, grid, s);
+    else if (pl.bn == 128) launch_16<bf16_t, 64, 128>(p, ak, bk, grid, s);
+    else launch_16<bf16_t, 64, 64>(p, ak, bk, grid, s);
+  }
+  check_launch("gemm_mfma");
+  if (pl.splits > 1) {
+    int64_t total = g.batch * g.M * g.N;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce<T>), dim3((unsigned)blocks), dim3(256), 0, s, p));
+    check_launch("splitk_reduce");
+  }
+}
+
+}  // namespace k
+}  // namespace agpu

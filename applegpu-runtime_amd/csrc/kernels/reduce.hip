@@ -1,0 +1,233 @@
+// Reductions (sum over one dim, whole-tensor sum / squared-error sum, MSE
+// backward) and index kernels (embedding, index_select, gather).
+//
+// Reference semantics:
+//   sum_dim output shape, keepdim                 crates/core/src/eager.rs:827-855
+//   mean_all -> one element                       crates/core/src/eager.rs:710-769
+//   mse_loss = mean((a-b)^2), grad = (a-b)*2/n*g  backend_cpp/applegpu_backend.cpp:801-867
+//   embedding out[i,:] = W[idx[i],:]              crates/core/src/kernel_templates.rs:1119-1143
+//   gather / index_select                         crates/core/src/kernel_templates.rs:870-975
+// The reference's mean_all chains thread-per-row mean kernels; here a
+// two-stage tree reduction with a fixed order (deterministic, no atomics).
+#include "device.hpp"
+
+namespace agpu {
+namespace k {
+using namespace dev;
+
+namespace {
+
+// [outer, red, inner] -> [outer, inner]; inner == 1 uses a wavefront per row.
+template <typename T>
+__global__ void __launch_bounds__(256) sum_last(const T* __restrict__ x, T* __restrict__ y, int64_t rows,
+                                                int64_t red, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * red;
+  float s = 0.f;
+  for (int64_t c = lane; c < red; c += 64) s += to_f(xr[c]);
+  s = wave_sum(s);
+  if (lane == 0) y[row] = from_f<T>(s * scale);
+}
+
+// Column sums: a 256-thread block covers 64 columns x 4 row-slices, then the
+// four partial sums meet in LDS.
+template <typename T>
+__global__ void __launch_bounds__(256) sum_cols(const T* __restrict__ x, T* __restrict__ y, int64_t outer,
+                                                int64_t red, int64_t inner, float scale) {
+  __shared__ float sh[4][64];
+  const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t o = blockIdx.y;
+  float s = 0.f;
+  if (col < inner) {
+    const T* base = x + o * red * inner + col;
+    for (int64_t r = slice; r < red; r += 4) s += to_f(base[r * inner]);
+  }
+  sh[slice][lane] = s;
+  __syncthreads();
+  if (slice == 0 && col < inner)
+    y[o * inner + col] = from_f<T>((sh[0][lane] + sh[1][lane] + sh[2][lane] + sh[3][lane]) * scale);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) sum_int_dim(const T* __restrict__ x, T* __restrict__ y, int64_t outer,
+                                                   int64_t red, int64_t inner) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= outer * inner) return;
+  int64_t o = i / inner, c = i % inner;
+  long long s = 0;
+  for (int64_t r = 0; r < red; ++r) s += (long long)x[(o * red + r) * inner + c];
+  y[i] = (T)s;
+}
+
+constexpr int kPartials = 512;
+
+// Stage 1: each block writes one fp32 partial.
+template <typename T>
+__global__ void __launch_bounds__(256) reduce_stage1(int kind, const T* __restrict__ a, const T* __restrict__ b,
+                                                     int64_t n, float* __restrict__ part) {
+  __shared__ float sh[4];
+  float s = 0.f;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float v = to_f(a[i]);
+    if (kind == 1) {
+      v -= to_f(b[i]);
+      v *= v;
+    }
+    s += v;
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = sh[0] + sh[1] + sh[2] + sh[3];
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) reduce_stage2(const float* __restrict__ part, int nparts, float scale,
+                                                     T* __restrict__ out) {
+  __shared__ float sh[4];
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nparts; i += 256) s += part[i];
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = from_f<T>((sh[0] + sh[1] + sh[2] + sh[3]) * scale);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) mse_bwd_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                      const T* __restrict__ g, T* __restrict__ dx, int64_t n,
+                                                      float two_over_n) {
+  const float gs = to_f(g[0]);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    dx[i] = from_f<T>((to_f(a[i]) - to_f(b[i])) * two_over_n * gs);
+}
+
+// Rows with an index outside [0, vocab) come out as zeros.
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) embedding_kernel(const T* __restrict__ w, int64_t vocab, int64_t dim,
+                                                        const I* __restrict__ idx, int64_t n,
+                                                        T* __restrict__ out) {
+  const int64_t row = blockIdx.y;
+  for (int64_t r = row; r < n; r += gridDim.y) {
+    const int64_t id = (int64_t)idx[r];
+    const bool ok = id >= 0 && id < vocab;
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < dim; c += (int64_t)gridDim.x * 256)
+      out[r * dim + c] = ok ? w[id * dim + c] : T(0);
+  }
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) index_select_kernel(const T* __restrict__ x, int64_t outer, int64_t size,
+                                                           int64_t inner, const I* __restrict__ idx, int64_t m,
+                                                           T* __restrict__ out) {
+  const int64_t n = outer * m * inner;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    int64_t c = i % inner, j = (i / inner) % m, o = i / (inner * m);
+    int64_t id = (int64_t)idx[j];
+    out[i] = (id >= 0 && id < size) ? x[(o * size + id) * inner + c] : T(0);
+  }
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) gather_kernel(const T* __restrict__ x, int64_t outer, int64_t size,
+                                                     int64_t inner, const I* __restrict__ idx, int64_t m,
+                                                     T* __restrict__ out) {
+  const int64_t n = outer * m * inner;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    int64_t c = i % inner, o = i / (inner * m);
+    int64_t id = (int64_t)idx[i];
+    out[i] = (id >= 0 && id < size) ? x[(o * size + id) * inner + c] : T(0);
+  }
+}
+
+unsigned grid_for(int64_t n) {
+  int64_t b = (n + 255) / 256;
+  if (b > 65536) b = 65536;
+  return (unsigned)(b < 1 ? 1 : b);
+}
+
+}  // namespace
+
+void sum_dim(DType dt, const void* x, void* y, int64_t outer, int64_t red, int64_t inner, float scale,
+             hipStream_t s) {
+  if (outer * inner == 0) return;
+  if (!dtype_is_float(dt)) {
+    AGPU_ALL_SWITCH(dt, hipLaunchKernelGGL((sum_int_dim<T>), dim3(grid_for(outer * inner)), dim3(256), 0, s,
+                                           (const T*)x, (T*)y, outer, red, inner));
+  } else if (inner == 1) {
+    AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((sum_last<T>), dim3((unsigned)((outer + 3) / 4)), dim3(256), 0, s,
+                                             (const T*)x, (T*)y, outer, red, scale));
+  } else {
+    if (outer > 65535) fail("sum_dim: outer extent %lld too large", (long long)outer);
+    dim3 grid((unsigned)((inner + 63) / 64), (unsigned)outer);
+    AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((sum_cols<T>), grid, dim3(256), 0, s, (const T*)x, (T*)y, outer,
+                                             red, inner, scale));
+  }
+  check_launch("sum_dim");
+}
+
+size_t reduce_all_ws_bytes() { return kPartials * sizeof(float); }
+
+void reduce_all(int kind, DType dt, const void* a, const void* b, int64_t n, float scale, void* out, void* ws,
+                hipStream_t s) {
+  int64_t blocks = (n + 255) / 256;
+  if (blocks > kPartials) blocks = kPartials;
+  if (blocks < 1) blocks = 1;
+  AGPU_FLOAT_SWITCH(dt, {
+    hipLaunchKernelGGL((reduce_stage1<T>), dim3((unsigned)blocks), dim3(256), 0, s, kind, (const T*)a,
+                       (const T*)b, n, (float*)ws);
+    hipLaunchKernelGGL((reduce_stage2<T>), dim3(1), dim3(256), 0, s, (const float*)ws, (int)blocks, scale,
+                       (T*)out);
+  });
+  check_launch("reduce_all");
+}
+
+void mse_backward(DType dt, const void* a, const void* b, const void* g, void* dx, int64_t n, hipStream_t s) {
+  if (n == 0) return;
+  float two_over_n = 2.f / (float)n;
+  AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((mse_bwd_kernel<T>), dim3(grid_for(n)), dim3(256), 0, s, (const T*)a,
+                                           (const T*)b, (const T*)g, (T*)dx, n, two_over_n));
+  check_launch("mse_backward");
+}
+
+void embedding(DType dt, const void* w, int64_t vocab, int64_t dim, DType idx_dt, const void* idx, int64_t n,
+               void* out, hipStream_t s) {
+  if (n == 0 || dim == 0) return;
+  dim3 grid((unsigned)((dim + 255) / 256), (unsigned)(n < 65535 ? n : 65535));
+  AGPU_ALL_SWITCH(dt, {
+    typedef T TV;
+    AGPU_INT_SWITCH(idx_dt, hipLaunchKernelGGL((embedding_kernel<TV, I>), grid, dim3(256), 0, s, (const TV*)w,
+                                               vocab, dim, (const I*)idx, n, (TV*)out));
+  });
+  check_launch("embedding");
+}
+
+void index_select(DType dt, const void* x, int64_t outer, int64_t size, int64_t inner, DType idx_dt,
+                  const void* idx, int64_t m, void* out, hipStream_t s) {
+  int64_t n = outer * m * inner;
+  if (n == 0) return;
+  AGPU_ALL_SWITCH(dt, {
+    typedef T TV;
+    AGPU_INT_SWITCH(idx_dt, hipLaunchKernelGGL((index_select_kernel<TV, I>), dim3(grid_for(n)), dim3(256), 0, s,
+                                               (const TV*)x, outer, size, inner, (const I*)idx, m, (TV*)out));
+  });
+  check_launch("index_select");
+}
+
+void gather(DType dt, const void* x, int64_t outer, int64_t size, int64_t inner, DType idx_dt, const void* idx,
+            int64_t m, void* out, hipStream_t s) {
+  int64_t n = outer * m * inner;
+  if (n == 0) return;
+  AGPU_ALL_SWITCH(dt, {
+    typedef T TV;
+    AGPU_INT_SWITCH(idx_dt, hipLaunchKernelGGL((gather_kernel<TV, I>), dim3(grid_for(n)), dim3(256), 0, s,
+                                               (const TV*)x, outer, size, inner, (const I*)idx, m, (TV*)out));
+  });
+  check_launch("gather");
+}
+
+}  // namespace k
+}  // namespace agpu

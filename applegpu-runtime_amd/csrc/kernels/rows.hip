@@ -1,0 +1,563 @@
+// Row kernels over the last dimension: softmax, log_softmax, softmax_causal,
+// layer_norm, row reductions (sum/mean/amax/argmax/var), softmax backward and
+// the symmetric per-row int8 quantize / dequantize pair.
+//
+// Reference semantics (crates/core/src/kernel_templates.rs):
+//   softmax: m = max, e = exp(x-m), out = e / sum(e)           :398-430
+//   log_softmax: x - m - log(sum(exp(x-m)))                    :434-465
+//   softmax_causal: columns j <= row only, zeros above          :468-497
+//   argmax: strict > so the first maximum wins, int32 output    :500-520
+//   layer_norm: two-pass mean, population variance,
+//               y = gamma*(x-mean)*inv_std + beta              :1075-1116
+// The reference runs one thread per row; here one 64-lane wavefront owns a
+// row (rows up to 2048 columns stay in registers: a single HBM read and a
+// single write), and a 256-thread workgroup owns longer rows.
+#include "device.hpp"
+
+namespace agpu {
+namespace k {
+using namespace dev;
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one wavefront per row
+
+// Loads 4 consecutive elements at column c (c % 4 == 0) as float, with a
+// per-element guard against `limit`; masked lanes get `fill`.
+template <typename T>
+__device__ __forceinline__ void load4(const T* __restrict__ row, int64_t c, int64_t limit, bool vec,
+                                      float fill, float out[4]) {
+  if (vec && c + 4 <= limit) {
+    if constexpr (sizeof(T) == 4) {
+      float4 v = *(const float4*)(row + c);
+      out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+    } else {
+      T tmp[4];
+      *(float2*)tmp = *(const float2*)(row + c);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[j] = to_f(tmp[j]);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = (c + j < limit) ? to_f(row[c + j]) : fill;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* __restrict__ row, int64_t c, int64_t limit, bool vec,
+                                       const float v[4]) {
+  if (vec && c + 4 <= limit) {
+    if constexpr (sizeof(T) == 4) {
+      *(float4*)(row + c) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      T tmp[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmp[j] = from_f<T>(v[j]);
+      *(float2*)(row + c) = *(float2*)tmp;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c + j < limit) row[c + j] = from_f<T>(v[j]);
+  }
+}
+
+// ── softmax family, register-resident (cols <= 256 * NV) ─────────────────
+template <typename T, int NV>
+__global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict__ x, int64_t ldx,
+                                                    T* __restrict__ y, int64_t ldy, int64_t rows,
+                                                    int64_t cols, int64_t causal_rows, bool vec) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * ldx;
+  T* yr = y + row * ldy;
+  int64_t valid = cols;
+  if (op == kSoftmaxCausal) {
+    int64_t r = row % causal_rows;
+    valid = r + 1 < cols ? r + 1 : cols;
+  }
+  float v[NV][4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 64 + lane) * 4;
+    load4(xr, c, valid, vec, -INFINITY, v[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, v[i][j]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float e = (c + j < valid) ? expf(v[i][j] - mx) : 0.f;
+      sum += e;
+      if (op != kLogSoftmax) v[i][j] = e;
+    }
+  }
+  sum = wave_sum(sum);
+  if (op == kLogSoftmax) {
+    const float ls = logf(sum);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = v[i][j] - mx - ls;
+      store4(yr, c, cols, vec, v[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = (c + j < valid) ? v[i][j] / sum : 0.f;
+      store4(yr, c, cols, vec, v[i]);
+    }
+  }
+}
+
+// Block-wide reductions for 256 threads.
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  return sh[0] + sh[1] + sh[2] + sh[3];
+}
+__device__ __forceinline__ float block_max(float v, float* sh) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+}
+
+// ── softmax family, long rows: one 256-thread block per row, online max/sum ─
+template <typename T>
+__global__ void __launch_bounds__(256) softmax_block(int op, const T* __restrict__ x, int64_t ldx,
+                                                     T* __restrict__ y, int64_t ldy, int64_t cols,
+                                                     int64_t causal_rows) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  T* yr = y + row * ldy;
+  int64_t valid = cols;
+  if (op == kSoftmaxCausal) {
+    int64_t r = row % causal_rows;
+    valid = r + 1 < cols ? r + 1 : cols;
+  }
+  float m = -INFINITY, s = 0.f;
+  for (int64_t c = threadIdx.x; c < valid; c += 256) {
+    float v = to_f(xr[c]);
+    if (v > m) { s = s * expf(m - v) + 1.f; m = v; }
+    else s += expf(v - m);
+  }
+  float gm = block_max(m, sh);
+  float part = (m == -INFINITY) ? 0.f : s * expf(m - gm);
+  float gs = block_sum(part, sh);
+  const float ls = logf(gs);
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    float out;
+    if (c >= valid) out = 0.f;
+    else if (op == kLogSoftmax) out = to_f(xr[c]) - gm - ls;
+    else out = expf(to_f(xr[c]) - gm) / gs;
+    yr[c] = from_f<T>(out);
+  }
+}
+
+// ── layer_norm ────────────────────────────────────────────────────────────
+template <typename T, int NV>
+__global__ void __launch_bounds__(256) layer_norm_wave(const T* __restrict__ x, int64_t ldx,
+                                                       const T* __restrict__ g, const T* __restrict__ b,
+                                                       T* __restrict__ y, int64_t rows, int64_t cols,
+                                                       float eps, bool vec) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * ldx;
+  T* yr = y + row * cols;
+  float v[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 64 + lane) * 4;
+    load4(xr, c, cols, vec, 0.f, v[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += v[i][j];
+  }
+  const float mean = wave_sum(s) / (float)cols;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float d = (c + j < cols) ? v[i][j] - mean : 0.f;
+      q += d * d;
+    }
+  }
+  const float var = wave_sum(q) / (float)cols;
+  const float inv = 1.f / sqrtf(var + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float gv[4], bv[4];
+    load4(g, c, cols, vec, 0.f, gv);
+    load4(b, c, cols, vec, 0.f, bv);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i][j] = gv[j] * (v[i][j] - mean) * inv + bv[j];
+    store4(yr, c, cols, vec, v[i]);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) layer_norm_block(const T* __restrict__ x, int64_t ldx,
+                                                        const T* __restrict__ g, const T* __restrict__ b,
+                                                        T* __restrict__ y, int64_t cols, float eps) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * ldx;
+  T* yr = y + row * cols;
+  float s = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) s += to_f(xr[c]);
+  const float mean = block_sum(s, sh) / (float)cols;
+  float q = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    float d = to_f(xr[c]) - mean;
+    q += d * d;
+  }
+  const float var = block_sum(q, sh) / (float)cols;
+  const float inv = 1.f / sqrtf(var + eps);
+  for (int64_t c = threadIdx.x; c < cols; c += 256)
+    yr[c] = from_f<T>(to_f(g[c]) * (to_f(xr[c]) - mean) * inv + to_f(b[c]));
+}
+
+// ── row reductions (one wavefront per row) ───────────────────────────────
+template <typename TI, typename TO>
+__global__ void __launch_bounds__(256) row_reduce_wave(int op, const TI* __restrict__ x, int64_t ldx,
+                                                       TO* __restrict__ y, int64_t rows, int64_t cols,
+                                                       int correction) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TI* xr = x + row * ldx;
+  if (op == kRArgmax) {
+    // First occurrence of the maximum; NaN counts as the maximum (the first
+    // NaN wins), as torch.argmax on the CPU does.
+    float best = -INFINITY;
+    int64_t bi = -1;
+    for (int64_t c = lane; c < cols; c += 64) {
+      float v = to_f(xr[c]);
+      bool better = bi < 0 || (isnan(v) && !isnan(best)) || (!isnan(best) && v > best);
+      if (better) { best = v; bi = c; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      float ob = __shfl_xor(best, m, 64);
+      int64_t oi = __shfl_xor(bi, m, 64);
+      bool take;
+      if (oi < 0) take = false;
+      else if (bi < 0) take = true;
+      else if (isnan(ob) != isnan(best)) take = isnan(ob);
+      else if (isnan(ob)) take = oi < bi;
+      else take = ob > best || (ob == best && oi < bi);
+      if (take) { best = ob; bi = oi; }
+    }
+    if (lane == 0) y[row] = (TO)(bi < 0 ? 0 : bi);
+    return;
+  }
+  if (op == kRAmax) {
+    float m = -INFINITY;
+    for (int64_t c = lane; c < cols; c += 64) {
+      float v = to_f(xr[c]);
+      m = (isnan(v) || isnan(m)) ? NAN : fmaxf(m, v);
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) {
+      float o = __shfl_xor(m, s, 64);
+      m = (isnan(o) || isnan(m)) ? NAN : fmaxf(m, o);
+    }
+    if (lane == 0) y[row] = (TO)m;
+    return;
+  }
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) s += to_f(xr[c]);
+  s = wave_sum(s);
+  if (op == kRSum) { if (lane == 0) y[row] = (TO)s; return; }
+  float mean = s / (float)cols;
+  if (op == kRMean) { if (lane == 0) y[row] = (TO)mean; return; }
+  float q = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) {
+    float d = to_f(xr[c]) - mean;
+    q += d * d;
+  }
+  q = wave_sum(q);
+  if (lane == 0) y[row] = (TO)(q / (float)(cols - correction));
+}
+
+// Integer sums stay exact in 64-bit.
+template <typename TI, typename TO>
+__global__ void __launch_bounds__(256) row_sum_int(const TI* __restrict__ x, int64_t ldx, TO* __restrict__ y,
+                                                   int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const TI* xr = x + row * ldx;
+  long long s = 0;
+  for (int64_t c = lane; c < cols; c += 64) s += (long long)xr[c];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+  if (lane == 0) y[row] = (TO)s;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) softmax_bwd_wave(const T* __restrict__ dy, const T* __restrict__ yv,
+                                                        T* __restrict__ dx, int64_t rows, int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* a = dy + row * cols;
+  const T* b = yv + row * cols;
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) s += to_f(a[c]) * to_f(b[c]);
+  s = wave_sum(s);
+  for (int64_t c = lane; c < cols; c += 64) dx[row * cols + c] = from_f<T>(to_f(b[c]) * (to_f(a[c]) - s));
+}
+
+// ── per-row int8 quantize: one 256-thread block per row ───────────────────
+// scale = absmax/127 (fp32), q = clamp(rint(x / scale), -128, 127); x / scale
+// is IEEE division and rint rounds half to even, as torch.round does.  A row
+// of zeros gets scale 0 and codes 0.
+template <typename T, int NV>
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const T* __restrict__ x, int8_t* __restrict__ q,
+                                                            float* __restrict__ scale, int64_t cols, bool vec) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * cols;
+  int8_t* qr = q + row * cols;
+  float v[NV][4];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 256 + threadIdx.x) * 4;
+    load4(xr, c, cols, vec, 0.f, v[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fabsf(v[i][j]));
+  }
+  const float amax = block_max(m, sh);
+  const float sc = amax / 127.f;
+  if (threadIdx.x == 0) scale[row] = sc;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 256 + threadIdx.x) * 4;
+    int8_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float r = sc == 0.f ? 0.f : rintf(v[i][j] / sc);
+      r = fminf(fmaxf(r, -128.f), 127.f);
+      b[j] = (int8_t)(int)r;
+    }
+    if (vec && c + 4 <= cols) {
+      *(int32_t*)(qr + c) = *(int32_t*)b;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c + j < cols) qr[c + j] = b[j];
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) quantize_rows_loop(const T* __restrict__ x, int8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int64_t cols) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * cols;
+  float m = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) m = fmaxf(m, fabsf(to_f(xr[c])));
+  const float sc = block_max(m, sh) / 127.f;
+  if (threadIdx.x == 0) scale[row] = sc;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    float r = sc == 0.f ? 0.f : rintf(to_f(xr[c]) / sc);
+    q[row * cols + c] = (int8_t)(int)fminf(fmaxf(r, -128.f), 127.f);
+  }
+}
+
+// y[r, c] = q[r, c] * scale[r]; grid.y walks rows, 4 codes per thread.
+template <typename T>
+__global__ void __launch_bounds__(256) dequantize_rows_kernel(const int8_t* __restrict__ q,
+                                                              const float* __restrict__ scale,
+                                                              T* __restrict__ y, int64_t rows, int64_t cols,
+                                                              bool vec) {
+  const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c >= cols) return;
+  for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
+  const float sc = scale[row];
+  const int8_t* qr = q + row * cols;
+  T* yr = y + row * cols;
+  float v[4];
+  if (vec && c + 4 <= cols) {
+    int32_t w = *(const int32_t*)(qr + c);
+    const int8_t* b = (const int8_t*)&w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (float)b[j] * sc;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = c + j < cols ? (float)qr[c + j] * sc : 0.f;
+  }
+  store4(yr, c, cols, vec, v);
+  }
+}
+
+bool vec_ok(const void* p, int64_t ld, size_t esz) {
+  return (((uintptr_t)p) % (4 * esz)) == 0 && (ld % 4) == 0;
+}
+
+unsigned rows_grid(int64_t rows) { return (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock); }
+
+template <typename T, int NV>
+void sm_nv(int op, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols, int64_t crow,
+           bool vec, hipStream_t s) {
+  hipLaunchKernelGGL((softmax_wave<T, NV>), dim3(rows_grid(rows)), dim3(256), 0, s, op, (const T*)x, ldx, (T*)y, ldy,
+                     rows, cols, crow, vec);
+}
+
+template <typename T>
+void sm_launch(int op, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols, int64_t crow,
+               hipStream_t s) {
+  bool vec = vec_ok(x, ldx, sizeof(T)) && vec_ok(y, ldy, sizeof(T));
+  switch ((cols + 255) / 256) {
+    case 1: sm_nv<T, 1>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 2: sm_nv<T, 2>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 3: sm_nv<T, 3>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 4: sm_nv<T, 4>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 5: sm_nv<T, 5>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 6: sm_nv<T, 6>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 7: sm_nv<T, 7>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    case 8: sm_nv<T, 8>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
+    default:
+      hipLaunchKernelGGL((softmax_block<T>), dim3((unsigned)rows), dim3(256), 0, s, op, (const T*)x, ldx, (T*)y, ldy,
+                         cols, crow);
+  }
+}
+
+template <typename T, int NV>
+void ln_nv(const void* x, int64_t ldx, const void* g, const void* b, void* y, int64_t rows, int64_t cols, float eps,
+           bool vec, hipStream_t s) {
+  hipLaunchKernelGGL((layer_norm_wave<T, NV>), dim3(rows_grid(rows)), dim3(256), 0, s, (const T*)x, ldx, (const T*)g,
+                     (const T*)b, (T*)y, rows, cols, eps, vec);
+}
+
+template <typename T>
+void ln_launch(const void* x, int64_t ldx, const void* g, const void* b, void* y, int64_t rows, int64_t cols,
+               float eps, hipStream_t s) {
+  bool vec = vec_ok(x, ldx, sizeof(T)) && vec_ok(y, cols, sizeof(T)) && vec_ok(g, 0, sizeof(T)) &&
+             vec_ok(b, 0, sizeof(T));
+  switch ((cols + 255) / 256) {
+    case 1: ln_nv<T, 1>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 2: ln_nv<T, 2>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 3: ln_nv<T, 3>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 4: ln_nv<T, 4>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 5: ln_nv<T, 5>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 6: ln_nv<T, 6>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 7: ln_nv<T, 7>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    case 8: ln_nv<T, 8>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
+    default:
+      hipLaunchKernelGGL((layer_norm_block<T>), dim3((unsigned)rows), dim3(256), 0, s, (const T*)x, ldx, (const T*)g,
+                         (const T*)b, (T*)y, cols, eps);
+  }
+}
+
+template <typename T>
+void q_launch(const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols, hipStream_t s) {
+  bool vec = vec_ok(x, cols, sizeof(T)) && vec_ok(q, cols, 1);
+  int64_t nv = (cols + 1023) / 1024;
+  dim3 g((unsigned)rows);
+  if (nv <= 1) hipLaunchKernelGGL((quantize_rows_kernel<T, 1>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
+  else if (nv <= 2) hipLaunchKernelGGL((quantize_rows_kernel<T, 2>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
+  else if (nv <= 4) hipLaunchKernelGGL((quantize_rows_kernel<T, 4>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
+  else if (nv <= 8) hipLaunchKernelGGL((quantize_rows_kernel<T, 8>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
+  else hipLaunchKernelGGL((quantize_rows_loop<T>), g, dim3(256), 0, s, (const T*)x, q, scale, cols);
+}
+
+}  // namespace
+
+void softmax_rows(int op, DType dt, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows,
+                  int64_t cols, int64_t causal_rows, hipStream_t s) {
+  if (rows == 0 || cols == 0) return;
+  if (causal_rows <= 0) causal_rows = rows;
+  AGPU_FLOAT_SWITCH(dt, sm_launch<T>(op, x, ldx, y, ldy, rows, cols, causal_rows, s));
+  check_launch("softmax_rows");
+}
+
+void layer_norm(DType dt, const void* x, int64_t ldx, const void* gamma, const void* beta, void* y,
+                int64_t rows, int64_t cols, float eps, hipStream_t s) {
+  if (rows == 0 || cols == 0) return;
+  AGPU_FLOAT_SWITCH(dt, ln_launch<T>(x, ldx, gamma, beta, y, rows, cols, eps, s));
+  check_launch("layer_norm");
+}
+
+void row_reduce(int op, DType in, DType out, const void* x, int64_t ldx, void* y, int64_t rows,
+                int64_t cols, int correction, hipStream_t s) {
+  if (rows == 0) return;
+  if (op == kRArgmax) {
+    if (out != DType::I32) fail("argmax output must be int32");
+    AGPU_ALL_SWITCH(in, {
+      if constexpr (!std::is_same<T, int64_t>::value)
+        hipLaunchKernelGGL((row_reduce_wave<T, int32_t>), dim3(rows_grid(rows)), dim3(256), 0, s, op,
+                           (const T*)x, ldx, (int32_t*)y, rows, cols, correction);
+      else
+        fail("argmax over int64 is not supported");
+    });
+  } else if (dtype_is_float(in)) {
+    if (out != in) fail("row reduction output dtype must match input");
+    AGPU_FLOAT_SWITCH(in, hipLaunchKernelGGL((row_reduce_wave<T, T>), dim3(rows_grid(rows)), dim3(256), 0, s,
+                                             op, (const T*)x, ldx, (T*)y, rows, cols, correction));
+  } else if (op == kRSum) {
+    AGPU_ALL_SWITCH(in, {
+      typedef T TI;
+      AGPU_ALL_SWITCH(out, hipLaunchKernelGGL((row_sum_int<TI, T>), dim3(rows_grid(rows)), dim3(256), 0, s,
+                                              (const TI*)x, ldx, (T*)y, rows, cols));
+    });
+  } else if (op == kRAmax) {
+    AGPU_ALL_SWITCH(in, hipLaunchKernelGGL((row_reduce_wave<T, T>), dim3(rows_grid(rows)), dim3(256), 0, s,
+                                           op, (const T*)x, ldx, (T*)y, rows, cols, correction));
+  } else {
+    fail("row reduction %d needs a float dtype", op);
+  }
+  check_launch("row_reduce");
+}
+
+void softmax_backward(DType dt, const void* dy, const void* y, void* dx, int64_t rows, int64_t cols,
+                      hipStream_t s) {
+  if (rows == 0) return;
+  AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((softmax_bwd_wave<T>), dim3(rows_grid(rows)), dim3(256), 0, s,
+                                           (const T*)dy, (const T*)y, (T*)dx, rows, cols));
+  check_launch("softmax_backward");
+}
+
+void quantize_rows(DType in, const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols,
+                   hipStream_t s) {
+  if (rows == 0) return;
+  AGPU_FLOAT_SWITCH(in, q_launch<T>(x, q, scale, rows, cols, s));
+  check_launch("quantize_rows");
+}
+
+void dequantize_rows(DType out, const int8_t* q, const float* scale, void* y, int64_t rows, int64_t cols,
+                     hipStream_t s) {
+  if (rows == 0 || cols == 0) return;
+  AGPU_FLOAT_SWITCH(out, {
+    bool vec = vec_ok(q, cols, 1) && vec_ok(y, cols, sizeof(T));
+    dim3 grid((unsigned)((cols + 1023) / 1024), (unsigned)(rows < 65535 ? rows : 65535));
+    hipLaunchKernelGGL((dequantize_rows_kernel<T>), grid, dim3(256), 0, s, q, scale, (T*)y, rows, cols, vec);
+  });
+  check_launch("dequantize_rows");
+}
+
+}  // namespace k
+}  // namespace agpu

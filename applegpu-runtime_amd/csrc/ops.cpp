@@ -1,0 +1,862 @@
+// Op layer: validation (the reference's dtype/shape rules), layouts, launches.
+//
+// Reference rules followed (crates/core/src/ops.rs unless noted):
+//   dtype classes per op              :29-170 (validate_op_dtype)
+//   binary: same dtype, broadcast     :172-202; comparisons -> bool :222-246
+//   matmul: >=2-D, inner dims match, batch dims broadcast            :390-462
+//   softmax / log_softmax >=1-D       :464-508; softmax_causal >=2-D :1367-1388
+//   layer_norm gamma/beta shape [C]   :618-653
+//   embedding: W 2-D, int32 indices   :1194-1232
+//   slice / concat / add_bias         :1234-1365
+//   argmax -> int32, [...,C] -> [...] (1-D -> [1])                   :1390-1415
+//   gather / index_select             :1729-1835
+//   quantize / dequantize             :2250-2297
+//   sum_dim output shape              crates/core/src/eager.rs:827-855
+#include "ops.hpp"
+#include "graph.hpp"
+
+#include <cmath>
+
+namespace agpu {
+namespace ops {
+
+static Runtime& rt() { return Runtime::get(); }
+
+// In meta mode (lazy recording) outputs are descriptions without storage and
+// nothing is launched.
+static TensorP alloc_out(DType dt, const std::vector<int64_t>& dims) {
+  if (meta_mode()) return make_meta(dt, dims);
+  return rt().alloc(dt, dims);
+}
+static BufferP scratch(size_t bytes) {
+  if (meta_mode()) return nullptr;
+  return rt().pool().acquire(bytes);
+}
+#define LAUNCH if (!meta_mode())
+
+// ── dtype rules ────────────────────────────────────────────────────────────
+enum Cls { kFloatOnly, kNumeric, kAny, kNotBool, kOrdered, kEquality, kIntOrBool, kIntOnly };
+
+static void check_dtype(const char* op, Cls c, DType d) {
+  if (d == DType::F64) fail("%s: float64 is not supported on this device path", op);
+  bool ok = true;
+  switch (c) {
+    case kFloatOnly: ok = dtype_is_float(d); break;
+    case kNumeric: ok = !(d == DType::Bool || d == DType::I8 || d == DType::I16); break;
+    case kAny: ok = true; break;
+    case kNotBool: ok = d != DType::Bool; break;
+    case kOrdered:
+      ok = dtype_is_float(d) || d == DType::I32 || d == DType::I64 || d == DType::U8 || d == DType::U32;
+      break;
+    case kEquality:
+      ok = dtype_is_float(d) || d == DType::I32 || d == DType::I64 || d == DType::U8 || d == DType::U32 ||
+           d == DType::Bool;
+      break;
+    case kIntOrBool:
+      ok = d == DType::I32 || d == DType::I64 || d == DType::U8 || d == DType::U32 || d == DType::Bool;
+      break;
+    case kIntOnly: ok = d == DType::I32 || d == DType::I64 || d == DType::U8 || d == DType::U32; break;
+  }
+  if (!ok) fail("%s does not support dtype %s", op, dtype_name(d));
+}
+
+static const char* bin_name(int op) {
+  static const char* n[] = {"add", "sub", "mul", "div", "elem_min", "elem_max", "mod", "bitwise_and",
+                            "bitwise_or", "bitwise_xor", "lt", "gt", "le", "ge", "eq", "ne",
+                            "threshold_backward"};
+  return op >= 0 && op <= k::kThresholdBwd ? n[op] : "binary";
+}
+
+static Cls bin_class(int op) {
+  switch (op) {
+    case k::kAdd: case k::kSub: case k::kMul: case k::kDiv: return kNumeric;
+    case k::kMin: case k::kMax: case k::kMod: return kNumeric;
+    case k::kAnd: case k::kOr: case k::kXor: return kIntOrBool;
+    case k::kLt: case k::kGt: case k::kLe: case k::kGe: return kOrdered;
+    case k::kEq: case k::kNe: return kEquality;
+    case k::kThresholdBwd: return kFloatOnly;
+  }
+  return kAny;
+}
+
+// ── layouts ────────────────────────────────────────────────────────────────
+k::ND nd_shape(const std::vector<int64_t>& dims) {
+  k::ND s;
+  s.ndim = (int)dims.size();
+  int64_t st = 1;
+  for (int i = s.ndim - 1; i >= 0; --i) {
+    s.shape[i] = dims[i];
+    s.stride[i] = st;
+    st *= dims[i];
+  }
+  return s;
+}
+
+k::ND nd_for(const Tensor& t, const std::vector<int64_t>& out) {
+  k::ND s;
+  s.ndim = (int)out.size();
+  const int off = s.ndim - t.ndim;
+  if (off < 0) fail("internal: operand has more dims than the output");
+  for (int i = 0; i < s.ndim; ++i) {
+    s.shape[i] = out[i];
+    if (i < off) { s.stride[i] = 0; continue; }
+    const int ti = i - off;
+    s.stride[i] = (t.shape[ti] == out[i] && t.shape[ti] != 1) ? t.strides[ti] : 0;
+  }
+  return s;
+}
+
+static TensorP materialize(const TensorP& t) {
+  TensorP out = alloc_out(t->dtype, t->dims());
+  auto dims = t->dims();
+  LAUNCH k::unary(k::kCopy, t->dtype, t->dtype, t->data(), nd_for(*t, dims), out->data(), nd_shape(dims), 0, 0,
+           rt().stream());
+  return out;
+}
+
+TensorP contiguous(const TensorP& t) {
+  if (meta_mode()) return t->is_contiguous() ? t : make_meta(t->dtype, t->dims());
+  if (t->pending()) fail("internal: tensor still pending");
+  if (t->is_contiguous()) return t;
+  return materialize(t);
+}
+
+bool as_rows(const Tensor& t, int64_t* rows, int64_t* ld) {
+  if (t.ndim == 0) { *rows = 1; *ld = 1; return true; }
+  const int64_t cols = t.shape[t.ndim - 1];
+  if (cols > 1 && t.strides[t.ndim - 1] != 1) return false;
+  int64_t r = 1;
+  for (int i = 0; i < t.ndim - 1; ++i) r *= t.shape[i];
+  // leading dims must collapse to a single row stride
+  int64_t stride = -1;
+  int64_t expect_inner = -1;
+  for (int i = t.ndim - 2; i >= 0; --i) {
+    if (t.shape[i] == 1) continue;
+    if (stride < 0) {
+      stride = t.strides[i];
+      expect_inner = stride * t.shape[i];
+    } else {
+      if (t.strides[i] != expect_inner) return false;
+      expect_inner *= t.shape[i];
+    }
+  }
+  if (stride < 0) stride = cols;
+  if (r > 1 && stride < cols) return false;
+  *rows = r;
+  *ld = stride;
+  return true;
+}
+
+TensorP view(const TensorP& base, const std::vector<int64_t>& shape, const std::vector<int64_t>& strides,
+             int64_t offset_elems) {
+  if (shape.size() != strides.size()) fail("view: shape and strides differ in length");
+  auto t = make_meta(base->dtype, shape);
+  for (size_t i = 0; i < shape.size(); ++i) t->strides[i] = strides[i];
+  t->buf = base->buf;
+  t->offset = base->offset + offset_elems * (int64_t)dtype_size(base->dtype);
+  // Bounds: the view must stay inside the base allocation.
+  int64_t last = 0;
+  for (size_t i = 0; i < shape.size(); ++i) {
+    if (shape[i] == 0) { last = -1; break; }
+    if (strides[i] < 0) fail("view: negative strides are not supported");
+    last += (shape[i] - 1) * strides[i];
+  }
+  if (base->buf && last >= 0 &&
+      (size_t)(t->offset + (last + 1) * (int64_t)dtype_size(base->dtype)) > base->buf->bytes)
+    fail("view: shape %s with the given strides/offset exceeds the base storage", shape_str(shape).c_str());
+  return t;
+}
+
+TensorP reshape(const TensorP& t, const std::vector<int64_t>& shape) {
+  int64_t n = 1;
+  for (auto d : shape) n *= d;
+  if (n != t->numel())
+    fail("Cannot reshape: old shape %s has %lld elements, new shape %s has %lld",
+         shape_str(t->dims()).c_str(), (long long)t->numel(), shape_str(shape).c_str(), (long long)n);
+  TensorP src = t;
+  // Try to express the new shape as a view: split/merge dims only inside
+  // runs that are contiguous with each other.
+  std::vector<int64_t> nstr(shape.size());
+  {
+    int oi = src->ndim - 1, ni = (int)shape.size() - 1;
+    bool ok = true;
+    while (ok && (oi >= 0 || ni >= 0)) {
+      // skip size-1 dims
+      if (ni >= 0 && shape[ni] == 1) { nstr[ni] = ni + 1 < (int)shape.size() ? nstr[ni + 1] * shape[ni + 1] : 1; --ni; continue; }
+      if (oi >= 0 && src->shape[oi] == 1) { --oi; continue; }
+      if (oi < 0 || ni < 0) { ok = false; break; }
+      // gather a group of old dims and new dims with equal products
+      int64_t op = src->shape[oi], np = shape[ni];
+      int o_lo = oi, n_lo = ni;
+      while (op != np) {
+        if (op < np) { if (--o_lo < 0) { ok = false; break; } op *= src->shape[o_lo]; }
+        else { if (--n_lo < 0) { ok = false; break; } np *= shape[n_lo]; }
+      }
+      if (!ok) break;
+      // old dims o_lo..oi must be mutually contiguous (ignoring size-1 dims)
+      int64_t inner_stride = src->strides[oi];
+      int64_t expect = inner_stride;
+      for (int j = oi; j >= o_lo; --j) {
+        if (src->shape[j] == 1) continue;
+        if (src->strides[j] != expect) { ok = false; break; }
+        expect *= src->shape[j];
+      }
+      if (!ok) break;
+      int64_t s = inner_stride;
+      for (int j = ni; j >= n_lo; --j) {
+        nstr[j] = s;
+        s *= shape[j];
+      }
+      oi = o_lo - 1;
+      ni = n_lo - 1;
+    }
+    if (ok && !src->pending()) {
+      auto v = make_meta(src->dtype, shape);
+      for (size_t i = 0; i < shape.size(); ++i) v->strides[i] = nstr[i];
+      v->buf = src->buf;
+      v->offset = src->offset;
+      return v;
+    }
+  }
+  TensorP c = materialize(src);
+  auto v = make_meta(c->dtype, shape);
+  v->buf = c->buf;
+  v->offset = c->offset;
+  return v;
+}
+
+TensorP transpose_dims(const TensorP& t, int d0, int d1) {
+  if (d0 < 0 || d1 < 0 || d0 >= t->ndim || d1 >= t->ndim)
+    fail("transpose dims (%d, %d) out of range for %dD tensor", d0, d1, t->ndim);
+  auto v = std::make_shared<Tensor>(*t);
+  v->node = nullptr;
+  v->ext_refs = 0;
+  std::swap(v->shape[d0], v->shape[d1]);
+  std::swap(v->strides[d0], v->strides[d1]);
+  return v;
+}
+
+TensorP slice(const TensorP& t, int dim, int64_t start, int64_t end) {
+  if (dim < 0 || dim >= t->ndim) fail("slice dim %d >= ndim %d", dim, t->ndim);
+  if (start >= end) fail("slice start %lld >= end %lld", (long long)start, (long long)end);
+  if (end > t->shape[dim]) fail("slice end %lld > shape[%d] = %lld", (long long)end, dim, (long long)t->shape[dim]);
+  auto v = std::make_shared<Tensor>(*t);
+  v->node = nullptr;
+  v->ext_refs = 0;
+  v->shape[dim] = end - start;
+  v->offset = t->offset + start * t->strides[dim] * (int64_t)dtype_size(t->dtype);
+  return v;
+}
+
+// ── elementwise ────────────────────────────────────────────────────────────
+TensorP binary(int op, const TensorP& a, const TensorP& b, float p0) {
+  if (a->dtype != b->dtype) fail("Dtype mismatch: %s vs %s", dtype_name(a->dtype), dtype_name(b->dtype));
+  check_dtype(bin_name(op), bin_class(op), a->dtype);
+  auto out_dims = broadcast_shapes(a->dims(), b->dims());
+  bool cmp = op >= k::kLt && op <= k::kNe;
+  DType odt = cmp ? DType::Bool : a->dtype;
+  TensorP out = alloc_out(odt, out_dims);
+  LAUNCH k::binary(op, a->dtype, odt, a->data(), nd_for(*a, out_dims), b->data(), nd_for(*b, out_dims), out->data(),
+            nd_shape(out_dims), p0, rt().stream());
+  return out;
+}
+
+static const char* un_name(int op) {
+  switch (op) {
+    case k::kNeg: return "neg"; case k::kRelu: return "relu"; case k::kExp: return "exp";
+    case k::kLog: return "log"; case k::kSqrt: return "sqrt"; case k::kAbs: return "abs";
+    case k::kSign: return "sign"; case k::kTanh: return "tanh"; case k::kSin: return "sin";
+    case k::kCos: return "cos"; case k::kSigmoid: return "sigmoid"; case k::kGelu: return "gelu";
+    case k::kGeluExact: return "gelu_exact"; case k::kScale: return "scalar_mul"; case k::kPow: return "pow";
+    case k::kClamp: return "clamp"; case k::kBitNot: return "bitwise_not"; case k::kLogicalNot: return "logical_not";
+    case k::kShl: return "shl"; case k::kShr: return "shr"; case k::kCopy: return "copy";
+  }
+  return "unary";
+}
+
+static Cls un_class(int op) {
+  switch (op) {
+    case k::kNeg: case k::kAbs: case k::kSign: case k::kScale: case k::kClamp: return kNumeric;
+    case k::kBitNot: return kIntOrBool;
+    case k::kShl: case k::kShr: return kIntOnly;
+    case k::kLogicalNot: case k::kCopy: return kAny;
+    case k::kPow: return kFloatOnly;
+  }
+  return kFloatOnly;
+}
+
+TensorP unary(int op, const TensorP& x, float p0, float p1) {
+  check_dtype(un_name(op), un_class(op), x->dtype);
+  DType odt = op == k::kLogicalNot ? DType::Bool : x->dtype;
+  auto dims = x->dims();
+  TensorP out = alloc_out(odt, dims);
+  LAUNCH k::unary(op, x->dtype, odt, x->data(), nd_for(*x, dims), out->data(), nd_shape(dims), p0, p1, rt().stream());
+  return out;
+}
+
+TensorP cast(const TensorP& x, DType dt) {
+  if (x->dtype == DType::F64 || dt == DType::F64) fail("cast: float64 is not supported on this device path");
+  if (x->dtype == dt) return x;
+  auto dims = x->dims();
+  TensorP out = alloc_out(dt, dims);
+  LAUNCH k::unary(k::kCopy, x->dtype, dt, x->data(), nd_for(*x, dims), out->data(), nd_shape(dims), 0, 0, rt().stream());
+  return out;
+}
+
+TensorP quantize(const TensorP& x, DType dt, float scale, int zp) {
+  if (!dtype_is_float(x->dtype) || x->dtype == DType::F64) fail("Quantize input must be a float dtype");
+  if (dt != DType::I8 && dt != DType::U8) fail("Quantize target must be Int8 or UInt8");
+  if (scale == 0.f) fail("Quantize scale must be non-zero");
+  auto dims = x->dims();
+  TensorP out = alloc_out(dt, dims);
+  LAUNCH k::unary(k::kQuantize, x->dtype, dt, x->data(), nd_for(*x, dims), out->data(), nd_shape(dims), scale, (float)zp,
+           rt().stream());
+  return out;
+}
+
+TensorP dequantize(const TensorP& x, DType dt, float scale, int zp) {
+  if (x->dtype != DType::I8 && x->dtype != DType::U8) fail("Dequantize input must be Int8 or UInt8");
+  if (!dtype_is_float(dt) || dt == DType::F64) fail("Dequantize target must be a float dtype");
+  auto dims = x->dims();
+  TensorP out = alloc_out(dt, dims);
+  LAUNCH k::unary(k::kDequantize, x->dtype, dt, x->data(), nd_for(*x, dims), out->data(), nd_shape(dims), scale,
+           (float)zp, rt().stream());
+  return out;
+}
+
+TensorP where(const TensorP& c, const TensorP& x, const TensorP& y) {
+  if (x->dtype != y->dtype) fail("where: dtype mismatch %s vs %s", dtype_name(x->dtype), dtype_name(y->dtype));
+  check_dtype("where", kAny, x->dtype);
+  auto dims = broadcast_shapes(broadcast_shapes(c->dims(), x->dims()), y->dims());
+  TensorP out = alloc_out(x->dtype, dims);
+  LAUNCH k::where(c->dtype, x->dtype, c->data(), nd_for(*c, dims), x->data(), nd_for(*x, dims), y->data(),
+           nd_for(*y, dims), out->data(), nd_shape(dims), rt().stream());
+  return out;
+}
+
+TensorP full(DType dt, const std::vector<int64_t>& dims, float value) {
+  TensorP out = alloc_out(dt, dims);
+  LAUNCH k::unary(k::kFill, dt, dt, out->data(), nd_shape(dims), out->data(), nd_shape(dims), value, 0, rt().stream());
+  return out;
+}
+
+TensorP masked_fill(const TensorP& x, const TensorP& mask, float value) {
+  TensorP v = full(x->dtype, {1}, value);
+  return where(mask, v, x);
+}
+
+TensorP tri(const TensorP& x, bool upper, int64_t diag) {
+  if (x->ndim < 2) fail("%s requires at least 2D tensor", upper ? "triu" : "tril");
+  TensorP c = contiguous(x);
+  int64_t rows = c->shape[c->ndim - 2], cols = c->shape[c->ndim - 1];
+  TensorP out = alloc_out(c->dtype, c->dims());
+  LAUNCH k::tri(c->dtype, upper, diag, c->data(), out->data(), c->numel() / std::max<int64_t>(rows * cols, 1), rows,
+         cols, rt().stream());
+  return out;
+}
+
+TensorP threshold_backward(const TensorP& grad, const TensorP& input, float thr) {
+  if (grad->dtype != input->dtype)
+    fail("dtype mismatch: %s vs %s", dtype_name(grad->dtype), dtype_name(input->dtype));
+  return binary(k::kThresholdBwd, grad, input, thr);
+}
+
+TensorP add_bias(const TensorP& x, const TensorP& bias) {
+  check_dtype("add_bias", kFloatOnly, x->dtype);
+  if (x->dtype != bias->dtype)
+    fail("add_bias dtype mismatch: %s vs %s", dtype_name(x->dtype), dtype_name(bias->dtype));
+  if (x->ndim < 2) fail("add_bias requires >= 2D input, got %s", shape_str(x->dims()).c_str());
+  if (bias->ndim != 1) fail("add_bias requires 1D bias, got %s", shape_str(bias->dims()).c_str());
+  if (bias->shape[0] != x->shape[1])
+    fail("add_bias bias length %lld != input dim 1 %lld", (long long)bias->shape[0], (long long)x->shape[1]);
+  TensorP c = contiguous(x);
+  TensorP b = contiguous(bias);
+  int64_t cs = 1;
+  for (int i = 2; i < c->ndim; ++i) cs *= c->shape[i];
+  TensorP out = alloc_out(c->dtype, c->dims());
+  LAUNCH k::add_bias(c->dtype, c->data(), b->data(), out->data(), c->numel(), c->shape[1], cs, rt().stream());
+  return out;
+}
+
+void axpy_inplace(const TensorP& self, const TensorP& other, float alpha) {
+  if (!self->is_contiguous()) fail("in-place op on non-contiguous tensor not yet supported");
+  if (self->dtype != other->dtype)
+    fail("dtype mismatch: %s vs %s", dtype_name(self->dtype), dtype_name(other->dtype));
+  check_dtype("add_scaled_inplace", kFloatOnly, self->dtype);
+  auto dims = self->dims();
+  broadcast_shapes(dims, other->dims());  // validates
+  if (other->ndim > self->ndim) fail("in-place add: other has more dims than self");
+  for (int i = 0; i < other->ndim; ++i) {
+    int64_t od = other->shape[other->ndim - 1 - i], sd = self->shape[self->ndim - 1 - i];
+    if (od != sd && od != 1) fail("in-place add: cannot broadcast %s onto %s", shape_str(other->dims()).c_str(),
+                                  shape_str(dims).c_str());
+  }
+  LAUNCH k::axpy(self->dtype, self->data(), nd_shape(dims), other->data(), nd_for(*other, dims), alpha, rt().stream());
+}
+
+void copy_into(const TensorP& dst, const TensorP& src) {
+  auto dims = dst->dims();
+  if (src->numel() != dst->numel()) fail("copy: element counts differ (%lld vs %lld)", (long long)src->numel(),
+                                         (long long)dst->numel());
+  TensorP s = src;
+  if (src->dims() != dims) s = reshape(src, dims);
+  if (dst->is_contiguous()) {
+    LAUNCH k::unary(k::kCopy, s->dtype, dst->dtype, s->data(), nd_for(*s, dims), dst->data(), nd_shape(dims), 0, 0,
+             rt().stream());
+    return;
+  }
+  fail("copy into a non-contiguous destination is not supported");
+}
+
+// ── rows ───────────────────────────────────────────────────────────────────
+TensorP softmax(const TensorP& x, int mode) {
+  const char* name = mode == k::kSoftmax ? "softmax" : mode == k::kLogSoftmax ? "log_softmax" : "softmax_causal";
+  check_dtype(name, kFloatOnly, x->dtype);
+  if (mode == k::kSoftmaxCausal) {
+    if (x->ndim < 2) fail("softmax_causal requires at least 2D tensor, got %s", shape_str(x->dims()).c_str());
+  } else if (x->ndim < 1) {
+    fail("%s requires at least 1D tensor", name);
+  }
+  TensorP src = x;
+  int64_t rows, ld;
+  if (!as_rows(*src, &rows, &ld)) {
+    src = contiguous(x);
+    as_rows(*src, &rows, &ld);
+  }
+  const int64_t cols = x->shape[x->ndim - 1];
+  TensorP out = alloc_out(x->dtype, x->dims());
+  int64_t crow = mode == k::kSoftmaxCausal ? x->shape[x->ndim - 2] : rows;
+  LAUNCH k::softmax_rows(mode, x->dtype, src->data(), ld, out->data(), cols, rows, cols, crow, rt().stream());
+  return out;
+}
+
+TensorP layer_norm(const TensorP& x, const TensorP& g, const TensorP& b, float eps) {
+  check_dtype("layer_norm", kFloatOnly, x->dtype);
+  if (x->ndim < 1) fail("layer_norm requires at least 1D input");
+  const int64_t cols = x->shape[x->ndim - 1];
+  if (!(g->ndim == 1 && g->shape[0] == cols)) fail("gamma shape %s must be [%lld]", shape_str(g->dims()).c_str(), (long long)cols);
+  if (!(b->ndim == 1 && b->shape[0] == cols)) fail("beta shape %s must be [%lld]", shape_str(b->dims()).c_str(), (long long)cols);
+  if (g->dtype != x->dtype || b->dtype != x->dtype) fail("layer_norm: gamma/beta dtype must match the input");
+  TensorP src = x;
+  int64_t rows, ld;
+  if (!as_rows(*src, &rows, &ld)) {
+    src = contiguous(x);
+    as_rows(*src, &rows, &ld);
+  }
+  TensorP gc = contiguous(g), bc = contiguous(b);
+  TensorP out = alloc_out(x->dtype, x->dims());
+  LAUNCH k::layer_norm(x->dtype, src->data(), ld, gc->data(), bc->data(), out->data(), rows, cols, eps, rt().stream());
+  return out;
+}
+
+TensorP row_reduce(int op, const TensorP& x, int correction) {
+  const char* name = op == k::kRSum ? "sum" : op == k::kRMean ? "mean" : op == k::kRAmax ? "amax"
+                     : op == k::kRArgmax ? "argmax" : "var";
+  if (op == k::kRSum || op == k::kRArgmax) check_dtype(name, kNotBool, x->dtype);
+  else if (op == k::kRAmax) check_dtype(name, kNotBool, x->dtype);
+  else check_dtype(name, kFloatOnly, x->dtype);
+  if (x->ndim < 1) fail("%s requires at least 1D tensor", name);
+  std::vector<int64_t> od(x->shape, x->shape + x->ndim - 1);
+  if (od.empty()) od = {1};
+  TensorP src = x;
+  int64_t rows, ld;
+  if (!as_rows(*src, &rows, &ld)) {
+    src = contiguous(x);
+    as_rows(*src, &rows, &ld);
+  }
+  DType odt = op == k::kRArgmax ? DType::I32 : x->dtype;
+  TensorP out = alloc_out(odt, od);
+  LAUNCH k::row_reduce(op, x->dtype, odt, src->data(), ld, out->data(), rows, x->shape[x->ndim - 1], correction,
+                rt().stream());
+  return out;
+}
+
+TensorP softmax_backward(const TensorP& dy, const TensorP& y) {
+  check_dtype("softmax_backward", kFloatOnly, dy->dtype);
+  if (dy->dims() != y->dims() || dy->dtype != y->dtype) fail("softmax_backward: shape/dtype mismatch");
+  TensorP a = contiguous(dy), b = contiguous(y);
+  int64_t cols = a->shape[a->ndim - 1];
+  TensorP out = alloc_out(a->dtype, a->dims());
+  LAUNCH k::softmax_backward(a->dtype, a->data(), b->data(), out->data(), a->numel() / std::max<int64_t>(cols, 1), cols,
+                      rt().stream());
+  return out;
+}
+
+std::pair<TensorP, TensorP> quantize_per_row(const TensorP& x) {
+  check_dtype("quantize_per_row", kFloatOnly, x->dtype);
+  if (x->ndim < 1) fail("quantize_per_row requires at least 1D input");
+  TensorP c = contiguous(x);
+  int64_t cols = c->shape[c->ndim - 1];
+  int64_t rows = cols ? c->numel() / cols : 0;
+  std::vector<int64_t> sd(c->shape, c->shape + c->ndim - 1);
+  if (sd.empty()) sd = {1};
+  TensorP q = alloc_out(DType::I8, c->dims());
+  TensorP s = alloc_out(DType::F32, sd);
+  LAUNCH k::quantize_rows(c->dtype, c->data(), (int8_t*)q->data(), (float*)s->data(), rows, cols, rt().stream());
+  return {q, s};
+}
+
+TensorP dequantize_per_row(const TensorP& q, const TensorP& scale, DType dt) {
+  if (q->dtype != DType::I8) fail("dequantize_per_row: codes must be int8");
+  if (scale->dtype != DType::F32) fail("dequantize_per_row: scales must be float32");
+  if (!dtype_is_float(dt) || dt == DType::F64) fail("dequantize_per_row: target must be a float dtype");
+  TensorP qc = contiguous(q), sc = contiguous(scale);
+  int64_t cols = qc->shape[qc->ndim - 1];
+  int64_t rows = cols ? qc->numel() / cols : 0;
+  if (sc->numel() != rows) fail("dequantize_per_row: %lld scales for %lld rows", (long long)sc->numel(), (long long)rows);
+  TensorP out = alloc_out(dt, qc->dims());
+  LAUNCH k::dequantize_rows(dt, (const int8_t*)qc->data(), (const float*)sc->data(), out->data(), rows, cols, rt().stream());
+  return out;
+}
+
+// ── reductions ─────────────────────────────────────────────────────────────
+TensorP sum_dim(const TensorP& x, int64_t dim, bool keepdim, float scale) {
+  const int nd = x->ndim;
+  if (dim < 0) dim += nd;
+  if (dim < 0 || dim >= nd) fail("sum dim %lld out of range for %d-D tensor", (long long)dim, nd);
+  check_dtype("sum_dim", kNotBool, x->dtype);
+  TensorP c = contiguous(x);
+  int64_t outer = 1, inner = 1;
+  for (int i = 0; i < dim; ++i) outer *= c->shape[i];
+  for (int i = (int)dim + 1; i < nd; ++i) inner *= c->shape[i];
+  std::vector<int64_t> od;
+  for (int i = 0; i < nd; ++i) {
+    if (i == dim) { if (keepdim) od.push_back(1); }
+    else od.push_back(c->shape[i]);
+  }
+  if (od.empty()) od = {1};
+  TensorP out = alloc_out(c->dtype, od);
+  LAUNCH k::sum_dim(c->dtype, c->data(), out->data(), outer, c->shape[dim], inner, scale, rt().stream());
+  return out;
+}
+
+TensorP mean_all(const TensorP& x) {
+  if (x->ndim == 0) fail("mean_all requires at least 1D tensor");
+  check_dtype("mean_all", kFloatOnly, x->dtype);
+  TensorP c = contiguous(x);
+  TensorP out = alloc_out(c->dtype, {1});
+  BufferP ws = scratch(k::reduce_all_ws_bytes());
+  int64_t n = c->numel();
+  LAUNCH k::reduce_all(0, c->dtype, c->data(), nullptr, n, n ? 1.f / (float)n : NAN, out->data(), ws->ptr, rt().stream());
+  return out;
+}
+
+TensorP mse_loss(const TensorP& a, const TensorP& b) {
+  if (a->dims() != b->dims()) fail("mse_loss: shape mismatch %s vs %s", shape_str(a->dims()).c_str(),
+                                   shape_str(b->dims()).c_str());
+  if (a->dtype != b->dtype) fail("mse_loss: dtype mismatch");
+  check_dtype("mse_loss", kFloatOnly, a->dtype);
+  TensorP ac = contiguous(a), bc = contiguous(b);
+  TensorP out = alloc_out(a->dtype, {1});
+  BufferP ws = scratch(k::reduce_all_ws_bytes());
+  int64_t n = ac->numel();
+  LAUNCH k::reduce_all(1, a->dtype, ac->data(), bc->data(), n, n ? 1.f / (float)n : NAN, out->data(), ws->ptr, rt().stream());
+  return out;
+}
+
+TensorP mse_loss_backward(const TensorP& g, const TensorP& a, const TensorP& b) {
+  if (a->dims() != b->dims()) fail("mse_loss_backward: shape mismatch");
+  if (g->numel() != 1) fail("mse_loss_backward: grad_output must have one element");
+  if (a->dtype != b->dtype || g->dtype != a->dtype) fail("mse_loss_backward: dtype mismatch");
+  check_dtype("mse_loss_backward", kFloatOnly, a->dtype);
+  TensorP ac = contiguous(a), bc = contiguous(b);
+  TensorP out = alloc_out(a->dtype, a->dims());
+  LAUNCH k::mse_backward(a->dtype, ac->data(), bc->data(), g->data(), out->data(), ac->numel(), rt().stream());
+  return out;
+}
+
+// ── indexing ───────────────────────────────────────────────────────────────
+TensorP embedding(const TensorP& w, const TensorP& idx) {
+  if (w->ndim != 2) fail("embedding weights must be 2D [vocab_size, embed_dim]");
+  if (idx->ndim < 1) fail("embedding indices must have at least 1 dimension");
+  if (idx->dtype != DType::I32 && idx->dtype != DType::I64)
+    fail("embedding indices must be Int32, got %s", dtype_name(idx->dtype));
+  TensorP wc = contiguous(w), ic = contiguous(idx);
+  std::vector<int64_t> od = idx->dims();
+  od.push_back(w->shape[1]);
+  TensorP out = alloc_out(w->dtype, od);
+  LAUNCH k::embedding(w->dtype, wc->data(), w->shape[0], w->shape[1], ic->dtype, ic->data(), ic->numel(), out->data(),
+               rt().stream());
+  return out;
+}
+
+TensorP index_select(const TensorP& x, int dim, const TensorP& idx) {
+  check_dtype("index_select", kNotBool, x->dtype);
+  if (idx->ndim != 1) fail("index_select index must be 1D");
+  if (idx->dtype != DType::I32 && idx->dtype != DType::I64) fail("index_select indices must be Int32");
+  if (dim < 0 || dim >= x->ndim) fail("index_select dim %d out of range", dim);
+  TensorP c = contiguous(x), ic = contiguous(idx);
+  int64_t outer = 1, inner = 1;
+  for (int i = 0; i < dim; ++i) outer *= c->shape[i];
+  for (int i = dim + 1; i < c->ndim; ++i) inner *= c->shape[i];
+  auto od = c->dims();
+  od[dim] = idx->shape[0];
+  TensorP out = alloc_out(c->dtype, od);
+  LAUNCH k::index_select(c->dtype, c->data(), outer, c->shape[dim], inner, ic->dtype, ic->data(), idx->shape[0],
+                  out->data(), rt().stream());
+  return out;
+}
+
+TensorP gather(const TensorP& x, int dim, const TensorP& idx) {
+  check_dtype("gather", kNotBool, x->dtype);
+  if (idx->dtype != DType::I32 && idx->dtype != DType::I64) fail("gather indices must be Int32");
+  if (idx->ndim != x->ndim) fail("gather index must have the same ndim as the input");
+  if (dim < 0 || dim >= x->ndim) fail("gather dim %d out of range", dim);
+  for (int i = 0; i < x->ndim; ++i)
+    if (i != dim && idx->shape[i] != x->shape[i])
+      fail("gather dim=%d: index dim %d (%lld) must match input (%lld)", dim, i, (long long)idx->shape[i],
+           (long long)x->shape[i]);
+  TensorP c = contiguous(x), ic = contiguous(idx);
+  int64_t outer = 1, inner = 1;
+  for (int i = 0; i < dim; ++i) outer *= c->shape[i];
+  for (int i = dim + 1; i < c->ndim; ++i) inner *= c->shape[i];
+  TensorP out = alloc_out(c->dtype, idx->dims());
+  LAUNCH k::gather(c->dtype, c->data(), outer, c->shape[dim], inner, ic->dtype, ic->data(), idx->shape[dim], out->data(),
+            rt().stream());
+  return out;
+}
+
+TensorP concat(const TensorP& a, const TensorP& b, int dim) {
+  if (a->dtype != b->dtype) fail("concat dtype mismatch: %s vs %s", dtype_name(a->dtype), dtype_name(b->dtype));
+  if (a->ndim != b->ndim) fail("concat ndim mismatch: %s vs %s", shape_str(a->dims()).c_str(), shape_str(b->dims()).c_str());
+  if (dim < 0 || dim >= a->ndim) fail("concat dim %d >= ndim %d", dim, a->ndim);
+  for (int i = 0; i < a->ndim; ++i)
+    if (i != dim && a->shape[i] != b->shape[i])
+      fail("concat shape mismatch on dim %d: %lld vs %lld", i, (long long)a->shape[i], (long long)b->shape[i]);
+  auto od = a->dims();
+  od[dim] += b->shape[dim];
+  TensorP out = alloc_out(a->dtype, od);
+  // Each half is a strided copy into a slice of the output.
+  TensorP oa = slice(out, dim, 0, a->shape[dim]);
+  auto ad = a->dims();
+  k::ND so_a = nd_for(*oa, ad);
+  // Copy kernels write contiguously; write each half as "out slice = in" by
+  // iterating in the output slice's index space through a temporary when the
+  // slice is not contiguous (dim > 0).
+  if (dim == 0) {
+    LAUNCH k::unary(k::kCopy, a->dtype, a->dtype, a->data(), nd_for(*a, ad), oa->data(), nd_shape(ad), 0, 0, rt().stream());
+    TensorP ob = slice(out, dim, a->shape[dim], od[dim]);
+    auto bd = b->dims();
+    LAUNCH k::unary(k::kCopy, b->dtype, b->dtype, b->data(), nd_for(*b, bd), ob->data(), nd_shape(bd), 0, 0, rt().stream());
+    (void)so_a;
+    return out;
+  }
+  // General dim: build the output as where(select) over a broadcast index is
+  // wasteful; instead move `dim` to the front, concat there, and move back.
+  TensorP at = contiguous(transpose_dims(a, 0, dim));
+  TensorP bt = contiguous(transpose_dims(b, 0, dim));
+  TensorP ct = concat(at, bt, 0);
+  return contiguous(transpose_dims(ct, 0, dim));
+}
+
+// ── GEMM ───────────────────────────────────────────────────────────────────
+// Collapse the (already broadcast) batch dims of an operand into one stride.
+static bool batch_stride(const Tensor& t, const std::vector<int64_t>& bdims, int64_t* stride) {
+  // strides of t's batch dims aligned to bdims (0 = broadcast)
+  const int nb = (int)bdims.size();
+  const int tb = t.ndim - 2;
+  std::vector<int64_t> st(nb, 0);
+  for (int i = 0; i < nb; ++i) {
+    int ti = i - (nb - tb);
+    if (ti >= 0 && t.shape[ti] == bdims[i] && bdims[i] != 1) st[i] = t.strides[ti];
+  }
+  // collapsible if st[i] == st[i+1] * bdims[i+1] for non-unit dims
+  int64_t s = -1, expect = 0;
+  for (int i = nb - 1; i >= 0; --i) {
+    if (bdims[i] == 1) continue;
+    if (s < 0) { s = st[i]; expect = st[i] * bdims[i]; continue; }
+    if (st[i] != expect) return false;
+    expect *= bdims[i];
+  }
+  *stride = s < 0 ? 0 : s;
+  return true;
+}
+
+TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi) {
+  TensorP a = ta ? transpose_dims(a_in, a_in->ndim - 2, a_in->ndim - 1) : a_in;
+  TensorP b = tb ? transpose_dims(b_in, b_in->ndim - 2, b_in->ndim - 1) : b_in;
+  if (a_in->ndim < 2 || b_in->ndim < 2) fail("matmul requires at least 2D tensors, got %s and %s",
+                                             shape_str(a_in->dims()).c_str(), shape_str(b_in->dims()).c_str());
+  check_dtype("matmul", kFloatOnly, a->dtype);
+  if (a->dtype != b->dtype) fail("Dtype mismatch: %s vs %s", dtype_name(a->dtype), dtype_name(b->dtype));
+  const int64_t M = a->shape[a->ndim - 2], K = a->shape[a->ndim - 1];
+  const int64_t K2 = b->shape[b->ndim - 2], N = b->shape[b->ndim - 1];
+  if (K != K2)
+    fail("matmul inner dimensions mismatch: A[...,%lld,%lld] * B[...,%lld,%lld]", (long long)M, (long long)K,
+         (long long)K2, (long long)N);
+  std::vector<int64_t> ab(a->shape, a->shape + a->ndim - 2), bb(b->shape, b->shape + b->ndim - 2);
+  std::vector<int64_t> bdims = broadcast_shapes(ab.empty() ? std::vector<int64_t>{1} : ab,
+                                                bb.empty() ? std::vector<int64_t>{1} : bb);
+  std::vector<int64_t> od = bdims;
+  if (ab.empty() && bb.empty()) od.clear();
+  od.push_back(M);
+  od.push_back(N);
+  int64_t batch = 1;
+  for (auto d : bdims) batch *= d;
+
+  int64_t a_sb, b_sb;
+  if (!batch_stride(*a, bdims, &a_sb)) {
+    // expand to the broadcast batch shape, contiguous
+    std::vector<int64_t> full = bdims;
+    full.push_back(M); full.push_back(K);
+    TensorP ex = alloc_out(a->dtype, full);
+    LAUNCH k::unary(k::kCopy, a->dtype, a->dtype, a->data(), nd_for(*a, full), ex->data(), nd_shape(full), 0, 0, rt().stream());
+    a = ex;
+    batch_stride(*a, bdims, &a_sb);
+  }
+  if (!batch_stride(*b, bdims, &b_sb)) {
+    std::vector<int64_t> full = bdims;
+    full.push_back(K); full.push_back(N);
+    TensorP ex = alloc_out(b->dtype, full);
+    LAUNCH k::unary(k::kCopy, b->dtype, b->dtype, b->data(), nd_for(*b, full), ex->data(), nd_shape(full), 0, 0, rt().stream());
+    b = ex;
+    batch_stride(*b, bdims, &b_sb);
+  }
+  TensorP out = alloc_out(a->dtype, od);
+
+  k::Gemm g;
+  g.dt = a->dtype;
+  g.b_dt = b->dtype;
+  g.M = M; g.N = N; g.K = K; g.batch = batch;
+  g.A = a->data(); g.a_sm = a->strides[a->ndim - 2]; g.a_sk = a->strides[a->ndim - 1]; g.a_sb = a_sb;
+  g.B = b->data(); g.b_sk = b->strides[b->ndim - 2]; g.b_sn = b->strides[b->ndim - 1]; g.b_sb = b_sb;
+  // Unit extents: pick the stride that makes the operand look contiguous.
+  if (M == 1) g.a_sm = g.a_sk == 1 ? K : 1;
+  if (K == 1) { if (g.a_sm != 1) g.a_sk = 1; if (g.b_sn != 1) g.b_sk = 1; }
+  if (N == 1) g.b_sn = g.b_sk == 1 ? K : 1;
+  g.C = out->data(); g.c_sm = N; g.c_sb = M * N;
+  TensorP keep_res, keep_mask, keep_bias;
+  if (epi) {
+    g.alpha = epi->alpha;
+    g.act = epi->act;
+    if (epi->bias) {
+      if (epi->bias->dtype != g.dt || epi->bias->numel() != N) fail("matmul epilogue: bias must be [%lld]", (long long)N);
+      keep_bias = contiguous(epi->bias);
+      g.bias = keep_bias->data();
+    }
+    auto side = [&](const TensorP& t, const void** ptr, int64_t* sm, int64_t* sb, TensorP* keep) {
+      if (t->dtype != g.dt) fail("matmul epilogue: operand dtype mismatch");
+      if (t->dims() != od) {
+        // broadcast residual: expand through strides (must collapse)
+        *keep = alloc_out(g.dt, od);
+        LAUNCH k::unary(k::kCopy, t->dtype, t->dtype, t->data(), nd_for(*t, od), (*keep)->data(), nd_shape(od), 0, 0,
+                 rt().stream());
+      } else {
+        *keep = t;
+      }
+      const Tensor& r = **keep;
+      int64_t rsb;
+      if (r.strides[r.ndim - 1] != 1 && N > 1) { *keep = contiguous(*keep); }
+      const Tensor& r2 = **keep;
+      if (!batch_stride(r2, bdims, &rsb)) { *keep = contiguous(*keep); batch_stride(**keep, bdims, &rsb); }
+      *ptr = (*keep)->data();
+      *sm = (*keep)->strides[(*keep)->ndim - 2];
+      if (M == 1) *sm = N;
+      *sb = rsb;
+    };
+    if (epi->residual) side(epi->residual, &g.residual, &g.r_sm, &g.r_sb, &keep_res);
+    if (epi->mask) side(epi->mask, &g.mask, &g.k_sm, &g.k_sb, &keep_mask);
+  }
+  size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
+  BufferP ws;
+  if (wsb) ws = scratch(wsb);
+  LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
+  return out;
+}
+
+TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale) {
+  check_dtype("linear_int8", kFloatOnly, x->dtype);
+  if (q->dtype != DType::I8 || q->ndim != 2) fail("linear_int8: weights must be 2-D int8");
+  if (scale->dtype != DType::F32 || scale->numel() != q->shape[0]) fail("linear_int8: scales must be f32 [out]");
+  if (x->shape[x->ndim - 1] != q->shape[1]) fail("linear_int8: inner dimension mismatch");
+  TensorP xc = contiguous(x), qc = contiguous(q), sc = contiguous(scale);
+  const int64_t K = q->shape[1], N = q->shape[0];
+  const int64_t M = xc->numel() / K;
+  std::vector<int64_t> od = xc->dims();
+  od.back() = N;
+  TensorP out = alloc_out(x->dtype, od);
+  k::Gemm g;
+  g.dt = x->dtype; g.b_dt = DType::I8;
+  g.M = M; g.N = N; g.K = K; g.batch = 1;
+  g.A = xc->data(); g.a_sm = K; g.a_sk = 1;
+  g.B = qc->data(); g.b_sk = 1; g.b_sn = K;
+  g.b_scale = (const float*)sc->data();
+  g.C = out->data(); g.c_sm = N;
+  LAUNCH k::gemm(g, nullptr, rt().stream());
+  return out;
+}
+
+// ── attention ──────────────────────────────────────────────────────────────
+TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool causal, bool out_layout_thd) {
+  const char* name = causal ? "attention_causal" : "attention";
+  if (q->ndim < 2 || kk->ndim < 2 || v->ndim < 2) fail("%s requires at least 2D tensors for Q, K, V", name);
+  check_dtype(name, kFloatOnly, q->dtype);
+  if (q->dtype != kk->dtype || q->dtype != v->dtype) fail("%s: Q, K, V dtypes differ", name);
+  const int64_t D = q->shape[q->ndim - 1];
+  if (kk->shape[kk->ndim - 1] != D)
+    fail("Q and K must have same d_k: %lld vs %lld", (long long)D, (long long)kk->shape[kk->ndim - 1]);
+  const int64_t Tk = kk->shape[kk->ndim - 2];
+  if (v->shape[v->ndim - 2] != Tk)
+    fail("K and V must have same kv_len: %lld vs %lld", (long long)Tk, (long long)v->shape[v->ndim - 2]);
+  const int64_t Dv = v->shape[v->ndim - 1];
+  const int64_t Tq = q->shape[q->ndim - 2];
+  const float scale = 1.0f / std::sqrt((float)D);
+  std::vector<int64_t> lead(q->shape, q->shape + q->ndim - 2);
+  bool same_lead = q->ndim == kk->ndim && q->ndim == v->ndim;
+  for (int i = 0; same_lead && i < q->ndim - 2; ++i)
+    same_lead = kk->shape[i] == q->shape[i] && v->shape[i] == q->shape[i];
+
+  k::Attn a;
+  a.dt = q->dtype;
+  a.Tq = Tq; a.Tk = Tk; a.D = D;
+  a.causal = causal;
+  a.scale = scale;
+  bool fused = same_lead && Dv == D && k::attention_supported(a) && q->ndim <= 4 &&
+               q->strides[q->ndim - 1] == 1 && kk->strides[kk->ndim - 1] == 1 && v->strides[v->ndim - 1] == 1;
+  if (!fused) {
+    // Composition, as the reference records it: Q K^T, scale, softmax, @ V.
+    Epilogue e;
+    e.alpha = scale;
+    TensorP s = matmul(q, kk, false, true, &e);
+    TensorP p = softmax(s, causal ? k::kSoftmaxCausal : k::kSoftmax);
+    return matmul(p, v);
+  }
+  // leading dims -> (B, H)
+  auto lead_strides = [](const Tensor& t, int64_t* sb, int64_t* sh) {
+    if (t.ndim == 2) { *sb = 0; *sh = 0; }
+    else if (t.ndim == 3) { *sb = 0; *sh = t.strides[0]; }
+    else { *sb = t.strides[0]; *sh = t.strides[1]; }
+  };
+  a.B = q->ndim == 4 ? q->shape[0] : 1;
+  a.H = q->ndim == 4 ? q->shape[1] : (q->ndim == 3 ? q->shape[0] : 1);
+  a.q = q->data(); lead_strides(*q, &a.q_sb, &a.q_sh); a.q_st = q->strides[q->ndim - 2];
+  a.k = kk->data(); lead_strides(*kk, &a.k_sb, &a.k_sh); a.k_st = kk->strides[kk->ndim - 2];
+  a.v = v->data(); lead_strides(*v, &a.v_sb, &a.v_sh); a.v_st = v->strides[v->ndim - 2];
+  std::vector<int64_t> od = q->dims();
+  TensorP out;
+  if (out_layout_thd && q->ndim >= 3) {
+    // physical [B, T, H, D]; logical [B, H, T, D]
+    std::vector<int64_t> phys;
+    if (q->ndim == 4) phys = {a.B, Tq, a.H, D};
+    else phys = {Tq, a.H, D};
+    TensorP base = alloc_out(q->dtype, phys);
+    out = make_meta(q->dtype, od);
+    out->buf = base->buf;
+    out->offset = base->offset;
+    if (q->ndim == 4) {
+      out->strides[0] = Tq * a.H * D; out->strides[1] = D; out->strides[2] = a.H * D; out->strides[3] = 1;
+    } else {
+      out->strides[0] = D; out->strides[1] = a.H * D; out->strides[2] = 1;
+    }
+  } else {
+    out = alloc_out(q->dtype, od);
+  }
+  a.o = out->data();
+  lead_strides(*out, &a.o_sb, &a.o_sh);
+  a.o_st = out->strides[out->ndim - 2];
+  LAUNCH k::attention(a, rt().stream());
+  return out;
+}
+
+}  // namespace ops
+}  // namespace agpu

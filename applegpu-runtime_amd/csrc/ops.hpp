@@ -1,0 +1,80 @@
+// Host-side op layer: validates shapes and dtypes (the reference's rules),
+// picks layouts, allocates outputs from the pool and enqueues kernels on the
+// runtime stream.  Used by both the eager C ABI and the lazy graph executor.
+#pragma once
+
+#include "core.hpp"
+#include "kernels.hpp"
+
+namespace agpu {
+namespace ops {
+
+// Layout helpers
+TensorP contiguous(const TensorP& t);               // t itself when already contiguous
+k::ND nd_for(const Tensor& t, const std::vector<int64_t>& out_dims);  // broadcast strides
+k::ND nd_shape(const std::vector<int64_t>& dims);
+// View of t as [rows, cols] with unit column stride; false if not expressible.
+bool as_rows(const Tensor& t, int64_t* rows, int64_t* ld);
+TensorP view(const TensorP& base, const std::vector<int64_t>& shape, const std::vector<int64_t>& strides,
+             int64_t offset_elems);
+TensorP reshape(const TensorP& t, const std::vector<int64_t>& shape);   // view when possible
+TensorP transpose_dims(const TensorP& t, int d0, int d1);                // always a view
+TensorP slice(const TensorP& t, int dim, int64_t start, int64_t end);    // always a view
+
+// Elementwise
+TensorP binary(int op, const TensorP& a, const TensorP& b, float p0 = 0.f);
+TensorP unary(int op, const TensorP& x, float p0 = 0.f, float p1 = 0.f);
+TensorP cast(const TensorP& x, DType dt);
+TensorP quantize(const TensorP& x, DType dt, float scale, int zero_point);
+TensorP dequantize(const TensorP& x, DType dt, float scale, int zero_point);
+TensorP where(const TensorP& c, const TensorP& x, const TensorP& y);
+TensorP masked_fill(const TensorP& x, const TensorP& mask, float value);
+TensorP tri(const TensorP& x, bool upper, int64_t diag);
+TensorP threshold_backward(const TensorP& grad, const TensorP& input, float thr);
+TensorP add_bias(const TensorP& x, const TensorP& bias);
+TensorP full(DType dt, const std::vector<int64_t>& dims, float value);
+void axpy_inplace(const TensorP& self, const TensorP& other, float alpha);  // self += alpha*other
+void copy_into(const TensorP& dst, const TensorP& src);                      // dst (any strides) = src
+
+// Rows
+TensorP softmax(const TensorP& x, int mode /* k::RowOp */);
+TensorP layer_norm(const TensorP& x, const TensorP& g, const TensorP& b, float eps);
+TensorP row_reduce(int op /* k::RedOp */, const TensorP& x, int correction = 0);
+TensorP softmax_backward(const TensorP& dy, const TensorP& y);
+std::pair<TensorP, TensorP> quantize_per_row(const TensorP& x);             // (int8 codes, f32 scales)
+TensorP dequantize_per_row(const TensorP& q, const TensorP& scale, DType dt);
+
+// Reductions
+TensorP sum_dim(const TensorP& x, int64_t dim, bool keepdim, float scale = 1.f);
+TensorP mean_all(const TensorP& x);
+TensorP mse_loss(const TensorP& a, const TensorP& b);
+TensorP mse_loss_backward(const TensorP& g, const TensorP& a, const TensorP& b);
+
+// Indexing
+TensorP embedding(const TensorP& w, const TensorP& idx);
+TensorP index_select(const TensorP& x, int dim, const TensorP& idx);
+TensorP gather(const TensorP& x, int dim, const TensorP& idx);
+TensorP concat(const TensorP& a, const TensorP& b, int dim);
+
+// GEMM.  Batch dims of A and B broadcast (the lazy path's rule); `ta`/`tb`
+// swap the last two dims of an operand in place (matmul_ex).
+struct Epilogue {
+  TensorP bias;       // [N]
+  int act = k::kActNone;
+  TensorP residual;   // same shape as the output
+  TensorP mask;       // same shape as the output: out = mask > 0 ? out : 0
+  float alpha = 1.f;
+};
+TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = false,
+               const Epilogue* epi = nullptr);
+// int8 weights with per-row scales (out = x @ (q * scale[:,None])^T)
+TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
+
+// Attention over [..., T, D] operands (leading dims shared by q, k, v).
+// out_layout_thd: store the output physically as [..., T, H, D] (the result
+// is still logically [..., H, T, D]) so a following head merge is free.
+TensorP attention(const TensorP& q, const TensorP& k, const TensorP& v, bool causal,
+                  bool out_layout_thd = false);
+
+}  // namespace ops
+}  // namespace agpu

@@ -1,0 +1,227 @@
+/*
+ * applegpu_ffi.h — C ABI of the MI355X (gfx950) backend for applegpu-runtime.
+ *
+ * Part 1 declares, with identical C signatures, every symbol of the
+ * reference header backend_cpp/applegpu_ffi.h:11-92 (graph path
+ * applegpu_ffi_*, eager path applegpu_eager_*), plus the exported-but-
+ * undeclared applegpu_eager_execute_graph (crates/core/src/eager_ffi.rs:661-708).
+ * Conventions are the reference's (crates/core/src/eager_ffi.rs:38-46,
+ * backend_ffi.rs:26-34):
+ *   - pointer-returning ops return the output's data pointer (base + byte
+ *     offset) or NULL on failure; u64 id returns use 0 for failure; i32
+ *     returns use 0 for success and -1 for failure; dtype returns -1 for an
+ *     unknown id;
+ *   - on failure a thread-local C string is set (applegpu_eager_last_error /
+ *     applegpu_ffi_last_error), valid until the next error on that thread;
+ *   - *out_id is written only on success;
+ *   - dtype wire codes: 0 f32, 1 f16, 2 f64, 3 i8, 4 i16, 5 i32, 6 i64, 7 u8,
+ *     8 u32, 9 bool, 10 bf16 (crates/core/src/tensor.rs:59-90);
+ *   - shapes have at most 8 dims; one global lock serialises all calls.
+ *
+ * Memory: returned data pointers are HBM device pointers on MI355X (the
+ * reference's were host-coherent Metal shared buffers).  Host reads and writes
+ * go through the copy entry points in Part 2; setting APPLEGPU_HOST_VISIBLE=1
+ * before init makes every allocation pinned host memory that both sides can
+ * dereference (slow; compatibility only).
+ *
+ * Part 2 declares the additions this backend needs for the hot path; each
+ * names the reference interface it replaces.
+ */
+#ifndef APPLEGPU_FFI_H
+#define APPLEGPU_FFI_H
+
+#include <stdint.h>
+#include <stdbool.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ════════════════════ Part 1: reference surface ════════════════════════ */
+
+/* Lifecycle */
+bool applegpu_ffi_init(void);
+const char* applegpu_ffi_last_error(void);
+
+/* Allocation */
+uint8_t* applegpu_ffi_alloc(uint64_t size_bytes, int8_t dtype_i8, uint64_t* out_tensor_id);
+void applegpu_ffi_free(uint64_t tensor_id);
+
+/* Tensor metadata */
+int32_t applegpu_ffi_register_tensor(uint64_t tensor_id, const uint64_t* dims, uint32_t ndim, int8_t dtype_i8);
+int32_t applegpu_ffi_shape(uint64_t tensor_id, uint64_t* out_dims, uint32_t* out_ndim);
+int8_t applegpu_ffi_dtype(uint64_t tensor_id);
+
+/* Ops (return output tensor_id, 0 on failure) */
+uint64_t applegpu_ffi_add(uint64_t a_id, uint64_t b_id);
+uint64_t applegpu_ffi_matmul(uint64_t a_id, uint64_t b_id);
+uint64_t applegpu_ffi_relu(uint64_t input_id);
+uint64_t applegpu_ffi_mul(uint64_t a_id, uint64_t b_id);
+uint64_t applegpu_ffi_sub(uint64_t a_id, uint64_t b_id);
+uint64_t applegpu_ffi_neg(uint64_t input_id);
+int32_t applegpu_ffi_copy(uint64_t src_id, uint64_t dst_id);
+
+/* Ops with output allocation (return data_ptr, write tensor_id to *out_id) */
+uint8_t* applegpu_ffi_add_out(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_mul_out(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_sub_out(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_matmul_out(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_relu_out(uint64_t input_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_neg_out(uint64_t input_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_div_out(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_ffi_threshold_backward_out(uint64_t grad_id, uint64_t input_id, float threshold, uint64_t* out_id);
+uint8_t* applegpu_ffi_scalar_mul_out(uint64_t input_id, float scale, uint64_t* out_id);
+uint8_t* applegpu_ffi_mean_all_out(uint64_t input_id, uint64_t* out_id);
+
+/* Eval / sync */
+int32_t applegpu_ffi_eval(uint64_t tensor_id);
+void applegpu_ffi_synchronize(void);
+
+/* Readback */
+int32_t applegpu_ffi_read_f32(uint64_t tensor_id, float* out_ptr, uint64_t max_elements);
+
+/* ── Eager dispatch (bypasses graph engine) ── */
+bool applegpu_eager_init(void);
+const char* applegpu_eager_last_error(void);
+
+uint8_t* applegpu_eager_alloc(const uint64_t* dims, uint32_t ndim, int8_t dtype, uint64_t* out_id);
+void applegpu_eager_free(uint64_t id);
+int32_t applegpu_eager_register_shape(uint64_t id, const uint64_t* dims, uint32_t ndim);
+int32_t applegpu_eager_shape(uint64_t id, uint64_t* out_dims, uint32_t* out_ndim);
+int8_t applegpu_eager_dtype(uint64_t id);
+
+uint8_t* applegpu_eager_add(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_eager_sub(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_eager_mul(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_eager_div(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_eager_relu(uint64_t input_id, uint64_t* out_id);
+uint8_t* applegpu_eager_neg(uint64_t input_id, uint64_t* out_id);
+uint8_t* applegpu_eager_matmul(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_eager_matmul_ex(uint64_t a_id, uint64_t b_id, bool transpose_a, bool transpose_b, uint64_t* out_id);
+
+uint8_t* applegpu_eager_threshold_backward(uint64_t grad_id, uint64_t input_id, float threshold, uint64_t* out_id);
+uint8_t* applegpu_eager_scalar_mul(uint64_t input_id, float scale, uint64_t* out_id);
+uint8_t* applegpu_eager_mean_all(uint64_t input_id, uint64_t* out_id);
+
+uint8_t* applegpu_eager_sum_dim(uint64_t input_id, int64_t dim, bool keepdim, uint64_t* out_id);
+
+uint8_t* applegpu_eager_create_view(uint64_t base_id, const uint64_t* shape, const uint64_t* strides, uint32_t ndim, uint64_t offset, uint64_t* out_id);
+
+int32_t applegpu_eager_add_inplace(uint64_t self_id, uint64_t other_id);
+int32_t applegpu_eager_add_scaled_inplace(uint64_t self_id, uint64_t other_id, float alpha);
+
+void applegpu_eager_flush_and_wait(void);
+void applegpu_eager_synchronize(void);
+
+/* GPT-2 ops */
+uint8_t* applegpu_eager_embedding(uint64_t weight_id, uint64_t indices_id, uint64_t* out_id);
+uint8_t* applegpu_eager_layer_norm(uint64_t input_id, uint64_t gamma_id, uint64_t beta_id, float eps, uint64_t* out_id);
+uint8_t* applegpu_eager_gelu(uint64_t input_id, uint64_t* out_id);
+uint8_t* applegpu_eager_softmax(uint64_t input_id, uint64_t* out_id);
+
+/* Reverse lookup: find tensor_id by buffer data pointer. Returns 0 if not found. */
+uint64_t applegpu_eager_find_by_data_ptr(const uint8_t* ptr);
+
+/* Exported but undeclared in the reference (eager_ffi.rs:661-708; bound via
+ * ctypes in python/applegpu_runtime/compile_backend.py:961-1030).  The
+ * torch.compile bytecode executor is not part of this backend: returns -1
+ * with an "unsupported" error. */
+int32_t applegpu_eager_execute_graph(const uint8_t* ops_data, uint32_t ops_len,
+                                     const uint64_t* input_tids, uint32_t n_inputs,
+                                     const uint16_t* output_indices, uint32_t n_outputs,
+                                     uint64_t* out_tids, uint8_t** out_ptrs);
+
+/* ════════════════════ Part 2: MI355X additions ═════════════════════════ */
+
+/* Generic lazy op: records op `op` (a name of the Python surface: "softmax",
+ * "layer_norm", "attention_causal", "quantize_per_row", ...) on the given
+ * input ids with float/int parameters; writes up to max_out new ids and
+ * returns their number, or -1 (error in applegpu_ffi_last_error).
+ * Replaces the PyO3 module's BACKEND.<op> calls (crates/python/src/lib.rs:830-1258,
+ * Backend trait crates/python/src/backend.rs:17-204) into LazyRuntime ops
+ * (crates/core/src/ops.rs). */
+int32_t applegpu_graph_op(const char* op, const uint64_t* inputs, uint32_t n_inputs,
+                          const double* fparams, uint32_t n_f, const int64_t* iparams, uint32_t n_i,
+                          uint64_t* out_ids, uint32_t max_out);
+
+/* Host <-> device copies for the graph path: write_bytes replaces the host
+ * memcpy into a shared buffer behind from_numpy/from_bytes
+ * (crates/python/src/lib.rs:419-512); read_bytes evaluates a pending tensor
+ * and copies its logical (row-major) bytes out, replacing
+ * LazyRuntime::read_bytes behind to_numpy (crates/python/src/lib.rs:140-160).
+ * nbytes must equal numel * element size. */
+int32_t applegpu_ffi_write_bytes(uint64_t tensor_id, const void* src, uint64_t nbytes);
+int32_t applegpu_ffi_read_bytes(uint64_t tensor_id, void* dst, uint64_t nbytes);
+/* 1 when the tensor still has unevaluated ops, 0 when materialised, -1 unknown. */
+int32_t applegpu_ffi_is_pending(uint64_t tensor_id);
+/* Element strides of a tensor (views are strided). */
+int32_t applegpu_ffi_strides(uint64_t tensor_id, int64_t* out_strides, uint32_t* out_ndim);
+
+/* Runtime introspection and setters of the Python surface: pool_stats,
+ * pool_drain, set_pool_watermark, memory_usage, tensor_count, set_limits,
+ * device_name (crates/python/src/lib.rs:386-395, 788-806, 1136-1151;
+ * crates/core/src/pool.rs:7-12, limits.rs:39-77).
+ * out[0..5] = hits, misses, pooled_bytes, bucket_count, live_bytes. */
+int32_t applegpu_ffi_pool_stats(uint64_t* out5);
+void applegpu_ffi_pool_drain(void);
+void applegpu_ffi_set_pool_watermark(uint64_t bytes);
+uint64_t applegpu_ffi_memory_usage(void);
+uint64_t applegpu_ffi_tensor_count(void);
+void applegpu_ffi_set_limits(uint64_t max_tensor_bytes, uint64_t max_memory_bytes, uint64_t max_tensors);
+int32_t applegpu_ffi_device_name(char* out, uint32_t cap);
+/* out[0..4] = evals, nodes, fused GEMM epilogues, launches saved by fusion */
+int32_t applegpu_ffi_graph_stats(uint64_t* out4);
+/* Test hook (no reference counterpart): the next n device allocations fail,
+ * so the out-of-memory path can be exercised from the host. */
+void applegpu_ffi_inject_alloc_failures(int32_t n);
+/* Measurement (no reference counterpart; the reference times with
+ * time.perf_counter around a flush, benchmarks/bench_mlp_cpp.py:39-45):
+ * record a HIP event in slot 0..15 on the library's stream, and the elapsed
+ * milliseconds between two recorded slots (waits for the later one). */
+int32_t applegpu_ffi_event_record(uint32_t slot);
+float applegpu_ffi_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
+
+/* Generic eager op: runs `op` at once (same names and parameters as
+ * applegpu_graph_op), registers the outputs, writes their ids to out_ids and
+ * returns their number (or -1).  Replaces the aten kernels of the
+ * PrivateUse1 shim that the reference runs through CPU fallback or several
+ * eager calls (backend_cpp/applegpu_backend.cpp:753-764 masked ops,
+ * :801-867 mse_loss, :943-951 softmax, :1055-1096 registrations). */
+int32_t applegpu_eager_op(const char* op, const uint64_t* inputs, uint32_t n_inputs,
+                          const double* fparams, uint32_t n_f, const int64_t* iparams, uint32_t n_i,
+                          uint64_t* out_ids, uint32_t max_out);
+
+/* Host <-> device copies for eager tensors (any strides on the device side):
+ * replace the shim's host memcpy on shared buffers in copy_/_copy_from
+ * (backend_cpp/applegpu_backend.cpp:267-341). nbytes = numel * element size. */
+int32_t applegpu_eager_copy_from_host(uint64_t id, const void* src, uint64_t nbytes);
+int32_t applegpu_eager_copy_to_host(uint64_t id, void* dst, uint64_t nbytes);
+/* dst = src on the device (dtype cast allowed, dst contiguous): replaces the
+ * scalar_mul(view, 1.0) + storage swap copy idiom
+ * (backend_cpp/applegpu_backend.cpp:274-299). */
+int32_t applegpu_eager_copy_(uint64_t dst_id, uint64_t src_id);
+/* Fill with a value on the device: replaces the CPU memset of fill_/zero_
+ * (backend_cpp/applegpu_backend.cpp:729-751). */
+int32_t applegpu_eager_fill(uint64_t id, double value);
+/* y = act(x W^T + b) in one GEMM with a fused epilogue (act: 0 none, 1 relu,
+ * 2 gelu-tanh, 3 gelu-erf; bias_id 0 = none): replaces addmm's W^T copy +
+ * matmul + bias add (backend_cpp/applegpu_backend.cpp:584-620). */
+uint8_t* applegpu_eager_linear(uint64_t x_id, uint64_t w_id, uint64_t bias_id, int32_t act, uint64_t* out_id);
+/* C = op(A) op(B) with a fused "mask" epilogue: out = (mask > 0) ? A@B : 0,
+ * i.e. matmul followed by threshold_backward(., mask, 0) in one kernel
+ * (eager.rs:485-560 + eager.rs:775-818). */
+uint8_t* applegpu_eager_matmul_masked(uint64_t a_id, uint64_t b_id, bool transpose_a, bool transpose_b,
+                                      uint64_t mask_id, uint64_t* out_id);
+/* loss = mean((a-b)^2) as one fused reduction, and its gradient
+ * (a-b) * 2/n * g: replace the shim's sub/mul/mean_all decomposition
+ * (backend_cpp/applegpu_backend.cpp:801-867). */
+uint8_t* applegpu_eager_mse_loss(uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+uint8_t* applegpu_eager_mse_loss_backward(uint64_t grad_id, uint64_t a_id, uint64_t b_id, uint64_t* out_id);
+/* Element strides of an eager tensor. */
+int32_t applegpu_eager_strides(uint64_t id, int64_t* out_strides, uint32_t* out_ndim);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* APPLEGPU_FFI_H */

@@ -1,0 +1,177 @@
+"""int8 quantize/dequantize (bit-exact codes), the fused int8 GEMM, and the
+model-level paths: GPT-2 forward (config 2 recipe) and the MLP training step
+(configs 1 and 3) against the oracle."""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from oracle import models as M
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(99)
+
+
+def test_quantize_per_row_golden_bit_exact(gpu, fixtures):
+    q, s = gpu.quantize_per_row(gpu.from_numpy(fixtures["quant_w"]))
+    assert q.dtype == "int8" and s.dtype == "float32"
+    np.testing.assert_array_equal(q.to_numpy(), fixtures["quant_q"])
+    np.testing.assert_array_equal(s.to_numpy(), fixtures["quant_scale"])
+    d = gpu.dequantize_per_row(q, s).to_numpy()
+    np.testing.assert_array_equal(d, O.dequantize_per_row(fixtures["quant_q"], fixtures["quant_scale"]))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (16, 1023), (8, 1024), (5, 3000), (4, 8192), (2, 9000)])
+def test_quantize_per_row_shapes_bit_exact(gpu, rows, cols):
+    w = (RNG.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    q, s = gpu.quantize_per_row(gpu.from_numpy(w))
+    qr, sr = O.quantize_per_row(w)
+    np.testing.assert_array_equal(s.to_numpy(), sr)
+    np.testing.assert_array_equal(q.to_numpy(), qr)
+
+
+def test_quantize_per_row_many_ties(gpu):
+    # scale 2^-10 exactly; codes k + 0.5 for many k: every tie must round to even
+    k = np.arange(-127, 127, dtype=np.float32) + np.float32(0.5)
+    row = np.concatenate([[127.0], k]).astype(np.float32) * np.float32(2.0 ** -10)
+    w = np.stack([row, -row])
+    q, s = gpu.quantize_per_row(gpu.from_numpy(w))
+    qr, sr = O.quantize_per_row(w)
+    np.testing.assert_array_equal(q.to_numpy(), qr)
+    assert s.to_list() == [2.0 ** -10] * 2
+
+
+def test_quantize_per_tensor_half_away_bit_exact(gpu):
+    x = np.array([0.25, -0.25, 0.75, -0.75, 1.25, 0.049999997, 100.0, -100.0, 0.0], np.float32)
+    q = gpu.quantize(gpu.from_numpy(x), "int8", 0.5)
+    np.testing.assert_array_equal(q.to_numpy(), O.quantize_per_tensor(x, 0.5))
+    big = (RNG.standard_normal((33, 77)) * 3).astype(np.float32)
+    for dt, zp in (("int8", 0), ("uint8", 128), ("int8", -3)):
+        qq = gpu.quantize(gpu.from_numpy(big), dt, 0.037, zp).to_numpy()
+        np.testing.assert_array_equal(qq, O.quantize_per_tensor(big, 0.037, zp, dt))
+        dq = gpu.dequantize(gpu.quantize(gpu.from_numpy(big), dt, 0.037, zp), "float32", 0.037, zp).to_numpy()
+        np.testing.assert_array_equal(dq, O.dequantize_per_tensor(qq, 0.037, zp))
+
+
+def test_int8_linear_config5_shape(gpu):
+    """Config 5 at full size: W [8192, 8192] per-row int8, X [64, 8192]."""
+    w = (RNG.standard_normal((8192, 8192), dtype=np.float32) * np.float32(0.02))
+    x = RNG.standard_normal((64, 8192), dtype=np.float32)
+    q, s = gpu.quantize_per_row(gpu.from_numpy(w))
+    qr, sr = O.quantize_per_row(w)
+    np.testing.assert_array_equal(s.to_numpy(), sr)
+    assert np.array_equal(q.to_numpy(), qr)
+    deq = gpu.dequantize_per_row(q, s)
+    tx = gpu.from_numpy(x)
+    y = (tx @ gpu.transpose(deq)).to_numpy()
+    deq_np = O.dequantize_per_row(qr, sr)
+    ref = O.matmul(x, deq_np.T)
+    assert rel_err(y, ref) < 1e-3
+    y8 = gpu.linear_int8(tx, q, s).to_numpy()
+    assert rel_err(y8, ref) < 1e-3
+
+
+# ── GPT-2 forward ──────────────────────────────────────────────────────────
+def _gpt2(cfg, seed=42, std=0.02):
+    from applegpu_runtime.models import gpt2 as G
+    w = G.random_weights(cfg, seed=seed, std=std)
+    return G, w
+
+
+def test_gpt2_tiny_layers_vs_oracle(gpu):
+    cfg = dict(n_layer=2, n_head=4, n_embd=64, vocab_size=97, n_positions=32)
+    G, w = _gpt2(cfg, seed=3, std=0.2)
+    model = G.load_model(w, cfg)
+    ids = [5, 17, 3, 96, 0, 42, 42, 8, 1, 77, 31]
+    logits, _ = G.gpt2_forward(model, ids)
+    got = logits.to_numpy()
+    ref, _ = M.gpt2_forward_np(w, cfg, ids)
+    assert rel_err(got, ref) < 1e-3
+    np.testing.assert_array_equal(got.argmax(-1), ref.argmax(-1))
+
+
+def test_gpt2_small_seq128_config2(gpu):
+    """Config 2 at full size: GPT-2 small, fp32, random init N(0, 0.02), seq 128."""
+    cfg = G_CFG = dict(n_layer=12, n_head=12, n_embd=768, vocab_size=50257, n_positions=1024)
+    G, w = _gpt2(cfg)
+    model = G.load_model(w, cfg)
+    ids = np.random.default_rng(42).integers(0, 50257, 128)
+    logits, _ = G.gpt2_forward(model, ids)
+    got = logits.to_numpy()
+    ref, _ = M.gpt2_forward_np(w, G_CFG, ids)
+    assert got.shape == (128, 50257)
+    assert rel_err(got, ref) < 1e-3
+    stats = gpu.graph_stats()
+    assert stats["fused_gemm_epilogues"] >= 48
+
+
+def test_gpt2_kv_cache_decode_step(gpu):
+    cfg = dict(n_layer=2, n_head=4, n_embd=64, vocab_size=97, n_positions=32)
+    G, w = _gpt2(cfg, seed=5, std=0.2)
+    model = G.load_model(w, cfg)
+    ids = [3, 9, 27, 81, 50, 6, 18]
+    _, cache = G.gpt2_forward(model, ids[:-1])
+    inc, _ = G.gpt2_forward(model, ids, kv_cache=cache)
+    full, _ = M.gpt2_forward_np(w, cfg, ids)
+    assert rel_err(inc.to_numpy()[0], full[-1]) < 1e-3
+
+
+# ── MLP training (eager C ABI) ─────────────────────────────────────────────
+def test_mlp_config1_step_vs_torch_golden(gpu, fixtures):
+    from applegpu_runtime import eager as E
+    from applegpu_runtime.models.mlp import EagerMLP
+    params = [(fixtures["mlp_w0"], fixtures["mlp_b0"]), (fixtures["mlp_w1"], fixtures["mlp_b1"])]
+    mlp = EagerMLP(params)
+    x, y = E.from_numpy(fixtures["mlp_x"]), E.from_numpy(fixtures["mlp_y"])
+    out, _ = mlp.forward(x)
+    np.testing.assert_allclose(out.numpy(), fixtures["mlp_out"], rtol=1e-4, atol=1e-5)
+    loss = mlp.train_step(x, y, lr=0.01)
+    np.testing.assert_allclose(loss.numpy(), fixtures["mlp_loss"], rtol=1e-5)
+    new = mlp.numpy_params()
+    for i in range(2):
+        np.testing.assert_allclose(new[i][0], fixtures[f"mlp_w{i}_after"], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(new[i][1], fixtures[f"mlp_b{i}_after"], rtol=1e-5, atol=1e-6)
+
+
+def test_mlp_config1_gradients_vs_oracle(gpu, fixtures):
+    """Gradients compared elementwise (the reference only checks they exist)."""
+    from applegpu_runtime import eager as E
+    params = [(fixtures["mlp_w0"], fixtures["mlp_b0"]), (fixtures["mlp_w1"], fixtures["mlp_b1"])]
+    x, y = fixtures["mlp_x"], fixtures["mlp_y"]
+    _, _, grads, _ = M.mlp_train_step_np(params, x, y)
+    w0, b0, w1, b1 = (E.from_numpy(a) for a in (params[0][0], params[0][1], params[1][0], params[1][1]))
+    tx, ty = E.from_numpy(x), E.from_numpy(y)
+    h = E.linear(tx, w0, b0, act=1)
+    out = E.linear(h, w1, b1)
+    one = E.from_numpy(np.ones(1, np.float32))
+    g = E.mse_loss_backward(one, out, ty)
+    np.testing.assert_allclose(E.matmul_ex(g, h, True, False).numpy(), fixtures["mlp_gw1"], rtol=1e-4, atol=1e-7)
+    np.testing.assert_allclose(E.sum_dim(g, 0).numpy(), fixtures["mlp_gb1"], rtol=1e-4, atol=1e-7)
+    gh = E.matmul_masked(g, w1, False, False, h)
+    np.testing.assert_allclose(E.matmul_ex(gh, tx, True, False).numpy(), grads[0][0], rtol=1e-3, atol=1e-7)
+    np.testing.assert_allclose(E.sum_dim(gh, 0).numpy(), grads[0][1], rtol=1e-4, atol=1e-7)
+    # the unfused reference decomposition gives the same dh
+    gh2 = E.threshold_backward(E.matmul(g, w1), h, 0.0)
+    np.testing.assert_allclose(gh.numpy(), gh2.numpy(), rtol=1e-6, atol=1e-9)
+
+
+def test_mlp_config3_step_vs_oracle(gpu):
+    """Config 3 at full size: 4096 -> 4096 -> 4096 -> 1, batch 256, one step."""
+    from applegpu_runtime import eager as E
+    from applegpu_runtime.models.mlp import EagerMLP, torch_default_init
+    params = torch_default_init([4096, 4096, 4096, 1], seed=42)
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((256, 4096), dtype=np.float32)
+    y = rng.standard_normal((256, 1), dtype=np.float32)
+    loss_ref, out_ref, _, new_ref = M.mlp_train_step_np(params, x, y, lr=0.01)
+    mlp = EagerMLP(params)
+    tx, ty = E.from_numpy(x), E.from_numpy(y)
+    out, _ = mlp.forward(tx)
+    assert rel_err(out.numpy(), out_ref) < 1e-3
+    loss = mlp.train_step(tx, ty, lr=0.01)
+    np.testing.assert_allclose(loss.numpy(), loss_ref, rtol=1e-3)
+    new = mlp.numpy_params()
+    for (w, b), (wr, br) in zip(new, new_ref):
+        assert rel_err(w, wr) < 1e-5  # update is small against the weights
+        assert rel_err(b, br) < 1e-4
