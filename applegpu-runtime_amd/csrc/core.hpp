@@ -59,6 +59,7 @@ void check_launch(const char* what);
 struct Buffer {
   void* ptr = nullptr;
   size_t bytes = 0;       // capacity (a power of two when pooled)
+  size_t requested = 0;   // bytes the current owner asked for (bounds of views)
   bool host_visible = false;
 };
 using BufferP = std::shared_ptr<Buffer>;
@@ -68,7 +69,7 @@ struct PoolStats {
   size_t pooled_bytes = 0, bucket_count = 0, live_bytes = 0;
 };
 
-// Power-of-two bucketed pool over hipMalloc.  Every kernel runs on the one
+// Power-of-two bucketed pool over stream-ordered hipMallocAsync.  Every kernel runs on the one
 // runtime stream, so a buffer released on the host can be handed to the next
 // op at once: the next op's kernels are ordered after the last user's.
 class Pool {
@@ -111,6 +112,13 @@ struct Tensor {
     return n;
   }
   size_t nbytes() const { return (size_t)numel() * dtype_size(dtype); }
+  // Bytes from data() to one past the last element the strides reach.
+  size_t extent_bytes() const {
+    if (numel() == 0) return 0;
+    int64_t last = 0;
+    for (int i = 0; i < ndim; ++i) last += (shape[i] - 1) * strides[i];
+    return (size_t)(last + 1) * dtype_size(dtype);
+  }
   bool is_contiguous() const;
   bool pending() const { return node != nullptr; }
   char* data() const { return buf ? (char*)buf->ptr + offset : nullptr; }

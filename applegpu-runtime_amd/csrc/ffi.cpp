@@ -76,9 +76,11 @@ uint8_t* publish(const TensorP& t, uint64_t* out_id) {
 
 void check_capacity(const Tensor& t) {
   if (!t.buf) return;
-  if ((size_t)t.offset + t.nbytes() > t.buf->bytes)
-    fail("shape %s (%zu bytes) does not fit the %zu-byte allocation", shape_str(t.dims()).c_str(), t.nbytes(),
-         t.buf->bytes - (size_t)t.offset);
+  // Bounds are the owner's requested size, not the pool's rounded capacity.
+  const size_t have = t.buf->requested > (size_t)t.offset ? t.buf->requested - (size_t)t.offset : 0;
+  if (t.extent_bytes() > have)
+    fail("shape %s with these strides reaches %zu bytes, past the %zu bytes of the allocation",
+         shape_str(t.dims()).c_str(), t.extent_bytes(), have);
 }
 
 void copy_to_host(const TensorP& t0, void* dst, uint64_t nbytes) {
@@ -243,7 +245,7 @@ int32_t applegpu_ffi_copy(uint64_t src_id, uint64_t dst_id) {
     if (dst->pending()) fail("copy: dst tensor %llu has pending ops", (unsigned long long)dst_id);
     TensorP s = ops::contiguous(src);
     size_t nb = s->nbytes();
-    if (!dst->buf || (size_t)dst->offset + nb > dst->buf->bytes) fail("copy: destination too small");
+    if (!dst->buf || (size_t)dst->offset + nb > dst->buf->requested) fail("copy: destination too small");
     if (nb) AGPU_HIP(hipMemcpyAsync(dst->data(), s->data(), nb, hipMemcpyDeviceToDevice, rt().stream()));
     return 0;
   });

@@ -379,7 +379,9 @@ void eval(const TensorP& root) {
 
   for (size_t i = 0; i < order.size(); ++i) {
     TensorP t = order[i];
-    if (absorbed.count(t.get())) {
+    // Absorbed into a fused GEMM, or already filled by its multi-output
+    // producer earlier in this walk.
+    if (absorbed.count(t.get()) || !t->pending()) {
       order[i].reset();
       continue;
     }

@@ -57,7 +57,10 @@ static void check_dtype(const char* op, Cls c, DType d) {
       break;
     case kIntOnly: ok = d == DType::I32 || d == DType::I64 || d == DType::U8 || d == DType::U32; break;
   }
-  if (!ok) fail("%s does not support dtype %s", op, dtype_name(d));
+  static const char* kWant[] = {"a float dtype", "a numeric dtype", "any dtype", "a non-bool dtype",
+                                "an ordered dtype", "a comparable dtype", "an integer or bool dtype",
+                                "an integer dtype"};
+  if (!ok) fail("%s does not support dtype %s (needs %s)", op, dtype_name(d), kWant[(int)c]);
 }
 
 static const char* bin_name(int op) {
@@ -162,7 +165,7 @@ TensorP view(const TensorP& base, const std::vector<int64_t>& shape, const std::
     last += (shape[i] - 1) * strides[i];
   }
   if (base->buf && last >= 0 &&
-      (size_t)(t->offset + (last + 1) * (int64_t)dtype_size(base->dtype)) > base->buf->bytes)
+      (size_t)(t->offset + (last + 1) * (int64_t)dtype_size(base->dtype)) > base->buf->requested)
     fail("view: shape %s with the given strides/offset exceeds the base storage", shape_str(shape).c_str());
   return t;
 }

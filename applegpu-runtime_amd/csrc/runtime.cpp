@@ -154,6 +154,10 @@ BufferP Pool::acquire(size_t nbytes) {
   Buffer* b = nullptr;
   {
     std::lock_guard<std::mutex> g(mu_);
+    if (inject_fail_ > 0) {
+      --inject_fail_;
+      fail("device allocation of %zu bytes failed: injected failure (test hook)", cap);
+    }
     auto it = buckets_.find(cap);
     if (it != buckets_.end() && !it->second.empty()) {
       b = it->second.back();
@@ -169,21 +173,18 @@ BufferP Pool::acquire(size_t nbytes) {
     b = new Buffer();
     b->bytes = cap;
     hipError_t e;
-    if (inject_fail_ > 0) {
-      --inject_fail_;
-      e = hipErrorOutOfMemory;
-    } else if (Runtime::get().host_visible) {
+    if (Runtime::get().host_visible) {
       e = hipHostMalloc(&b->ptr, cap, hipHostMallocDefault);
       b->host_visible = true;
     } else {
-      e = hipMalloc(&b->ptr, cap);
+      e = hipMallocAsync(&b->ptr, cap, Runtime::get().stream());
     }
     if (e != hipSuccess) {
       // A failed allocation may be fragmentation: give back what the pool
       // holds and try once more.
       (void)hipGetLastError();
       drain();
-      if (inject_fail_ == 0 && !b->host_visible) e = hipMalloc(&b->ptr, cap);
+      if (!b->host_visible) e = hipMallocAsync(&b->ptr, cap, Runtime::get().stream());
       if (e != hipSuccess) {
         (void)hipGetLastError();
         delete b;
@@ -193,6 +194,7 @@ BufferP Pool::acquire(size_t nbytes) {
       }
     }
   }
+  b->requested = nbytes;
   return BufferP(b, [this](Buffer* x) { release(x); });
 }
 
@@ -317,6 +319,15 @@ bool Runtime::init(std::string* err) {
       delete rt;
       return;
     }
+    // Stream-ordered allocations come from the device's default pool; keep
+    // what it holds across synchronisations (the pool above caches buffers
+    // by size class, so the driver pool only backs misses).
+    hipMemPool_t mp;
+    if (hipDeviceGetDefaultMemPool(&mp, 0) == hipSuccess) {
+      uint64_t keep_all = UINT64_MAX;
+      (void)hipMemPoolSetAttribute(mp, hipMemPoolAttrReleaseThreshold, &keep_all);
+    }
+    (void)hipGetLastError();
     const char* hv = getenv("APPLEGPU_HOST_VISIBLE");
     rt->host_visible = hv && *hv && *hv != '0';
     // The reference pool keeps 256 MB (crates/core/src/eager.rs:83); one
