@@ -101,6 +101,9 @@ _SIGS = {
     "applegpu_ffi_device_name": (c_int32, [c_char_p, c_uint32]),
     "applegpu_ffi_graph_stats": (c_int32, [u64p]),
     "applegpu_ffi_inject_alloc_failures": (None, [c_int32]),
+    "applegpu_ffi_gemm_tune": (c_int32, [c_int32, c_int32, c_int32]),
+    "applegpu_ffi_gemm_plan": (c_int32, [c_int64, c_int64, c_int64, c_int64, c_int8, c_bool, c_bool, c_char_p,
+                                         c_uint32]),
     "applegpu_ffi_event_record": (c_int32, [c_uint32]),
     "applegpu_ffi_event_elapsed_ms": (c_float, [c_uint32, c_uint32]),
     "applegpu_eager_op": (c_int32, [c_char_p, u64p, c_uint32, POINTER(c_double), c_uint32, i64p, c_uint32, u64p,

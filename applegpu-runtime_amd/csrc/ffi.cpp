@@ -5,10 +5,12 @@
 // last-error slot (eager_ffi.rs:38-46, backend_ffi.rs:26-34).
 #include "../../include/applegpu_ffi.h"
 
+#include <cstdio>
 #include <cstring>
 
 #include "core.hpp"
 #include "graph.hpp"
+#include "kernels.hpp"
 #include "ops.hpp"
 
 using namespace agpu;
@@ -374,6 +376,33 @@ int32_t applegpu_ffi_graph_stats(uint64_t* out4) {
   GraphStats s = graph_stats();
   out4[0] = s.evals; out4[1] = s.nodes; out4[2] = s.fused_gemm_epilogues; out4[3] = s.launches_saved;
   return 0;
+}
+
+int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (f32_mode != k::kF32Split3 && f32_mode != k::kF32Native) fail("gemm_tune: f32_mode must be 0 or 1");
+    if (cfg < -1 || cfg >= k::kMfConfigs) fail("gemm_tune: cfg must be -1..%d", k::kMfConfigs - 1);
+    if (splits < 0 || splits > 64) fail("gemm_tune: splits must be 0..64");
+    k::GemmTune& t = k::gemm_tune();
+    t.f32_mode = f32_mode;
+    t.cfg = cfg;
+    t.splits = splits;
+    return 0;
+  });
+}
+
+int32_t applegpu_ffi_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int8_t dtype_i8, bool a_kcontig,
+                               bool b_kcontig, char* out, uint32_t cap) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (!out || cap == 0) fail("gemm_plan: null output buffer");
+    k::Gemm g;
+    g.dt = g.b_dt = wire(dtype_i8);
+    g.M = M; g.N = N; g.K = K; g.batch = batch;
+    g.a_sk = a_kcontig ? 1 : M; g.a_sm = a_kcontig ? K : 1;
+    g.b_sk = b_kcontig ? 1 : N; g.b_sn = b_kcontig ? K : 1;
+    snprintf(out, cap, "%s", k::gemm_plan_name(g));
+    return 0;
+  });
 }
 
 void applegpu_ffi_inject_alloc_failures(int32_t n) {

@@ -117,6 +117,21 @@ struct Gemm {
 size_t gemm_workspace_bytes(const Gemm& g);
 void gemm(const Gemm& g, void* workspace, hipStream_t s);
 
+// How fp32 GEMMs compute: kF32Split3 splits each operand into bf16 hi + lo
+// and accumulates hi*hi + hi*lo + lo*hi on bf16 MFMA in fp32 (default);
+// kF32Native runs v_mfma_f32_32x32x2_f32.  `cfg` (-1 = heuristic) and
+// `splits` (0 = heuristic) force a tile configuration for tuning sweeps.
+enum F32Mode : int { kF32Split3 = 0, kF32Native = 1 };
+constexpr int kMfConfigs = 11;  // tile configurations of the bf16-MFMA kernels
+struct GemmTune {
+  int f32_mode = kF32Split3;
+  int cfg = -1;
+  int splits = 0;
+};
+GemmTune& gemm_tune();
+// Name of the configuration the heuristic (or a forced tune) picks.
+const char* gemm_plan_name(const Gemm& g);
+
 // ── fused attention ───────────────────────────────────────────────────────
 struct Attn {
   DType dt = DType::F32;

@@ -8,12 +8,15 @@
 // with an online softmax (running max and sum per query row), so scores never
 // reach HBM.
 //
-// Layout: one 256-thread block owns 64 query rows of one (batch, head); four
-// threads share a row.  Thread (r, sub) keeps its query row in registers,
-// scores keys sub, sub+4, ..., and accumulates output dims
-// {sub*4 + 16*i + 0..3}.  Q, K, V and O are read/written through their own
-// (batch, head, token) strides with unit stride along d, so head splits of a
-// fused QKV projection and the head-merge transpose cost nothing.
+// Layout: one 256-thread block owns 16 query rows of one (batch, head); 16
+// threads share a row (lanes of a row are one 16-lane group of a wavefront,
+// so row max/sum are 4 xor-shuffles).  Thread (r, sub) keeps its query row in
+// registers, scores keys sub, sub+16, ... of each 64-key tile (K tile rows
+// padded to D+4 floats: the 16 lanes' float4 reads hit distinct banks), and
+// accumulates output dims [sub*D/16, (sub+1)*D/16) from a P tile in LDS.
+// Q, K, V and O are read/written through their own (batch, head, token)
+// strides with unit stride along d, so head splits of a fused QKV projection
+// and the head-merge transpose cost nothing.
 #include "device.hpp"
 
 namespace agpu {
@@ -22,8 +25,9 @@ using namespace dev;
 
 namespace {
 
-constexpr int kQT = 64;  // query rows per block
+constexpr int kQT = 16;  // query rows per block
 constexpr int kKT = 64;  // keys per LDS tile
+constexpr int kTPR = 16; // threads per query row
 
 struct AArgs {
   const void* q; const void* k; const void* v; void* o;
@@ -36,15 +40,16 @@ struct AArgs {
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
-  constexpr int KP = D + 4;   // K row pitch (floats), keeps float4 reads conflict-free
-  constexpr int PP = kKT + 1; // P row pitch
-  constexpr int DO = D / 4;   // output dims per thread
+  constexpr int KP = D + 4;     // K row pitch (floats)
+  constexpr int PP = kKT + 4;   // P row pitch
+  constexpr int DPT = D / kTPR; // output dims per thread
+  constexpr int KPT = kKT / kTPR;  // keys per thread per tile
   __shared__ __attribute__((aligned(16))) float Ks[kKT * KP];
   __shared__ __attribute__((aligned(16))) float Vs[kKT * D];
-  __shared__ float Ps[kQT * PP];
+  __shared__ __attribute__((aligned(16))) float Ps[kQT * PP];
 
   const int tid = threadIdx.x;
-  const int r = tid >> 2, sub = tid & 3;
+  const int r = tid / kTPR, sub = tid % kTPR;
   const int64_t bh = blockIdx.x / p.q_tiles;
   const int qt = (int)(blockIdx.x % p.q_tiles);
   const int64_t b = bh / p.H, h = bh % p.H;
@@ -58,16 +63,16 @@ __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
 
   float q[D];
 #pragma unroll
-  for (int d = 0; d < D; ++d) q[d] = row_ok ? to_f(Q[qi * p.q_st + d]) : 0.f;
+  for (int d = 0; d < D; ++d) q[d] = row_ok ? to_f(Q[qi * p.q_st + d]) * p.scale : 0.f;
 
-  float o[DO];
+  float o[DPT];
 #pragma unroll
-  for (int i = 0; i < DO; ++i) o[i] = 0.f;
+  for (int i = 0; i < DPT; ++i) o[i] = 0.f;
   float m = -INFINITY, l = 0.f;
 
   int64_t kv_end = p.Tk;
   if (p.causal) {
-    int64_t last_q = q0 + kQT - 1 < p.Tq - 1 ? q0 + kQT - 1 : p.Tq - 1;
+    const int64_t last_q = q0 + kQT - 1 < p.Tq - 1 ? q0 + kQT - 1 : p.Tq - 1;
     kv_end = last_q + 1 < p.Tk ? last_q + 1 : p.Tk;
   }
 
@@ -82,59 +87,53 @@ __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
     }
     __syncthreads();
 
-    float s[kKT / 4];
+    float s[KPT];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int jj = 0; jj < kKT / 4; ++jj) {
-      const int c = sub + 4 * jj;
+    for (int jj = 0; jj < KPT; ++jj) {
+      const int c = sub + kTPR * jj;
       const float* kr = &Ks[c * KP];
       float acc = 0.f;
 #pragma unroll
       for (int d = 0; d < D; d += 4) {
-        float4 kv = *(const float4*)&kr[d];
+        const float4 kv = *(const float4*)&kr[d];
         acc += q[d] * kv.x;
         acc += q[d + 1] * kv.y;
         acc += q[d + 2] * kv.z;
         acc += q[d + 3] * kv.w;
       }
       const int64_t j = j0 + c;
-      bool vis = j < p.Tk && (!p.causal || j <= qi);
-      s[jj] = vis ? acc * p.scale : -INFINITY;
+      const bool vis = j < p.Tk && (!p.causal || j <= qi);
+      s[jj] = vis ? acc : -INFINITY;
       tmax = fmaxf(tmax, s[jj]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 1, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 2, 64));
+#pragma unroll
+    for (int x = 1; x < kTPR; x <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, x, 64));
     const float m_new = fmaxf(m, tmax);
-    // m_new is finite for every row that has a visible key in this tile or
-    // an earlier one; rows with none keep zero weight.
+    // m_new is finite for every row that has a visible key in this tile or an
+    // earlier one; rows with none keep zero weight.
     const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
     float psum = 0.f;
 #pragma unroll
-    for (int jj = 0; jj < kKT / 4; ++jj) {
+    for (int jj = 0; jj < KPT; ++jj) {
       const float pv = (s[jj] == -INFINITY) ? 0.f : expf(s[jj] - m_new);
       psum += pv;
-      Ps[r * PP + sub + 4 * jj] = pv;
+      Ps[r * PP + sub + kTPR * jj] = pv;
     }
-    psum += __shfl_xor(psum, 1, 64);
-    psum += __shfl_xor(psum, 2, 64);
+#pragma unroll
+    for (int x = 1; x < kTPR; x <<= 1) psum += __shfl_xor(psum, x, 64);
     l = l * alpha + psum;
     m = m_new;
 #pragma unroll
-    for (int i = 0; i < DO; ++i) o[i] *= alpha;
+    for (int i = 0; i < DPT; ++i) o[i] *= alpha;
     __syncthreads();
 
-#pragma unroll 4
-    for (int c = 0; c < kKT; ++c) {
+    const int c_end = (int)(kv_end - j0 < kKT ? kv_end - j0 : kKT);
+    for (int c = 0; c < c_end; ++c) {
       const float pv = Ps[r * PP + c];
-      const float* vr = &Vs[c * D];
+      const float* vr = &Vs[c * D + sub * DPT];
 #pragma unroll
-      for (int i = 0; i < D / 16; ++i) {
-        float4 vv = *(const float4*)&vr[sub * 4 + 16 * i];
-        o[4 * i] += pv * vv.x;
-        o[4 * i + 1] += pv * vv.y;
-        o[4 * i + 2] += pv * vv.z;
-        o[4 * i + 3] += pv * vv.w;
-      }
+      for (int i = 0; i < DPT; ++i) o[i] += pv * vr[i];
     }
     __syncthreads();
   }
@@ -143,9 +142,7 @@ __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
   T* O = (T*)p.o + b * p.o_sb + h * p.o_sh + qi * p.o_st;
   const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
-  for (int i = 0; i < D / 16; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) O[sub * 4 + 16 * i + e] = from_f<T>(o[4 * i + e] * inv);
+  for (int i = 0; i < DPT; ++i) O[sub * DPT + i] = from_f<T>(o[i] * inv);
 }
 
 }  // namespace

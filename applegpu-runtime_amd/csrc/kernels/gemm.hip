@@ -1,86 +1,32 @@
-// Batched GEMM C(m,n) = epilogue(sum_k A(m,k) B(k,n)) for gfx950.
+// Batched GEMM C(m,n) = epilogue(sum_k A(m,k) B(k,n)) for gfx950: planning,
+// launch, and the kernels outside the bf16-MFMA family of gemm_kernels.hpp.
 //
 // Reference semantics: row-major batched matmul with fp32 accumulate
 // (crates/core/src/kernel_templates.rs:987-1072, crates/core/src/eager.rs:403-479),
 // transposed operands read in place (crates/core/src/eager.rs:485-560), and
 // Linear = x W^T + b (backend_cpp/applegpu_backend.cpp:584-620).
 //
-// fp32 path: v_mfma_f32_32x32x2_f32 (gfx950 has no xf32 MFMA; this keeps full
-// fp32 products).  256 threads = 4 wavefronts in a 2x2 grid, a BMxBNx16 tile
-// staged through LDS with register prefetch of the next K slice, operands
-// stored k-major in LDS ([k][m], [k][n]) so each MFMA operand read is 32
-// consecutive floats per half-wave whatever the global layout (row- or
-// column-major A and B are both loaded with 16-byte vector loads).  Skinny
-// problems split K across blocks into an fp32 workspace that a second kernel
-// reduces in a fixed order (deterministic) while applying the epilogue.
-// Block ids are remapped so that consecutive tiles land on the same XCD
-// (blocks are dealt round-robin over the 8 XCDs, each with its own L2), then
-// grouped 8 tile-rows at a time for L2 reuse of B.
-//
-// fp16/bf16 path: v_mfma_f32_32x32x16_{f16,bf16} with the same tiling and fp32
-// accumulation.
-#include "device.hpp"
+// fp32, fp16 and bf16 GEMMs run gemm_mf (gemm_kernels.hpp): bf16/fp16 MFMA
+// 32x32x16 tiles, with fp32 operands split into bf16 hi + lo (three MFMAs per
+// product: hi*hi + hi*lo + lo*hi, fp32 accumulate).  gfx950 has no xf32
+// MFMA; the native fp32 alternative, v_mfma_f32_32x32x2_f32, is kept below
+// (gemm_f32_mfma) and selected with GemmTune::f32_mode = kF32Native.
+// Problems with too few tiles for the CU count split K across blocks into an
+// fp32 workspace that splitk_reduce sums in a fixed order (deterministic)
+// while applying the epilogue.  Block ids are remapped so that consecutive
+// tiles land on the same XCD (blocks are dealt round-robin over the 8 XCDs,
+// each with its own L2), then grouped 8 tile-rows at a time for L2 reuse of B.
+#include "gemm_kernels.hpp"
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
 
 namespace agpu {
 namespace k {
 using namespace dev;
 
 namespace {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-
-struct GArgs {
-  const void* A; const void* B; void* C;
-  int64_t M, N, K;
-  int64_t a_sm, a_sk, a_sb, b_sk, b_sn, b_sb, c_sm, c_sb;
-  int64_t batch;
-  int splits;
-  int64_t k_per_split;
-  float alpha;
-  const void* bias;
-  int act;
-  const void* res; int64_t r_sm, r_sb;
-  const void* mask; int64_t k_sm, k_sb;
-  float* ws;
-  int tiles_m, tiles_n;
-  bool vec_a, vec_b;
-  const float* b_scale;
-};
-
-__device__ __forceinline__ float gelu_tanh(float x) {
-  float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-  inner = fminf(fmaxf(inner, -10.f), 10.f);
-  return 0.5f * x * (1.f + tanhf(inner));
-}
-
-template <typename T>
-__device__ __forceinline__ void epilogue_store(const GArgs& p, int64_t b, int64_t row, int64_t col, float acc) {
-  float v = p.alpha * acc;
-  if (p.bias) v += to_f(((const T*)p.bias)[col]);
-  if (p.act == kActRelu) v = fmaxf(v, 0.f);
-  else if (p.act == kActGelu) v = gelu_tanh(v);
-  else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
-  if (p.res) v += to_f(((const T*)p.res)[b * p.r_sb + row * p.r_sm + col]);
-  if (p.mask) v = to_f(((const T*)p.mask)[b * p.k_sb + row * p.k_sm + col]) > 0.f ? v : 0.f;
-  ((T*)p.C)[b * p.c_sb + row * p.c_sm + col] = from_f<T>(v);
-}
-
-// Tile scheduling: XCD-aware remap, then 8-row tile groups.
-__device__ __forceinline__ void tile_coords(const GArgs& p, int& tm, int& tn) {
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  const int GM = 8;
-  const int per_group = GM * p.tiles_n;
-  const int group = bid / per_group;
-  const int first_m = group * GM;
-  const int gsz = min(p.tiles_m - first_m, GM);
-  const int in_group = bid % per_group;
-  tm = first_m + in_group % gsz;
-  tn = in_group / gsz;
-}
 
 // ── fp32 MFMA kernel ──────────────────────────────────────────────────────
 // Loads a ROWSxBK (KCONT: k contiguous) or BKxROWS (!KCONT) fp32 tile slice
@@ -234,168 +180,43 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma(GArgs p) {
     }
 }
 
-// ── 16-bit MFMA kernel (f16 / bf16 operands, fp32 accumulate) ─────────────
-// LDS tiles are [rows][BK] with k contiguous so one lane's 8 consecutive k
-// values are one 16-byte read; rows are padded by 8 elements.
-template <typename T, int ROWS, bool KCONT>
-struct Tile16 {
-  static constexpr int BK = 32;
-  static constexpr int EPT = ROWS * BK / 256;  // elements per thread (8 or 16)
-  static constexpr int LD = BK + 8;
-  T v[EPT];
-
-  __device__ __forceinline__ void load(const T* __restrict__ base, int64_t s_row, int64_t s_k, int64_t r0,
-                                       int64_t rmax, int64_t k, int64_t kmax, bool vec) {
-    const int t = threadIdx.x;
-    if constexpr (KCONT) {
-      constexpr int TPR = BK / EPT;
-      const int r = t / TPR, kk = (t % TPR) * EPT;
-      const int64_t gr = r0 + r, gk = k + kk;
-      const T* src = base + gr * s_row + gk;
-      if (vec && gr < rmax && gk + EPT <= kmax) {
-#pragma unroll
-        for (int i = 0; i < EPT; i += 8) *(float4*)&v[i] = *(const float4*)(src + i);
-      } else {
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) v[i] = (gr < rmax && gk + i < kmax) ? src[i] : T(0);
-      }
-    } else {
-      constexpr int TPK = ROWS / EPT;
-      const int kk = t / TPK, r = (t % TPK) * EPT;
-      const int64_t gr = r0 + r, gk = k + kk;
-      const T* src = base + gk * s_k + gr;
-      if (vec && gk < kmax && gr + EPT <= rmax) {
-#pragma unroll
-        for (int i = 0; i < EPT; i += 8) *(float4*)&v[i] = *(const float4*)(src + i);
-      } else {
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) v[i] = (gk < kmax && gr + i < rmax) ? src[i] : T(0);
-      }
-    }
-  }
-
-  __device__ __forceinline__ void store(T* __restrict__ lds) const {
-    const int t = threadIdx.x;
-    if constexpr (KCONT) {
-      constexpr int TPR = BK / EPT;
-      const int r = t / TPR, kk = (t % TPR) * EPT;
-#pragma unroll
-      for (int i = 0; i < EPT; i += 8) *(float4*)&lds[r * LD + kk + i] = *(const float4*)&v[i];
-    } else {
-      constexpr int TPK = ROWS / EPT;
-      const int kk = t / TPK, r = (t % TPK) * EPT;
-#pragma unroll
-      for (int i = 0; i < EPT; ++i) lds[(r + i) * LD + kk] = v[i];
-    }
-  }
-};
-
-template <typename T> struct Mfma16;
-template <> struct Mfma16<half_t> {
-  static __device__ __forceinline__ f32x16 run(const half_t* a, const half_t* b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)a, *(const f16x8*)b, c, 0, 0, 0);
-  }
-};
-template <> struct Mfma16<bf16_t> {
-  static __device__ __forceinline__ f32x16 run(const bf16_t* a, const bf16_t* b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)a, *(const bf16x8*)b, c, 0, 0, 0);
-  }
-};
-
-template <typename T, int BM, int BN, bool AK, bool BKC>
-__global__ void __launch_bounds__(256) gemm_16_mfma(GArgs p) {
-  constexpr int BK = 32;
-  constexpr int LD = BK + 8;
-  constexpr int TM = BM / 64, TN = BN / 64;
-  __shared__ __attribute__((aligned(16))) T As[2][BM * LD];
-  __shared__ __attribute__((aligned(16))) T Bs[2][BN * LD];
-
-  int tm, tn;
-  tile_coords(p, tm, tn);
-  const int64_t z = blockIdx.y;
-  const int64_t b = z / p.splits;
-  const int split = (int)(z % p.splits);
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t kbeg = (int64_t)split * p.k_per_split;
-  int64_t kend = kbeg + p.k_per_split;
-  if (kend > p.K) kend = p.K;
-  const T* A = (const T*)p.A + b * p.a_sb;
-  const T* B = (const T*)p.B + b * p.b_sb;
-
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  Tile16<T, BM, AK> ta;
-  Tile16<T, BN, BKC> tb;
-  const int64_t nk = (kend - kbeg + BK - 1) / BK;
-  if (nk > 0) {
-    ta.load(A, p.a_sm, p.a_sk, m0, p.M, kbeg, kend, p.vec_a);
-    tb.load(B, p.b_sn, p.b_sk, n0, p.N, kbeg, kend, p.vec_b);
-    ta.store(As[0]);
-    tb.store(Bs[0]);
-  }
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = (int)(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const int64_t kn = kbeg + (kt + 1) * BK;
-      ta.load(A, p.a_sm, p.a_sk, m0, p.M, kn, kend, p.vec_a);
-      tb.load(B, p.b_sn, p.b_sk, n0, p.N, kn, kend, p.vec_b);
-    }
-    const T* as = As[buf];
-    const T* bs = Bs[buf];
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      // lane l holds A[row = l%32][k = 8*(l/32) .. +8] (and likewise B[k][col])
-      const int ko = kk + 8 * (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = Mfma16<T>::run(&as[(wm + i * 32 + (lane & 31)) * LD + ko],
-                                     &bs[(wn + j * 32 + (lane & 31)) * LD + ko], acc[i][j]);
-    }
-    if (more) {
-      ta.store(As[buf ^ 1]);
-      tb.store(Bs[buf ^ 1]);
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t col = n0 + wn + j * 32 + (lane & 31);
-      if (col >= p.N) continue;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row >= p.M) continue;
-        if (p.splits > 1)
-          p.ws[((int64_t)split * p.batch + b) * p.M * p.N + row * p.N + col] = acc[i][j][r];
-        else
-          epilogue_store<T>(p, b, row, col, acc[i][j][r]);
-      }
-    }
-}
-
-// Split-K reduction in split order, then the epilogue.
+// Split-K reduction in split order, then the epilogue.  Four outputs per
+// thread; every split's partial is loaded before the first add, so the
+// loads overlap instead of costing one memory latency per split.
 template <typename T>
 __global__ void __launch_bounds__(256) splitk_reduce(GArgs p) {
+  constexpr int kMaxSplits = 8;
   const int64_t total = p.batch * p.M * p.N;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    float s = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) s += p.ws[(int64_t)sp * total + i];
-    const int64_t col = i % p.N, row = (i / p.N) % p.M, b = i / (p.M * p.N);
-    epilogue_store<T>(p, b, row, col, s);
+  const bool vec = (total & 3) == 0;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < total; i += (int64_t)gridDim.x * 1024) {
+    float part[kMaxSplits][4];
+    const int ns = p.splits < kMaxSplits ? p.splits : kMaxSplits;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp) {
+      if (sp >= ns) break;
+      const float* src = p.ws + (int64_t)sp * total + i;
+      if (vec) {
+        const float4 v = *(const float4*)src;
+        part[sp][0] = v.x; part[sp][1] = v.y; part[sp][2] = v.z; part[sp][3] = v.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) part[sp][e] = i + e < total ? src[e] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (i + e >= total) break;
+      float s = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < kMaxSplits; ++sp) {
+        if (sp >= ns) break;
+        s += part[sp][e];
+      }
+      for (int sp = kMaxSplits; sp < p.splits; ++sp) s += p.ws[(int64_t)sp * total + i + e];
+      const int64_t ie = i + e;
+      const int64_t col = ie % p.N, row = (ie / p.N) % p.M, b = ie / (p.M * p.N);
+      epilogue_store<T>(p, b, row, col, s);
+    }
   }
 }
 
@@ -444,30 +265,71 @@ __global__ void __launch_bounds__(256) gemm_generic(GArgs p) {
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+enum PlanKind { kGeneric = 0, kNative32 = 1, kMf = 2 };
+
 struct Plan {
-  int bm, bn, splits;
-  int64_t kps;
-  bool mfma;
+  int kind;
+  int cfg;          // gemm_mf configuration (kMf)
+  int bm, bn, bk;
+  int splits;
+  int64_t kps;      // k per split, a multiple of bk
 };
 
+int64_t tiles_for(const Gemm& g, int bm, int bn) {
+  return ((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * g.batch;
+}
+
 Plan make_plan(const Gemm& g, int cus) {
+  const GemmTune& tu = gemm_tune();
   Plan pl{};
   const bool is16 = g.dt == DType::F16 || g.dt == DType::BF16;
   const bool a_ok = g.a_sk == 1 || g.a_sm == 1;
   const bool b_ok = g.b_sk == 1 || g.b_sn == 1;
-  pl.mfma = a_ok && b_ok && g.b_dt == g.dt && !g.b_scale && (g.dt == DType::F32 || is16);
-  pl.bm = g.M <= 64 ? 64 : 128;
-  pl.bn = g.N <= 64 ? 64 : 128;
-  const int BK = is16 ? 32 : 16;
-  int64_t tiles = ((g.M + pl.bm - 1) / pl.bm) * ((g.N + pl.bn - 1) / pl.bn) * g.batch;
-  int64_t nk = (g.K + BK - 1) / BK;
+  pl.splits = 1;
+  if (!(a_ok && b_ok && g.b_dt == g.dt && !g.b_scale && (g.dt == DType::F32 || is16))) {
+    pl.kind = kGeneric;
+    pl.bm = pl.bn = 64;
+    pl.bk = 16;
+    pl.kps = g.K;
+    return pl;
+  }
+  if (g.dt == DType::F32 && tu.f32_mode == kF32Native) {
+    pl.kind = kNative32;
+    pl.bm = g.M <= 64 ? 64 : 128;
+    pl.bn = g.N <= 64 ? 64 : 128;
+    pl.bk = 16;
+  } else {
+    pl.kind = kMf;
+    if (tu.cfg >= 0 && tu.cfg < kMfConfigs) {
+      pl.cfg = tu.cfg;
+    } else {
+      // Measured on MI355X (fp32 via bf16x3 and fp16, shapes of the GPT-2,
+      // MLP and int8 workloads): 128x128 tiles win once they alone give every
+      // CU a block (fp16: with 64-deep K slices); below that, 64x64 tiles
+      // with 64-deep K slices, split across blocks until about two blocks
+      // per CU.
+      pl.cfg = tiles_for(g, 128, 128) >= cus ? (is16 ? 5 : 0) : 6;
+    }
+    pl.bm = kMfShape[pl.cfg].bm;
+    pl.bn = kMfShape[pl.cfg].bn;
+    pl.bk = kMfShape[pl.cfg].bk;
+  }
+  const int64_t tiles = tiles_for(g, pl.bm, pl.bn);
+  const int64_t nk = (g.K + pl.bk - 1) / pl.bk;
   int splits = 1;
-  const int64_t target = 2LL * cus;
-  while (pl.mfma && tiles * splits < target && nk / (splits * 2) >= 8 && splits < 32 &&
-         g.batch * splits * 2 <= 65535)
-    splits *= 2;
+  if (tu.splits > 0) {
+    splits = tu.splits;
+  } else if (pl.kind == kMf) {
+    // Split K across blocks while the grid is short of two blocks per CU and
+    // every split keeps at least 3 K slices (at most 8 splits).
+    while (tiles * splits < 2LL * cus && nk / (splits * 2) >= 3 && splits < 8) splits *= 2;
+  } else {
+    while (tiles * splits * 2 <= cus && nk / (splits * 2) >= 8 && splits < 32) splits *= 2;
+  }
+  if (splits > nk) splits = (int)(nk > 0 ? nk : 1);
+  while (splits > 1 && g.batch * splits > 65535) splits /= 2;
   pl.splits = splits;
-  pl.kps = ((nk + splits - 1) / splits) * BK;
+  pl.kps = ((nk + splits - 1) / splits) * pl.bk;
   return pl;
 }
 
@@ -491,7 +353,7 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   p.b_scale = g.b_scale;
   const size_t esz = dtype_size(g.dt);
   const int vw = (int)(16 / esz);  // elements per 16-byte vector
-  // Vector loads need 16-byte aligned rows along the contiguous axis.
+  // Vector loads need 16-byte aligned runs along the contiguous axis.
   const int64_t a_lead = g.a_sk == 1 ? g.a_sm : g.a_sk;
   const int64_t b_lead = g.b_sk == 1 ? g.b_sn : g.b_sk;
   p.vec_a = al16(g.A) && (a_lead % vw == 0) && (g.a_sb % vw == 0);
@@ -507,14 +369,6 @@ void launch_f32(const GArgs& p, bool ak, bool bk, dim3 grid, hipStream_t s) {
   else hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, false, false>), grid, dim3(256), 0, s, p);
 }
 
-template <typename T, int BM, int BN>
-void launch_16(const GArgs& p, bool ak, bool bk, dim3 grid, hipStream_t s) {
-  if (ak && bk) hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, true, true>), grid, dim3(256), 0, s, p);
-  else if (ak) hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, true, false>), grid, dim3(256), 0, s, p);
-  else if (bk) hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, false, true>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((gemm_16_mfma<T, BM, BN, false, false>), grid, dim3(256), 0, s, p);
-}
-
 int cu_count() {
   static int cus = 0;
   if (!cus) {
@@ -525,6 +379,25 @@ int cu_count() {
 }
 
 }  // namespace
+
+GemmTune& gemm_tune() {
+  static GemmTune t = [] {
+    GemmTune d;
+    const char* m = getenv("APPLEGPU_GEMM_F32");
+    if (m && (!strcmp(m, "native") || !strcmp(m, "f32"))) d.f32_mode = kF32Native;
+    return d;
+  }();
+  return t;
+}
+
+const char* gemm_plan_name(const Gemm& g) {
+  static thread_local char buf[96];
+  Plan pl = make_plan(g, cu_count());
+  const char* kind = pl.kind == kGeneric ? "generic" : pl.kind == kNative32 ? "f32-native" : "mf";
+  snprintf(buf, sizeof buf, "%s cfg%d %dx%dx%d splits=%d", kind, pl.kind == kMf ? pl.cfg : -1, pl.bm, pl.bn, pl.bk,
+           pl.splits);
+  return buf;
+}
 
 size_t gemm_workspace_bytes(const Gemm& g) {
   Plan pl = make_plan(g, cu_count());
@@ -538,7 +411,8 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   GArgs p = make_args(g, pl);
   p.ws = (float*)workspace;
   if (pl.splits > 1 && !workspace) fail("gemm: split-K workspace missing");
-  if (!pl.mfma) {
+  if (pl.kind == kGeneric) {
+    if (g.batch > 65535) fail("gemm: batch %lld too large", (long long)g.batch);
     dim3 grid((unsigned)((g.N + 63) / 64), (unsigned)((g.M + 63) / 64), (unsigned)g.batch);
     p.splits = 1;
     if (g.b_scale) {
@@ -551,28 +425,30 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     return;
   }
   if (g.batch * pl.splits > 65535) fail("gemm: batch %lld too large", (long long)g.batch);
+  const int64_t nblocks = (int64_t)p.tiles_m * p.tiles_n;
+  if (nblocks > 0x7fffffff) fail("gemm: too many tiles");
   const bool ak = g.a_sk == 1, bk = g.b_sk == 1;
-  dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)(g.batch * pl.splits));
-  if (g.dt == DType::F32) {
+  dim3 grid((unsigned)nblocks, (unsigned)(g.batch * pl.splits));
+  if (pl.kind == kNative32) {
     if (pl.bm == 128 && pl.bn == 128) launch_f32<128, 128>(p, ak, bk, grid, s);
     else if (pl.bm == 128) launch_f32<128, 64>(p, ak, bk, grid, s);
     else if (pl.bn == 128) launch_f32<64, 128>(p, ak, bk, grid, s);
     else launch_f32<64, 64>(p, ak, bk, grid, s);
-  } else if (g.dt == DType::F16) {
-    if (pl.bm == 128 && pl.bn == 128) launch_16<half_t, 128, 128>(p, ak, bk, grid, s);
-    else if (pl.bm == 128) launch_16<half_t, 128, 64>(p, ak, bk, grid, s);
-    else if (pl.bn == 128) launch_16<half_t, 64, 128>(p, ak, bk, grid, s);
-    else launch_16<half_t, 64, 64>(p, ak, bk, grid, s);
   } else {
-    if (pl.bm == 128 && pl.bn == 128) launch_16<bf16_t, 128, 128>(p, ak, bk, grid, s);
-    else if (pl.bm == 128) launch_16<bf16_t, 128, 64>(p, ak, bk, grid, s);
-    else if (pl.bn == 128) launch_16<bf16_t, 64, 128>(p, ak, bk, grid, s);
-    else launch_16<bf16_t, 64, 64>(p, ak, bk, grid, s);
+    // Unmasked loads need 16-byte aligned runs and whole 16-byte vectors:
+    // K % VW == 0 for an operand contiguous along k, rows % VW == 0 for one
+    // contiguous along its rows.
+    const int64_t vw = 16 / (int64_t)dtype_size(g.dt);
+    const bool fast = p.vec_a && p.vec_b && (ak ? g.K % vw == 0 : g.M % vw == 0) &&
+                      (bk ? g.K % vw == 0 : g.N % vw == 0);
+    if (g.dt == DType::F32) launch_mf_f32(p, pl.cfg, ak, bk, fast, grid, s);
+    else if (g.dt == DType::F16) launch_mf_f16(p, pl.cfg, ak, bk, fast, grid, s);
+    else launch_mf_bf16(p, pl.cfg, ak, bk, fast, grid, s);
   }
   check_launch("gemm_mfma");
   if (pl.splits > 1) {
     int64_t total = g.batch * g.M * g.N;
-    int64_t blocks = (total + 255) / 256;
+    int64_t blocks = (total + 1023) / 1024;
     if (blocks > 65536) blocks = 65536;
     AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce<T>), dim3((unsigned)blocks), dim3(256), 0, s, p));
     check_launch("splitk_reduce");

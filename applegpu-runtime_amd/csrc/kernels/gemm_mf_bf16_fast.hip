@@ -1,0 +1,14 @@
+// Instantiates the gemm_mf kernels for bf16 operands that qualify for the
+// unmasked fast loads (see gemm_kernels.hpp).
+#include "gemm_kernels.hpp"
+
+namespace agpu {
+namespace k {
+using namespace dev;
+
+void launch_mf_bf16_fast(const GArgs& p, int cfg, bool ak, bool bk, dim3 grid, hipStream_t s) {
+  launch_mf<bf16_t, bf16_t, true>(p, cfg, ak, bk, grid, s);
+}
+
+}  // namespace k
+}  // namespace agpu

@@ -181,6 +181,22 @@ void applegpu_ffi_inject_alloc_failures(int32_t n);
 int32_t applegpu_ffi_event_record(uint32_t slot);
 float applegpu_ffi_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
 
+/* GEMM tuning (no reference counterpart; the reference chooses between
+ * MPSMatrixMultiplication and its tiled kernel inside
+ * swift/Sources/AppleGPUBridge/compute.swift:1544-1630).  f32_mode: 0 = fp32
+ * operands split into bf16 hi/lo with three bf16 MFMAs per product (default),
+ * 1 = native fp32 MFMA (v_mfma_f32_32x32x2_f32; also APPLEGPU_GEMM_F32=native).
+ * cfg: -1 = heuristic, 0..10 = tile configuration (BM x BN x BK: 128x128x32,
+ * 64x128x32, 64x64x64, 32x64x64, 32x32x64, 128x128x64, 64x64x64, 64x128x64,
+ * 32x32x256, 32x64x256, 64x64x128).  splits: 0 = heuristic, n = split K across n blocks.
+ * Returns 0, or -1 for an out-of-range value. */
+int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits);
+/* The plan the GEMM heuristic picks for an M x N x K (batch) problem of the
+ * given dtype and operand layouts (a_kcontig: A(m,k) has unit k stride;
+ * b_kcontig: B(k,n) has unit k stride), written as text into out. */
+int32_t applegpu_ffi_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int8_t dtype_i8,
+                               bool a_kcontig, bool b_kcontig, char* out, uint32_t cap);
+
 /* Generic eager op: runs `op` at once (same names and parameters as
  * applegpu_graph_op), registers the outputs, writes their ids to out_ids and
  * returns their number (or -1).  Replaces the aten kernels of the
