@@ -90,6 +90,21 @@ class GpuTensor:
             raw = (raw.astype(np.uint32) << 16).view(np.float32)
         return raw.reshape(shape)
 
+    def write(self, arr) -> None:
+        """Overwrites this (materialised) tensor with host data of the same
+        shape; bfloat16 tensors take float32 data, rounded to nearest even."""
+        dt = self.dtype
+        a = np.asarray(arr)
+        if list(a.shape) != self.shape and a.size != int(np.prod(self.shape) if self.shape else 1):
+            raise ValueError(f"write: shape {list(a.shape)} does not match {self.shape}")
+        if dt == "bfloat16":
+            u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+            raw = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        else:
+            raw = np.ascontiguousarray(a, dtype=np.bool_ if dt == "bool" else np.dtype(dt))
+        if lib.applegpu_ffi_write_bytes(self._id, raw.ctypes.data, raw.nbytes) != 0:
+            raise ValueError(ffi_error())
+
     def to_numpy(self) -> np.ndarray:
         """Evaluates if lazy and returns a copy (bfloat16 comes back as float32)."""
         return self._read_raw()
@@ -485,3 +500,63 @@ def linear_int8(x, q, scale):
 def blit_copy(src, dst):
     if lib.applegpu_ffi_copy(_t(src)._id, _t(dst)._id) != 0:
         raise ValueError(ffi_error())
+
+
+# ── graph capture ────────────────────────────────────────────────────────────
+class CapturedGraph:
+    """The launch sequence of one call, recorded as a HIP graph.
+
+    `replay()` re-runs every recorded kernel (hipGraphLaunch on the library
+    stream, asynchronous) from the current contents of the tensors the call
+    read, into the same output buffers: write new inputs with
+    `GpuTensor.write` (or eager `copy_from`) between replays, then read
+    `outputs`.  The reference has no counterpart: it re-encodes every op of
+    every eval (crates/core/src/lazy.rs:369-474)."""
+
+    def __init__(self, handle: int, outputs):
+        self._handle = handle
+        self.outputs = outputs
+
+    @property
+    def handle(self) -> int:
+        return self._handle
+
+    def replay(self) -> None:
+        if lib.applegpu_graph_replay(self._handle) != 0:
+            raise ValueError(ffi_error())
+
+    def nbytes(self) -> int:
+        return int(lib.applegpu_graph_bytes(self._handle))
+
+    def destroy(self) -> None:
+        if self._handle:
+            lib.applegpu_graph_destroy(self._handle)
+            self._handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+def capture(fn, *args, **kwargs) -> CapturedGraph:
+    """Runs `fn(*args, **kwargs)` once under stream capture and returns the
+    recorded graph; its `outputs` are fn's return value, with lazy tensors
+    evaluated inside the capture.  Inputs must already be materialised on
+    the device (no host reads or writes are allowed inside `fn`)."""
+    _check_init()
+    if lib.applegpu_capture_begin() != 0:
+        raise ValueError(ffi_error())
+    try:
+        out = fn(*args, **kwargs)
+        for t in (out if isinstance(out, (list, tuple)) else [out]):
+            if isinstance(t, GpuTensor):
+                t.eval()
+    except BaseException:
+        lib.applegpu_capture_abort()
+        raise
+    handle = lib.applegpu_capture_end()
+    if handle <= 0:
+        raise ValueError(ffi_error())
+    return CapturedGraph(int(handle), out)

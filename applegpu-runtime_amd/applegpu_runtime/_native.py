@@ -101,6 +101,12 @@ _SIGS = {
     "applegpu_ffi_device_name": (c_int32, [c_char_p, c_uint32]),
     "applegpu_ffi_graph_stats": (c_int32, [u64p]),
     "applegpu_ffi_inject_alloc_failures": (None, [c_int32]),
+    "applegpu_capture_begin": (c_int32, []),
+    "applegpu_capture_end": (c_int64, []),
+    "applegpu_capture_abort": (c_int32, []),
+    "applegpu_graph_replay": (c_int32, [c_int64]),
+    "applegpu_graph_destroy": (c_int32, [c_int64]),
+    "applegpu_graph_bytes": (c_uint64, [c_int64]),
     "applegpu_ffi_gemm_tune": (c_int32, [c_int32, c_int32, c_int32]),
     "applegpu_ffi_gemm_plan": (c_int32, [c_int64, c_int64, c_int64, c_int64, c_int8, c_bool, c_bool, c_char_p,
                                          c_uint32]),

@@ -77,24 +77,33 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32") -> dict:
     return {"weights": w, "config": dict(cfg), "dtype": dtype}
 
 
-def gpt2_forward(model: dict, input_ids, kv_cache=None):
+def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
     """Returns (logits [seq, vocab], new_kv_cache) for one sequence.
 
-    input_ids: list/array of token ids.  With kv_cache (list of (k, v) per
-    layer, each [n_head, past, d_head]) only the last token is processed.
+    input_ids: list/array of token ids, or an int32 GpuTensor [T] already on
+    the device (then `positions`, an int32 GpuTensor [T], may be given too;
+    both device-resident inputs let the forward run under `gpu.capture`).
+    With kv_cache (list of (k, v) per layer, each [n_head, past, d_head]) only
+    the last token is processed.
     """
     w = model["weights"]
     cfg = model["config"]
     L, H, d = cfg["n_layer"], cfg["n_head"], cfg["n_embd"]
     hd = d // H
-    ids = list(np.asarray(input_ids).reshape(-1))
     cached = kv_cache is not None
-    toks = ids[-1:] if cached else ids
-    start = len(ids) - 1 if cached else 0
-    T = len(toks)
-
-    idx = gpu.from_numpy(np.asarray(toks, dtype=np.int32))
-    pos = gpu.from_numpy(np.arange(start, start + T, dtype=np.int32))
+    if isinstance(input_ids, gpu.GpuTensor):
+        if cached:
+            raise ValueError("gpt2_forward: device-resident ids take no kv_cache")
+        idx = input_ids
+        T = idx.shape[0]
+        pos = positions if positions is not None else gpu.from_numpy(np.arange(T, dtype=np.int32))
+    else:
+        ids = list(np.asarray(input_ids).reshape(-1))
+        toks = ids[-1:] if cached else ids
+        start = len(ids) - 1 if cached else 0
+        T = len(toks)
+        idx = gpu.from_numpy(np.asarray(toks, dtype=np.int32))
+        pos = gpu.from_numpy(np.arange(start, start + T, dtype=np.int32))
     x = gpu.embedding(w["transformer.wte.weight"], idx) + gpu.embedding(w["transformer.wpe.weight"], pos)
 
     new_cache = []

@@ -56,13 +56,30 @@ struct Error : std::runtime_error {
 void check_launch(const char* what);
 
 // ── device buffers ────────────────────────────────────────────────────────
+struct Arena;
+
 struct Buffer {
   void* ptr = nullptr;
   size_t bytes = 0;       // capacity (a power of two when pooled)
   size_t requested = 0;   // bytes the current owner asked for (bounds of views)
   bool host_visible = false;
+  bool stream_ordered = true;  // hipMallocAsync'd; false: hipMalloc'd during a capture
+  bool out = false;            // handed out and not yet released
+  Arena* arena = nullptr;      // set while a captured graph owns the buffer
 };
 using BufferP = std::shared_ptr<Buffer>;
+
+// The buffers of one captured graph: every buffer handed out while its
+// capture is active.  Buffers released during the capture go back to the
+// arena's own free lists (later ops of the same capture reuse them, in stream
+// order); none leaves the arena until the graph is destroyed, because every
+// replay writes them again.
+struct Arena {
+  std::vector<Buffer*> owned;
+  std::map<size_t, std::vector<Buffer*>> free;
+  bool capturing = true;
+  size_t bytes = 0;
+};
 
 struct PoolStats {
   uint64_t hits = 0, misses = 0;
@@ -82,8 +99,17 @@ class Pool {
   // Test hook: make the next `n` device allocations fail.
   void inject_failures(int n) { inject_fail_ = n; }
 
+  // Graph capture: route allocations through `a` until end_capture; then
+  // the arena holds its buffers until release_arena hands them back.
+  void begin_capture(Arena* a);
+  void end_capture();
+  void release_arena(Arena* a);
+  bool capturing();
+
  private:
   void release(Buffer* b);
+  void free_now(Buffer* b);
+  Arena* active_ = nullptr;
   std::mutex mu_;
   std::map<size_t, std::vector<Buffer*>> buckets_;
   size_t watermark_;

@@ -7,6 +7,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <unordered_map>
 
 #include "core.hpp"
 #include "graph.hpp"
@@ -85,7 +86,12 @@ void check_capacity(const Tensor& t) {
          shape_str(t.dims()).c_str(), t.extent_bytes(), have);
 }
 
+void no_capture(const char* what) {
+  if (rt().pool().capturing()) fail("%s is not allowed while a graph capture is active", what);
+}
+
 void copy_to_host(const TensorP& t0, void* dst, uint64_t nbytes) {
+  no_capture("reading a tensor to the host");
   TensorP t = t0;
   if (t->pending()) eval(t);
   if (nbytes != t->nbytes())
@@ -97,6 +103,7 @@ void copy_to_host(const TensorP& t0, void* dst, uint64_t nbytes) {
 }
 
 void copy_from_host(const TensorP& t, const void* src, uint64_t nbytes) {
+  no_capture("writing a tensor from the host");
   if (t->pending()) fail("cannot write into a tensor with pending ops");
   if (nbytes != t->nbytes())
     fail("write of %llu bytes into a tensor of %zu bytes", (unsigned long long)nbytes, t->nbytes());
@@ -282,6 +289,7 @@ void applegpu_ffi_synchronize(void) {
 
 int32_t applegpu_ffi_read_f32(uint64_t tensor_id, float* out_ptr, uint64_t max_elements) {
   return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    no_capture("read_f32");
     TensorP t = rt().lookup(tensor_id);
     if (t->pending()) eval(t);
     TensorP f = ops::cast(t, DType::F32);
@@ -378,6 +386,120 @@ int32_t applegpu_ffi_graph_stats(uint64_t* out4) {
   return 0;
 }
 
+// ── graph capture ──────────────────────────────────────────────────────────
+namespace {
+struct Captured {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  Arena* arena = nullptr;
+};
+std::unordered_map<int64_t, Captured*>& graphs() {
+  static auto* m = new std::unordered_map<int64_t, Captured*>();
+  return *m;
+}
+int64_t g_next_graph = 1;
+Arena* g_capture = nullptr;
+
+void drop_capture_state(Arena* a, hipGraph_t graph) {
+  if (graph) (void)hipGraphDestroy(graph);
+  rt().pool().release_arena(a);
+  delete a;
+}
+}  // namespace
+
+int32_t applegpu_capture_begin(void) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (g_capture) fail("a graph capture is already active");
+    auto* a = new Arena();
+    rt().pool().begin_capture(a);
+    hipError_t e = hipStreamBeginCapture(rt().stream(), hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      rt().pool().end_capture();
+      drop_capture_state(a, nullptr);
+      fail("hipStreamBeginCapture failed: %s", hipGetErrorString(e));
+    }
+    g_capture = a;
+    return 0;
+  });
+}
+
+int64_t applegpu_capture_end(void) {
+  return guarded<int64_t>(kFfi, -1, [&]() -> int64_t {
+    if (!g_capture) fail("no graph capture is active");
+    Arena* a = g_capture;
+    g_capture = nullptr;
+    rt().pool().end_capture();
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(rt().stream(), &graph);
+    if (e != hipSuccess || !graph) {
+      (void)hipGetLastError();
+      drop_capture_state(a, graph);
+      fail("hipStreamEndCapture failed: %s", hipGetErrorString(e));
+    }
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      drop_capture_state(a, graph);
+      fail("hipGraphInstantiate failed: %s", hipGetErrorString(e));
+    }
+    auto* c = new Captured{graph, exec, a};
+    const int64_t id = g_next_graph++;
+    graphs()[id] = c;
+    return id;
+  });
+}
+
+int32_t applegpu_capture_abort(void) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (!g_capture) return 0;
+    Arena* a = g_capture;
+    g_capture = nullptr;
+    rt().pool().end_capture();
+    hipGraph_t graph = nullptr;
+    (void)hipStreamEndCapture(rt().stream(), &graph);
+    (void)hipGetLastError();
+    drop_capture_state(a, graph);
+    return 0;
+  });
+}
+
+int32_t applegpu_graph_replay(int64_t handle) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (g_capture) fail("cannot replay a graph while a capture is active");
+    auto it = graphs().find(handle);
+    if (it == graphs().end()) fail("graph %lld not found", (long long)handle);
+    AGPU_HIP(hipGraphLaunch(it->second->exec, rt().stream()));
+    return 0;
+  });
+}
+
+int32_t applegpu_graph_destroy(int64_t handle) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (!Runtime::initialized()) return 0;
+    auto it = graphs().find(handle);
+    if (it == graphs().end()) fail("graph %lld not found", (long long)handle);
+    Captured* c = it->second;
+    graphs().erase(it);
+    // A replay may still be running: the graph's buffers return to the pool
+    // only after the stream drains.
+    AGPU_HIP(hipStreamSynchronize(rt().stream()));
+    (void)hipGraphExecDestroy(c->exec);
+    drop_capture_state(c->arena, c->graph);
+    delete c;
+    return 0;
+  });
+}
+
+uint64_t applegpu_graph_bytes(int64_t handle) {
+  return guarded<uint64_t>(kFfi, 0, [&]() -> uint64_t {
+    auto it = graphs().find(handle);
+    if (it == graphs().end()) fail("graph %lld not found", (long long)handle);
+    return it->second->arena->bytes;
+  });
+}
+
 int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits) {
   return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
     if (f32_mode != k::kF32Split3 && f32_mode != k::kF32Native) fail("gemm_tune: f32_mode must be 0 or 1");
@@ -423,6 +545,7 @@ int32_t applegpu_ffi_event_record(uint32_t slot) {
 float applegpu_ffi_event_elapsed_ms(uint32_t a, uint32_t b) {
   return guarded<float>(kFfi, -1.f, [&]() -> float {
     if (a >= 16 || b >= 16 || !g_events[a] || !g_events[b]) fail("event slots not recorded");
+    no_capture("event_elapsed_ms");
     AGPU_HIP(hipEventSynchronize(g_events[b]));
     float ms = 0.f;
     AGPU_HIP(hipEventElapsedTime(&ms, g_events[a], g_events[b]));

@@ -61,9 +61,14 @@ __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
   const T* K = (const T*)p.k + b * p.k_sb + h * p.k_sh;
   const T* V = (const T*)p.v + b * p.v_sb + h * p.v_sh;
 
+  // Loads use clamped, always-legal rows and are masked afterwards: no
+  // per-thread branches around global loads, so they all stay in flight.
+  const int64_t qrow = row_ok ? qi : p.Tq - 1;
   float q[D];
 #pragma unroll
-  for (int d = 0; d < D; ++d) q[d] = row_ok ? to_f(Q[qi * p.q_st + d]) * p.scale : 0.f;
+  for (int d = 0; d < D; ++d) q[d] = to_f(Q[qrow * p.q_st + d]);
+#pragma unroll
+  for (int d = 0; d < D; ++d) q[d] = row_ok ? q[d] * p.scale : 0.f;
 
   float o[DPT];
 #pragma unroll
@@ -77,13 +82,24 @@ __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
   }
 
   for (int64_t j0 = 0; j0 < kv_end; j0 += kKT) {
-    // stage K and V tiles as fp32
-    for (int e = tid; e < kKT * D; e += 256) {
+    // stage K and V tiles as fp32: all loads first, then the LDS stores
+    constexpr int EPT = kKT * D / 256;
+    float kr[EPT], vr[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = tid + 256 * i;
       const int c = e / D, d = e % D;
-      const int64_t j = j0 + c;
-      const bool ok = j < p.Tk;
-      Ks[c * KP + d] = ok ? to_f(K[j * p.k_st + d]) : 0.f;
-      Vs[c * D + d] = ok ? to_f(V[j * p.v_st + d]) : 0.f;
+      const int64_t j = j0 + c < p.Tk ? j0 + c : p.Tk - 1;
+      kr[i] = to_f(K[j * p.k_st + d]);
+      vr[i] = to_f(V[j * p.v_st + d]);
+    }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = tid + 256 * i;
+      const int c = e / D, d = e % D;
+      const bool ok = j0 + c < p.Tk;
+      Ks[c * KP + d] = ok ? kr[i] : 0.f;
+      Vs[c * D + d] = ok ? vr[i] : 0.f;
     }
     __syncthreads();
 

@@ -152,20 +152,32 @@ static size_t next_pow2(size_t n) {
 BufferP Pool::acquire(size_t nbytes) {
   size_t cap = next_pow2(nbytes < 4 ? 4 : nbytes);
   Buffer* b = nullptr;
+  Arena* arena = nullptr;
   {
     std::lock_guard<std::mutex> g(mu_);
     if (inject_fail_ > 0) {
       --inject_fail_;
       fail("device allocation of %zu bytes failed: injected failure (test hook)", cap);
     }
-    auto it = buckets_.find(cap);
-    if (it != buckets_.end() && !it->second.empty()) {
-      b = it->second.back();
-      it->second.pop_back();
-      pooled_ -= cap;
-      ++hits_;
-    } else {
-      ++misses_;
+    arena = active_;
+    if (arena) {
+      auto it = arena->free.find(cap);
+      if (it != arena->free.end() && !it->second.empty()) {
+        b = it->second.back();
+        it->second.pop_back();
+        ++hits_;
+      }
+    }
+    if (!b) {
+      auto it = buckets_.find(cap);
+      if (it != buckets_.end() && !it->second.empty()) {
+        b = it->second.back();
+        it->second.pop_back();
+        pooled_ -= cap;
+        ++hits_;
+      } else {
+        ++misses_;
+      }
     }
     live_ += cap;
   }
@@ -176,26 +188,53 @@ BufferP Pool::acquire(size_t nbytes) {
     if (Runtime::get().host_visible) {
       e = hipHostMalloc(&b->ptr, cap, hipHostMallocDefault);
       b->host_visible = true;
+    } else if (arena) {
+      // No stream-ordered allocation inside a captured stream: it would
+      // become a node of the graph.
+      e = hipMalloc(&b->ptr, cap);
+      b->stream_ordered = false;
     } else {
       e = hipMallocAsync(&b->ptr, cap, Runtime::get().stream());
     }
-    if (e != hipSuccess) {
+    if (e != hipSuccess && !arena) {
       // A failed allocation may be fragmentation: give back what the pool
       // holds and try once more.
       (void)hipGetLastError();
       drain();
       if (!b->host_visible) e = hipMallocAsync(&b->ptr, cap, Runtime::get().stream());
-      if (e != hipSuccess) {
-        (void)hipGetLastError();
-        delete b;
-        std::lock_guard<std::mutex> g(mu_);
-        live_ -= cap;
-        fail("device allocation of %zu bytes failed: %s", cap, hipGetErrorString(e));
-      }
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      delete b;
+      std::lock_guard<std::mutex> g(mu_);
+      live_ -= cap;
+      fail("device allocation of %zu bytes failed: %s", cap, hipGetErrorString(e));
     }
   }
   b->requested = nbytes;
+  b->out = true;
+  if (arena && b->arena != arena) {
+    std::lock_guard<std::mutex> g(mu_);
+    b->arena = arena;
+    arena->owned.push_back(b);
+    arena->bytes += b->bytes;
+  }
   return BufferP(b, [this](Buffer* x) { release(x); });
+}
+
+void Pool::free_now(Buffer* b) {
+  // Work still queued on the stream may read this buffer: free in stream
+  // order (or after the stream drains, for memory that is not stream-ordered).
+  if (b->host_visible) {
+    (void)hipStreamSynchronize(Runtime::get().stream());
+    (void)hipHostFree(b->ptr);
+  } else if (b->stream_ordered) {
+    (void)hipFreeAsync(b->ptr, Runtime::get().stream());
+  } else {
+    (void)hipStreamSynchronize(Runtime::get().stream());
+    (void)hipFree(b->ptr);
+  }
+  delete b;
 }
 
 void Pool::release(Buffer* b) {
@@ -203,29 +242,65 @@ void Pool::release(Buffer* b) {
   {
     std::lock_guard<std::mutex> g(mu_);
     live_ -= b->bytes;
-    keep = pooled_ + b->bytes <= watermark_;
+    b->out = false;
+    if (b->arena) {
+      // Owned by a captured graph: reusable within its own capture only.
+      if (b->arena->capturing) b->arena->free[b->bytes].push_back(b);
+      return;
+    }
+    // Nothing is freed while a capture records the stream.
+    keep = active_ != nullptr || pooled_ + b->bytes <= watermark_;
     if (keep) {
       buckets_[b->bytes].push_back(b);
       pooled_ += b->bytes;
     }
   }
-  if (!keep) {
-    // Work still queued on the stream may read this buffer: free in stream
-    // order.
-    if (b->host_visible) {
-      (void)hipStreamSynchronize(Runtime::get().stream());
-      (void)hipHostFree(b->ptr);
-    } else {
-      (void)hipFreeAsync(b->ptr, Runtime::get().stream());
+  if (!keep) free_now(b);
+}
+
+void Pool::begin_capture(Arena* a) {
+  std::lock_guard<std::mutex> g(mu_);
+  if (active_) fail("a graph capture is already active");
+  active_ = a;
+}
+
+void Pool::end_capture() {
+  std::lock_guard<std::mutex> g(mu_);
+  if (active_) active_->capturing = false;
+  active_ = nullptr;
+}
+
+bool Pool::capturing() {
+  std::lock_guard<std::mutex> g(mu_);
+  return active_ != nullptr;
+}
+
+void Pool::release_arena(Arena* a) {
+  std::vector<Buffer*> drop;
+  {
+    std::lock_guard<std::mutex> g(mu_);
+    if (active_ == a) active_ = nullptr;
+    for (Buffer* b : a->owned) {
+      b->arena = nullptr;
+      if (b->out) continue;  // still referenced: pooled when its last owner lets go
+      if (pooled_ + b->bytes <= watermark_) {
+        buckets_[b->bytes].push_back(b);
+        pooled_ += b->bytes;
+      } else {
+        drop.push_back(b);
+      }
     }
-    delete b;
+    a->owned.clear();
+    a->free.clear();
   }
+  for (Buffer* b : drop) free_now(b);
 }
 
 void Pool::set_watermark(size_t bytes) {
   std::vector<Buffer*> drop;
   {
     std::lock_guard<std::mutex> g(mu_);
+    if (active_) fail("the pool cannot shrink while a graph capture is active");
     watermark_ = bytes;
     while (pooled_ > watermark_ && !buckets_.empty()) {
       auto it = std::prev(buckets_.end());  // largest bucket first
@@ -236,15 +311,7 @@ void Pool::set_watermark(size_t bytes) {
       if (it->second.empty()) buckets_.erase(it);
     }
   }
-  for (Buffer* b : drop) {
-    if (b->host_visible) {
-      (void)hipStreamSynchronize(Runtime::get().stream());
-      (void)hipHostFree(b->ptr);
-    } else {
-      (void)hipFreeAsync(b->ptr, Runtime::get().stream());
-    }
-    delete b;
-  }
+  for (Buffer* b : drop) free_now(b);
 }
 
 void Pool::drain() {
@@ -364,7 +431,12 @@ TensorP Runtime::alloc(DType dt, const std::vector<int64_t>& dims) {
   return t;
 }
 
-void Runtime::sync() { AGPU_HIP(hipStreamSynchronize(stream_)); }
+void Runtime::sync() {
+  // While a capture records the stream nothing executes, so there is
+  // nothing to wait for (and a synchronize would end the capture).
+  if (pool_->capturing()) return;
+  AGPU_HIP(hipStreamSynchronize(stream_));
+}
 
 uint64_t Runtime::insert(TensorP t) { return insert_with_id(next_tensor_id(), std::move(t)); }
 

@@ -3,12 +3,23 @@ GPT-2-small forward ms at seq 128 (config 2) + MLP h=4096 train ms/step
 (config 3), on one MI355X, with the roofline fraction of the dominant kernel.
 
 A step = one GPT-2-small fp32 forward over 128 token ids (the lazy graph of
-the reference's gpt2_forward recipe, evaluated on the device; logits stay in
-HBM) + one training step of Linear(4096,4096)-ReLU-Linear(4096,4096)-ReLU-
-Linear(4096,1) at batch 256 (forward, MSE, backward, SGD lr 0.01) through
-the eager C ABI.  Weights are random (N(0,0.02) for GPT-2; torch's default
-Linear init for the MLP) and inputs synthetic, seeded; everything is resident
-in HBM before the timed region.
+the reference's gpt2_forward recipe) + one training step of
+Linear(4096,4096)-ReLU-Linear(4096,4096)-ReLU-Linear(4096,1) at batch 256
+(forward, MSE, backward, SGD lr 0.01, parameters updated in place) through
+the eager C ABI.  Both are recorded once with gpu.capture and replayed as HIP
+graphs; the same work issued op by op (no capture) is reported beside it.
+Weights are random (N(0,0.02) for GPT-2; torch's default Linear init for the
+MLP) and inputs synthetic, seeded; everything is resident in HBM before the
+timed region.  value = gpt2_fwd_ms + mlp_train_ms, each the mean over
+--steps replays bracketed by stream synchronisations.
+
+Roofline: the dominant single kernel of the step, the MLP weight-gradient
+GEMM dW = g^T h (M = N = 4096, K = 256; fp32 operands split into bf16 hi/lo,
+three bf16 MFMAs per product), timed with HIP events on the library stream
+over back-to-back launches; algorithmic work 2*M*N*K flop per launch.  Its
+HBM traffic comes from the rocprofv3 --pmc summaries committed under
+profiles/ (FETCH_SIZE, WRITE_SIZE of that kernel, scaled by the same counters
+read for the 256 MiB calibration copy this script runs), when present.
 
 Prints ONE JSON line.  `python bench.py --gpus N` with N > 1 exits: this
 build runs on one GPU.
@@ -29,10 +40,14 @@ import numpy as np  # noqa: E402
 
 METRIC = "GPT-2-small fwd ms @seq128 + MLP h=4096 train ms/step, 1 MI355X; % roofline"
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2516.6
+HBM_PEAK_GBS = 8000.0
 GPT2_CFG = dict(n_layer=12, n_head=12, n_embd=768, vocab_size=50257, n_positions=1024)
 MLP_SIZES = [4096, 4096, 4096, 1]
 MLP_BATCH = 256
 SEQ = 128
+CALIB_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mlp_dw_gemm_traffic.json")
 
 
 def gpt2_flops(cfg, T):
@@ -52,10 +67,20 @@ def mlp_flops(sizes, B):
     return f
 
 
+def load_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed PMC summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return float(t["bytes_per_launch"]), t
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
@@ -77,7 +102,9 @@ def main():
     # ── inputs resident in HBM ──────────────────────────────────────────────
     wnp = G.random_weights(GPT2_CFG, seed=42)
     model = G.load_model(wnp, GPT2_CFG)
-    ids = np.random.default_rng(42).integers(0, GPT2_CFG["vocab_size"], SEQ)
+    ids = np.random.default_rng(42).integers(0, GPT2_CFG["vocab_size"], SEQ).astype(np.int32)
+    idx = gpu.from_numpy(ids)
+    pos = gpu.from_numpy(np.arange(SEQ, dtype=np.int32))
 
     params = torch_default_init(MLP_SIZES, seed=42)
     rng = np.random.default_rng(42)
@@ -85,52 +112,86 @@ def main():
     ynp = rng.standard_normal((MLP_BATCH, MLP_SIZES[-1]), dtype=np.float32)
     mlp = EagerMLP(params)
     x, y = E.from_numpy(xnp), E.from_numpy(ynp)
+
+    # calibration kernel for the PMC traffic counters: a plain 256 MiB copy
+    csrc, cdst = E.empty((CALIB_BYTES // 4,)), E.empty((CALIB_BYTES // 4,))
+    E.fill_(csrc, 1.0)
+    if lib.applegpu_eager_copy_(cdst.id, csrc.id) != 0:
+        raise RuntimeError("calibration copy failed")
+    del csrc, cdst
     lib.applegpu_ffi_synchronize()
 
-    def gpt2_step():
-        logits, _ = G.gpt2_forward(model, ids)
-        logits.eval()
-        return logits
+    # ── op-by-op (uncaptured) reference timing ──────────────────────────────
+    def gpt2_eager():
+        G.gpt2_forward(model, idx, positions=pos)[0].eval()
 
-    def mlp_step():
-        return mlp.train_step(x, y, lr=0.01)
+    eager_mlp = EagerMLP(params)
+    for _ in range(2):
+        gpt2_eager()
+        eager_mlp.train_step(x, y, lr=0.01)
+    lib.applegpu_ffi_synchronize()
+    n_eager = max(3, args.steps // 5)
+    t0 = time.perf_counter()
+    for _ in range(n_eager):
+        gpt2_eager()
+    lib.applegpu_ffi_synchronize()
+    t1 = time.perf_counter()
+    for _ in range(n_eager):
+        eager_mlp.train_step(x, y, lr=0.01)
+    lib.applegpu_ffi_synchronize()
+    t2 = time.perf_counter()
+    gpt2_eager_ms = 1e3 * (t1 - t0) / n_eager
+    mlp_eager_ms = 1e3 * (t2 - t1) / n_eager
+    del eager_mlp
 
+    # ── captured graphs ──────────────────────────────────────────────────────
+    g_fwd = gpu.capture(lambda: G.gpt2_forward(model, idx, positions=pos)[0])
+    g_train = gpu.capture(lambda: mlp.train_step(x, y, lr=0.01))
     for _ in range(args.warmup):
-        gpt2_step()
-        mlp_step()
+        g_fwd.replay()
+        g_train.replay()
     lib.applegpu_ffi_synchronize()
 
-    # ── timed region: K steps, each = GPT-2 forward + MLP train step ────────
-    t_g = t_m = 0.0
+    # ── timed region ─────────────────────────────────────────────────────────
+    lib.applegpu_ffi_synchronize()
+    t0 = time.perf_counter()
     for _ in range(args.steps):
-        lib.applegpu_ffi_synchronize()
-        t0 = time.perf_counter()
-        gpt2_step()
-        lib.applegpu_ffi_synchronize()
-        t1 = time.perf_counter()
-        mlp_step()
-        lib.applegpu_ffi_synchronize()
-        t2 = time.perf_counter()
-        t_g += t1 - t0
-        t_m += t2 - t1
-    gpt2_ms = 1e3 * t_g / args.steps
-    mlp_ms = 1e3 * t_m / args.steps
+        g_fwd.replay()
+    lib.applegpu_ffi_synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        g_train.replay()
+    lib.applegpu_ffi_synchronize()
+    t2 = time.perf_counter()
+    gpt2_ms = 1e3 * (t1 - t0) / args.steps
+    mlp_ms = 1e3 * (t2 - t1) / args.steps
     ms_per_step = gpt2_ms + mlp_ms
+    logits = g_fwd.outputs.to_numpy()
+    loss = float(g_train.outputs.numpy()[0])
+    if not (np.isfinite(logits).all() and np.isfinite(loss)):
+        raise RuntimeError("non-finite results")
 
-    # ── dominant kernel: the MLP forward GEMM (x W^T, 256x4096x4096 fp32 on
-    #    v_mfma_f32_32x32x2_f32), timed with HIP events on the library stream ─
-    w0 = mlp.params[1][0]
-    h = E.from_numpy(rng.standard_normal((MLP_BATCH, 4096), dtype=np.float32))
+    # ── roofline: the MLP weight-gradient GEMM dW = g^T h ────────────────────
+    K_, M_, N_ = MLP_BATCH, MLP_SIZES[1], MLP_SIZES[0]
+    g_act = E.from_numpy(rng.standard_normal((K_, M_), dtype=np.float32) * np.float32(1e-3))
+    h_act = E.from_numpy(np.maximum(rng.standard_normal((K_, N_), dtype=np.float32), 0))
     for _ in range(3):
-        E.linear(h, w0, None, 0)
+        E.matmul_ex(g_act, h_act, True, False)
+    lib.applegpu_ffi_synchronize()
     reps = 50
     lib.applegpu_ffi_event_record(0)
-    outs = [E.linear(h, w0, None, 0) for _ in range(reps)]
+    out = None
+    for _ in range(reps):
+        out = None
+        out = E.matmul_ex(g_act, h_act, True, False)
     lib.applegpu_ffi_event_record(1)
     gemm_ms = lib.applegpu_ffi_event_elapsed_ms(0, 1) / reps
-    del outs
-    gemm_flop = 2.0 * MLP_BATCH * 4096 * 4096
+    gemm_flop = 2.0 * M_ * N_ * K_
     achieved = gemm_flop / (gemm_ms * 1e-3) / 1e12
+    import ctypes
+    plan = ctypes.create_string_buffer(96)
+    lib.applegpu_ffi_gemm_plan(M_, N_, K_, 1, 0, False, False, plan, 96)
+    traffic, tinfo = load_traffic()
 
     result = {
         "metric": METRIC,
@@ -147,28 +208,35 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "C2 GPT-2 small fp32 fwd (1x128 tokens, random N(0,0.02) weights) + C3 MLP "
-                        "4096-4096-4096-1 fp32 train step (batch 256, MSE, SGD lr 0.01)",
+                        "4096-4096-4096-1 fp32 train step (batch 256, MSE, SGD lr 0.01); each replayed "
+                        "as a captured HIP graph",
             "gpt2_fwd_ms": round(gpt2_ms, 4),
             "mlp_train_ms": round(mlp_ms, 4),
+            "gpt2_fwd_eager_ms": round(gpt2_eager_ms, 4),
+            "mlp_train_eager_ms": round(mlp_eager_ms, 4),
             "gpt2_fwd_tflops": round(gpt2_flops(GPT2_CFG, SEQ) / (gpt2_ms * 1e-3) / 1e12, 2),
             "mlp_train_tflops": round(mlp_flops(MLP_SIZES, MLP_BATCH) / (mlp_ms * 1e-3) / 1e12, 2),
+            "fp32_gemm": "bf16x3 split on bf16 MFMA, fp32 accumulate",
             "device": dev,
         },
         "roofline": {
-            "kernel": "gemm_f32_mfma (x W^T, M=256 N=4096 K=4096, split-K + reduce)",
+            "kernel": "gemm_mf dW = g^T h (M=4096 N=4096 K=256, fp32 via bf16x3), plan " + plan.value.decode(),
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": FP32_MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+            "traffic": traffic,
             "avg_launch_ms": round(gemm_ms, 5),
             "flop_per_launch": gemm_flop,
-            "traffic": None,
+            "bf16_mfma_utilisation": round(3 * achieved / BF16_MFMA_PEAK_TFLOPS, 4),
+            "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if tinfo else None,
         },
     }
-
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wnp, params, ids, xnp, ynp, args.cpu_sample_s)
+    g_fwd.destroy()
+    g_train.destroy()
     print(json.dumps(result), flush=True)
 
 

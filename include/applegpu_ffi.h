@@ -181,6 +181,27 @@ void applegpu_ffi_inject_alloc_failures(int32_t n);
 int32_t applegpu_ffi_event_record(uint32_t slot);
 float applegpu_ffi_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
 
+/* Graph capture (no reference counterpart; the reference re-encodes every op
+ * of every eval into a Metal command buffer, crates/core/src/lazy.rs:369-474,
+ * crates/core/src/compute.rs:2598-2698).  capture_begin starts recording the
+ * library's stream: ops issued until capture_end (eager ops, and the kernels
+ * of lazy evals run in between) are recorded instead of executed, into a
+ * HIP graph whose handle (> 0) capture_end returns (-1 on failure).  Every
+ * buffer allocated during the capture belongs to the graph until
+ * graph_destroy: graph_replay (asynchronous, on the library stream)
+ * recomputes the same ops from the current contents of their inputs into
+ * the same output buffers.  While capturing, host reads/writes of tensors,
+ * read_f32 and event_elapsed_ms fail and synchronize returns at once;
+ * capture_abort ends a capture and drops what it recorded.  Calls that
+ * overlap on one stream race like any other work on it. */
+int32_t applegpu_capture_begin(void);
+int64_t applegpu_capture_end(void);
+int32_t applegpu_capture_abort(void);
+int32_t applegpu_graph_replay(int64_t handle);
+int32_t applegpu_graph_destroy(int64_t handle);
+/* Device bytes the graph's buffers occupy (0 for an unknown handle). */
+uint64_t applegpu_graph_bytes(int64_t handle);
+
 /* GEMM tuning (no reference counterpart; the reference chooses between
  * MPSMatrixMultiplication and its tiled kernel inside
  * swift/Sources/AppleGPUBridge/compute.swift:1544-1630).  f32_mode: 0 = fp32
