@@ -78,8 +78,36 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
     return LIB
 
 
+SHIM_SRC = os.path.join(HERE, "torch_shim", "applegpu_backend.cpp")
+SHIM_LIB = os.path.join(HERE, "applegpu_runtime", "applegpu_backend.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+
+def build_torch_shim(verbose: bool = True) -> str:
+    """Builds the PrivateUse1 torch extension (plain C++ against the installed
+    PyTorch; it calls only the C ABI of libapplegpu_core.so, found through
+    $ORIGIN next to it)."""
+    import torch
+    from torch.utils import cpp_extension as ce
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", SHIM_SRC, "-o", SHIM_LIB + ".tmp",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-I{INCLUDE}", "-w"]
+    cmd += [f"-I{p}" for p in ce.include_paths()]
+    cmd += [f"-L{p}" for p in ce.library_paths()] + ["-lc10", "-ltorch", "-ltorch_cpu"]
+    cmd += [f"-L{os.path.dirname(LIB)}", "-lapplegpu_core", "-Wl,-rpath,$ORIGIN"]
+    cmd += [f"-Wl,-rpath,{p}" for p in ce.library_paths()]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError("torch shim build failed:\n" + p.stdout + p.stderr)
+    if verbose and (p.stdout or p.stderr).strip():
+        print(p.stdout + p.stderr, file=sys.stderr)
+    shutil.move(SHIM_LIB + ".tmp", SHIM_LIB)
+    return SHIM_LIB
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     a = ap.parse_args()
     print(build(a.j))
+    print(build_torch_shim())

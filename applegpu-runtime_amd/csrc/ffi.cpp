@@ -658,6 +658,22 @@ uint8_t* applegpu_eager_create_view(uint64_t base_id, const uint64_t* shape, con
   });
 }
 
+uint8_t* applegpu_eager_data_ptr(uint64_t id) {
+  return guarded<uint8_t*>(kEager, nullptr, [&]() -> uint8_t* {
+    TensorP t = eager_in(id);
+    return (uint8_t*)t->data();
+  });
+}
+
+uint8_t* applegpu_eager_view_typed(uint64_t base_id, const uint64_t* shape, const uint64_t* strides, uint32_t ndim,
+                                   uint64_t offset_bytes, int8_t dtype_i8, uint64_t* out_id) {
+  return eager_out(out_id, [&] {
+    TensorP base = eager_in(base_id);
+    std::vector<int64_t> sh = dims_of(shape, ndim), st = dims_of(strides, ndim);
+    return ops::view_bytes(base, wire(dtype_i8), sh, st, (int64_t)offset_bytes);
+  });
+}
+
 int32_t applegpu_eager_add_inplace(uint64_t self_id, uint64_t other_id) {
   return guarded<int32_t>(kEager, -1, [&]() -> int32_t {
     ops::axpy_inplace(eager_in(self_id), eager_in(other_id), 1.f);
@@ -728,9 +744,7 @@ int32_t applegpu_eager_copy_to_host(uint64_t id, void* dst, uint64_t nbytes) {
 
 int32_t applegpu_eager_copy_(uint64_t dst_id, uint64_t src_id) {
   return guarded<int32_t>(kEager, -1, [&]() -> int32_t {
-    TensorP dst = eager_in(dst_id);
-    if (!dst->is_contiguous()) fail("copy_: destination must be contiguous");
-    ops::copy_into(dst, eager_in(src_id));
+    ops::copy_into(eager_in(dst_id), eager_in(src_id));
     return 0;
   });
 }
@@ -738,7 +752,6 @@ int32_t applegpu_eager_copy_(uint64_t dst_id, uint64_t src_id) {
 int32_t applegpu_eager_fill(uint64_t id, double value) {
   return guarded<int32_t>(kEager, -1, [&]() -> int32_t {
     TensorP t = eager_in(id);
-    if (!t->is_contiguous()) fail("fill: tensor must be contiguous");
     TensorP f = ops::full(t->dtype, t->dims(), (float)value);
     ops::copy_into(t, f);
     return 0;

@@ -31,6 +31,17 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// GELU, tanh approximation (crates/core/src/kernel_templates.rs:272-307):
+// 0.5 x (1 + tanh(u)), u = clamp(0.7978845608 (x + 0.044715 x^3), -10, 10).
+// Evaluated through the identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)): one
+// exp and one division instead of tanh, the same function to within fp32
+// rounding (no cancellation: the 1 + tanh sum is formed exactly).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  float u = 0.7978845608f * (x + 0.044715f * x * x * x);
+  u = fminf(fmaxf(u, -10.f), 10.f);
+  return x / (1.f + expf(-2.f * u));
+}
+
 // Launch geometry helpers
 inline unsigned blocks_for(int64_t n, int per_block) {
   int64_t b = (n + per_block - 1) / per_block;

@@ -31,11 +31,6 @@ template <> __device__ __forceinline__ bool is_float_t<float>() { return true; }
 
 // gelu with the tanh approximation; the reference clamps the inner term to
 // +-10 before tanh (kernel_templates.rs:300-301), a no-op for fp32 tanh.
-__device__ __forceinline__ float gelu_tanh(float x) {
-  float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-  inner = fminf(fmaxf(inner, -10.f), 10.f);
-  return 0.5f * x * (1.f + tanhf(inner));
-}
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
 
 template <typename C>

@@ -286,14 +286,23 @@ Plan make_plan(const Gemm& g, int cus) {
   const bool a_ok = g.a_sk == 1 || g.a_sm == 1;
   const bool b_ok = g.b_sk == 1 || g.b_sn == 1;
   pl.splits = 1;
-  if (!(a_ok && b_ok && g.b_dt == g.dt && !g.b_scale && (g.dt == DType::F32 || is16))) {
+  // fp32 activations times int8 codes with per-n scales, B k-contiguous.
+  const bool int8_b = g.dt == DType::F32 && g.b_dt == DType::I8 && g.b_scale && g.b_sk == 1 && a_ok;
+  if (int8_b) {
+    pl.kind = kMf;
+    pl.cfg = (tu.cfg == 0 || tu.cfg == 6) ? tu.cfg : (tiles_for(g, 128, 128) >= cus ? 0 : 6);
+    pl.bm = kMfShape[pl.cfg].bm;
+    pl.bn = kMfShape[pl.cfg].bn;
+    pl.bk = kMfShape[pl.cfg].bk;
+  } else if (!(a_ok && b_ok && g.b_dt == g.dt && !g.b_scale && (g.dt == DType::F32 || is16))) {
     pl.kind = kGeneric;
     pl.bm = pl.bn = 64;
     pl.bk = 16;
     pl.kps = g.K;
     return pl;
   }
-  if (g.dt == DType::F32 && tu.f32_mode == kF32Native) {
+  if (int8_b) {
+  } else if (g.dt == DType::F32 && tu.f32_mode == kF32Native) {
     pl.kind = kNative32;
     pl.bm = g.M <= 64 ? 64 : 128;
     pl.bn = g.N <= 64 ? 64 : 128;
@@ -357,7 +366,8 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   const int64_t a_lead = g.a_sk == 1 ? g.a_sm : g.a_sk;
   const int64_t b_lead = g.b_sk == 1 ? g.b_sn : g.b_sk;
   p.vec_a = al16(g.A) && (a_lead % vw == 0) && (g.a_sb % vw == 0);
-  p.vec_b = al16(g.B) && (b_lead % vw == 0) && (g.b_sb % vw == 0);
+  const int vwb = (int)(16 / dtype_size(g.b_dt));
+  p.vec_b = al16(g.B) && (b_lead % vwb == 0) && (g.b_sb % vwb == 0);
   return p;
 }
 
@@ -439,9 +449,11 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     // K % VW == 0 for an operand contiguous along k, rows % VW == 0 for one
     // contiguous along its rows.
     const int64_t vw = 16 / (int64_t)dtype_size(g.dt);
+    const int64_t vwb = 16 / (int64_t)dtype_size(g.b_dt);
     const bool fast = p.vec_a && p.vec_b && (ak ? g.K % vw == 0 : g.M % vw == 0) &&
-                      (bk ? g.K % vw == 0 : g.N % vw == 0);
-    if (g.dt == DType::F32) launch_mf_f32(p, pl.cfg, ak, bk, fast, grid, s);
+                      (bk ? g.K % vwb == 0 : g.N % vwb == 0);
+    if (g.b_dt == DType::I8) launch_mf_f32_i8(p, pl.cfg, ak, fast, grid, s);
+    else if (g.dt == DType::F32) launch_mf_f32(p, pl.cfg, ak, bk, fast, grid, s);
     else if (g.dt == DType::F16) launch_mf_f16(p, pl.cfg, ak, bk, fast, grid, s);
     else launch_mf_bf16(p, pl.cfg, ak, bk, fast, grid, s);
   }

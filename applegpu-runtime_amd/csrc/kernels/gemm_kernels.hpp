@@ -36,12 +36,6 @@ struct GArgs {
   const float* b_scale;
 };
 
-__device__ __forceinline__ float gelu_tanh(float x) {
-  float inner = 0.7978845608f * (x + 0.044715f * x * x * x);
-  inner = fminf(fmaxf(inner, -10.f), 10.f);
-  return 0.5f * x * (1.f + tanhf(inner));
-}
-
 template <typename T>
 __device__ __forceinline__ void epilogue_store(const GArgs& p, int64_t b, int64_t row, int64_t col, float acc) {
   float v = p.alpha * acc;
@@ -206,9 +200,11 @@ struct GLoad {
     else return v[e];
   }
 
-  // fp32 operand -> hi/lo bf16 LDS tiles (row pitch LD elements).
+  // fp32 (or int8 codes times a per-row scale `rs`, KCONT only) operand ->
+  // hi/lo bf16 LDS tiles (row pitch LD elements).
   template <bool MASKED>
-  __device__ __forceinline__ void store_split(bf16_t* __restrict__ hi, bf16_t* __restrict__ lo, int LD) const {
+  __device__ __forceinline__ void store_split(bf16_t* __restrict__ hi, bf16_t* __restrict__ lo, int LD,
+                                              float rs = 1.f) const {
     int r, kk;
     coords(r, kk);
     if constexpr (KCONT) {
@@ -218,7 +214,8 @@ struct GLoad {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           bf16_t a, b;
-          split_bf16((float)at<MASKED>(i + e), a, b);
+          const float x = std::is_same<TI, int8_t>::value ? (float)at<MASKED>(i + e) * rs : (float)at<MASKED>(i + e);
+          split_bf16(x, a, b);
           h[e] = a;
           l[e] = b;
         }
@@ -285,10 +282,13 @@ template <int A, int B> struct CMax { static constexpr int v = A > B ? A : B; };
 // K remainder (K mod BK of this block's range) is multiplied first, from a
 // masked load, and every later slice is full.  !FAST: every slice is loaded
 // with GLoad::load_edge.
-template <typename TI, typename E, int BM, int BN, int WM, int WN, int WK, int KW, int ST, bool AK, bool BKC,
-          bool FAST>
+template <typename TI, typename TB, typename E, int BM, int BN, int WM, int WN, int WK, int KW, int ST, bool AK,
+          bool BKC, bool FAST>
 __global__ void __launch_bounds__(256) gemm_mf(GArgs p) {
   constexpr bool X3 = sizeof(TI) == 4;
+  // TB = int8: B holds int8 codes, B(k, n) = code * b_scale[n] (KCONT only).
+  constexpr bool QB = std::is_same<TB, int8_t>::value;
+  static_assert(!QB || (X3 && BKC), "int8 B operand: fp32 A, k-contiguous B");
   static_assert(WM * WN * WK == 4, "four wavefronts per block");
   constexpr int BK = KW * WK;
   constexpr int LD = BK + 8;
@@ -313,11 +313,17 @@ __global__ void __launch_bounds__(256) gemm_mf(GArgs p) {
   int64_t kend = kbeg + p.k_per_split;
   if (kend > p.K) kend = p.K;
   const TI* A = (const TI*)p.A + b * p.a_sb;
-  const TI* B = (const TI*)p.B + b * p.b_sb;
+  const TB* B = (const TB*)p.B + b * p.b_sb;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wk = wave / (WM * WN), wmn = wave % (WM * WN);
   const int wm = (wmn / WN) * (BM / WM), wn = (wmn % WN) * (BN / WN);
+  float bscale = 1.f;  // QB: the scale of this thread's B row
+  if constexpr (QB) {
+    int r, kk;
+    GLoad<TB, BN, KW * WK, BKC>::coords(r, kk);
+    bscale = p.b_scale[n0 + r < p.N ? n0 + r : p.N - 1];
+  }
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -328,13 +334,13 @@ __global__ void __launch_bounds__(256) gemm_mf(GArgs p) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   GLoad<TI, BM, BK, AK> ga;
-  GLoad<TI, BN, BK, BKC> gb;
+  GLoad<TB, BN, BK, BKC> gb;
   auto put = [&](auto masked, int stage) {
     constexpr bool MK = decltype(masked)::value;
     E* s = lds + stage * STAGE;
     if constexpr (X3) {
       ga.template store_split<MK>(s, s + AE, LD);
-      gb.template store_split<MK>(s + 2 * AE, s + 2 * AE + BE, LD);
+      gb.template store_split<MK>(s + 2 * AE, s + 2 * AE + BE, LD, bscale);
     } else {
       ga.template store_plain<MK>(s, LD);
       gb.template store_plain<MK>(s + AE, LD);
@@ -522,13 +528,13 @@ void launch_mf(const GArgs& p, int cfg, bool ak, bool bk, dim3 grid, hipStream_t
 #define AGPU_MF_CASE(ID, BM, BN, WM, WN, WK, KW, ST)                                                       \
   case ID:                                                                                                \
     if (ak && bk)                                                                                         \
-      hipLaunchKernelGGL((gemm_mf<TI, E, BM, BN, WM, WN, WK, KW, ST, true, true, FAST>), grid, dim3(256), 0, s, p);   \
+      hipLaunchKernelGGL((gemm_mf<TI, TI, E, BM, BN, WM, WN, WK, KW, ST, true, true, FAST>), grid, dim3(256), 0, s, p);   \
     else if (ak)                                                                                          \
-      hipLaunchKernelGGL((gemm_mf<TI, E, BM, BN, WM, WN, WK, KW, ST, true, false, FAST>), grid, dim3(256), 0, s, p);  \
+      hipLaunchKernelGGL((gemm_mf<TI, TI, E, BM, BN, WM, WN, WK, KW, ST, true, false, FAST>), grid, dim3(256), 0, s, p);  \
     else if (bk)                                                                                          \
-      hipLaunchKernelGGL((gemm_mf<TI, E, BM, BN, WM, WN, WK, KW, ST, false, true, FAST>), grid, dim3(256), 0, s, p);  \
+      hipLaunchKernelGGL((gemm_mf<TI, TI, E, BM, BN, WM, WN, WK, KW, ST, false, true, FAST>), grid, dim3(256), 0, s, p);  \
     else                                                                                                  \
-      hipLaunchKernelGGL((gemm_mf<TI, E, BM, BN, WM, WN, WK, KW, ST, false, false, FAST>), grid, dim3(256), 0, s, p); \
+      hipLaunchKernelGGL((gemm_mf<TI, TI, E, BM, BN, WM, WN, WK, KW, ST, false, false, FAST>), grid, dim3(256), 0, s, p); \
     break;
   switch (cfg) {
     AGPU_MF_CONFIGS(AGPU_MF_CASE)
@@ -544,6 +550,9 @@ void launch_mf_bf16(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 g
 void launch_mf_f32_fast(const GArgs& p, int cfg, bool ak, bool bk, dim3 grid, hipStream_t s);
 void launch_mf_f16_fast(const GArgs& p, int cfg, bool ak, bool bk, dim3 grid, hipStream_t s);
 void launch_mf_bf16_fast(const GArgs& p, int cfg, bool ak, bool bk, dim3 grid, hipStream_t s);
+// fp32 A times int8 B codes with per-n scales (k-contiguous B), configs 0
+// and 6 only; defined in gemm_mf_i8.hip.
+void launch_mf_f32_i8(const GArgs& p, int cfg, bool ak, bool fast, dim3 grid, hipStream_t s);
 
 }  // namespace k
 }  // namespace agpu

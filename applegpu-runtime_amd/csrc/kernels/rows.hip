@@ -23,11 +23,14 @@ namespace {
 constexpr int kRowsPerBlock = 4;  // one wavefront per row
 
 // Loads 4 consecutive elements at column c (c % 4 == 0) as float, with a
-// per-element guard against `limit`; masked lanes get `fill`.
-template <typename T>
+// per-element guard against `limit`; masked lanes get `fill`.  FULL: the
+// row is an exact multiple of the wavefront's vectors and 16-byte aligned,
+// so every lane loads unconditionally (no per-lane branch around the load,
+// which would make each load wait as it issues).
+template <typename T, bool FULL = false>
 __device__ __forceinline__ void load4(const T* __restrict__ row, int64_t c, int64_t limit, bool vec,
                                       float fill, float out[4]) {
-  if (vec && c + 4 <= limit) {
+  if (FULL || (vec && c + 4 <= limit)) {
     if constexpr (sizeof(T) == 4) {
       float4 v = *(const float4*)(row + c);
       out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
@@ -43,10 +46,10 @@ __device__ __forceinline__ void load4(const T* __restrict__ row, int64_t c, int6
   }
 }
 
-template <typename T>
+template <typename T, bool FULL = false>
 __device__ __forceinline__ void store4(T* __restrict__ row, int64_t c, int64_t limit, bool vec,
                                        const float v[4]) {
-  if (vec && c + 4 <= limit) {
+  if (FULL || (vec && c + 4 <= limit)) {
     if constexpr (sizeof(T) == 4) {
       *(float4*)(row + c) = make_float4(v[0], v[1], v[2], v[3]);
     } else {
@@ -63,7 +66,7 @@ __device__ __forceinline__ void store4(T* __restrict__ row, int64_t c, int64_t l
 }
 
 // ── softmax family, register-resident (cols <= 256 * NV) ─────────────────
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict__ x, int64_t ldx,
                                                     T* __restrict__ y, int64_t ldy, int64_t rows,
                                                     int64_t cols, int64_t causal_rows, bool vec) {
@@ -82,9 +85,17 @@ __global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict_
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     int64_t c = ((int64_t)i * 64 + lane) * 4;
-    load4(xr, c, valid, vec, -INFINITY, v[i]);
+    if constexpr (FULL) load4<T, true>(xr, c, cols, vec, -INFINITY, v[i]);
+    else load4(xr, c, valid, vec, -INFINITY, v[i]);
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, v[i][j]);
+  for (int i = 0; i < NV; ++i) {
+    int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (FULL && c + j >= valid) v[i][j] = -INFINITY;  // causal mask
+      mx = fmaxf(mx, v[i][j]);
+    }
   }
   mx = wave_max(mx);
   float sum = 0.f;
@@ -106,15 +117,16 @@ __global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict_
       int64_t c = ((int64_t)i * 64 + lane) * 4;
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[i][j] = v[i][j] - mx - ls;
-      store4(yr, c, cols, vec, v[i]);
+      store4<T, FULL>(yr, c, cols, vec, v[i]);
     }
   } else {
+    const float inv = 1.f / sum;  // one division per row, then products
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       int64_t c = ((int64_t)i * 64 + lane) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[i][j] = (c + j < valid) ? v[i][j] / sum : 0.f;
-      store4(yr, c, cols, vec, v[i]);
+      for (int j = 0; j < 4; ++j) v[i][j] = (c + j < valid) ? v[i][j] * inv : 0.f;
+      store4<T, FULL>(yr, c, cols, vec, v[i]);
     }
   }
 }
@@ -171,7 +183,7 @@ __global__ void __launch_bounds__(256) softmax_block(int op, const T* __restrict
 }
 
 // ── layer_norm ────────────────────────────────────────────────────────────
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ void __launch_bounds__(256) layer_norm_wave(const T* __restrict__ x, int64_t ldx,
                                                        const T* __restrict__ g, const T* __restrict__ b,
                                                        T* __restrict__ y, int64_t rows, int64_t cols,
@@ -186,7 +198,7 @@ __global__ void __launch_bounds__(256) layer_norm_wave(const T* __restrict__ x, 
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     int64_t c = ((int64_t)i * 64 + lane) * 4;
-    load4(xr, c, cols, vec, 0.f, v[i]);
+    load4<T, FULL>(xr, c, cols, vec, 0.f, v[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) s += v[i][j];
   }
@@ -207,11 +219,11 @@ __global__ void __launch_bounds__(256) layer_norm_wave(const T* __restrict__ x, 
   for (int i = 0; i < NV; ++i) {
     int64_t c = ((int64_t)i * 64 + lane) * 4;
     float gv[4], bv[4];
-    load4(g, c, cols, vec, 0.f, gv);
-    load4(b, c, cols, vec, 0.f, bv);
+    load4<T, FULL>(g, c, cols, vec, 0.f, gv);
+    load4<T, FULL>(b, c, cols, vec, 0.f, bv);
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[i][j] = gv[j] * (v[i][j] - mean) * inv + bv[j];
-    store4(yr, c, cols, vec, v[i]);
+    store4<T, FULL>(yr, c, cols, vec, v[i]);
   }
 }
 
@@ -333,7 +345,7 @@ __global__ void __launch_bounds__(256) softmax_bwd_wave(const T* __restrict__ dy
 // scale = absmax/127 (fp32), q = clamp(rint(x / scale), -128, 127); x / scale
 // is IEEE division and rint rounds half to even, as torch.round does.  A row
 // of zeros gets scale 0 and codes 0.
-template <typename T, int NV>
+template <typename T, int NV, bool FULL>
 __global__ void __launch_bounds__(256) quantize_rows_kernel(const T* __restrict__ x, int8_t* __restrict__ q,
                                                             float* __restrict__ scale, int64_t cols, bool vec) {
   __shared__ float sh[4];
@@ -345,7 +357,7 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const T* __restrict_
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     int64_t c = ((int64_t)i * 256 + threadIdx.x) * 4;
-    load4(xr, c, cols, vec, 0.f, v[i]);
+    load4<T, FULL>(xr, c, cols, vec, 0.f, v[i]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) m = fmaxf(m, fabsf(v[i][j]));
   }
@@ -362,7 +374,7 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const T* __restrict_
       r = fminf(fmaxf(r, -128.f), 127.f);
       b[j] = (int8_t)(int)r;
     }
-    if (vec && c + 4 <= cols) {
+    if (FULL || (vec && c + 4 <= cols)) {
       *(int32_t*)(qr + c) = *(int32_t*)b;
     } else {
 #pragma unroll
@@ -388,29 +400,74 @@ __global__ void __launch_bounds__(256) quantize_rows_loop(const T* __restrict__ 
   }
 }
 
-// y[r, c] = q[r, c] * scale[r]; grid.y walks rows, 4 codes per thread.
-template <typename T>
+// y[r, c] = q[r, c] * scale[r]; grid.y walks rows, 4 codes per thread (one
+// 4-byte load, one 16-byte fp32 store).  VEC: cols % 4 == 0 and both sides
+// aligned, so every thread in range takes the vector path.
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(256) dequantize_rows_kernel(const int8_t* __restrict__ q,
                                                               const float* __restrict__ scale,
-                                                              T* __restrict__ y, int64_t rows, int64_t cols,
-                                                              bool vec) {
+                                                              T* __restrict__ y, int64_t rows, int64_t cols) {
   const int64_t c = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (c >= cols) return;
   for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
-  const float sc = scale[row];
-  const int8_t* qr = q + row * cols;
-  T* yr = y + row * cols;
-  float v[4];
-  if (vec && c + 4 <= cols) {
-    int32_t w = *(const int32_t*)(qr + c);
-    const int8_t* b = (const int8_t*)&w;
+    const float sc = scale[row];
+    const int8_t* qr = q + row * cols;
+    T* yr = y + row * cols;
+    float v[4];
+    if constexpr (VEC) {
+      const int32_t w = *(const int32_t*)(qr + c);
+      const int8_t* b = (const int8_t*)&w;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = (float)b[j] * sc;
-  } else {
+      for (int j = 0; j < 4; ++j) v[j] = (float)b[j] * sc;
+      store4<T, true>(yr, c, cols, true, v);
+    } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = c + j < cols ? (float)qr[c + j] * sc : 0.f;
+      for (int j = 0; j < 4; ++j) v[j] = c + j < cols ? (float)qr[c + j] * sc : 0.f;
+      store4(yr, c, cols, false, v);
+    }
   }
-  store4(yr, c, cols, vec, v);
+}
+
+// Per-row int8 quantize with one wavefront per row for rows of up to 2048
+// columns: the row stays in registers, the absmax is a wave reduction (no
+// block barrier), then the codes are written 4 per lane.  Longer rows take
+// one 256-thread block each (quantize_rows_kernel), measured faster there.
+template <typename T, int NV, bool FULL>
+__global__ void __launch_bounds__(256) quantize_rows_wave(const T* __restrict__ x, int8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int64_t rows, int64_t cols,
+                                                          bool vec) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  int8_t* qr = q + row * cols;
+  float v[NV][4];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) load4<T, FULL>(xr, ((int64_t)i * 64 + lane) * 4, cols, vec, 0.f, v[i]);
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = fmaxf(m, fabsf(v[i][j]));
+  const float sc = wave_max(m) / 127.f;
+  if (lane == 0) scale[row] = sc;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    int8_t b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float r = sc == 0.f ? 0.f : rintf(v[i][j] / sc);
+      r = fminf(fmaxf(r, -128.f), 127.f);
+      b[j] = (int8_t)(int)r;
+    }
+    if (FULL || (vec && c + 4 <= cols)) {
+      *(int32_t*)(qr + c) = *(int32_t*)b;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c + j < cols) qr[c + j] = b[j];
+    }
   }
 }
 
@@ -423,8 +480,12 @@ unsigned rows_grid(int64_t rows) { return (unsigned)((rows + kRowsPerBlock - 1) 
 template <typename T, int NV>
 void sm_nv(int op, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols, int64_t crow,
            bool vec, hipStream_t s) {
-  hipLaunchKernelGGL((softmax_wave<T, NV>), dim3(rows_grid(rows)), dim3(256), 0, s, op, (const T*)x, ldx, (T*)y, ldy,
-                     rows, cols, crow, vec);
+  if (vec && cols == NV * 256)
+    hipLaunchKernelGGL((softmax_wave<T, NV, true>), dim3(rows_grid(rows)), dim3(256), 0, s, op, (const T*)x, ldx,
+                       (T*)y, ldy, rows, cols, crow, vec);
+  else
+    hipLaunchKernelGGL((softmax_wave<T, NV, false>), dim3(rows_grid(rows)), dim3(256), 0, s, op, (const T*)x, ldx,
+                       (T*)y, ldy, rows, cols, crow, vec);
 }
 
 template <typename T>
@@ -449,8 +510,12 @@ void sm_launch(int op, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t
 template <typename T, int NV>
 void ln_nv(const void* x, int64_t ldx, const void* g, const void* b, void* y, int64_t rows, int64_t cols, float eps,
            bool vec, hipStream_t s) {
-  hipLaunchKernelGGL((layer_norm_wave<T, NV>), dim3(rows_grid(rows)), dim3(256), 0, s, (const T*)x, ldx, (const T*)g,
-                     (const T*)b, (T*)y, rows, cols, eps, vec);
+  if (vec && cols == NV * 256)
+    hipLaunchKernelGGL((layer_norm_wave<T, NV, true>), dim3(rows_grid(rows)), dim3(256), 0, s, (const T*)x, ldx,
+                       (const T*)g, (const T*)b, (T*)y, rows, cols, eps, vec);
+  else
+    hipLaunchKernelGGL((layer_norm_wave<T, NV, false>), dim3(rows_grid(rows)), dim3(256), 0, s, (const T*)x, ldx,
+                       (const T*)g, (const T*)b, (T*)y, rows, cols, eps, vec);
 }
 
 template <typename T>
@@ -476,12 +541,31 @@ void ln_launch(const void* x, int64_t ldx, const void* g, const void* b, void* y
 template <typename T>
 void q_launch(const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols, hipStream_t s) {
   bool vec = vec_ok(x, cols, sizeof(T)) && vec_ok(q, cols, 1);
+  if (cols <= 2048) {
+    const int64_t nw = (cols + 255) / 256;  // float4 groups per lane
+    dim3 gw(rows_grid(rows));
+#define AGPU_QW(NV)                                                                                     \
+  if (vec && cols == NV * 256)                                                                          \
+    hipLaunchKernelGGL((quantize_rows_wave<T, NV, true>), gw, dim3(256), 0, s, (const T*)x, q, scale, rows, cols, vec); \
+  else                                                                                                  \
+    hipLaunchKernelGGL((quantize_rows_wave<T, NV, false>), gw, dim3(256), 0, s, (const T*)x, q, scale, rows, cols, vec);
+    if (nw <= 4) { AGPU_QW(4) }
+    else { AGPU_QW(8) }
+#undef AGPU_QW
+    return;
+  }
   int64_t nv = (cols + 1023) / 1024;
   dim3 g((unsigned)rows);
-  if (nv <= 1) hipLaunchKernelGGL((quantize_rows_kernel<T, 1>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
-  else if (nv <= 2) hipLaunchKernelGGL((quantize_rows_kernel<T, 2>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
-  else if (nv <= 4) hipLaunchKernelGGL((quantize_rows_kernel<T, 4>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
-  else if (nv <= 8) hipLaunchKernelGGL((quantize_rows_kernel<T, 8>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
+#define AGPU_Q(NV)                                                                                   \
+  if (vec && cols == NV * 1024)                                                                      \
+    hipLaunchKernelGGL((quantize_rows_kernel<T, NV, true>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec); \
+  else                                                                                               \
+    hipLaunchKernelGGL((quantize_rows_kernel<T, NV, false>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec);
+  if (nv <= 1) { AGPU_Q(1) }
+  else if (nv <= 2) { AGPU_Q(2) }
+  else if (nv <= 4) { AGPU_Q(4) }
+  else if (nv <= 8) { AGPU_Q(8) }
+#undef AGPU_Q
   else hipLaunchKernelGGL((quantize_rows_loop<T>), g, dim3(256), 0, s, (const T*)x, q, scale, cols);
 }
 
@@ -552,9 +636,10 @@ void dequantize_rows(DType out, const int8_t* q, const float* scale, void* y, in
                      hipStream_t s) {
   if (rows == 0 || cols == 0) return;
   AGPU_FLOAT_SWITCH(out, {
-    bool vec = vec_ok(q, cols, 1) && vec_ok(y, cols, sizeof(T));
+    const bool vec = ((uintptr_t)q % 4) == 0 && ((uintptr_t)y % (4 * sizeof(T))) == 0 && cols % 4 == 0;
     dim3 grid((unsigned)((cols + 1023) / 1024), (unsigned)(rows < 65535 ? rows : 65535));
-    hipLaunchKernelGGL((dequantize_rows_kernel<T>), grid, dim3(256), 0, s, q, scale, (T*)y, rows, cols, vec);
+    if (vec) hipLaunchKernelGGL((dequantize_rows_kernel<T, true>), grid, dim3(256), 0, s, q, scale, (T*)y, rows, cols);
+    else hipLaunchKernelGGL((dequantize_rows_kernel<T, false>), grid, dim3(256), 0, s, q, scale, (T*)y, rows, cols);
   });
   check_launch("dequantize_rows");
 }

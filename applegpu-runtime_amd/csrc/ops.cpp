@@ -150,6 +150,24 @@ bool as_rows(const Tensor& t, int64_t* rows, int64_t* ld) {
   return true;
 }
 
+TensorP view_bytes(const TensorP& base, DType dt, const std::vector<int64_t>& shape,
+                   const std::vector<int64_t>& strides, int64_t offset_bytes) {
+  if (shape.size() != strides.size()) fail("view: shape and strides differ in length");
+  if (!base->buf) fail("view: base tensor has no storage");
+  if (offset_bytes < 0) fail("view: negative byte offset");
+  auto t = make_meta(dt, shape);
+  for (size_t i = 0; i < shape.size(); ++i) {
+    if (strides[i] < 0) fail("view: negative strides are not supported");
+    t->strides[i] = strides[i];
+  }
+  t->buf = base->buf;
+  t->offset = base->offset + offset_bytes;
+  if ((size_t)t->offset + t->extent_bytes() > base->buf->requested)
+    fail("view: shape %s (%s) with the given strides and byte offset exceeds the base storage",
+         shape_str(shape).c_str(), dtype_name(dt));
+  return t;
+}
+
 TensorP view(const TensorP& base, const std::vector<int64_t>& shape, const std::vector<int64_t>& strides,
              int64_t offset_elems) {
   if (shape.size() != strides.size()) fail("view: shape and strides differ in length");
@@ -785,7 +803,10 @@ TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale) {
   g.B = qc->data(); g.b_sk = 1; g.b_sn = K;
   g.b_scale = (const float*)sc->data();
   g.C = out->data(); g.c_sm = N;
-  LAUNCH k::gemm(g, nullptr, rt().stream());
+  size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
+  BufferP ws;
+  if (wsb) ws = scratch(wsb);
+  LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
   return out;
 }
 

@@ -15,6 +15,10 @@ k::ND nd_for(const Tensor& t, const std::vector<int64_t>& out_dims);  // broadca
 k::ND nd_shape(const std::vector<int64_t>& dims);
 // View of t as [rows, cols] with unit column stride; false if not expressible.
 bool as_rows(const Tensor& t, int64_t* rows, int64_t* ld);
+// A view of base's storage read as `dt`, at a byte offset from base's data
+// (bounds-checked against the allocation).
+TensorP view_bytes(const TensorP& base, DType dt, const std::vector<int64_t>& shape,
+                   const std::vector<int64_t>& strides, int64_t offset_bytes);
 TensorP view(const TensorP& base, const std::vector<int64_t>& shape, const std::vector<int64_t>& strides,
              int64_t offset_elems);
 TensorP reshape(const TensorP& t, const std::vector<int64_t>& shape);   // view when possible

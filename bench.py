@@ -84,7 +84,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=15.0)
+    ap.add_argument("--suite", action="store_true",
+                    help="instead of the headline line, print one JSON line per hot-path kernel "
+                         "(cache-busting working sets, roofline fractions)")
     args = ap.parse_args()
+    if args.suite:
+        kernel_suite()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is described in DESIGN.md, not built).", file=sys.stderr)
@@ -238,6 +244,100 @@ def main():
     g_fwd.destroy()
     g_train.destroy()
     print(json.dumps(result), flush=True)
+
+
+def kernel_suite():
+    """One JSON line per HBM-bound hot-path kernel and for the C4/C5 shapes.
+
+    Inputs rotate over enough buffers that every launch reads data not in
+    the 256 MB Infinity Cache; each line is the HIP-event mean over
+    back-to-back launches on the library stream, with algorithmic bytes
+    (each input read once, each output written once) over 8 TB/s."""
+    import applegpu_runtime as gpu  # noqa: F401
+    from applegpu_runtime import eager as E
+    from applegpu_runtime._native import lib
+
+    gpu.init_backend()
+    rng = np.random.default_rng(0)
+
+    def timed(fn, inputs, reps):
+        for i in range(2):
+            fn(inputs[i % len(inputs)])
+        lib.applegpu_ffi_synchronize()
+        lib.applegpu_ffi_event_record(0)
+        out = None
+        for i in range(reps):
+            out = None
+            out = fn(inputs[i % len(inputs)])
+        lib.applegpu_ffi_event_record(1)
+        return lib.applegpu_ffi_event_elapsed_ms(0, 1) / reps, out
+
+    def line(name, shape, nbytes, ms, flop=None, peak_tflops=None):
+        r = {"kernel": name, "shape": shape, "us": round(ms * 1e3, 2),
+             "bytes": int(nbytes), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+             "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if flop:
+            r["TFLOP/s"] = round(flop / (ms * 1e-3) / 1e12, 2)
+            r["mfma_frac"] = round(flop / (ms * 1e-3) / 1e12 / peak_tflops, 4)
+        print(json.dumps(r), flush=True)
+
+    def randn(shape, dtype=np.float32, scale=1.0):
+        return E.from_numpy((rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(dtype))
+
+    # row kernels at [262144, 768] fp32: 805 MB per read, two inputs rotate
+    R, C = 262144, 768
+    xs = [randn((R, C)) for _ in range(2)]
+    g, b = randn((C,)), randn((C,))
+    row_bytes = 2 * R * C * 4
+    ms, _ = timed(lambda x: E.softmax(x), xs, 20)
+    line("softmax", [R, C], row_bytes, ms)
+    ms, _ = timed(lambda x: E.op("log_softmax", [x]), xs, 20)
+    line("log_softmax", [R, C], row_bytes, ms)
+    ms, _ = timed(lambda x: E.op("softmax_causal", [x]), xs, 20)
+    line("softmax_causal", [R, C], row_bytes, ms)
+    ms, _ = timed(lambda x: E.layer_norm(x, g, b), xs, 20)
+    line("layer_norm", [R, C], row_bytes + 2 * C * 4, ms)
+    ms, _ = timed(lambda x: E.gelu(x), xs, 20)
+    line("gelu", [R, C], row_bytes, ms)
+    ms, _ = timed(lambda x: E.add(x, xs[0]), xs[1:], 20)
+    line("add", [R, C], 3 * R * C * 4, ms)
+    del xs
+
+    # C5: per-row int8 quantize / dequantize of W [8192, 8192] fp32, three rotating inputs
+    N = 8192
+    ws = [randn((N, N), scale=0.02) for _ in range(3)]
+    qbytes = 4 * N * N + N * N + 4 * N
+    ms, qs = timed(lambda w: E.op("quantize_per_row", [w], nout=2), ws, 12)
+    line("quantize_per_row", [N, N], qbytes, ms)
+    q, sc = qs
+    ms, _ = timed(lambda qq: E.op("dequantize_per_row", [qq, sc]), [q], 12)
+    line("dequantize_per_row", [N, N], qbytes, ms)
+    deq = E.op("dequantize_per_row", [q, sc])
+    del ws
+    X = randn((64, N))
+    ms, _ = timed(lambda w: E.matmul_ex(X, w, False, True), [deq], 20)
+    line("gemm_c5 x @ deq^T", [64, N, N], 4 * (64 * N + N * N + 64 * N), ms, 2.0 * 64 * N * N, FP32_MFMA_PEAK_TFLOPS)
+    ms, _ = timed(lambda qq: E.op("linear_int8", [X, qq, sc]), [q], 20)
+    line("linear_int8 x @ (q*s)^T", [64, N, N], 4 * 64 * N + N * N + 4 * N + 4 * 64 * N, ms, 2.0 * 64 * N * N,
+         FP32_MFMA_PEAK_TFLOPS)
+    del q, sc, deq, X
+
+    # C4 shapes, fp16: prefill GEMMs at 8 x 512 tokens and causal attention
+    M, d = 4096, 1280
+    a16 = [randn((M, d), np.float16)]
+    w16 = randn((d, 3 * d), np.float16, 0.02)
+    ms, _ = timed(lambda a: E.matmul(a, w16), a16, 20)
+    line("gemm_c4_qkv f16", [M, 3 * d, d], 2 * (M * d + d * 3 * d + M * 3 * d), ms, 2.0 * M * 3 * d * d,
+         BF16_MFMA_PEAK_TFLOPS)
+    BH, T, hd = 160, 512, 64
+    qkv = [randn((BH, T, hd), np.float16) for _ in range(3)]
+    ms, _ = timed(lambda q: E.op("attention_causal", [q, qkv[1], qkv[2]]), [qkv[0]], 20)
+    line("attention_causal f16", [BH, T, hd], 2 * 4 * BH * T * hd, ms, 4.0 * BH * T * T * hd / 2,
+         BF16_MFMA_PEAK_TFLOPS)
+    kc = [randn((BH, 640, hd), np.float16) for _ in range(2)]
+    q1 = randn((BH, 1, hd), np.float16)
+    ms, _ = timed(lambda k: E.op("attention", [q1, k, kc[1]]), [kc[0]], 20)
+    line("attention decode f16 (q_len 1, ctx 640)", [BH, 640, hd], 2 * (2 * BH * 640 * hd + 2 * BH * hd), ms)
 
 
 def cpu_baseline(wnp, params, ids, xnp, ynp, budget_s):

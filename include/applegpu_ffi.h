@@ -233,13 +233,25 @@ int32_t applegpu_eager_op(const char* op, const uint64_t* inputs, uint32_t n_inp
  * (backend_cpp/applegpu_backend.cpp:267-341). nbytes = numel * element size. */
 int32_t applegpu_eager_copy_from_host(uint64_t id, const void* src, uint64_t nbytes);
 int32_t applegpu_eager_copy_to_host(uint64_t id, void* dst, uint64_t nbytes);
-/* dst = src on the device (dtype cast allowed, dst contiguous): replaces the
- * scalar_mul(view, 1.0) + storage swap copy idiom
+/* dst = src on the device (dtype cast allowed, dst of any strides): replaces
+ * the scalar_mul(view, 1.0) + storage swap copy idiom
  * (backend_cpp/applegpu_backend.cpp:274-299). */
 int32_t applegpu_eager_copy_(uint64_t dst_id, uint64_t src_id);
-/* Fill with a value on the device: replaces the CPU memset of fill_/zero_
- * (backend_cpp/applegpu_backend.cpp:729-751). */
+/* Fill with a value on the device (any strides): replaces the CPU memset of
+ * fill_/zero_ (backend_cpp/applegpu_backend.cpp:729-751). */
 int32_t applegpu_eager_fill(uint64_t id, double value);
+/* Data pointer (buffer base + byte offset) of an eager tensor, evaluating it
+ * first if it is pending; NULL for an unknown id.  The pointer-returning
+ * eager calls give it directly; this serves ids returned by applegpu_eager_op
+ * (the reference's eager ops return it with the id, eager_ffi.rs:234-262). */
+uint8_t* applegpu_eager_data_ptr(uint64_t id);
+/* A view of base's storage read as dtype `dtype_i8`, with element strides and
+ * a byte offset from base's data (bounds-checked against the allocation):
+ * maps a torch tensor (storage, dtype, storage offset, strides) exactly.
+ * Replaces resolve_tensor_id's create_view (backend_cpp/applegpu_backend.cpp:
+ * 37-93), whose views keep the storage's registration dtype. */
+uint8_t* applegpu_eager_view_typed(uint64_t base_id, const uint64_t* shape, const uint64_t* strides, uint32_t ndim,
+                                   uint64_t offset_bytes, int8_t dtype_i8, uint64_t* out_id);
 /* y = act(x W^T + b) in one GEMM with a fused epilogue (act: 0 none, 1 relu,
  * 2 gelu-tanh, 3 gelu-erf; bias_id 0 = none): replaces addmm's W^T copy +
  * matmul + bias add (backend_cpp/applegpu_backend.cpp:584-620). */
