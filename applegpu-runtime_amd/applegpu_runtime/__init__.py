@@ -417,6 +417,17 @@ def concat(a, b, dim): return _op(b"concat", [_t(a), _t(b)], i=(int(dim),))
 def contiguous(t): return _op(b"contiguous", [_t(t)])
 
 
+def full(shape, value, dtype="float32") -> GpuTensor:
+    """A new device tensor of `shape` filled with `value` (materialised)."""
+    t = _op(b"full", [], f=(float(value),), i=(DTYPE_CODES[canon_dtype(dtype)],) + tuple(int(s) for s in shape))
+    t.eval()
+    return t
+
+
+def zeros(shape, dtype="float32") -> GpuTensor:
+    return full(shape, 0.0, dtype)
+
+
 def concat_all(tensors, dim=0):
     tensors = list(tensors)
     if not tensors:
@@ -498,8 +509,30 @@ def linear_int8(x, q, scale):
 
 
 def blit_copy(src, dst):
+    """dst = src on the device, at once; dst may be a view (a slice of a
+    larger tensor, any strides), which is then written in place."""
     if lib.applegpu_ffi_copy(_t(src)._id, _t(dst)._id) != 0:
         raise ValueError(ffi_error())
+
+
+def kv_write(cache, rows, pos):
+    """cache[b, h, pos[b] + t, :] = rows[b, h, t, :], in place, at once.
+
+    cache [B, H, Tmax, D] and rows [B, H, T, D] share a dtype; pos is an
+    int32 device tensor [B] read by the kernel (so a captured graph can be
+    replayed with advancing positions).  Rows that would land outside the
+    cache are not written."""
+    if lib.applegpu_kv_write(_t(cache)._id, _t(rows)._id, _t(pos)._id) != 0:
+        raise ValueError(ffi_error())
+
+
+def decode_attention(q, k_cache, v_cache, lens):
+    """softmax(q K^T / sqrt(D)) V of q [B, H, Tq, D] over the first lens[b]
+    rows of the [B, H, Tmax, D] caches (lens: int32 device tensor [B]); query
+    row i of sequence b sees cache rows j <= lens[b] - Tq + i.  With Tq = 1
+    this is the reference's decode step, non-causal attention of the new
+    token over the whole cache (python/applegpu_runtime/models/gpt2.py:132-135)."""
+    return _op(b"decode_attention", [_t(q), _t(k_cache), _t(v_cache), _t(lens)])
 
 
 # ── graph capture ────────────────────────────────────────────────────────────

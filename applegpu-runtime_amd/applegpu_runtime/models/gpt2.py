@@ -133,3 +133,193 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
     logits = x @ gpu.transpose(w["transformer.wte.weight"])
     return logits, new_cache
+
+
+# ── batched prefill + greedy decode over a preallocated KV cache ────────────
+class KVCache:
+    """Per-layer K and V caches, [batch, n_head, max_len, d_head] each, plus
+    `pos`, an int32 device tensor [batch] holding the rows filled so far.
+
+    The reference grows its cache by concatenation every step
+    (python/applegpu_runtime/models/gpt2.py:122-126); here the cache is
+    allocated once and written in place (`gpu.kv_write`), and every length
+    the decode step needs lives in device memory, so one decode step can be
+    captured as a HIP graph and replayed for every generated token."""
+
+    def __init__(self, cfg: dict, batch: int, max_len: int, dtype: str = "float16"):
+        gpu.init_backend()
+        H, d = cfg["n_head"], cfg["n_embd"]
+        if max_len > cfg["n_positions"]:
+            raise ValueError(f"max_len {max_len} exceeds n_positions {cfg['n_positions']}")
+        shape = [batch, H, max_len, d // H]
+        self.batch, self.max_len, self.dtype = batch, max_len, dtype
+        self.k = [gpu.zeros(shape, dtype) for _ in range(cfg["n_layer"])]
+        self.v = [gpu.zeros(shape, dtype) for _ in range(cfg["n_layer"])]
+        self.pos = gpu.from_numpy(np.zeros(batch, np.int32))
+        self.one = gpu.from_numpy(np.ones(1, np.int32))
+        self.length = 0   # host mirror of pos (all sequences advance together)
+
+    def nbytes(self) -> int:
+        n = 0
+        for t in self.k + self.v:
+            c = 1
+            for s in t.shape:
+                c *= s
+            n += c * gpu.dtype_size(self.dtype)
+        return n
+
+
+def _block(model, i, x, B, T, attend):
+    """One transformer layer on x [B*T, d]; `attend(i, q, k, v)` gets the
+    heads as [B, H, T, hd] views of the fused QKV projection and returns the
+    attention output [B, H, T, hd]."""
+    w = model["weights"]
+    cfg = model["config"]
+    H, d = cfg["n_head"], cfg["n_embd"]
+    hd = d // H
+    p = f"transformer.h.{i}"
+    h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
+    qkv = gpu.add_bias(h @ w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"])
+
+    def heads(lo):
+        part = gpu.slice(qkv, 1, lo, lo + d)
+        return gpu.transpose_dims(gpu.reshape(part, [B, T, H, hd]), 1, 2)
+
+    a = attend(i, heads(0), heads(d), heads(2 * d))
+    a = gpu.reshape(gpu.transpose_dims(a, 1, 2), [B * T, d])
+    x = x + gpu.add_bias(a @ w[f"{p}.attn.c_proj.weight"], w[f"{p}.attn.c_proj.bias"])
+    h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
+    f = gpu.gelu(gpu.add_bias(h @ w[f"{p}.mlp.c_fc.weight"], w[f"{p}.mlp.c_fc.bias"]))
+    return x + gpu.add_bias(f @ w[f"{p}.mlp.c_proj.weight"], w[f"{p}.mlp.c_proj.bias"])
+
+
+def _head(model, x):
+    w = model["weights"]
+    x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
+    return x @ gpu.transpose(w["transformer.wte.weight"])
+
+
+def gpt2_prefill(model: dict, ids, cache: KVCache, positions=None):
+    """Causal forward of a batch of prompts [B, T] into an empty cache.
+
+    Returns (logits [B*T, vocab], next_tokens int32 [B] on the device: the
+    greedy pick at each prompt's last position).  Follows the reference's
+    first generate step (python/applegpu_runtime/models/generate.py:110-119:
+    gpt2_forward over the prompt, argmax of the last position's logits) for B
+    prompts at once; the K/V rows of every layer are written into `cache`.
+    `ids` may be a numpy array or an int32 GpuTensor [B, T]; `positions`
+    (int32 GpuTensor [B*T], 0..T-1 per sequence) keeps the call free of host
+    copies so it can be captured."""
+    w = model["weights"]
+    cfg = model["config"]
+    if isinstance(ids, gpu.GpuTensor):
+        B, T = ids.shape
+        idx = gpu.reshape(ids, [B * T])
+    else:
+        ids = np.asarray(ids, dtype=np.int32)
+        B, T = ids.shape
+        idx = gpu.from_numpy(ids.reshape(-1))
+    if B != cache.batch:
+        raise ValueError(f"batch {B} does not match the cache's {cache.batch}")
+    if T > cache.max_len:
+        raise ValueError(f"prompt length {T} exceeds the cache length {cache.max_len}")
+    if cache.length != 0:
+        raise ValueError("gpt2_prefill needs an empty cache")
+    if positions is None:
+        positions = gpu.from_numpy(np.tile(np.arange(T, dtype=np.int32), B))
+    x = gpu.embedding(w["transformer.wte.weight"], idx) + gpu.embedding(w["transformer.wpe.weight"], positions)
+
+    def attend(i, q, k, v):
+        gpu.kv_write(cache.k[i], k, cache.pos)
+        gpu.kv_write(cache.v[i], v, cache.pos)
+        return gpu.attention_causal(q, k, v)
+
+    for i in range(cfg["n_layer"]):
+        x = _block(model, i, x, B, T, attend)
+    logits = _head(model, x)
+    V = logits.shape[-1]
+    last = gpu.reshape(gpu.slice(gpu.reshape(logits, [B, T, V]), 1, T - 1, T), [B, V])
+    return logits, gpu.argmax(last)
+
+
+def gpt2_decode_step(model: dict, tokens, cache: KVCache):
+    """One greedy decode step for the whole batch: tokens int32 [B] (device)
+    at positions cache.pos.  Appends each layer's K/V row in place, attends
+    over the first pos+1 cache rows, and returns (logits [B, vocab],
+    next_tokens int32 [B], lens int32 [B] = pos + 1), all on the device.
+
+    The reference's decode step (python/applegpu_runtime/models/gpt2.py:84-178
+    with kv_cache, generate.py:110-119) processes the last token of one
+    sequence against its concatenated cache with non-causal attention; this
+    is the same computation for B sequences, with the cache append and the
+    lengths on the device.  The caller advances the cache with
+    `gpu.blit_copy(lens, cache.pos)` once the step's results are consumed."""
+    w = model["weights"]
+    cfg = model["config"]
+    B = cache.batch
+    x = gpu.embedding(w["transformer.wte.weight"], tokens) + gpu.embedding(w["transformer.wpe.weight"], cache.pos)
+    lens = cache.pos + cache.one
+
+    def attend(i, q, k, v):
+        gpu.kv_write(cache.k[i], k, cache.pos)
+        gpu.kv_write(cache.v[i], v, cache.pos)
+        return gpu.decode_attention(q, cache.k[i], cache.v[i], lens)
+
+    for i in range(cfg["n_layer"]):
+        x = _block(model, i, x, B, 1, attend)
+    logits = _head(model, x)
+    return logits, gpu.argmax(logits), lens
+
+
+def generate_greedy(model: dict, prompt_ids, n_steps: int, cache: KVCache = None, capture: bool = True,
+                    keep_logits: bool = False):
+    """Greedy generation for a batch of equal-length prompts [B, T]: one
+    prefill, then `n_steps` decode steps.  Returns int32 tokens [B, n_steps+1]
+    (the prefill's pick, then one per decode step), plus the per-step logits
+    (numpy [n_steps+1, B, vocab]) when keep_logits.
+
+    With capture=True the decode step is recorded once as a HIP graph and
+    replayed for every token: positions, the cache append and the next-token
+    argmax all stay on the device, so a step costs one graph launch."""
+    prompt_ids = np.asarray(prompt_ids, dtype=np.int32)
+    B, T = prompt_ids.shape
+    if cache is None:
+        cache = KVCache(model["config"], B, T + n_steps, model.get("dtype", "float16"))
+    if T + n_steps > cache.max_len:
+        raise ValueError(f"prompt {T} + {n_steps} steps exceeds the cache length {cache.max_len}")
+    logits, nxt = gpt2_prefill(model, prompt_ids, cache)
+    tokens = gpu.zeros([B], "int32")
+    gpu.blit_copy(nxt, tokens)
+    gpu.blit_copy(cache.pos + gpu.from_numpy(np.full(1, T, np.int32)), cache.pos)
+    cache.length = T
+    out = gpu.zeros([n_steps + 1, B], "int32")
+    gpu.blit_copy(tokens, gpu.slice(out, 0, 0, 1))
+    kept = []
+    if keep_logits:
+        V = logits.shape[-1]
+        kept.append(gpu.reshape(gpu.slice(gpu.reshape(logits, [B, T, V]), 1, T - 1, T), [B, V]).to_numpy())
+    del logits, nxt
+
+    def step():
+        lg, nx, lens = gpt2_decode_step(model, tokens, cache)
+        gpu.blit_copy(nx, tokens)
+        gpu.blit_copy(lens, cache.pos)
+        return lg
+
+    graph = gpu.capture(step) if capture and n_steps > 0 else None
+    for s in range(n_steps):
+        if graph is not None:
+            graph.replay()
+            lg = graph.outputs
+        else:
+            lg = step()
+        cache.length += 1
+        gpu.blit_copy(tokens, gpu.slice(out, 0, s + 1, s + 2))
+        if keep_logits:
+            kept.append(lg.to_numpy())
+    toks = out.to_numpy().T.copy()
+    if graph is not None:
+        graph.destroy()
+    if keep_logits:
+        return toks, np.stack(kept)
+    return toks

@@ -248,14 +248,34 @@ uint64_t applegpu_ffi_neg(uint64_t x) { return lazy1("neg", {x}); }
 
 int32_t applegpu_ffi_copy(uint64_t src_id, uint64_t dst_id) {
   return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    // dst = src element-wise (crates/core/src/backend_ffi.rs copy); dst may be
+    // a view of another tensor (e.g. a slice of a KV cache, evaluated here to
+    // a view of that tensor's storage) with any strides.
     TensorP src = rt().lookup(src_id);
     if (src->pending()) eval(src);
     TensorP dst = rt().lookup(dst_id);
-    if (dst->pending()) fail("copy: dst tensor %llu has pending ops", (unsigned long long)dst_id);
-    TensorP s = ops::contiguous(src);
-    size_t nb = s->nbytes();
-    if (!dst->buf || (size_t)dst->offset + nb > dst->buf->requested) fail("copy: destination too small");
-    if (nb) AGPU_HIP(hipMemcpyAsync(dst->data(), s->data(), nb, hipMemcpyDeviceToDevice, rt().stream()));
+    if (dst->pending()) eval(dst);
+    if (!dst->buf) fail("copy: destination has no storage");
+    if (dst->extent_bytes() + (size_t)dst->offset > dst->buf->requested) fail("copy: destination too small");
+    ops::copy_into(dst, src);
+    return 0;
+  });
+}
+
+int32_t applegpu_kv_write(uint64_t cache_id, uint64_t rows_id, uint64_t pos_id) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    // In-place KV append at device-resident positions; replaces the
+    // reference's per-step concat of the whole cache
+    // (python/applegpu_runtime/models/gpt2.py:122-126).
+    TensorP rows = rt().lookup(rows_id);
+    if (rows->pending()) eval(rows);
+    TensorP pos = rt().lookup(pos_id);
+    if (pos->pending()) eval(pos);
+    TensorP cache = rt().lookup(cache_id);
+    if (cache->pending()) eval(cache);
+    if (!cache->buf) fail("kv_write: cache has no storage");
+    if (cache->extent_bytes() + (size_t)cache->offset > cache->buf->requested) fail("kv_write: cache view out of bounds");
+    ops::kv_write(cache, rows, pos);
     return 0;
   });
 }

@@ -30,6 +30,7 @@ enum Op : int {
   OP_MATMUL, OP_MATMUL_EX, OP_LINEAR, OP_ADD_BIAS, OP_ATTENTION, OP_ATTENTION_CAUSAL,
   OP_WHERE, OP_MASKED_FILL, OP_TRIU, OP_TRIL,
   OP_QUANTIZE_PER_ROW, OP_DEQUANTIZE_PER_ROW, OP_LINEAR_INT8, OP_CONTIGUOUS, OP_FULL,
+  OP_DECODE_ATTENTION,
   OP_COUNT
 };
 
@@ -46,6 +47,7 @@ static const char* kNames[OP_COUNT] = {
     "matmul", "matmul_ex", "linear", "add_bias", "attention", "attention_causal",
     "where", "masked_fill", "triu", "tril",
     "quantize_per_row", "dequantize_per_row", "linear_int8", "contiguous", "full",
+    "decode_attention",
 };
 
 int op_code(const char* name) {
@@ -190,6 +192,7 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       need(in, 2, code);
       return {dequantize_per_row(in[0], in[1], iv.empty() ? DType::F32 : dt_param(iv[0]))};
     case OP_LINEAR_INT8: need(in, 3, code); return {linear_int8(in[0], in[1], in[2])};
+    case OP_DECODE_ATTENTION: need(in, 4, code); return {decode_attention(in[0], in[1], in[2], in[3])};
     case OP_CONTIGUOUS: {
       need(in, 1, code);
       TensorP c = contiguous(in[0]);

@@ -146,5 +146,38 @@ struct Attn {
 bool attention_supported(const Attn& a);
 void attention(const Attn& a, hipStream_t s);
 
+// ── KV-cache decode ───────────────────────────────────────────────────────
+// Attention of Tq new query rows per (batch, head) over the first lens[b]
+// rows of a [B, H, Tmax, D] cache whose last Tq valid rows are the queries'
+// own keys: query row i sees keys j <= lens[b] - Tq + i.  lens is int32 [B]
+// in device memory (clamped to [0, Tmax]).
+struct DecodeAttn {
+  DType dt = DType::F16;
+  int64_t B = 1, H = 1, Tq = 1, Tmax = 0, D = 0;
+  const void* q = nullptr; int64_t q_sb = 0, q_sh = 0, q_st = 0;  // unit d stride
+  const void* k = nullptr; int64_t k_sb = 0, k_sh = 0, k_st = 0;
+  const void* v = nullptr; int64_t v_sb = 0, v_sh = 0, v_st = 0;
+  void* o = nullptr; int64_t o_sb = 0, o_sh = 0, o_st = 0;
+  const int32_t* lens = nullptr;
+  float scale = 1.f;
+};
+bool decode_attention_supported(const DecodeAttn& a);
+int decode_attention_splits(const DecodeAttn& a, int64_t* chunk);
+size_t decode_attention_ws_bytes(const DecodeAttn& a);
+void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s);
+// cache[b, h, pos[b] + t, :] = src[b, h, t, :] for t < T (rows that would
+// land at or past Tmax are dropped); pos is int32 [B] in device memory.
+struct KvWrite {
+  DType dt = DType::F16;
+  int64_t B = 1, H = 1, T = 0, D = 0, Tmax = 0;
+  void* cache = nullptr; int64_t c_sb = 0, c_sh = 0, c_st = 0;      // unit d stride
+  const void* src = nullptr; int64_t x_sb = 0, x_sh = 0, x_st = 0;  // unit d stride
+  const int32_t* pos = nullptr;
+};
+void kv_write(const KvWrite& a, hipStream_t s);
+// o = x elementwise with dtype conversion, o written through the strides of
+// `so` (shape and destination strides) and x read through `sx`.
+void copy_strided(DType in, DType out, const void* x, const ND& sx, void* o, const ND& so, hipStream_t s);
+
 }  // namespace k
 }  // namespace agpu

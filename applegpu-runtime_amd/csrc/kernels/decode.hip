@@ -1,0 +1,313 @@
+// Decode-time attention over a preallocated KV cache, and the in-place append
+// that fills it.
+//
+// The reference decodes by concatenating each step's K/V rows onto the
+// previous cache (python/applegpu_runtime/models/gpt2.py:122-126: a fresh copy
+// of the whole cache, per layer, per step) and then running non-causal
+// attention of the one new query over it (gpt2.py:132-135 through
+// crates/core/src/ops.rs:1531-1620).  Here each layer's cache is one
+// [B, H, Tmax, D] allocation: kv_write stores the new rows at each sequence's
+// position, read from device memory, and decode_attention reads each
+// sequence's length from device memory.  Nothing a decode step launches then
+// depends on a host-side length, so the step can be recorded once as a HIP
+// graph and replayed for every token.
+//
+// decode_attention splits each (batch, head, query row) over the key axis
+// (split-KV): block (split s, row) scores keys [s*chunk, (s+1)*chunk) with an
+// online softmax and leaves an unnormalised partial (max, sum, acc[D]); a
+// second kernel merges the partials of a row.  Within a block, D/8 lanes own
+// one key, 8 elements each (one 16-byte load for 16-bit types), so a wave
+// covers 64/(D/8) keys per step and the dot product is log2(D/8) xor
+// shuffles.  A row with no visible key gets zeros (the fused attention kernel
+// uses the same convention).
+#include "device.hpp"
+
+namespace agpu {
+namespace k {
+using namespace dev;
+
+namespace {
+
+constexpr int kDWaves = 4;   // waves per decode block
+constexpr int kDUnroll = 2;  // key steps each wave keeps in flight
+
+struct DArgs {
+  const void* q; const void* k; const void* v; void* o;
+  const int32_t* lens;
+  float* part;  // [rows][splits][D + 2]: acc[D], max, sum (unused when splits == 1)
+  int64_t H, Tq, Tmax;
+  int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
+  float scale;
+  int splits, chunk;
+};
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void load8(const T* p, float (&x)[8]) {
+  if constexpr (VEC && sizeof(T) == 2) {
+    uint4 u = *(const uint4*)p;
+    T e[8];
+    __builtin_memcpy(e, &u, 16);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = to_f(e[i]);
+  } else if constexpr (VEC && sizeof(T) == 4) {
+    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = to_f(p[i]);
+  }
+}
+
+// Number of keys visible to query row i of a sequence holding `len` keys
+// whose last Tq entries are the queries themselves: keys j <= len - Tq + i.
+__device__ __forceinline__ int64_t visible_keys(const DArgs& p, int64_t b, int64_t i) {
+  int64_t len = p.lens[b];
+  len = len < 0 ? 0 : (len > p.Tmax ? p.Tmax : len);
+  int64_t vis = len - p.Tq + i + 1;
+  return vis < 0 ? 0 : (vis > len ? len : vis);
+}
+
+template <typename T, int D, bool VEC>
+__global__ void __launch_bounds__(256) decode_attn(DArgs p) {
+  constexpr int LPK = D / 8;           // lanes per key
+  constexpr int KPS = 64 / LPK;        // keys per wave step
+  constexpr int NG = kDWaves * KPS;    // key groups per block
+  constexpr int BS = NG * kDUnroll;    // keys per block iteration
+  __shared__ float sm_acc[NG][D];
+  __shared__ float sm_m[NG], sm_l[NG];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int g = lane / LPK, sub = lane % LPK;
+  const int s = blockIdx.x;
+  const int64_t row = blockIdx.y;
+  const int64_t i = row % p.Tq, bh = row / p.Tq;
+  const int64_t h = bh % p.H, b = bh / p.H;
+  const int64_t vis = visible_keys(p, b, i);
+  const int64_t j_lo = (int64_t)s * p.chunk;
+  const int64_t j_hi = j_lo + p.chunk < vis ? j_lo + p.chunk : vis;
+
+  float q[8];
+  load8<T, VEC>((const T*)p.q + b * p.q_sb + h * p.q_sh + i * p.q_st + sub * 8, q);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) q[e] *= p.scale;
+  const T* K = (const T*)p.k + b * p.k_sb + h * p.k_sh + sub * 8;
+  const T* V = (const T*)p.v + b * p.v_sb + h * p.v_sh + sub * 8;
+
+  float m = -INFINITY, l = 0.f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+
+  for (int64_t base = j_lo; base < j_hi; base += BS) {
+    // all loads of the iteration first (rows clamped into the cache, masked
+    // below), then the arithmetic
+    float kx[kDUnroll][8], vx[kDUnroll][8];
+    int64_t jj[kDUnroll];
+#pragma unroll
+    for (int u = 0; u < kDUnroll; ++u) {
+      const int64_t j = base + (int64_t)(u * kDWaves + w) * KPS + g;
+      jj[u] = j;
+      const int64_t jc = j < p.Tmax ? j : p.Tmax - 1;
+      load8<T, VEC>(K + jc * p.k_st, kx[u]);
+      load8<T, VEC>(V + jc * p.v_st, vx[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < kDUnroll; ++u) {
+      float dot = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot += q[e] * kx[u][e];
+#pragma unroll
+      for (int x = 1; x < LPK; x <<= 1) dot += __shfl_xor(dot, x, 64);
+      const bool ok = jj[u] < j_hi;
+      const float sc = ok ? dot : -INFINITY;
+      const float m_new = fmaxf(m, sc);
+      const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
+      const float pe = ok ? expf(sc - m_new) : 0.f;
+      l = l * alpha + pe;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] = acc[e] * alpha + pe * vx[u][e];
+      m = m_new;
+    }
+  }
+
+  const int grp = w * KPS + g;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sm_acc[grp][sub * 8 + e] = acc[e];
+  if (sub == 0) { sm_m[grp] = m; sm_l[grp] = l; }
+  __syncthreads();
+  if (tid >= D) return;
+
+  float M = -INFINITY;
+  for (int x = 0; x < NG; ++x) M = fmaxf(M, sm_m[x]);
+  float L = 0.f, A = 0.f;
+  if (M != -INFINITY) {
+    for (int x = 0; x < NG; ++x) {
+      const float mx = sm_m[x];
+      const float f = mx == -INFINITY ? 0.f : expf(mx - M);
+      L += sm_l[x] * f;
+      A += sm_acc[x][tid] * f;
+    }
+  }
+  if (p.splits == 1) {
+    T* O = (T*)p.o + b * p.o_sb + h * p.o_sh + i * p.o_st;
+    O[tid] = from_f<T>(L > 0.f ? A / L : 0.f);
+  } else {
+    float* P = p.part + (row * p.splits + s) * (D + 2);
+    P[tid] = A;
+    if (tid == 0) { P[D] = M; P[D + 1] = L; }
+  }
+}
+
+// One block of D threads per row: merges the row's split partials.
+template <typename T, int D>
+__global__ void __launch_bounds__(128) decode_merge(DArgs p) {
+  const int64_t row = blockIdx.x;
+  const int64_t i = row % p.Tq, bh = row / p.Tq;
+  const int64_t h = bh % p.H, b = bh / p.H;
+  const int t = threadIdx.x;
+  const float* P = p.part + row * p.splits * (D + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < p.splits; ++s) M = fmaxf(M, P[s * (D + 2) + D]);
+  float L = 0.f, A = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < p.splits; ++s) {
+      const float ms = P[s * (D + 2) + D];
+      const float f = ms == -INFINITY ? 0.f : expf(ms - M);
+      L += P[s * (D + 2) + D + 1] * f;
+      A += P[s * (D + 2) + t] * f;
+    }
+  }
+  T* O = (T*)p.o + b * p.o_sb + h * p.o_sh + i * p.o_st;
+  O[t] = from_f<T>(L > 0.f ? A / L : 0.f);
+}
+
+// dst rows [pos[b] + t] of the cache = src rows t, as raw elements of E.
+template <typename E>
+__global__ void __launch_bounds__(256) kv_write_kernel(E* __restrict__ c, const E* __restrict__ x,
+                                                       const int32_t* __restrict__ pos, int64_t H, int64_t T,
+                                                       int64_t D, int64_t Tmax, int64_t c_sb, int64_t c_sh,
+                                                       int64_t c_st, int64_t x_sb, int64_t x_sh, int64_t x_st,
+                                                       int64_t n) {
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t d = idx % D, r = idx / D;
+    const int64_t t = r % T, bh = r / T;
+    const int64_t h = bh % H, b = bh / H;
+    const int64_t dt = (int64_t)pos[b] + t;
+    if (dt < 0 || dt >= Tmax) continue;  // rows past the cache's capacity are dropped
+    c[b * c_sb + h * c_sh + dt * c_st + d] = x[b * x_sb + h * x_sh + t * x_st + d];
+  }
+}
+
+bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <typename T, int D>
+void launch_decode(const DArgs& p, bool vec, int64_t rows, hipStream_t s) {
+  const dim3 grid((unsigned)p.splits, (unsigned)rows);
+  if (vec) hipLaunchKernelGGL((decode_attn<T, D, true>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((decode_attn<T, D, false>), grid, dim3(256), 0, s, p);
+  if (p.splits > 1) hipLaunchKernelGGL((decode_merge<T, D>), dim3((unsigned)rows), dim3(D), 0, s, p);
+}
+
+template <typename E>
+void launch_kv_write(const KvWrite& a, int64_t vec, hipStream_t s) {
+  // vec = elements of the dtype per E
+  const int64_t D = a.D / vec;
+  const int64_t n = a.B * a.H * a.T * D;
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  hipLaunchKernelGGL((kv_write_kernel<E>), dim3((unsigned)g), dim3(256), 0, s, (E*)a.cache, (const E*)a.src,
+                     a.pos, a.H, a.T, D, a.Tmax, a.c_sb / vec, a.c_sh / vec, a.c_st / vec, a.x_sb / vec,
+                     a.x_sh / vec, a.x_st / vec, n);
+}
+
+}  // namespace
+
+bool decode_attention_supported(const DecodeAttn& a) {
+  return (a.D == 32 || a.D == 64 || a.D == 128) &&
+         (a.dt == DType::F32 || a.dt == DType::F16 || a.dt == DType::BF16);
+}
+
+int decode_attention_splits(const DecodeAttn& a, int64_t* chunk) {
+  // keys per block iteration, as in decode_attn
+  const int64_t bs = (int64_t)kDWaves * (64 / (a.D / 8)) * kDUnroll;
+  const int64_t rows = a.B * a.H * a.Tq;
+  // aim for >= 2048 blocks over the 256 CUs, with at least one block
+  // iteration per split
+  int64_t want = rows >= 2048 ? 1 : (2048 + rows - 1) / rows;
+  const int64_t max_splits = (a.Tmax + bs - 1) / bs;
+  if (want > max_splits) want = max_splits;
+  if (want < 1) want = 1;
+  int64_t c = (a.Tmax + want - 1) / want;
+  c = (c + bs - 1) / bs * bs;
+  *chunk = c;
+  return (int)((a.Tmax + c - 1) / c);
+}
+
+size_t decode_attention_ws_bytes(const DecodeAttn& a) {
+  int64_t chunk;
+  const int splits = decode_attention_splits(a, &chunk);
+  if (splits <= 1) return 0;
+  return (size_t)(a.B * a.H * a.Tq) * splits * (a.D + 2) * sizeof(float);
+}
+
+void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s) {
+  if (!decode_attention_supported(a)) fail("decode_attention: head dim %lld not supported", (long long)a.D);
+  if (a.Tmax <= 0) fail("decode_attention: empty cache");
+  const int64_t rows = a.B * a.H * a.Tq;
+  if (rows == 0) return;
+  if (rows > 0x7fffffffLL) fail("decode_attention: too many rows");
+  DArgs p{};
+  p.q = a.q; p.k = a.k; p.v = a.v; p.o = a.o;
+  p.lens = a.lens;
+  p.H = a.H; p.Tq = a.Tq; p.Tmax = a.Tmax;
+  p.q_sb = a.q_sb; p.q_sh = a.q_sh; p.q_st = a.q_st;
+  p.k_sb = a.k_sb; p.k_sh = a.k_sh; p.k_st = a.k_st;
+  p.v_sb = a.v_sb; p.v_sh = a.v_sh; p.v_st = a.v_st;
+  p.o_sb = a.o_sb; p.o_sh = a.o_sh; p.o_st = a.o_st;
+  p.scale = a.scale;
+  int64_t chunk;
+  p.splits = decode_attention_splits(a, &chunk);
+  p.chunk = (int)chunk;
+  if (p.splits > 1) {
+    if (!ws) fail("decode_attention: split-KV workspace missing");
+    p.part = (float*)ws;
+  }
+  // 16-byte loads need every row of q, K and V 16-byte aligned
+  const size_t es = dtype_size(a.dt);
+  auto al = [&](const void* ptr, int64_t s0, int64_t s1, int64_t s2) {
+    return al16(ptr) && (s0 * es) % 16 == 0 && (s1 * es) % 16 == 0 && (s2 * es) % 16 == 0;
+  };
+  const bool vec = al(a.q, a.q_sb, a.q_sh, a.q_st) && al(a.k, a.k_sb, a.k_sh, a.k_st) &&
+                   al(a.v, a.v_sb, a.v_sh, a.v_st);
+  AGPU_FLOAT_SWITCH(a.dt, {
+    if (a.D == 32) launch_decode<T, 32>(p, vec, rows, s);
+    else if (a.D == 64) launch_decode<T, 64>(p, vec, rows, s);
+    else launch_decode<T, 128>(p, vec, rows, s);
+  });
+  check_launch("decode_attention");
+}
+
+void kv_write(const KvWrite& a, hipStream_t s) {
+  const int64_t n = a.B * a.H * a.T * a.D;
+  if (n == 0) return;
+  const size_t es = dtype_size(a.dt);
+  // widest element that divides every row and stride
+  auto fits = [&](size_t w) {
+    const int64_t v = (int64_t)(w / es);
+    if (w < es || w % es) return false;
+    auto ok = [&](int64_t x) { return x % v == 0; };
+    return ((uintptr_t)a.cache % w) == 0 && ((uintptr_t)a.src % w) == 0 && ok(a.D) && ok(a.c_sb) &&
+           ok(a.c_sh) && ok(a.c_st) && ok(a.x_sb) && ok(a.x_sh) && ok(a.x_st);
+  };
+  if (fits(16)) launch_kv_write<uint4>(a, (int64_t)(16 / es), s);
+  else if (fits(8)) launch_kv_write<uint2>(a, (int64_t)(8 / es), s);
+  else if (es == 4) launch_kv_write<uint32_t>(a, 1, s);
+  else if (es == 2) launch_kv_write<uint16_t>(a, 1, s);
+  else if (es == 1) launch_kv_write<uint8_t>(a, 1, s);
+  else launch_kv_write<uint2>(a, 1, s);
+  check_launch("kv_write");
+}
+
+}  // namespace k
+}  // namespace agpu

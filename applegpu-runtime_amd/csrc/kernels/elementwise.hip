@@ -344,7 +344,50 @@ void launch_unary(int op, const void* x, const ND& sx, void* o, const ND& so, fl
   check_launch("unary");
 }
 
+// o[offset(i) through so's strides] = x[offset(i) through sx's strides]
+template <typename I, typename TI, typename TO>
+__global__ void __launch_bounds__(256) copy_nd_strided(const TI* __restrict__ x, ND sx, TO* __restrict__ o,
+                                                       ND so, I n) {
+  typedef typename Compute<TI>::type C;
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (I)gridDim.x * blockDim.x)
+    o[nd_offset<I>(i, so, so)] = (TO)(C)x[nd_offset<I>(i, so, sx)];
+}
+
+template <typename TI, typename TO>
+void launch_copy_strided(const void* x, const ND& sx, void* o, const ND& so, hipStream_t s) {
+  int64_t n = numel_of(so);
+  if (n == 0) return;
+  if (fits32(n, sx, so))
+    hipLaunchKernelGGL((copy_nd_strided<uint32_t, TI, TO>), dim3(grid_for(n)), dim3(256), 0, s, (const TI*)x, sx,
+                       (TO*)o, so, (uint32_t)n);
+  else
+    hipLaunchKernelGGL((copy_nd_strided<uint64_t, TI, TO>), dim3(grid_for(n)), dim3(256), 0, s, (const TI*)x, sx,
+                       (TO*)o, so, (uint64_t)n);
+  check_launch("copy_strided");
+}
+
+template <typename TI>
+void copy_strided_to(DType out, const void* x, const ND& sx, void* o, const ND& so, hipStream_t s) {
+  switch (out) {
+    case DType::F32: launch_copy_strided<TI, float>(x, sx, o, so, s); break;
+    case DType::F16: launch_copy_strided<TI, half_t>(x, sx, o, so, s); break;
+    case DType::BF16: launch_copy_strided<TI, bf16_t>(x, sx, o, so, s); break;
+    case DType::I8: launch_copy_strided<TI, int8_t>(x, sx, o, so, s); break;
+    case DType::I16: launch_copy_strided<TI, int16_t>(x, sx, o, so, s); break;
+    case DType::I32: launch_copy_strided<TI, int32_t>(x, sx, o, so, s); break;
+    case DType::I64: launch_copy_strided<TI, int64_t>(x, sx, o, so, s); break;
+    case DType::U8: launch_copy_strided<TI, uint8_t>(x, sx, o, so, s); break;
+    case DType::U32: launch_copy_strided<TI, uint32_t>(x, sx, o, so, s); break;
+    case DType::Bool: launch_copy_strided<TI, bool>(x, sx, o, so, s); break;
+    default: fail("copy: unsupported destination dtype %s", dtype_name(out));
+  }
+}
+
 }  // namespace
+
+void copy_strided(DType in, DType out, const void* x, const ND& sx, void* o, const ND& so, hipStream_t s) {
+  AGPU_ALL_SWITCH(in, copy_strided_to<T>(out, x, sx, o, so, s));
+}
 
 void binary(int op, DType in, DType out, const void* a, const ND& sa, const void* b, const ND& sb,
             void* o, const ND& so, float p0, hipStream_t s) {

@@ -426,7 +426,17 @@ void copy_into(const TensorP& dst, const TensorP& src) {
              rt().stream());
     return;
   }
-  fail("copy into a non-contiguous destination is not supported");
+  // Strided destination (a slice or transpose of a larger tensor): every
+  // element must have its own address.
+  k::ND so;
+  so.ndim = dst->ndim;
+  for (int i = 0; i < dst->ndim; ++i) {
+    so.shape[i] = dst->shape[i];
+    so.stride[i] = dst->strides[i];
+    if (dst->shape[i] > 1 && dst->strides[i] == 0)
+      fail("copy: the destination has overlapping elements (stride 0 in dim %d)", i);
+  }
+  LAUNCH k::copy_strided(s->dtype, dst->dtype, s->data(), nd_for(*s, dims), dst->data(), so, rt().stream());
 }
 
 // ── rows ───────────────────────────────────────────────────────────────────
@@ -880,6 +890,85 @@ TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool ca
   a.o_st = out->strides[out->ndim - 2];
   LAUNCH k::attention(a, rt().stream());
   return out;
+}
+
+// ── KV-cache decode ────────────────────────────────────────────────────────
+// Shape checks shared by kv_write and decode_attention: 4-D [B, H, T, D]
+// operands with a unit stride along D.
+static void check_bhtd(const char* name, const char* what, const Tensor& t) {
+  if (t.ndim != 4) fail("%s: %s must be 4-D [batch, heads, tokens, head_dim], got %s", name, what,
+                        shape_str(t.dims()).c_str());
+  if (t.strides[3] != 1 && t.shape[3] > 1) fail("%s: %s must have a unit stride along head_dim", name, what);
+}
+
+static TensorP check_lens(const char* name, const char* what, const TensorP& lens, int64_t B) {
+  if (lens->dtype != DType::I32) fail("%s: %s must be int32, got %s", name, what, dtype_name(lens->dtype));
+  if (lens->numel() != B) fail("%s: %s must hold one entry per sequence (%lld), got %lld", name, what,
+                               (long long)B, (long long)lens->numel());
+  return contiguous(lens);
+}
+
+TensorP decode_attention(const TensorP& q, const TensorP& kc, const TensorP& vc, const TensorP& lens) {
+  const char* name = "decode_attention";
+  check_dtype(name, kFloatOnly, q->dtype);
+  if (kc->dtype != q->dtype || vc->dtype != q->dtype) fail("%s: q and the caches must share a dtype", name);
+  check_bhtd(name, "q", *q);
+  check_bhtd(name, "k_cache", *kc);
+  check_bhtd(name, "v_cache", *vc);
+  const int64_t B = q->shape[0], H = q->shape[1], Tq = q->shape[2], D = q->shape[3];
+  for (const Tensor* c : {kc.get(), vc.get()})
+    if (c->shape[0] != B || c->shape[1] != H || c->shape[3] != D)
+      fail("%s: cache shape %s does not match q %s", name, shape_str(c->dims()).c_str(), shape_str(q->dims()).c_str());
+  if (vc->shape[2] != kc->shape[2]) fail("%s: k_cache and v_cache lengths differ", name);
+  const int64_t Tmax = kc->shape[2];
+  if (Tmax < 1) fail("%s: empty cache", name);
+  if (Tq > Tmax) fail("%s: %lld query rows exceed the cache length %lld", name, (long long)Tq, (long long)Tmax);
+  TensorP lc = check_lens(name, "lens", lens, B);
+
+  k::DecodeAttn a;
+  a.dt = q->dtype;
+  a.B = B; a.H = H; a.Tq = Tq; a.Tmax = Tmax; a.D = D;
+  if (!k::decode_attention_supported(a)) fail("%s: head dim %lld not supported (32, 64 or 128)", name, (long long)D);
+  a.scale = 1.0f / std::sqrt((float)D);
+  a.q = q->data(); a.q_sb = q->strides[0]; a.q_sh = q->strides[1]; a.q_st = q->strides[2];
+  a.k = kc->data(); a.k_sb = kc->strides[0]; a.k_sh = kc->strides[1]; a.k_st = kc->strides[2];
+  a.v = vc->data(); a.v_sb = vc->strides[0]; a.v_sh = vc->strides[1]; a.v_st = vc->strides[2];
+  a.lens = (const int32_t*)lc->data();
+  // physical [B, Tq, H, D], logical [B, H, Tq, D]
+  TensorP base = alloc_out(q->dtype, {B, Tq, H, D});
+  TensorP out = make_meta(q->dtype, q->dims());
+  out->buf = base->buf;
+  out->offset = base->offset;
+  out->strides[0] = Tq * H * D; out->strides[1] = D; out->strides[2] = H * D; out->strides[3] = 1;
+  a.o = out->data(); a.o_sb = out->strides[0]; a.o_sh = out->strides[1]; a.o_st = out->strides[2];
+  size_t wsb = meta_mode() ? 0 : k::decode_attention_ws_bytes(a);
+  BufferP ws;
+  if (wsb) ws = scratch(wsb);
+  LAUNCH k::decode_attention(a, ws ? ws->ptr : nullptr, rt().stream());
+  return out;
+}
+
+void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos) {
+  const char* name = "kv_write";
+  if (cache->dtype != rows->dtype) fail("%s: cache is %s but rows are %s", name, dtype_name(cache->dtype),
+                                        dtype_name(rows->dtype));
+  check_bhtd(name, "cache", *cache);
+  check_bhtd(name, "rows", *rows);
+  const int64_t B = cache->shape[0], H = cache->shape[1], Tmax = cache->shape[2], D = cache->shape[3];
+  if (rows->shape[0] != B || rows->shape[1] != H || rows->shape[3] != D)
+    fail("%s: rows %s do not match cache %s", name, shape_str(rows->dims()).c_str(), shape_str(cache->dims()).c_str());
+  if (rows->shape[2] > Tmax) fail("%s: %lld rows exceed the cache length %lld", name, (long long)rows->shape[2],
+                                  (long long)Tmax);
+  for (int i = 0; i < 3; ++i)
+    if (cache->shape[i] > 1 && cache->strides[i] == 0) fail("%s: cache has overlapping rows", name);
+  TensorP pc = check_lens(name, "positions", pos, B);
+  k::KvWrite a;
+  a.dt = cache->dtype;
+  a.B = B; a.H = H; a.T = rows->shape[2]; a.D = D; a.Tmax = Tmax;
+  a.cache = cache->data(); a.c_sb = cache->strides[0]; a.c_sh = cache->strides[1]; a.c_st = cache->strides[2];
+  a.src = rows->data(); a.x_sb = rows->strides[0]; a.x_sh = rows->strides[1]; a.x_st = rows->strides[2];
+  a.pos = (const int32_t*)pc->data();
+  LAUNCH k::kv_write(a, rt().stream());
 }
 
 }  // namespace ops

@@ -79,6 +79,12 @@ TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
 // is still logically [..., H, T, D]) so a following head merge is free.
 TensorP attention(const TensorP& q, const TensorP& k, const TensorP& v, bool causal,
                   bool out_layout_thd = false);
+// q [B, H, Tq, D] against the first lens[b] rows of the [B, H, Tmax, D] caches
+// (lens int32 [B] on the device; the queries' own keys are the last Tq of
+// them); the output is logically [B, H, Tq, D], stored as [B, Tq, H, D].
+TensorP decode_attention(const TensorP& q, const TensorP& k_cache, const TensorP& v_cache, const TensorP& lens);
+// cache[b, h, pos[b] + t, :] = rows[b, h, t, :] (pos int32 [B] on the device).
+void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos);
 
 }  // namespace ops
 }  // namespace agpu

@@ -194,6 +194,21 @@ float applegpu_ffi_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
  * read_f32 and event_elapsed_ms fail and synchronize returns at once;
  * capture_abort ends a capture and drops what it recorded.  Calls that
  * overlap on one stream race like any other work on it. */
+/* KV-cache append for decode (replaces the reference's per-step concat of
+ * the whole cache, python/applegpu_runtime/models/gpt2.py:122-126, which
+ * copies every earlier K/V row again at each step): cache is a [B, H, Tmax, D]
+ * tensor (or view) with unit stride along D, rows is [B, H, T, D] of the same
+ * dtype, pos is int32 [B] in device memory.  Writes
+ * cache[b, h, pos[b] + t, :] = rows[b, h, t, :] in place, on the library
+ * stream; rows whose position falls outside [0, Tmax) are not written.  The
+ * positions are read by the kernel, not the host, so the call can sit inside
+ * a captured graph that is replayed with advancing positions.  The matching
+ * reader is the lazy op "decode_attention" (applegpu_graph_op): inputs q
+ * [B, H, Tq, D], k_cache, v_cache [B, H, Tmax, D] and lens int32 [B]; query
+ * row i of sequence b attends to cache rows j <= lens[b] - Tq + i.
+ * Returns 0, or -1 with the error set. */
+int32_t applegpu_kv_write(uint64_t cache_id, uint64_t rows_id, uint64_t pos_id);
+
 int32_t applegpu_capture_begin(void);
 int64_t applegpu_capture_end(void);
 int32_t applegpu_capture_abort(void);
