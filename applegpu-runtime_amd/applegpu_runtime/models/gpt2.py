@@ -64,17 +64,37 @@ def random_weights(cfg: dict, seed: int = 42, std: float = 0.02) -> dict:
     return out
 
 
-def load_model(np_weights: dict, cfg: dict, dtype: str = "float32") -> dict:
-    """Upload numpy weights; returns the model dict the forward pass takes."""
+CONV1D = (".attn.c_attn.weight", ".attn.c_proj.weight", ".mlp.c_fc.weight", ".mlp.c_proj.weight")
+
+
+def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None) -> dict:
+    """Upload numpy weights; returns the model dict the forward pass takes.
+
+    kmajor (default: on for fp16/bf16) stores the Conv1D projection weights
+    transposed, [out, in], contiguous along the reduction: the layout the
+    decode-step GEMM streams with one 16-byte load per MFMA operand.  The
+    forward multiplies by a transposed view of them, so the arithmetic is
+    the recipe's x @ W either way."""
     gpu.init_backend()
+    if kmajor is None:
+        kmajor = dtype != "float32"
     w = {}
     for k, v in np_weights.items():
-        t = gpu.from_numpy(np.ascontiguousarray(v, dtype=np.float32))
+        a = np.asarray(v, dtype=np.float32)
+        if kmajor and k.endswith(CONV1D):
+            a = a.T
+        t = gpu.from_numpy(np.ascontiguousarray(a))
         if dtype != "float32":
             t = gpu.cast(t, dtype)
             t.eval()
         w[k] = t
-    return {"weights": w, "config": dict(cfg), "dtype": dtype}
+    return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor)}
+
+
+def _mm(model: dict, x, name: str):
+    """x @ W for a Conv1D weight (HF layout [in, out]), whichever way it is stored."""
+    w = model["weights"][name]
+    return x @ (gpu.transpose(w) if model.get("kmajor") else w)
 
 
 def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
@@ -110,7 +130,7 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
     for i in range(L):
         p = f"transformer.h.{i}"
         h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
-        qkv = gpu.add_bias(h @ w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"])
+        qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
 
         def heads(lo):
             part = gpu.slice(qkv, 1, lo, lo + d)
@@ -124,11 +144,11 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
         new_cache.append((k, v))
         a = gpu.attention(q, k, v) if cached else gpu.attention_causal(q, k, v)
         a = gpu.reshape(gpu.transpose_dims(a, 0, 1), [T, d])
-        x = x + gpu.add_bias(a @ w[f"{p}.attn.c_proj.weight"], w[f"{p}.attn.c_proj.bias"])
+        x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
 
         h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
-        f = gpu.gelu(gpu.add_bias(h @ w[f"{p}.mlp.c_fc.weight"], w[f"{p}.mlp.c_fc.bias"]))
-        x = x + gpu.add_bias(f @ w[f"{p}.mlp.c_proj.weight"], w[f"{p}.mlp.c_proj.bias"])
+        f = gpu.gelu(gpu.add_bias(_mm(model, h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
+        x = x + gpu.add_bias(_mm(model, f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
 
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
     logits = x @ gpu.transpose(w["transformer.wte.weight"])
@@ -179,7 +199,7 @@ def _block(model, i, x, B, T, attend):
     hd = d // H
     p = f"transformer.h.{i}"
     h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
-    qkv = gpu.add_bias(h @ w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"])
+    qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
 
     def heads(lo):
         part = gpu.slice(qkv, 1, lo, lo + d)
@@ -187,10 +207,10 @@ def _block(model, i, x, B, T, attend):
 
     a = attend(i, heads(0), heads(d), heads(2 * d))
     a = gpu.reshape(gpu.transpose_dims(a, 1, 2), [B * T, d])
-    x = x + gpu.add_bias(a @ w[f"{p}.attn.c_proj.weight"], w[f"{p}.attn.c_proj.bias"])
+    x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
     h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
-    f = gpu.gelu(gpu.add_bias(h @ w[f"{p}.mlp.c_fc.weight"], w[f"{p}.mlp.c_fc.bias"]))
-    return x + gpu.add_bias(f @ w[f"{p}.mlp.c_proj.weight"], w[f"{p}.mlp.c_proj.bias"])
+    f = gpu.gelu(gpu.add_bias(_mm(model, h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
+    return x + gpu.add_bias(_mm(model, f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
 
 
 def _head(model, x):

@@ -533,6 +533,13 @@ int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits) {
   });
 }
 
+int32_t applegpu_ffi_gemm_skinny(int32_t enable) {
+  k::GemmTune& t = k::gemm_tune();
+  const int32_t prev = t.no_skinny ? 0 : 1;
+  t.no_skinny = enable == 0;
+  return prev;
+}
+
 int32_t applegpu_ffi_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int8_t dtype_i8, bool a_kcontig,
                                bool b_kcontig, char* out, uint32_t cap) {
   return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {

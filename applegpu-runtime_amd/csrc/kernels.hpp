@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <string>
 
 #include "core.hpp"
 
@@ -127,6 +128,7 @@ struct GemmTune {
   int f32_mode = kF32Split3;
   int cfg = -1;
   int splits = 0;
+  bool no_skinny = false;  // route M <= 16 through gemm_mf too
 };
 GemmTune& gemm_tune();
 // Name of the configuration the heuristic (or a forced tune) picks.

@@ -395,6 +395,8 @@ GemmTune& gemm_tune() {
     GemmTune d;
     const char* m = getenv("APPLEGPU_GEMM_F32");
     if (m && (!strcmp(m, "native") || !strcmp(m, "f32"))) d.f32_mode = kF32Native;
+    const char* sk = getenv("APPLEGPU_GEMM_SKINNY");
+    if (sk && *sk == '0') d.no_skinny = true;
     return d;
   }();
   return t;
@@ -402,6 +404,11 @@ GemmTune& gemm_tune() {
 
 const char* gemm_plan_name(const Gemm& g) {
   static thread_local char buf[96];
+  const SkinnyPlan sp = skinny_plan(g, cu_count());
+  if (sp.use) {
+    snprintf(buf, sizeof buf, "skinny mfma16 blocks=%lld", (long long)sp.blocks);
+    return buf;
+  }
   Plan pl = make_plan(g, cu_count());
   const char* kind = pl.kind == kGeneric ? "generic" : pl.kind == kNative32 ? "f32-native" : "mf";
   snprintf(buf, sizeof buf, "%s cfg%d %dx%dx%d splits=%d", kind, pl.kind == kMf ? pl.cfg : -1, pl.bm, pl.bn, pl.bk,
@@ -410,6 +417,8 @@ const char* gemm_plan_name(const Gemm& g) {
 }
 
 size_t gemm_workspace_bytes(const Gemm& g) {
+  const SkinnyPlan sp = skinny_plan(g, cu_count());
+  if (sp.use) return 0;
   Plan pl = make_plan(g, cu_count());
   if (pl.splits <= 1) return 0;
   return (size_t)pl.splits * g.batch * g.M * g.N * sizeof(float);
@@ -417,6 +426,15 @@ size_t gemm_workspace_bytes(const Gemm& g) {
 
 void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
+  const SkinnyPlan sp = skinny_plan(g, cu_count());
+  if (sp.use) {
+    Plan one{};
+    one.bm = one.bn = 1;
+    one.splits = 1;
+    one.kps = g.K;
+    gemm_skinny(g, sp, make_args(g, one), s);
+    return;
+  }
   Plan pl = make_plan(g, cu_count());
   GArgs p = make_args(g, pl);
   p.ws = (float*)workspace;

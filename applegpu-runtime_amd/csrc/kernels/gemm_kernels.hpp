@@ -543,6 +543,15 @@ void launch_mf(const GArgs& p, int cfg, bool ak, bool bk, dim3 grid, hipStream_t
 #undef AGPU_MF_CASE
 }
 
+// Skinny GEMM (M <= 16, one batch, 16-bit, B k-contiguous; gemm_skinny.hip):
+// use = false when the problem does not qualify.
+struct SkinnyPlan {
+  bool use = false;
+  int64_t blocks = 0;  // one block per 16 columns
+};
+SkinnyPlan skinny_plan(const Gemm& g, int cus);
+void gemm_skinny(const Gemm& g, const SkinnyPlan& pl, const GArgs& p, hipStream_t s);
+
 // Defined in gemm_mf_{f32,f16,bf16}_{fast,edge}.hip.
 void launch_mf_f32(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);
 void launch_mf_f16(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);

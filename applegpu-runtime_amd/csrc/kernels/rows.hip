@@ -312,6 +312,67 @@ __global__ void __launch_bounds__(256) row_reduce_wave(int op, const TI* __restr
   if (lane == 0) y[row] = (TO)(q / (float)(cols - correction));
 }
 
+// (value, index) candidate of an argmax: the first occurrence of the maximum,
+// NaN counting as the maximum (the first NaN wins), as torch.argmax on the
+// CPU does.  `bi` < 0 marks an empty candidate.
+__device__ __forceinline__ void argmax_take(float& best, int64_t& bi, float ob, int64_t oi) {
+  bool take;
+  if (oi < 0) take = false;
+  else if (bi < 0) take = true;
+  else if (isnan(ob) != isnan(best)) take = isnan(ob);
+  else if (isnan(ob)) take = oi < bi;
+  else take = ob > best || (ob == best && oi < bi);
+  if (take) { best = ob; bi = oi; }
+}
+
+// Argmax of long rows (e.g. [batch, vocab] logits): one 1024-thread block per
+// row, 16-byte loads over the aligned body of the row (rows of an odd length
+// start unaligned: a scalar head and tail cover the rest).
+template <typename TI>
+__global__ void __launch_bounds__(1024) argmax_row_block(const TI* __restrict__ x, int64_t ldx,
+                                                         int32_t* __restrict__ y, int64_t cols) {
+  constexpr int VE = 16 / sizeof(TI);
+  __shared__ float sb[16];
+  __shared__ int64_t si[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const TI* xr = x + row * ldx;
+  int64_t head = (int64_t)(((16 - ((uintptr_t)xr & 15)) & 15) / sizeof(TI));
+  if (head > cols) head = cols;
+  const int64_t nvec = (cols - head) / VE;
+  const int64_t tail0 = head + nvec * VE;
+  float best = -INFINITY;
+  int64_t bi = -1;
+  if (tid < head) argmax_take(best, bi, to_f(xr[tid]), tid);
+  const uint4* xv = (const uint4*)(xr + head);
+  for (int64_t v = tid; v < nvec; v += 1024) {
+    const uint4 u = xv[v];
+    TI e[VE];
+    __builtin_memcpy(e, &u, 16);
+#pragma unroll
+    for (int k = 0; k < VE; ++k) argmax_take(best, bi, to_f(e[k]), head + v * VE + k);
+  }
+  if (tail0 + tid < cols) argmax_take(best, bi, to_f(xr[tail0 + tid]), tail0 + tid);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(best, m, 64);
+    const int64_t oi = __shfl_xor(bi, m, 64);
+    argmax_take(best, bi, ob, oi);
+  }
+  if (lane == 0) { sb[w] = best; si[w] = bi; }
+  __syncthreads();
+  if (w != 0) return;
+  best = lane < 16 ? sb[lane] : -INFINITY;
+  bi = lane < 16 ? si[lane] : -1;
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(best, m, 64);
+    const int64_t oi = __shfl_xor(bi, m, 64);
+    argmax_take(best, bi, ob, oi);
+  }
+  if (lane == 0) y[row] = (int32_t)(bi < 0 ? 0 : bi);
+}
+
 // Integer sums stay exact in 64-bit.
 template <typename TI, typename TO>
 __global__ void __launch_bounds__(256) row_sum_int(const TI* __restrict__ x, int64_t ldx, TO* __restrict__ y,
@@ -591,12 +652,16 @@ void row_reduce(int op, DType in, DType out, const void* x, int64_t ldx, void* y
   if (rows == 0) return;
   if (op == kRArgmax) {
     if (out != DType::I32) fail("argmax output must be int32");
+    if (rows > 0x7fffffffLL) fail("argmax: too many rows");
     AGPU_ALL_SWITCH(in, {
-      if constexpr (!std::is_same<T, int64_t>::value)
+      if constexpr (std::is_same<T, int64_t>::value)
+        fail("argmax over int64 is not supported");
+      else if (cols >= 4096)
+        hipLaunchKernelGGL((argmax_row_block<T>), dim3((unsigned)rows), dim3(1024), 0, s, (const T*)x, ldx,
+                           (int32_t*)y, cols);
+      else
         hipLaunchKernelGGL((row_reduce_wave<T, int32_t>), dim3(rows_grid(rows)), dim3(256), 0, s, op,
                            (const T*)x, ldx, (int32_t*)y, rows, cols, correction);
-      else
-        fail("argmax over int64 is not supported");
     });
   } else if (dtype_is_float(in)) {
     if (out != in) fail("row reduction output dtype must match input");

@@ -87,9 +87,22 @@ def main():
     ap.add_argument("--suite", action="store_true",
                     help="instead of the headline line, print one JSON line per hot-path kernel "
                          "(cache-busting working sets, roofline fractions)")
+    ap.add_argument("--only", default="",
+                    help="with --suite: run only the sections whose name contains this text "
+                         "(rows, c5, c4, decode)")
+    ap.add_argument("--c4", action="store_true",
+                    help="instead of the headline line, run config C4 (GPT-2 large fp16 prefill + greedy "
+                         "decode over a KV cache) and print its JSON line")
+    ap.add_argument("--c4-steps", type=int, default=C4_STEPS)
+    ap.add_argument("--c4-reps", type=int, default=3)
+    ap.add_argument("--c4-eager", action="store_true",
+                    help="C4 with op-by-op launches instead of graph replays (same kernels; for kernel traces)")
     args = ap.parse_args()
     if args.suite:
-        kernel_suite()
+        kernel_suite(args.only)
+        return
+    if args.c4:
+        c4_generate(args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -246,7 +259,7 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def kernel_suite():
+def kernel_suite(only=""):
     """One JSON line per HBM-bound hot-path kernel and for the C4/C5 shapes.
 
     Inputs rotate over enough buffers that every launch reads data not in
@@ -284,6 +297,21 @@ def kernel_suite():
     def randn(shape, dtype=np.float32, scale=1.0):
         return E.from_numpy((rng.standard_normal(shape, dtype=np.float32) * np.float32(scale)).astype(dtype))
 
+    def want(section):
+        return not only or only in section
+
+    if want("rows"):
+        rows_section(timed, line, randn)
+    if want("c5"):
+        c5_section(timed, line, randn)
+    if want("c4"):
+        c4_section(timed, line, randn)
+    if want("decode"):
+        decode_section(timed, line, randn)
+
+
+def rows_section(timed, line, randn):
+    from applegpu_runtime import eager as E
     # row kernels at [262144, 768] fp32: 805 MB per read, two inputs rotate
     R, C = 262144, 768
     xs = [randn((R, C)) for _ in range(2)]
@@ -303,6 +331,9 @@ def kernel_suite():
     line("add", [R, C], 3 * R * C * 4, ms)
     del xs
 
+
+def c5_section(timed, line, randn):
+    from applegpu_runtime import eager as E
     # C5: per-row int8 quantize / dequantize of W [8192, 8192] fp32, three rotating inputs
     N = 8192
     ws = [randn((N, N), scale=0.02) for _ in range(3)]
@@ -322,6 +353,9 @@ def kernel_suite():
          FP32_MFMA_PEAK_TFLOPS)
     del q, sc, deq, X
 
+
+def c4_section(timed, line, randn):
+    from applegpu_runtime import eager as E
     # C4 shapes, fp16: prefill GEMMs at 8 x 512 tokens and causal attention
     M, d = 4096, 1280
     a16 = [randn((M, d), np.float16)]
@@ -338,6 +372,234 @@ def kernel_suite():
     q1 = randn((BH, 1, hd), np.float16)
     ms, _ = timed(lambda k: E.op("attention", [q1, k, kc[1]]), [kc[0]], 20)
     line("attention decode f16 (q_len 1, ctx 640)", [BH, 640, hd], 2 * (2 * BH * 640 * hd + 2 * BH * hd), ms)
+
+
+def decode_section(timed, line, randn):
+    """C4 decode-step shapes: 8 token rows against GPT-2 large weights (fp16,
+    stored k-major as the fp16 model keeps them), weights rotating over more
+    than the 256 MB Infinity Cache; each shape through the skinny kernel and
+    through the MFMA tiles."""
+    import ctypes
+    from applegpu_runtime import eager as E
+    from applegpu_runtime._native import lib
+    M, d, V = 8, 1280, 50257
+    for name, K, N, bk in [("qkv", d, 3 * d, True), ("proj", d, d, True), ("fc", d, 4 * d, True),
+                           ("fc2", 4 * d, d, True), ("lm_head", d, V, True)]:
+        copies = max(2, int(320e6 // (K * N * 2)) + 1)
+        ws = [randn((N, K) if bk else (K, N), np.float16, 0.02) for _ in range(copies)]
+        x = randn((M, K), np.float16)
+        for skinny in (1, 0):
+            prev = lib.applegpu_ffi_gemm_skinny(skinny)
+            plan = ctypes.create_string_buffer(96)
+            lib.applegpu_ffi_gemm_plan(M, N, K, 1, 1, True, bk, plan, 96)
+            ms, _ = timed(lambda w: E.matmul_ex(x, w, False, bk), ws, 4 * copies)
+            lib.applegpu_ffi_gemm_skinny(prev)
+            line(f"gemm_decode {name} f16 M={M} ({plan.value.decode()})", [M, K, N], 2 * (K * N + M * K + M * N),
+                 ms, 2.0 * M * N * K, BF16_MFMA_PEAK_TFLOPS)
+        del ws
+
+
+C4_B, C4_T, C4_STEPS = 8, 512, 128
+
+
+def c4_work(cfg, B, T, n):
+    """Algorithmic work of config C4: prefill FLOPs (full-square attention
+    count), and per decode step s (context T+1+s) FLOPs and HBM bytes (every
+    fp16 weight read once, plus the K/V cache rows attended to)."""
+    d, V, L, H = cfg["n_embd"], cfg["vocab_size"], cfg["n_layer"], cfg["n_head"]
+    hd = d // H
+    P = L * (d * 3 * d + d * d + 2 * d * 4 * d)
+    Pl = V * d
+    prefill = 2 * B * T * (P + Pl) + L * B * H * 2 * (2 * T * T * hd)
+    flop = byts = 0
+    for s in range(n):
+        ctx = T + 1 + s
+        flop += 2 * B * (P + Pl) + L * B * H * 2 * (2 * ctx * hd)
+        byts += 2 * (P + Pl) + L * 2 * B * H * ctx * hd * 2
+    return prefill, flop, byts
+
+
+def c4_generate(args):
+    """Config C4 end to end: GPT-2 large, fp16 weights and activations, random
+    N(0,0.02) init (drawn in fp32, rounded to fp16), 8 prompts of 512 random
+    ids, prefill then 128 greedy decode steps over a preallocated KV cache.
+    The prefill and one decode step are each captured once as HIP graphs; a
+    generation is one prefill replay and 128 decode replays (positions, the
+    cache append and the argmax stay on the device).  Prints one JSON line."""
+    import applegpu_runtime as gpu
+    from applegpu_runtime._native import lib
+    from applegpu_runtime.models import gpt2 as G
+
+    gpu.init_backend()
+    cfg = G.GPT2_CONFIGS["gpt2-large"]
+    B, T, n = C4_B, C4_T, args.c4_steps
+    wnp = G.random_weights(cfg, seed=42)
+    model = G.load_model(wnp, cfg, dtype="float16")
+    ids = np.random.default_rng(42).integers(0, cfg["vocab_size"], (B, T)).astype(np.int32)
+    ids_dev = gpu.from_numpy(ids)
+    pos_dev = gpu.from_numpy(np.tile(np.arange(T, dtype=np.int32), B))
+    cache = G.KVCache(cfg, B, T + n, "float16")
+    zeros_b = gpu.from_numpy(np.zeros(B, np.int32))
+    t_b = gpu.from_numpy(np.full(B, T, np.int32))
+    tokens = gpu.zeros([B], "int32")
+    out = gpu.zeros([n + 1, B], "int32")
+    print(f"c4: model and cache resident ({cache.nbytes() / 1e9:.2f} GB cache)", file=sys.stderr, flush=True)
+
+    def prefill():
+        gpu.blit_copy(zeros_b, cache.pos)
+        lg, nxt = G.gpt2_prefill(model, ids_dev, cache, positions=pos_dev)
+        gpu.blit_copy(nxt, tokens)
+        gpu.blit_copy(t_b, cache.pos)
+        return lg
+
+    def step():
+        lg, nx, lens = G.gpt2_decode_step(model, tokens, cache)
+        gpu.blit_copy(nx, tokens)
+        gpu.blit_copy(lens, cache.pos)
+        return lg
+
+    # eager (op-by-op) timings for comparison: one prefill, a few steps
+    lib.applegpu_ffi_synchronize()
+    t0 = time.perf_counter()
+    prefill().eval()
+    lib.applegpu_ffi_synchronize()
+    prefill_eager_ms = 1e3 * (time.perf_counter() - t0)
+    n_eager = min(8, n)
+    t0 = time.perf_counter()
+    for _ in range(n_eager):
+        step().eval()
+    lib.applegpu_ffi_synchronize()
+    step_eager_ms = 1e3 * (time.perf_counter() - t0) / n_eager
+
+    if args.c4_eager:
+        # the same kernels issued op by op (for kernel traces of the step)
+        g_pre = g_step = None
+        run_pre = lambda: prefill().eval()  # noqa: E731
+        run_step = lambda: step().eval()  # noqa: E731
+    else:
+        g_pre = gpu.capture(prefill)
+        g_step = gpu.capture(step)
+        run_pre, run_step = g_pre.replay, g_step.replay
+    slots = [gpu.slice(out, 0, s, s + 1) for s in range(n + 1)]
+
+    def generation():
+        run_pre()
+        gpu.blit_copy(tokens, slots[0])
+        for s in range(n):
+            run_step()
+            gpu.blit_copy(tokens, slots[s + 1])
+
+    for _ in range(args.warmup if args.warmup > 0 else 1):
+        generation()
+    lib.applegpu_ffi_synchronize()
+    reps = max(1, args.c4_reps)
+    pre_ms = dec_ms = 0.0
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        lib.applegpu_ffi_event_record(0)
+        run_pre()
+        gpu.blit_copy(tokens, slots[0])
+        lib.applegpu_ffi_event_record(1)
+        for s in range(n):
+            run_step()
+            gpu.blit_copy(tokens, slots[s + 1])
+        lib.applegpu_ffi_event_record(2)
+        pre_ms += lib.applegpu_ffi_event_elapsed_ms(0, 1)
+        dec_ms += lib.applegpu_ffi_event_elapsed_ms(1, 2)
+    lib.applegpu_ffi_synchronize()
+    wall_ms = 1e3 * (time.perf_counter() - t0) / reps
+    pre_ms /= reps
+    dec_ms /= reps
+    toks = out.to_numpy().T
+    if not ((toks >= 0) & (toks < cfg["vocab_size"])).all():
+        raise RuntimeError("generated ids out of range")
+
+    pre_flop, dec_flop, dec_bytes = c4_work(cfg, B, T, n)
+    step_ms = dec_ms / n
+    total_ms = pre_ms + dec_ms
+    tok_s = B * (n + 1) / (total_ms * 1e-3)
+    dec_gbs = dec_bytes / n / (step_ms * 1e-3) / 1e9
+    result = {
+        "metric": "C4 GPT-2 large fp16 greedy generation, tokens/s (8 prompts x 512 + 128 decode steps), 1 MI355X",
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"C4 GPT-2 large (36x1280, 20 heads, vocab 50257) fp16, random N(0,0.02) weights, "
+                        f"batch {B} prompts of {T} random ids, prefill + {n} greedy decode steps over a "
+                        f"preallocated KV cache; prefill and decode step each replayed as captured HIP graphs",
+            "prefill_ms": round(pre_ms, 3),
+            "decode_ms_total": round(dec_ms, 3),
+            "decode_ms_per_step": round(step_ms, 4),
+            "generation_ms": round(total_ms, 3),
+            "generation_wall_ms": round(wall_ms, 3),
+            "decode_tokens_per_s": round(B * n / (dec_ms * 1e-3), 1),
+            "prefill_tflops": round(pre_flop / (pre_ms * 1e-3) / 1e12, 1),
+            "prefill_mfma_frac": round(pre_flop / (pre_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+            "prefill_eager_ms": round(prefill_eager_ms, 3),
+            "decode_step_eager_ms": round(step_eager_ms, 4),
+            "kv_cache_gb": round(cache.nbytes() / 1e9, 3),
+            "launch_mode": "op-by-op" if args.c4_eager else "graph replay",
+            "reps": reps,
+        },
+        "roofline": {
+            "kernel": "whole decode step (all kernels of one graph replay)",
+            "bound": "hbm",
+            "achieved": round(dec_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_step_avg": int(dec_bytes / n),
+            "flop_per_step_avg": int(dec_flop / n),
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = c4_cpu_baseline(wnp, cfg, ids, args.cpu_sample_s)
+    if g_pre is not None:
+        g_pre.destroy()
+        g_step.destroy()
+    print(json.dumps(result), flush=True)
+
+
+def c4_cpu_baseline(wnp, cfg, ids, budget_s):
+    """torch CPU eager generation on the fp16-rounded weights in fp32: one
+    prefill of the same 8 x 512 prompts, then decode steps until ~budget_s;
+    tokens/s projected to the same prefill + 128 steps."""
+    import torch
+    from oracle.torch_cpu import TorchGPT2Decoder
+    w16 = {k: v.astype(np.float16).astype(np.float32) for k, v in wnp.items()}
+    dec = TorchGPT2Decoder(w16, cfg)
+    del w16
+    B, T = ids.shape
+    t0 = time.perf_counter()
+    lg = dec.prefill(ids, T + C4_STEPS)
+    pre_s = time.perf_counter() - t0
+    tok = lg[:, -1].argmax(-1)
+    k = 0
+    t1 = time.perf_counter()
+    while k < 2 or (time.perf_counter() - t0 < budget_s and k < C4_STEPS):
+        tok = dec.decode(tok).argmax(-1)
+        k += 1
+    step_s = (time.perf_counter() - t1) / k
+    total = pre_s + C4_STEPS * step_s
+    return {
+        "value": round(B * (C4_STEPS + 1) / total, 2),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"torch {torch.__version__} CPU eager fp32 on fp16-rounded weights: prefill {B}x{T} "
+                  f"{1e3 * pre_s:.0f} ms + {k} decode steps at {1e3 * step_s:.1f} ms/step, projected to "
+                  f"{C4_STEPS} steps; host cpus {os.cpu_count()}",
+    }
 
 
 def cpu_baseline(wnp, params, ids, xnp, ynp, budget_s):

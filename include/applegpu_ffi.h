@@ -227,6 +227,11 @@ uint64_t applegpu_graph_bytes(int64_t handle);
  * 32x32x256, 32x64x256, 64x64x128).  splits: 0 = heuristic, n = split K across n blocks.
  * Returns 0, or -1 for an out-of-range value. */
 int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits);
+/* GEMMs with at most 16 rows of A (decode steps) run a weight-streaming
+ * kernel instead of the MFMA tiles unless this is switched off (enable = 0;
+ * also APPLEGPU_GEMM_SKINNY=0) or a cfg/splits tune is forced.  Returns the
+ * previous setting (1 = on).  No reference counterpart (tuning). */
+int32_t applegpu_ffi_gemm_skinny(int32_t enable);
 /* The plan the GEMM heuristic picks for an M x N x K (batch) problem of the
  * given dtype and operand layouts (a_kcontig: A(m,k) has unit k stride;
  * b_kcontig: B(k,n) has unit k stride), written as text into out. */

@@ -178,6 +178,42 @@ def test_argmax_bit_exact(gpu, fixtures):
     assert one.shape == [1] and one.to_list() == [1]
 
 
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16", "int32", "int8", "uint8"])
+def test_argmax_long_rows_unaligned(gpu, dtype):
+    """Long rows take the block-per-row kernel; rows of odd length start
+    unaligned, so ties and NaNs sit in the scalar head, the 16-byte body and
+    the scalar tail of different rows."""
+    rows, cols = 7, 50257
+    if dtype in ("int8", "uint8"):
+        lo, hi = (-100, 100) if dtype == "int8" else (0, 200)
+        x = RNG.integers(lo, hi, (rows, cols)).astype(dtype)
+        top = np.array(120 if dtype == "int8" else 250, dtype)
+    elif dtype == "int32":
+        x = RNG.integers(-10**6, 10**6, (rows, cols)).astype(np.int32)
+        top = np.int32(2 * 10**6)
+    else:
+        x = f32(rows, cols)
+        top = np.float32(50.0)
+    # ties: first occurrence must win, wherever the copies fall
+    for r, (a, b) in enumerate([(0, 5), (3, cols - 1), (cols - 2, cols - 1), (1000, 1001), (7, 40000)]):
+        x[r, a] = top
+        x[r, b] = top
+    if dtype in ("float32", "float16", "bfloat16"):
+        x[5, 9] = np.nan         # NaN beats a larger value later on
+        x[5, 30000] = 99.0
+        x[6, cols - 1] = np.nan  # NaN in the tail
+        x[6, 2] = np.nan         # ... but the first NaN wins
+    t = gpu.from_numpy(x) if dtype not in ("float16", "bfloat16") else gpu.cast(gpu.from_numpy(x), dtype)
+    ref_in = x if dtype != "bfloat16" else gpu.cast(t, "float32").to_numpy()
+    if dtype == "float16":
+        ref_in = x.astype(np.float16)
+    got = gpu.argmax(t).to_numpy()
+    np.testing.assert_array_equal(got, O.argmax(ref_in))
+    # a row starting at an unaligned offset inside a wider tensor
+    sub = gpu.slice(t, 1, 3, cols)
+    np.testing.assert_array_equal(gpu.argmax(sub).to_numpy(), O.argmax(np.asarray(ref_in)[:, 3:]))
+
+
 def test_embedding_gather_index_select_bit_exact(gpu, fixtures):
     got = gpu.embedding(gpu.from_numpy(fixtures["emb_w"]), gpu.from_numpy(fixtures["emb_idx"])).to_numpy()
     np.testing.assert_array_equal(got, fixtures["emb_y"])

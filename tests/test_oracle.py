@@ -236,6 +236,29 @@ def test_torch_cpu_gpt2_matches_oracle():
                                rtol=1e-4, atol=1e-4)
 
 
+def test_torch_cpu_kv_decoder_matches_full_recompute():
+    """Batched prefill + KV-cache decode on the CPU (the C4 baseline) gives the
+    logits of a full causal forward over prompt + generated tokens, per
+    sequence, from the independent numpy oracle."""
+    from oracle.torch_cpu import TorchGPT2Decoder
+    cfg = _tiny_cfg()
+    w = _tiny_weights(cfg)
+    B, T, n = 3, 7, 4
+    ids = np.random.default_rng(0).integers(0, cfg["vocab_size"], (B, T))
+    dec = TorchGPT2Decoder(w, cfg)
+    lg = dec.prefill(ids, T + n)
+    steps = [lg[:, -1].numpy()]
+    toks = [steps[0].argmax(-1)]
+    for _ in range(n):
+        steps.append(dec.decode(toks[-1]).numpy())
+        toks.append(steps[-1].argmax(-1))
+    toks = np.stack(toks, 1)
+    for b in range(B):
+        ref, _ = M.gpt2_forward_np(w, cfg, np.concatenate([ids[b], toks[b, :-1]]))
+        np.testing.assert_allclose(np.stack([s[b] for s in steps]), ref[T - 1:], rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(lg[b].numpy(), ref[:T], rtol=1e-4, atol=1e-4)
+
+
 def test_oracle_catches_planted_mistakes():
     """The checks above fail on the typical slips (planted in copies, on the CPU)."""
     x = np.random.default_rng(0).standard_normal((4, 9)).astype(np.float32)
