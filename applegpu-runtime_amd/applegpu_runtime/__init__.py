@@ -503,6 +503,18 @@ def dequantize_per_row(q, scale, dtype="float32"):
     return _op(b"dequantize_per_row", [_t(q), _t(scale)], i=(DTYPE_CODES[canon_dtype(dtype)],))
 
 
+def pack_weight(wt):
+    """Decode-step weights: wt [out, in] (fp16/bf16, torch Linear layout)
+    rearranged so the skinny GEMM's loads are contiguous.  Use with
+    matmul_packed."""
+    return _op(b"pack_weight", [_t(wt)])
+
+
+def matmul_packed(x, packed, out_features):
+    """x [rows <= 16, in] @ wt^T for packed = pack_weight(wt), wt [out, in]."""
+    return _op(b"matmul_packed", [_t(x), _t(packed)], i=(int(out_features),))
+
+
 def linear_int8(x, q, scale):
     """x @ (q * scale[:, None])^T with the dequantisation fused into the GEMM."""
     return _op(b"linear_int8", [_t(x), _t(q), _t(scale)])
@@ -523,6 +535,13 @@ def kv_write(cache, rows, pos):
     replayed with advancing positions).  Rows that would land outside the
     cache are not written."""
     if lib.applegpu_kv_write(_t(cache)._id, _t(rows)._id, _t(pos)._id) != 0:
+        raise ValueError(ffi_error())
+
+
+def kv_write_pair(k_cache, v_cache, k_rows, v_rows, pos):
+    """kv_write of the K and the V rows of one layer in a single launch."""
+    if lib.applegpu_kv_write_pair(_t(k_cache)._id, _t(v_cache)._id, _t(k_rows)._id, _t(v_rows)._id,
+                                  _t(pos)._id) != 0:
         raise ValueError(ffi_error())
 
 

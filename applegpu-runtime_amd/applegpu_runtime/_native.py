@@ -102,6 +102,7 @@ _SIGS = {
     "applegpu_ffi_graph_stats": (c_int32, [u64p]),
     "applegpu_ffi_inject_alloc_failures": (None, [c_int32]),
     "applegpu_kv_write": (c_int32, [c_uint64, c_uint64, c_uint64]),
+    "applegpu_kv_write_pair": (c_int32, [c_uint64, c_uint64, c_uint64, c_uint64, c_uint64]),
     "applegpu_capture_begin": (c_int32, []),
     "applegpu_capture_end": (c_int64, []),
     "applegpu_capture_abort": (c_int32, []),

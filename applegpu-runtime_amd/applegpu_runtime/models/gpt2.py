@@ -67,17 +67,25 @@ def random_weights(cfg: dict, seed: int = 42, std: float = 0.02) -> dict:
 CONV1D = (".attn.c_attn.weight", ".attn.c_proj.weight", ".mlp.c_fc.weight", ".mlp.c_proj.weight")
 
 
-def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None) -> dict:
+def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None, packed=None) -> dict:
     """Upload numpy weights; returns the model dict the forward pass takes.
 
     kmajor (default: on for fp16/bf16) stores the Conv1D projection weights
     transposed, [out, in], contiguous along the reduction: the layout the
     decode-step GEMM streams with one 16-byte load per MFMA operand.  The
     forward multiplies by a transposed view of them, so the arithmetic is
-    the recipe's x @ W either way."""
+    the recipe's x @ W either way.  packed (default: on with kmajor) also
+    keeps every projection and the tied LM head in the skinny GEMM's packed
+    layout (gpu.pack_weight) for calls with at most 16 token rows: one more
+    copy of the weights (HBM is plentiful), read with contiguous 1 KB wave
+    loads during decode."""
     gpu.init_backend()
     if kmajor is None:
         kmajor = dtype != "float32"
+    if packed is None:
+        packed = kmajor
+    if packed and (dtype == "float32" or not kmajor):
+        raise ValueError("packed decode weights need fp16/bf16 k-major weights")
     w = {}
     for k, v in np_weights.items():
         a = np.asarray(v, dtype=np.float32)
@@ -88,12 +96,25 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None)
             t = gpu.cast(t, dtype)
             t.eval()
         w[k] = t
-    return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor)}
+    pk = {}
+    if packed:
+        for k, t in w.items():
+            if k.endswith(CONV1D) or k == "transformer.wte.weight":
+                p = gpu.pack_weight(t)
+                p.eval()
+                pk[k] = (p, t.shape[0])
+    return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor), "packed": pk}
 
 
-def _mm(model: dict, x, name: str):
-    """x @ W for a Conv1D weight (HF layout [in, out]), whichever way it is stored."""
+def _mm(model: dict, x, name: str, rows: int = None):
+    """x @ W for a Conv1D weight (HF layout [in, out]) or x @ wte^T, whichever
+    way the weight is stored; calls with at most 16 rows use the packed copy."""
+    pk = model.get("packed", {}).get(name)
+    if pk is not None and rows is not None and rows <= 16:
+        return gpu.matmul_packed(x, pk[0], pk[1])
     w = model["weights"][name]
+    if name == "transformer.wte.weight":
+        return x @ gpu.transpose(w)
     return x @ (gpu.transpose(w) if model.get("kmajor") else w)
 
 
@@ -198,8 +219,11 @@ def _block(model, i, x, B, T, attend):
     H, d = cfg["n_head"], cfg["n_embd"]
     hd = d // H
     p = f"transformer.h.{i}"
-    h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
-    qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
+    # layer-norm outputs stay anonymous temporaries: the graph can then fold
+    # each layer_norm into the projection that consumes it
+    R = B * T
+    qkv = gpu.add_bias(_mm(model, gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"]),
+                           f"{p}.attn.c_attn.weight", R), w[f"{p}.attn.c_attn.bias"])
 
     def heads(lo):
         part = gpu.slice(qkv, 1, lo, lo + d)
@@ -207,16 +231,16 @@ def _block(model, i, x, B, T, attend):
 
     a = attend(i, heads(0), heads(d), heads(2 * d))
     a = gpu.reshape(gpu.transpose_dims(a, 1, 2), [B * T, d])
-    x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
-    h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
-    f = gpu.gelu(gpu.add_bias(_mm(model, h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
-    return x + gpu.add_bias(_mm(model, f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
+    x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight", R), w[f"{p}.attn.c_proj.bias"])
+    f = gpu.gelu(gpu.add_bias(_mm(model, gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"]),
+                                  f"{p}.mlp.c_fc.weight", R), w[f"{p}.mlp.c_fc.bias"]))
+    return x + gpu.add_bias(_mm(model, f, f"{p}.mlp.c_proj.weight", R), w[f"{p}.mlp.c_proj.bias"])
 
 
-def _head(model, x):
+def _head(model, x, rows):
     w = model["weights"]
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
-    return x @ gpu.transpose(w["transformer.wte.weight"])
+    return _mm(model, x, "transformer.wte.weight", rows)
 
 
 def gpt2_prefill(model: dict, ids, cache: KVCache, positions=None):
@@ -250,13 +274,12 @@ def gpt2_prefill(model: dict, ids, cache: KVCache, positions=None):
     x = gpu.embedding(w["transformer.wte.weight"], idx) + gpu.embedding(w["transformer.wpe.weight"], positions)
 
     def attend(i, q, k, v):
-        gpu.kv_write(cache.k[i], k, cache.pos)
-        gpu.kv_write(cache.v[i], v, cache.pos)
+        gpu.kv_write_pair(cache.k[i], cache.v[i], k, v, cache.pos)
         return gpu.attention_causal(q, k, v)
 
     for i in range(cfg["n_layer"]):
         x = _block(model, i, x, B, T, attend)
-    logits = _head(model, x)
+    logits = _head(model, x, B * T)
     V = logits.shape[-1]
     last = gpu.reshape(gpu.slice(gpu.reshape(logits, [B, T, V]), 1, T - 1, T), [B, V])
     return logits, gpu.argmax(last)
@@ -281,13 +304,12 @@ def gpt2_decode_step(model: dict, tokens, cache: KVCache):
     lens = cache.pos + cache.one
 
     def attend(i, q, k, v):
-        gpu.kv_write(cache.k[i], k, cache.pos)
-        gpu.kv_write(cache.v[i], v, cache.pos)
+        gpu.kv_write_pair(cache.k[i], cache.v[i], k, v, cache.pos)
         return gpu.decode_attention(q, cache.k[i], cache.v[i], lens)
 
     for i in range(cfg["n_layer"]):
         x = _block(model, i, x, B, 1, attend)
-    logits = _head(model, x)
+    logits = _head(model, x, B)
     return logits, gpu.argmax(logits), lens
 
 

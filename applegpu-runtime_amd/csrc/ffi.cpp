@@ -262,20 +262,35 @@ int32_t applegpu_ffi_copy(uint64_t src_id, uint64_t dst_id) {
   });
 }
 
+static TensorP kv_operand(uint64_t id) {
+  TensorP t = rt().lookup(id);
+  if (t->pending()) eval(t);
+  return t;
+}
+
+static TensorP kv_cache_operand(uint64_t id) {
+  TensorP c = kv_operand(id);
+  if (!c->buf) fail("kv_write: cache has no storage");
+  if (c->extent_bytes() + (size_t)c->offset > c->buf->requested) fail("kv_write: cache view out of bounds");
+  return c;
+}
+
 int32_t applegpu_kv_write(uint64_t cache_id, uint64_t rows_id, uint64_t pos_id) {
   return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
     // In-place KV append at device-resident positions; replaces the
     // reference's per-step concat of the whole cache
     // (python/applegpu_runtime/models/gpt2.py:122-126).
-    TensorP rows = rt().lookup(rows_id);
-    if (rows->pending()) eval(rows);
-    TensorP pos = rt().lookup(pos_id);
-    if (pos->pending()) eval(pos);
-    TensorP cache = rt().lookup(cache_id);
-    if (cache->pending()) eval(cache);
-    if (!cache->buf) fail("kv_write: cache has no storage");
-    if (cache->extent_bytes() + (size_t)cache->offset > cache->buf->requested) fail("kv_write: cache view out of bounds");
-    ops::kv_write(cache, rows, pos);
+    TensorP rows = kv_operand(rows_id), pos = kv_operand(pos_id);
+    ops::kv_write(kv_cache_operand(cache_id), rows, pos);
+    return 0;
+  });
+}
+
+int32_t applegpu_kv_write_pair(uint64_t k_cache_id, uint64_t v_cache_id, uint64_t k_rows_id, uint64_t v_rows_id,
+                               uint64_t pos_id) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    TensorP kr = kv_operand(k_rows_id), vr = kv_operand(v_rows_id), pos = kv_operand(pos_id);
+    ops::kv_write(kv_cache_operand(k_cache_id), kr, pos, kv_cache_operand(v_cache_id), vr);
     return 0;
   });
 }

@@ -30,7 +30,7 @@ enum Op : int {
   OP_MATMUL, OP_MATMUL_EX, OP_LINEAR, OP_ADD_BIAS, OP_ATTENTION, OP_ATTENTION_CAUSAL,
   OP_WHERE, OP_MASKED_FILL, OP_TRIU, OP_TRIL,
   OP_QUANTIZE_PER_ROW, OP_DEQUANTIZE_PER_ROW, OP_LINEAR_INT8, OP_CONTIGUOUS, OP_FULL,
-  OP_DECODE_ATTENTION,
+  OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
   OP_COUNT
 };
 
@@ -47,7 +47,7 @@ static const char* kNames[OP_COUNT] = {
     "matmul", "matmul_ex", "linear", "add_bias", "attention", "attention_causal",
     "where", "masked_fill", "triu", "tril",
     "quantize_per_row", "dequantize_per_row", "linear_int8", "contiguous", "full",
-    "decode_attention",
+    "decode_attention", "pack_weight", "matmul_packed",
 };
 
 int op_code(const char* name) {
@@ -193,6 +193,8 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       return {dequantize_per_row(in[0], in[1], iv.empty() ? DType::F32 : dt_param(iv[0]))};
     case OP_LINEAR_INT8: need(in, 3, code); return {linear_int8(in[0], in[1], in[2])};
     case OP_DECODE_ATTENTION: need(in, 4, code); return {decode_attention(in[0], in[1], in[2], in[3])};
+    case OP_PACK_WEIGHT: need(in, 1, code); return {pack_weight(in[0])};
+    case OP_MATMUL_PACKED: need(in, 2, code); return {matmul_packed(in[0], in[1], ip(iv, 0, code))};
     case OP_CONTIGUOUS: {
       need(in, 1, code);
       TensorP c = contiguous(in[0]);
@@ -269,6 +271,9 @@ struct Group {
   int act = k::kActNone;
   TensorP residual;
   bool has_bias = false;
+  TensorP ln_gamma, ln_beta;  // a = layer_norm(a) folded into the GEMM
+  float ln_eps = 1e-5f;
+  int64_t packed_n = 0;       // b is packed decode weights of this many columns
 };
 
 bool is_single_internal_use(const TensorP& t, const std::unordered_map<Tensor*, int>& uses) {
@@ -341,11 +346,23 @@ void eval(const TensorP& root) {
     Node* n = t->node.get();
     if (n->code == OP_ADD_BIAS && t->ndim == 2) {
       const TensorP& x = n->in[0];
-      if (x->pending() && x->node->code == OP_MATMUL && x->ndim == 2 && is_single_internal_use(x, uses) &&
-          n->in[1]->ndim == 1) {
+      if (x->pending() && (x->node->code == OP_MATMUL || x->node->code == OP_MATMUL_PACKED) && x->ndim == 2 &&
+          is_single_internal_use(x, uses) && n->in[1]->ndim == 1) {
         Group g;
         g.mm = x.get();
-        g.a = x->node->in[0];
+        if (x->node->code == OP_MATMUL_PACKED) g.packed_n = x->node->iv[0];
+        // layer_norm -> matmul: the GEMM normalises its A rows itself when
+        // its kernel can (ops::matmul falls back to an explicit layer_norm)
+        const TensorP& la = x->node->in[0];
+        if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 && is_single_internal_use(la, uses)) {
+          g.ln_gamma = la->node->in[1];
+          g.ln_beta = la->node->in[2];
+          g.ln_eps = la->node->f.empty() ? 1e-5f : (float)la->node->f[0];
+          absorbed.insert(la.get());
+          g.a = la->node->in[0];
+        } else {
+          g.a = la;
+        }
         g.b = x->node->in[1];
         g.bias = n->in[1];
         g.has_bias = true;
@@ -397,7 +414,10 @@ void eval(const TensorP& root) {
       e.bias = g.bias;
       e.act = g.act;
       e.residual = g.residual;
-      res = {ops::matmul(g.a, g.b, false, false, &e)};
+      e.ln_gamma = g.ln_gamma;
+      e.ln_beta = g.ln_beta;
+      e.ln_eps = g.ln_eps;
+      res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e) : ops::matmul(g.a, g.b, false, false, &e)};
       g_stats.fused_gemm_epilogues++;
       g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0);
     } else if (n->code < 0) {

@@ -113,7 +113,24 @@ struct Gemm {
   // int8 B with per-n fp32 scales (dequant fused into the operand load)
   const float* b_scale = nullptr;
   DType b_dt = DType::F32;
+  // A rows layer-normalised on load (gamma, beta [K] of dtype dt; skinny
+  // kernel only, see gemm_skinny_ln_ok)
+  const void* ln_gamma = nullptr;
+  const void* ln_beta = nullptr;
+  float ln_eps = 1e-5f;
+  // B in the skinny kernel's packed layout (pack_weights), 16-bit, M <= 16
+  bool b_packed = false;
 };
+// Whether the skinny decode kernel takes this problem, and whether it can
+// also normalise the A rows (layer norm over K, K <= 4096) while loading them.
+bool gemm_is_skinny(const Gemm& g);
+bool gemm_skinny_ln_ok(const Gemm& g);
+// Packed decode weights: out[t][s][l][e] = W^T[16t + l%16][32s + 8(l/16) + e]
+// for W^T [N][K] read through strides (s_n, s_k), zero-padded to whole
+// 16-column tiles and 32-deep steps (packed_weight_elems elements).
+int64_t packed_weight_elems(int64_t N, int64_t K);
+void pack_weights(DType dt, const void* w, int64_t s_n, int64_t s_k, int64_t N, int64_t K, void* out,
+                  hipStream_t s);
 // Workspace bytes the launch needs (split-K partials); 0 when none.
 size_t gemm_workspace_bytes(const Gemm& g);
 void gemm(const Gemm& g, void* workspace, hipStream_t s);
@@ -168,12 +185,17 @@ int decode_attention_splits(const DecodeAttn& a, int64_t* chunk);
 size_t decode_attention_ws_bytes(const DecodeAttn& a);
 void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s);
 // cache[b, h, pos[b] + t, :] = src[b, h, t, :] for t < T (rows that would
-// land at or past Tmax are dropped); pos is int32 [B] in device memory.
+// land at or past Tmax are dropped); pos is int32 [B] in device memory.  A
+// second (cache2, src2) pair of the same shape (the V cache beside the K
+// cache) is written by the same launch.  Strides: (batch, head, token), unit
+// stride along D.
 struct KvWrite {
   DType dt = DType::F16;
   int64_t B = 1, H = 1, T = 0, D = 0, Tmax = 0;
-  void* cache = nullptr; int64_t c_sb = 0, c_sh = 0, c_st = 0;      // unit d stride
-  const void* src = nullptr; int64_t x_sb = 0, x_sh = 0, x_st = 0;  // unit d stride
+  void* cache = nullptr; int64_t cs[3] = {0, 0, 0};
+  const void* src = nullptr; int64_t xs[3] = {0, 0, 0};
+  void* cache2 = nullptr; int64_t c2s[3] = {0, 0, 0};
+  const void* src2 = nullptr; int64_t x2s[3] = {0, 0, 0};
   const int32_t* pos = nullptr;
 };
 void kv_write(const KvWrite& a, hipStream_t s);

@@ -12,14 +12,15 @@
 // depends on a host-side length, so the step can be recorded once as a HIP
 // graph and replayed for every token.
 //
-// decode_attention splits each (batch, head, query row) over the key axis
-// (split-KV): block (split s, row) scores keys [s*chunk, (s+1)*chunk) with an
-// online softmax and leaves an unnormalised partial (max, sum, acc[D]); a
-// second kernel merges the partials of a row.  Within a block, D/8 lanes own
-// one key, 8 elements each (one 16-byte load for 16-bit types), so a wave
-// covers 64/(D/8) keys per step and the dot product is log2(D/8) xor
-// shuffles.  A row with no visible key gets zeros (the fused attention kernel
-// uses the same convention).
+// decode_attention: within a block, D/8 lanes own one key, 8 elements each
+// (one 16-byte load for 16-bit types), so a wave covers 64/(D/8) keys per
+// step and the dot product is log2(D/8) xor shuffles; each key group keeps an
+// online softmax (running max, sum and output), and the groups and waves of
+// the block merge their states at the end.  With enough (batch, head, query
+// row) rows for the CUs a 16-wave block owns a whole row; otherwise the key
+// axis is split over blocks (split-KV), each leaving an unnormalised partial
+// (max, sum, acc[D]) that a second kernel merges.  A row with no visible key
+// gets zeros (the fused attention kernel uses the same convention).
 #include "device.hpp"
 
 namespace agpu {
@@ -28,8 +29,13 @@ using namespace dev;
 
 namespace {
 
-constexpr int kDWaves = 4;   // waves per decode block
-constexpr int kDUnroll = 2;  // key steps each wave keeps in flight
+// Two shapes of decode block: with enough (batch, head, query) rows to fill
+// the CUs, one 16-wave block per row covers the whole context (no partials,
+// no merge launch); with few rows, 4-wave blocks split the context and
+// decode_merge combines their partials.
+constexpr int kDRowsWhole = 128;          // rows at which a block takes a whole row
+constexpr int kDWavesWhole = 16, kDUnrollWhole = 4;
+constexpr int kDWavesSplit = 4, kDUnrollSplit = 2;
 
 struct DArgs {
   const void* q; const void* k; const void* v; void* o;
@@ -68,14 +74,27 @@ __device__ __forceinline__ int64_t visible_keys(const DArgs& p, int64_t b, int64
   return vis < 0 ? 0 : (vis > len ? len : vis);
 }
 
-template <typename T, int D, bool VEC>
-__global__ void __launch_bounds__(256) decode_attn(DArgs p) {
+// Merges online-softmax state (om, ol, oa) into (m, l, a).
+__device__ __forceinline__ void merge_state(float& m, float& l, float (&a)[8], float om, float ol,
+                                            const float (&oa)[8]) {
+  const float M = fmaxf(m, om);
+  if (M == -INFINITY) return;  // both empty
+  const float f1 = m == -INFINITY ? 0.f : expf(m - M);
+  const float f2 = om == -INFINITY ? 0.f : expf(om - M);
+  l = l * f1 + ol * f2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = a[e] * f1 + oa[e] * f2;
+  m = M;
+}
+
+// NW waves per block, UN key steps in flight per wave.
+template <typename T, int D, bool VEC, int NW, int UN>
+__global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
   constexpr int LPK = D / 8;           // lanes per key
   constexpr int KPS = 64 / LPK;        // keys per wave step
-  constexpr int NG = kDWaves * KPS;    // key groups per block
-  constexpr int BS = NG * kDUnroll;    // keys per block iteration
-  __shared__ float sm_acc[NG][D];
-  __shared__ float sm_m[NG], sm_l[NG];
+  constexpr int BS = NW * KPS * UN;    // keys per block iteration
+  __shared__ float sm_acc[NW][D];
+  __shared__ float sm_m[NW], sm_l[NW];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane / LPK, sub = lane % LPK;
@@ -101,18 +120,18 @@ __global__ void __launch_bounds__(256) decode_attn(DArgs p) {
   for (int64_t base = j_lo; base < j_hi; base += BS) {
     // all loads of the iteration first (rows clamped into the cache, masked
     // below), then the arithmetic
-    float kx[kDUnroll][8], vx[kDUnroll][8];
-    int64_t jj[kDUnroll];
+    float kx[UN][8], vx[UN][8];
+    int64_t jj[UN];
 #pragma unroll
-    for (int u = 0; u < kDUnroll; ++u) {
-      const int64_t j = base + (int64_t)(u * kDWaves + w) * KPS + g;
+    for (int u = 0; u < UN; ++u) {
+      const int64_t j = base + (int64_t)(u * NW + w) * KPS + g;
       jj[u] = j;
       const int64_t jc = j < p.Tmax ? j : p.Tmax - 1;
       load8<T, VEC>(K + jc * p.k_st, kx[u]);
       load8<T, VEC>(V + jc * p.v_st, vx[u]);
     }
 #pragma unroll
-    for (int u = 0; u < kDUnroll; ++u) {
+    for (int u = 0; u < UN; ++u) {
       float dot = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) dot += q[e] * kx[u][e];
@@ -130,18 +149,31 @@ __global__ void __launch_bounds__(256) decode_attn(DArgs p) {
     }
   }
 
-  const int grp = w * KPS + g;
+  // the wave's KPS key groups meet by xor shuffles over the group bits of
+  // the lane id, then the NW waves through LDS
 #pragma unroll
-  for (int e = 0; e < 8; ++e) sm_acc[grp][sub * 8 + e] = acc[e];
-  if (sub == 0) { sm_m[grp] = m; sm_l[grp] = l; }
+  for (int x = LPK; x < 64; x <<= 1) {
+    const float om = __shfl_xor(m, x, 64), ol = __shfl_xor(l, x, 64);
+    float oa[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) oa[e] = __shfl_xor(acc[e], x, 64);
+    merge_state(m, l, acc, om, ol, oa);
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm_acc[w][sub * 8 + e] = acc[e];
+    if (sub == 0) { sm_m[w] = m; sm_l[w] = l; }
+  }
   __syncthreads();
   if (tid >= D) return;
 
   float M = -INFINITY;
-  for (int x = 0; x < NG; ++x) M = fmaxf(M, sm_m[x]);
+#pragma unroll
+  for (int x = 0; x < NW; ++x) M = fmaxf(M, sm_m[x]);
   float L = 0.f, A = 0.f;
   if (M != -INFINITY) {
-    for (int x = 0; x < NG; ++x) {
+#pragma unroll
+    for (int x = 0; x < NW; ++x) {
       const float mx = sm_m[x];
       const float f = mx == -INFINITY ? 0.f : expf(mx - M);
       L += sm_l[x] * f;
@@ -181,44 +213,70 @@ __global__ void __launch_bounds__(128) decode_merge(DArgs p) {
   O[t] = from_f<T>(L > 0.f ? A / L : 0.f);
 }
 
-// dst rows [pos[b] + t] of the cache = src rows t, as raw elements of E.
+// dst rows [pos[b] + t] of the cache = src rows t, as raw elements of E;
+// blockIdx.y picks one of `pairs` (cache, rows) pairs of the same shape.
 template <typename E>
-__global__ void __launch_bounds__(256) kv_write_kernel(E* __restrict__ c, const E* __restrict__ x,
-                                                       const int32_t* __restrict__ pos, int64_t H, int64_t T,
-                                                       int64_t D, int64_t Tmax, int64_t c_sb, int64_t c_sh,
-                                                       int64_t c_st, int64_t x_sb, int64_t x_sh, int64_t x_st,
-                                                       int64_t n) {
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+struct KvArgs {
+  E* c[2];
+  const E* x[2];
+  int64_t cs[2][3], xs[2][3];  // (batch, head, token) strides in E elements
+  const int32_t* pos;
+  int64_t H, T, D, Tmax, n;
+};
+
+template <typename E>
+__global__ void __launch_bounds__(256) kv_write_kernel(KvArgs<E> a) {
+  const int j = blockIdx.y;
+  E* __restrict__ c = a.c[j];
+  const E* __restrict__ x = a.x[j];
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.n;
        idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t d = idx % D, r = idx / D;
-    const int64_t t = r % T, bh = r / T;
-    const int64_t h = bh % H, b = bh / H;
-    const int64_t dt = (int64_t)pos[b] + t;
-    if (dt < 0 || dt >= Tmax) continue;  // rows past the cache's capacity are dropped
-    c[b * c_sb + h * c_sh + dt * c_st + d] = x[b * x_sb + h * x_sh + t * x_st + d];
+    const int64_t d = idx % a.D, r = idx / a.D;
+    const int64_t t = r % a.T, bh = r / a.T;
+    const int64_t h = bh % a.H, b = bh / a.H;
+    const int64_t dt = (int64_t)a.pos[b] + t;
+    if (dt < 0 || dt >= a.Tmax) continue;  // rows past the cache's capacity are dropped
+    c[b * a.cs[j][0] + h * a.cs[j][1] + dt * a.cs[j][2] + d] = x[b * a.xs[j][0] + h * a.xs[j][1] + t * a.xs[j][2] + d];
   }
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <typename T, int D>
-void launch_decode(const DArgs& p, bool vec, int64_t rows, hipStream_t s) {
+void launch_decode(const DArgs& p, bool vec, int64_t rows, bool whole, hipStream_t s) {
   const dim3 grid((unsigned)p.splits, (unsigned)rows);
-  if (vec) hipLaunchKernelGGL((decode_attn<T, D, true>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((decode_attn<T, D, false>), grid, dim3(256), 0, s, p);
+  constexpr int NWW = kDWavesWhole, UW = kDUnrollWhole, NWS = kDWavesSplit, US = kDUnrollSplit;
+  if (whole) {
+    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW>), grid, dim3(64 * NWW), 0, s, p);
+    else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW>), grid, dim3(64 * NWW), 0, s, p);
+  } else {
+    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWS, US>), grid, dim3(64 * NWS), 0, s, p);
+    else hipLaunchKernelGGL((decode_attn<T, D, false, NWS, US>), grid, dim3(64 * NWS), 0, s, p);
+  }
   if (p.splits > 1) hipLaunchKernelGGL((decode_merge<T, D>), dim3((unsigned)rows), dim3(D), 0, s, p);
 }
 
 template <typename E>
 void launch_kv_write(const KvWrite& a, int64_t vec, hipStream_t s) {
   // vec = elements of the dtype per E
-  const int64_t D = a.D / vec;
-  const int64_t n = a.B * a.H * a.T * D;
-  int64_t g = (n + 255) / 256;
+  KvArgs<E> k{};
+  const int pairs = a.cache2 ? 2 : 1;
+  for (int j = 0; j < pairs; ++j) {
+    k.c[j] = (E*)(j ? a.cache2 : a.cache);
+    k.x[j] = (const E*)(j ? a.src2 : a.src);
+    const int64_t* cs = j ? a.c2s : a.cs;
+    const int64_t* xs = j ? a.x2s : a.xs;
+    for (int i = 0; i < 3; ++i) {
+      k.cs[j][i] = cs[i] / vec;
+      k.xs[j][i] = xs[i] / vec;
+    }
+  }
+  k.pos = a.pos;
+  k.H = a.H; k.T = a.T; k.D = a.D / vec; k.Tmax = a.Tmax;
+  k.n = a.B * a.H * a.T * k.D;
+  int64_t g = (k.n + 255) / 256;
   if (g > 65536) g = 65536;
-  hipLaunchKernelGGL((kv_write_kernel<E>), dim3((unsigned)g), dim3(256), 0, s, (E*)a.cache, (const E*)a.src,
-                     a.pos, a.H, a.T, D, a.Tmax, a.c_sb / vec, a.c_sh / vec, a.c_st / vec, a.x_sb / vec,
-                     a.x_sh / vec, a.x_st / vec, n);
+  hipLaunchKernelGGL((kv_write_kernel<E>), dim3((unsigned)g, (unsigned)pairs), dim3(256), 0, s, k);
 }
 
 }  // namespace
@@ -229,9 +287,13 @@ bool decode_attention_supported(const DecodeAttn& a) {
 }
 
 int decode_attention_splits(const DecodeAttn& a, int64_t* chunk) {
-  // keys per block iteration, as in decode_attn
-  const int64_t bs = (int64_t)kDWaves * (64 / (a.D / 8)) * kDUnroll;
   const int64_t rows = a.B * a.H * a.Tq;
+  if (rows >= kDRowsWhole) {
+    *chunk = a.Tmax;
+    return 1;
+  }
+  // keys per block iteration of the split kernel, as in decode_attn
+  const int64_t bs = (int64_t)kDWavesSplit * (64 / (a.D / 8)) * kDUnrollSplit;
   // aim for >= 2048 blocks over the 256 CUs, with at least one block
   // iteration per split
   int64_t want = rows >= 2048 ? 1 : (2048 + rows - 1) / rows;
@@ -281,9 +343,10 @@ void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s) {
   const bool vec = al(a.q, a.q_sb, a.q_sh, a.q_st) && al(a.k, a.k_sb, a.k_sh, a.k_st) &&
                    al(a.v, a.v_sb, a.v_sh, a.v_st);
   AGPU_FLOAT_SWITCH(a.dt, {
-    if (a.D == 32) launch_decode<T, 32>(p, vec, rows, s);
-    else if (a.D == 64) launch_decode<T, 64>(p, vec, rows, s);
-    else launch_decode<T, 128>(p, vec, rows, s);
+    const bool whole = rows >= kDRowsWhole;
+    if (a.D == 32) launch_decode<T, 32>(p, vec, rows, whole, s);
+    else if (a.D == 64) launch_decode<T, 64>(p, vec, rows, whole, s);
+    else launch_decode<T, 128>(p, vec, rows, whole, s);
   });
   check_launch("decode_attention");
 }
@@ -292,13 +355,21 @@ void kv_write(const KvWrite& a, hipStream_t s) {
   const int64_t n = a.B * a.H * a.T * a.D;
   if (n == 0) return;
   const size_t es = dtype_size(a.dt);
-  // widest element that divides every row and stride
+  // widest element that divides every row and stride of every pair
   auto fits = [&](size_t w) {
     const int64_t v = (int64_t)(w / es);
     if (w < es || w % es) return false;
     auto ok = [&](int64_t x) { return x % v == 0; };
-    return ((uintptr_t)a.cache % w) == 0 && ((uintptr_t)a.src % w) == 0 && ok(a.D) && ok(a.c_sb) &&
-           ok(a.c_sh) && ok(a.c_st) && ok(a.x_sb) && ok(a.x_sh) && ok(a.x_st);
+    bool r = ok(a.D);
+    for (int j = 0; j < (a.cache2 ? 2 : 1); ++j) {
+      const void* c = j ? a.cache2 : a.cache;
+      const void* x = j ? a.src2 : a.src;
+      const int64_t* cs = j ? a.c2s : a.cs;
+      const int64_t* xs = j ? a.x2s : a.xs;
+      r = r && ((uintptr_t)c % w) == 0 && ((uintptr_t)x % w) == 0 && ok(cs[0]) && ok(cs[1]) && ok(cs[2]) &&
+          ok(xs[0]) && ok(xs[1]) && ok(xs[2]);
+    }
+    return r;
   };
   if (fits(16)) launch_kv_write<uint4>(a, (int64_t)(16 / es), s);
   else if (fits(8)) launch_kv_write<uint2>(a, (int64_t)(8 / es), s);

@@ -360,6 +360,9 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   p.tiles_m = (int)((g.M + pl.bm - 1) / pl.bm);
   p.tiles_n = (int)((g.N + pl.bn - 1) / pl.bn);
   p.b_scale = g.b_scale;
+  p.ln_g = g.ln_gamma;
+  p.ln_b = g.ln_beta;
+  p.ln_eps = g.ln_eps;
   const size_t esz = dtype_size(g.dt);
   const int vw = (int)(16 / esz);  // elements per 16-byte vector
   // Vector loads need 16-byte aligned runs along the contiguous axis.
@@ -389,6 +392,8 @@ int cu_count() {
 }
 
 }  // namespace
+
+bool gemm_is_skinny(const Gemm& g) { return skinny_plan(g, cu_count()).use; }
 
 GemmTune& gemm_tune() {
   static GemmTune t = [] {
@@ -435,6 +440,8 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     gemm_skinny(g, sp, make_args(g, one), s);
     return;
   }
+  if (g.ln_gamma) fail("gemm: a layer-norm prologue needs the skinny kernel");
+  if (g.b_packed) fail("gemm: packed weights need the skinny kernel (at most 16 fp16/bf16 rows)");
   Plan pl = make_plan(g, cu_count());
   GArgs p = make_args(g, pl);
   p.ws = (float*)workspace;

@@ -34,6 +34,7 @@ struct GArgs {
   int tiles_m, tiles_n;
   bool vec_a, vec_b;
   const float* b_scale;
+  const void* ln_g; const void* ln_b; float ln_eps;
 };
 
 template <typename T>

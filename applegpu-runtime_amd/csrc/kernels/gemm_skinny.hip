@@ -1,28 +1,43 @@
 // Skinny GEMM for decode steps: C[M, N] = epilogue(A[M, K] B[K, N]) with
-// M <= 16 token rows, 16-bit operands and B contiguous along k (W^T: torch
-// Linear weights [N][K], the tied LM head, or GPT-2 Conv1D weights stored
-// k-major at load time).
+// M <= 16 token rows and 16-bit operands, B contiguous along k (W^T: torch
+// Linear weights [N][K], the tied LM head, GPT-2 Conv1D weights stored
+// k-major) or pre-packed for this kernel (pack_weights below).
 //
 // Same arithmetic as the reference's matmul/linear (fp32 accumulate,
 // crates/core/src/kernel_templates.rs:987-1072; Linear = x W^T + b,
 // backend_cpp/applegpu_backend.cpp:584-620).  At such M the weights are all
-// of the traffic, so the kernel is built to have as much of B in flight as
-// possible and nothing between the loads and the MFMAs:
-//  - one v_mfma_f32_16x16x32 per 16 columns x 32 k: lane l's A operand is
-//    row l%16 of A at k + 8*(l/16) .. +8 and its B operand column l%16 of
-//    W^T at the same k, each a single 16-byte global load (no LDS staging;
-//    rows >= M read row M-1 and columns >= N read column N-1, and those
-//    outputs are dropped);
-//  - a block of 16 waves owns 16 columns and splits K 16 ways, each wave
-//    issuing its next kSkUnroll steps' loads before multiplying;
+// of the traffic, so the kernel keeps as much of B in flight as it can and
+// puts nothing between the loads and the MFMAs:
+//  - one v_mfma_f32_16x16x32 per 16 columns x 32 k: lane l's B operand is
+//    column l%16 at k + 8*(l/16) .. +8 and its A operand row l%16 at the same
+//    k (rows >= M use row M-1 and columns >= N column N-1; those outputs are
+//    dropped);
+//  - a block of 16 waves owns 16 columns and splits the 32-deep k steps 16
+//    ways (wave w takes steps w, w+16, ...), each wave issuing its next 4
+//    (12 for long K) steps' loads before multiplying;
 //  - the 16 partial 16x16 tiles meet in LDS, are summed in wave order
 //    (deterministic) and pass through the fused epilogue (alpha, bias,
 //    activation, residual) once.
-// The k-reduction happens inside the MFMA accumulators, so there is no
-// cross-lane reduction, no split-K workspace and no second launch.  (A
-// scalar-FMA variant that streamed B and staged A in LDS was slower than the
-// 32x32 MFMA tiles at every decode shape: each weight needs M activation
-// values, so it was bound by LDS operand traffic.)
+// Memory layout matters more than anything else here (measured on MI355X,
+// 80 blocks streaming 13 MB: 9.6 us when each wave instruction reads 16
+// columns x 64 bytes of W^T, 5.2 us for contiguous 1 KB runs).  So:
+//  - PACKED: B comes in the layout [N/16][K/32][64 lanes][8]: the operands of
+//    one wave instruction are 1 KB contiguous; padding is zero;
+//  - XLDS: the M rows of A (M*K <= 16384 elements) are staged in LDS once
+//    per block, so A operands come from LDS instead of global memory.  With
+//    a layer-norm prologue (A = layer_norm(x) over K: the GPT-2 ln_1/ln_2 ->
+//    projection pairs) wave w computes mean and 1/std of row w by two passes
+//    over the row in registers (the reference's formula,
+//    crates/core/src/kernel_templates.rs:1075-1116) and stages the row
+//    normalised, g * (x - mean) * rstd + b rounded to the operand type, as
+//    the layer_norm kernel would have stored it.
+// The first steps' B loads are issued before the staging, so they are in
+// flight while it runs.  The k-reduction happens inside the MFMA
+// accumulators: no cross-lane reduction, no split-K workspace and no second
+// launch.  (A scalar-FMA variant that staged A in LDS and a split-K variant
+// that finished in the last block were both slower than the MFMA tiles: the
+// first is bound by LDS operand traffic, the second by the device-scope
+// fences, which write back and invalidate the XCD's L2.)
 #include "gemm_kernels.hpp"
 
 namespace agpu {
@@ -31,9 +46,10 @@ using namespace dev;
 
 namespace {
 
-constexpr int kSkWaves = 16;   // waves per block, splitting K
-constexpr int kSkUnroll = 4;   // 32-deep k steps each wave keeps in flight
+constexpr int kSkWaves = 16;        // waves per block, splitting K
 constexpr int kSkMaxM = 16;
+constexpr int kSkXlds = 16384;      // A elements staged in LDS (32 KB)
+constexpr int kSkRowMaxK = 4096;    // row a wave holds in registers while staging
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -51,42 +67,119 @@ template <> struct Mfma16<bf16_t> {
   }
 };
 
-template <typename T>
+// UN: steps in flight per wave; LN: layer-norm the A rows (needs XLDS);
+// PACKED: B in the packed layout; XLDS: A rows staged in LDS.
+template <typename T, int UN, bool LN, bool PACKED, bool XLDS>
 __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
+  static_assert(!LN || XLDS, "the layer-norm prologue stages A in LDS");
   typedef typename Mfma16<T>::vec V8;
   __shared__ float red[kSkWaves][16 * 16];
+  __shared__ __attribute__((aligned(16))) T xs[XLDS ? kSkXlds : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const int64_t row = (lane & 15) < p.M ? (lane & 15) : p.M - 1;
   const int64_t col = n0 + (lane & 15) < p.N ? n0 + (lane & 15) : p.N - 1;
   const int kq = 8 * (lane >> 4);  // this lane's k offset inside a step
   const int64_t steps = (p.K + 31) / 32;
-  const T* A0 = (const T*)p.A + row * p.a_sm;   // first 8-run of the row: always legal (K >= 8)
-  const T* B0 = (const T*)p.B + col * p.b_sn;
+  const T* A0 = (const T*)p.A + row * p.a_sm;   // global A row (!XLDS)
+  // B: packed -> this block's run of steps, else column `col` of W^T
+  const T* B0 = PACKED ? (const T*)p.B + ((int64_t)blockIdx.x * steps * 64 + lane) * 8 : (const T*)p.B + col * p.b_sn;
 
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  // wave w takes steps w, w + 16, w + 32, ...
-  for (int64_t s0 = w; s0 < steps; s0 += (int64_t)kSkWaves * kSkUnroll) {
-    V8 a[kSkUnroll], b[kSkUnroll];
+  auto load_b = [&](V8 (&b)[UN], int64_t s0) {
 #pragma unroll
-    for (int u = 0; u < kSkUnroll; ++u) {
+    for (int u = 0; u < UN; ++u) {
       const int64_t st = s0 + (int64_t)u * kSkWaves;
-      // a step past the last, or this lane's 8-run past K (K % 8 == 0, so
-      // runs are whole), reads the row's first run and multiplies zeros
-      const bool ok = st < steps && st * 32 + kq < p.K;
-      const int64_t kc = ok ? st * 32 + kq : 0;
-      a[u] = *(const V8*)(A0 + kc);
-      b[u] = *(const V8*)(B0 + kc);
-      if (!ok) {
+      if constexpr (PACKED) {
+        b[u] = *(const V8*)(B0 + (st < steps ? st : 0) * 512);
+        if (st >= steps) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          a[u][e] = T(0);
-          b[u][e] = T(0);
+          for (int e = 0; e < 8; ++e) b[u][e] = T(0);
+        }
+      } else {
+        // a step past the last, or this lane's 8-run past K (K % 8 == 0, so
+        // runs are whole), reads the column's first run and multiplies zeros
+        const bool ok = st < steps && st * 32 + kq < p.K;
+        b[u] = *(const V8*)(B0 + (ok ? st * 32 + kq : 0));
+        if (!ok) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) b[u][e] = T(0);
         }
       }
     }
+  };
+
+  V8 b[UN];
+  load_b(b, w);  // in flight during the staging below
+
+  if constexpr (XLDS) {
+    if (w < p.M) {
+      const T* xr = (const T*)p.A + w * p.a_sm;
+      constexpr int R = kSkRowMaxK / 512;  // 8-runs per lane
+      V8 run[R];
 #pragma unroll
-    for (int u = 0; u < kSkUnroll; ++u) acc = Mfma16<T>::run(a[u], b[u], acc);
+      for (int c = 0; c < R; ++c) {
+        const int64_t kk = (int64_t)(lane + 64 * c) * 8;
+        if (kk < p.K) run[c] = *(const V8*)(xr + kk);
+      }
+      if constexpr (LN) {
+        float sum = 0.f;
+#pragma unroll
+        for (int c = 0; c < R; ++c)
+          if ((int64_t)(lane + 64 * c) * 8 < p.K) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += (float)run[c][e];
+          }
+        const float mean = wave_sum(sum) / (float)p.K;
+        float sq = 0.f;
+#pragma unroll
+        for (int c = 0; c < R; ++c)
+          if ((int64_t)(lane + 64 * c) * 8 < p.K) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float d = (float)run[c][e] - mean;
+              sq += d * d;
+            }
+          }
+        const float rs = 1.f / sqrtf(wave_sum(sq) / (float)p.K + p.ln_eps);
+#pragma unroll
+        for (int c = 0; c < R; ++c) {
+          const int64_t kk = (int64_t)(lane + 64 * c) * 8;
+          if (kk < p.K) {
+            const V8 g = *(const V8*)((const T*)p.ln_g + kk);
+            const V8 bb = *(const V8*)((const T*)p.ln_b + kk);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              run[c][e] = T((float)g[e] * ((float)run[c][e] - mean) * rs + (float)bb[e]);
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < R; ++c) {
+        const int64_t kk = (int64_t)(lane + 64 * c) * 8;
+        if (kk < p.K) *(V8*)&xs[w * p.K + kk] = run[c];
+      }
+    }
+    __syncthreads();
+  }
+
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t s0 = w; s0 < steps; s0 += (int64_t)kSkWaves * UN) {
+    V8 a[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int64_t st = s0 + (int64_t)u * kSkWaves;
+      const bool ok = st < steps && st * 32 + kq < p.K;
+      const int64_t kc = ok ? st * 32 + kq : 0;
+      if constexpr (XLDS) a[u] = *(const V8*)&xs[row * p.K + kc];
+      else a[u] = *(const V8*)(A0 + kc);
+      if (!ok) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[u][e] = T(0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) acc = Mfma16<T>::run(a[u], b[u], acc);
+    if (s0 + (int64_t)kSkWaves * UN < steps) load_b(b, s0 + (int64_t)kSkWaves * UN);
   }
 
   // C layout of a 16x16 MFMA tile: lane l, register r -> row 4*(l/16) + r,
@@ -104,20 +197,65 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
   epilogue_store<T>(p, 0, m, n, v);
 }
 
+// out[t][s][l][e] = W^T[16t + l%16][32s + 8(l/16) + e], zero outside [N, K).
+template <typename T>
+__global__ void __launch_bounds__(256) pack_weights_kernel(const T* __restrict__ w, int64_t s_n, int64_t s_k,
+                                                           int64_t N, int64_t K, T* __restrict__ out,
+                                                           int64_t total) {
+  const int64_t steps = (K + 31) / 32;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t e = i & 7, l = (i >> 3) & 63, ts = i >> 9;
+    const int64_t s = ts % steps, t = ts / steps;
+    const int64_t n = 16 * t + (l & 15), k = 32 * s + 8 * (l >> 4) + e;
+    out[i] = (n < N && k < K) ? w[n * s_n + k * s_k] : T(0);
+  }
+}
+
 bool al16(const void* q) { return ((uintptr_t)q & 15) == 0; }
 
 }  // namespace
 
+int64_t packed_weight_elems(int64_t N, int64_t K) { return ((N + 15) / 16) * ((K + 31) / 32) * 512; }
+
+void pack_weights(DType dt, const void* w, int64_t s_n, int64_t s_k, int64_t N, int64_t K, void* out,
+                  hipStream_t s) {
+  const int64_t total = packed_weight_elems(N, K);
+  if (total == 0) return;
+  int64_t g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
+  if (dt == DType::F16)
+    hipLaunchKernelGGL((pack_weights_kernel<half_t>), dim3((unsigned)g), dim3(256), 0, s, (const half_t*)w, s_n, s_k,
+                       N, K, (half_t*)out, total);
+  else if (dt == DType::BF16)
+    hipLaunchKernelGGL((pack_weights_kernel<bf16_t>), dim3((unsigned)g), dim3(256), 0, s, (const bf16_t*)w, s_n, s_k,
+                       N, K, (bf16_t*)out, total);
+  else
+    fail("pack_weights: fp16 or bf16 weights only");
+  check_launch("pack_weights");
+}
+
+// A operand requirements shared by the layouts: 16-byte runs along k.
+static bool skinny_a_ok(const Gemm& g) {
+  const bool is16 = g.dt == DType::F16 || g.dt == DType::BF16;
+  return is16 && g.b_dt == g.dt && !g.b_scale && g.batch == 1 && g.M >= 1 && g.M <= kSkMaxM && al16(g.A) &&
+         g.a_sk == 1 && (g.M == 1 || g.a_sm % 8 == 0) && g.K % 8 == 0 && g.K >= 8 && !gemm_tune().no_skinny &&
+         gemm_tune().cfg < 0 && gemm_tune().splits == 0;
+}
+
+static bool skinny_xlds(const Gemm& g) { return g.M * g.K <= kSkXlds && g.K <= kSkRowMaxK; }
+
+bool gemm_skinny_ln_ok(const Gemm& g) {
+  Gemm probe = g;
+  probe.ln_gamma = probe.ln_beta = nullptr;
+  return skinny_plan(probe, 0).use && skinny_xlds(g) && g.ln_gamma && g.ln_beta && al16(g.ln_gamma) &&
+         al16(g.ln_beta);
+}
+
 SkinnyPlan skinny_plan(const Gemm& g, int cus) {
   (void)cus;
   SkinnyPlan pl{};
-  const bool is16 = g.dt == DType::F16 || g.dt == DType::BF16;
-  // 16-byte operand runs along k for both A rows and W^T columns
-  const bool aligned = al16(g.A) && al16(g.B) && g.a_sk == 1 && g.b_sk == 1 && g.a_sm % 8 == 0 &&
-                       g.b_sn % 8 == 0 && g.K % 8 == 0 && g.K >= 8;
-  if (!(is16 && g.b_dt == g.dt && !g.b_scale && g.batch == 1 && g.M >= 1 && g.M <= kSkMaxM && aligned &&
-        !gemm_tune().no_skinny && gemm_tune().cfg < 0 && gemm_tune().splits == 0))
-    return pl;
+  if (!skinny_a_ok(g)) return pl;
+  if (!g.b_packed && !(al16(g.B) && g.b_sk == 1 && g.b_sn % 8 == 0)) return pl;
   const int64_t blocks = (g.N + 15) / 16;
   if (blocks > 0x7fffffffLL) return pl;
   pl.use = true;
@@ -125,12 +263,34 @@ SkinnyPlan skinny_plan(const Gemm& g, int cus) {
   return pl;
 }
 
+template <typename T, bool PK>
+static void launch_skinny(const GArgs& p, dim3 grid, bool deep, bool ln, bool xlds, hipStream_t s) {
+  const dim3 blk(64 * kSkWaves);
+  if (ln) hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, true, PK, true>), grid, blk, 0, s, p);
+  else if (xlds) {
+    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, true>), grid, blk, 0, s, p);
+    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, true>), grid, blk, 0, s, p);
+  } else {
+    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, false>), grid, blk, 0, s, p);
+    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, false>), grid, blk, 0, s, p);
+  }
+}
+
 void gemm_skinny(const Gemm& g, const SkinnyPlan& pl, const GArgs& p, hipStream_t s) {
   const dim3 grid((unsigned)pl.blocks);
-  if (g.dt == DType::F16)
-    hipLaunchKernelGGL((gemm_skinny_mfma<half_t>), grid, dim3(64 * kSkWaves), 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_skinny_mfma<bf16_t>), grid, dim3(64 * kSkWaves), 0, s, p);
+  const bool ln = g.ln_gamma != nullptr;
+  if (ln && !gemm_skinny_ln_ok(g)) fail("gemm: layer-norm prologue not supported for this operand");
+  if (g.b_packed && !al16(g.B)) fail("gemm: packed weights must be 16-byte aligned");
+  // 4 steps in flight when each wave has at most 4 (K <= 2048), else 12
+  const bool deep = (g.K + 32 * kSkWaves - 1) / (32 * kSkWaves) > 4;
+  const bool xlds = skinny_xlds(g);
+  if (g.dt == DType::F16) {
+    if (g.b_packed) launch_skinny<half_t, true>(p, grid, deep, ln, xlds, s);
+    else launch_skinny<half_t, false>(p, grid, deep, ln, xlds, s);
+  } else {
+    if (g.b_packed) launch_skinny<bf16_t, true>(p, grid, deep, ln, xlds, s);
+    else launch_skinny<bf16_t, false>(p, grid, deep, ln, xlds, s);
+  }
   check_launch("gemm_skinny");
 }
 

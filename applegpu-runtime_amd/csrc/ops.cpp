@@ -703,6 +703,57 @@ static bool batch_stride(const Tensor& t, const std::vector<int64_t>& bdims, int
   return true;
 }
 
+// Epilogue operands of a GEMM (bias, residual, mask, layer-norm prologue);
+// `keep` holds the tensors the launch reads.
+struct EpiKeep {
+  TensorP res, mask, bias, ln_g, ln_b;
+};
+
+static void set_epilogue(k::Gemm& g, const Epilogue* epi, const std::vector<int64_t>& od,
+                         const std::vector<int64_t>& bdims, EpiKeep* keep) {
+  if (!epi) return;
+  const int64_t M = g.M, N = g.N;
+  g.alpha = epi->alpha;
+  g.act = epi->act;
+  if (epi->bias) {
+    if (epi->bias->dtype != g.dt || epi->bias->numel() != N) fail("matmul epilogue: bias must be [%lld]", (long long)N);
+    keep->bias = contiguous(epi->bias);
+    g.bias = keep->bias->data();
+  }
+  if (epi->ln_gamma) {
+    if (!epi->ln_beta || epi->ln_gamma->dtype != g.dt || epi->ln_beta->dtype != g.dt ||
+        epi->ln_gamma->numel() != g.K || epi->ln_beta->numel() != g.K)
+      fail("matmul: layer-norm gamma and beta must be [%lld] of the operand dtype", (long long)g.K);
+    keep->ln_g = contiguous(epi->ln_gamma);
+    keep->ln_b = contiguous(epi->ln_beta);
+    g.ln_gamma = keep->ln_g->data();
+    g.ln_beta = keep->ln_b->data();
+    g.ln_eps = epi->ln_eps;
+  }
+  auto side = [&](const TensorP& t, const void** ptr, int64_t* sm, int64_t* sb, TensorP* kp) {
+    if (t->dtype != g.dt) fail("matmul epilogue: operand dtype mismatch");
+    if (t->dims() != od) {
+      // broadcast residual: expand through strides (must collapse)
+      *kp = alloc_out(g.dt, od);
+      LAUNCH k::unary(k::kCopy, t->dtype, t->dtype, t->data(), nd_for(*t, od), (*kp)->data(), nd_shape(od), 0, 0,
+               rt().stream());
+    } else {
+      *kp = t;
+    }
+    const Tensor& r = **kp;
+    int64_t rsb;
+    if (r.strides[r.ndim - 1] != 1 && N > 1) { *kp = contiguous(*kp); }
+    const Tensor& r2 = **kp;
+    if (!batch_stride(r2, bdims, &rsb)) { *kp = contiguous(*kp); batch_stride(**kp, bdims, &rsb); }
+    *ptr = (*kp)->data();
+    *sm = (*kp)->strides[(*kp)->ndim - 2];
+    if (M == 1) *sm = N;
+    *sb = rsb;
+  };
+  if (epi->residual) side(epi->residual, &g.residual, &g.r_sm, &g.r_sb, &keep->res);
+  if (epi->mask) side(epi->mask, &g.mask, &g.k_sm, &g.k_sb, &keep->mask);
+}
+
 TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi) {
   TensorP a = ta ? transpose_dims(a_in, a_in->ndim - 2, a_in->ndim - 1) : a_in;
   TensorP b = tb ? transpose_dims(b_in, b_in->ndim - 2, b_in->ndim - 1) : b_in;
@@ -756,42 +807,71 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
   if (K == 1) { if (g.a_sm != 1) g.a_sk = 1; if (g.b_sn != 1) g.b_sk = 1; }
   if (N == 1) g.b_sn = g.b_sk == 1 ? K : 1;
   g.C = out->data(); g.c_sm = N; g.c_sb = M * N;
-  TensorP keep_res, keep_mask, keep_bias;
-  if (epi) {
-    g.alpha = epi->alpha;
-    g.act = epi->act;
-    if (epi->bias) {
-      if (epi->bias->dtype != g.dt || epi->bias->numel() != N) fail("matmul epilogue: bias must be [%lld]", (long long)N);
-      keep_bias = contiguous(epi->bias);
-      g.bias = keep_bias->data();
+  if (epi && epi->ln_gamma) {
+    bool ok = !ta && a_in->ndim == 2 && b_in->ndim == 2 && epi->ln_beta && epi->ln_gamma->dtype == g.dt &&
+              epi->ln_beta->dtype == g.dt && epi->ln_gamma->numel() == K && epi->ln_beta->numel() == K;
+    if (ok) {
+      k::Gemm probe = g;
+      probe.ln_gamma = epi->ln_gamma->data();
+      probe.ln_beta = epi->ln_beta->data();
+      ok = meta_mode() ? k::gemm_is_skinny(probe) : (epi->ln_gamma->is_contiguous() && epi->ln_beta->is_contiguous() &&
+                                                     k::gemm_skinny_ln_ok(probe));
     }
-    auto side = [&](const TensorP& t, const void** ptr, int64_t* sm, int64_t* sb, TensorP* keep) {
-      if (t->dtype != g.dt) fail("matmul epilogue: operand dtype mismatch");
-      if (t->dims() != od) {
-        // broadcast residual: expand through strides (must collapse)
-        *keep = alloc_out(g.dt, od);
-        LAUNCH k::unary(k::kCopy, t->dtype, t->dtype, t->data(), nd_for(*t, od), (*keep)->data(), nd_shape(od), 0, 0,
-                 rt().stream());
-      } else {
-        *keep = t;
-      }
-      const Tensor& r = **keep;
-      int64_t rsb;
-      if (r.strides[r.ndim - 1] != 1 && N > 1) { *keep = contiguous(*keep); }
-      const Tensor& r2 = **keep;
-      if (!batch_stride(r2, bdims, &rsb)) { *keep = contiguous(*keep); batch_stride(**keep, bdims, &rsb); }
-      *ptr = (*keep)->data();
-      *sm = (*keep)->strides[(*keep)->ndim - 2];
-      if (M == 1) *sm = N;
-      *sb = rsb;
-    };
-    if (epi->residual) side(epi->residual, &g.residual, &g.r_sm, &g.r_sb, &keep_res);
-    if (epi->mask) side(epi->mask, &g.mask, &g.k_sm, &g.k_sb, &keep_mask);
+    if (!ok) {
+      Epilogue plain = *epi;
+      plain.ln_gamma = plain.ln_beta = nullptr;
+      return matmul(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), b_in, ta, tb, &plain);
+    }
   }
+  EpiKeep keep;
+  set_epilogue(g, epi, od, bdims, &keep);
   size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
   BufferP ws;
   if (wsb) ws = scratch(wsb);
   LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
+  return out;
+}
+
+TensorP pack_weight(const TensorP& wt) {
+  if (wt->ndim != 2) fail("pack_weight: weights must be 2-D [out, in]");
+  if (wt->dtype != DType::F16 && wt->dtype != DType::BF16) fail("pack_weight: fp16 or bf16 weights only");
+  const int64_t N = wt->shape[0], K = wt->shape[1];
+  TensorP out = alloc_out(wt->dtype, {(N + 15) / 16, (K + 31) / 32, 64, 8});
+  LAUNCH k::pack_weights(wt->dtype, wt->data(), wt->strides[0], wt->strides[1], N, K, out->data(), rt().stream());
+  return out;
+}
+
+TensorP matmul_packed(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi) {
+  const char* name = "matmul_packed";
+  if (a_in->ndim != 2) fail("%s: activations must be 2-D [rows, in]", name);
+  if (pw->ndim != 4 || pw->shape[2] != 64 || pw->shape[3] != 8) fail("%s: weights are not packed (pack_weight)", name);
+  if (a_in->dtype != pw->dtype) fail("Dtype mismatch: %s vs %s", dtype_name(a_in->dtype), dtype_name(pw->dtype));
+  const int64_t M = a_in->shape[0], K = a_in->shape[1];
+  if (N < 1 || pw->shape[0] != (N + 15) / 16 || pw->shape[1] != (K + 31) / 32)
+    fail("%s: packed weights hold [%lld/16, %lld/32] tiles, not [out %lld, in %lld]", name,
+         (long long)pw->shape[0] * 16, (long long)pw->shape[1] * 32, (long long)N, (long long)K);
+  TensorP a = a_in;
+  if (!meta_mode() && (a->strides[1] != 1 || (M > 1 && a->strides[0] % 8 != 0) || ((uintptr_t)a->data() & 15)))
+    a = materialize(a);
+  TensorP pc = contiguous(pw);
+  const std::vector<int64_t> od{M, N};
+  TensorP out = alloc_out(a->dtype, od);
+  k::Gemm g;
+  g.dt = g.b_dt = a->dtype;
+  g.M = M; g.N = N; g.K = K; g.batch = 1;
+  g.A = a->data(); g.a_sm = M == 1 ? K : a->strides[0]; g.a_sk = 1;
+  g.B = pc->data(); g.b_packed = true; g.b_sk = 1; g.b_sn = K;
+  g.C = out->data(); g.c_sm = N; g.c_sb = M * N;
+  EpiKeep keep;
+  set_epilogue(g, epi, od, {}, &keep);
+  if (!meta_mode() && !k::gemm_is_skinny(g))
+    fail("%s: needs at most 16 fp16/bf16 rows with the reduction dim a multiple of 8", name);
+  if (epi && epi->ln_gamma && !meta_mode() && !k::gemm_skinny_ln_ok(g)) {
+    Epilogue plain = *epi;
+    plain.ln_gamma = plain.ln_beta = nullptr;
+    return matmul_packed(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), pw, N, &plain);
+  }
+  LAUNCH k::gemm(g, nullptr, rt().stream());
   return out;
 }
 
@@ -948,25 +1028,39 @@ TensorP decode_attention(const TensorP& q, const TensorP& kc, const TensorP& vc,
   return out;
 }
 
-void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos) {
-  const char* name = "kv_write";
+static void check_kv_pair(const char* name, const TensorP& cache, const TensorP& rows) {
   if (cache->dtype != rows->dtype) fail("%s: cache is %s but rows are %s", name, dtype_name(cache->dtype),
                                         dtype_name(rows->dtype));
   check_bhtd(name, "cache", *cache);
   check_bhtd(name, "rows", *rows);
-  const int64_t B = cache->shape[0], H = cache->shape[1], Tmax = cache->shape[2], D = cache->shape[3];
-  if (rows->shape[0] != B || rows->shape[1] != H || rows->shape[3] != D)
+  if (rows->shape[0] != cache->shape[0] || rows->shape[1] != cache->shape[1] || rows->shape[3] != cache->shape[3])
     fail("%s: rows %s do not match cache %s", name, shape_str(rows->dims()).c_str(), shape_str(cache->dims()).c_str());
-  if (rows->shape[2] > Tmax) fail("%s: %lld rows exceed the cache length %lld", name, (long long)rows->shape[2],
-                                  (long long)Tmax);
+  if (rows->shape[2] > cache->shape[2]) fail("%s: %lld rows exceed the cache length %lld", name,
+                                             (long long)rows->shape[2], (long long)cache->shape[2]);
   for (int i = 0; i < 3; ++i)
     if (cache->shape[i] > 1 && cache->strides[i] == 0) fail("%s: cache has overlapping rows", name);
+}
+
+void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos, const TensorP& cache2,
+              const TensorP& rows2) {
+  const char* name = "kv_write";
+  check_kv_pair(name, cache, rows);
+  if (cache2) {
+    check_kv_pair(name, cache2, rows2);
+    if (cache2->dims() != cache->dims() || rows2->dims() != rows->dims() || cache2->dtype != cache->dtype)
+      fail("%s: the two caches (and their rows) must have the same shape and dtype", name);
+  }
+  const int64_t B = cache->shape[0];
   TensorP pc = check_lens(name, "positions", pos, B);
   k::KvWrite a;
   a.dt = cache->dtype;
-  a.B = B; a.H = H; a.T = rows->shape[2]; a.D = D; a.Tmax = Tmax;
-  a.cache = cache->data(); a.c_sb = cache->strides[0]; a.c_sh = cache->strides[1]; a.c_st = cache->strides[2];
-  a.src = rows->data(); a.x_sb = rows->strides[0]; a.x_sh = rows->strides[1]; a.x_st = rows->strides[2];
+  a.B = B; a.H = cache->shape[1]; a.T = rows->shape[2]; a.D = cache->shape[3]; a.Tmax = cache->shape[2];
+  a.cache = cache->data(); a.src = rows->data();
+  for (int i = 0; i < 3; ++i) { a.cs[i] = cache->strides[i]; a.xs[i] = rows->strides[i]; }
+  if (cache2) {
+    a.cache2 = cache2->data(); a.src2 = rows2->data();
+    for (int i = 0; i < 3; ++i) { a.c2s[i] = cache2->strides[i]; a.x2s[i] = rows2->strides[i]; }
+  }
   a.pos = (const int32_t*)pc->data();
   LAUNCH k::kv_write(a, rt().stream());
 }

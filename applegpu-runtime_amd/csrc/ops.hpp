@@ -68,9 +68,19 @@ struct Epilogue {
   TensorP residual;   // same shape as the output
   TensorP mask;       // same shape as the output: out = mask > 0 ? out : 0
   float alpha = 1.f;
+  // A = layer_norm(a, ln_gamma, ln_beta, ln_eps) over its last dim, fused into
+  // the GEMM's operand load when the skinny kernel runs the product (else an
+  // explicit layer_norm first)
+  TensorP ln_gamma, ln_beta;
+  float ln_eps = 1e-5f;
 };
 TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = false,
                const Epilogue* epi = nullptr);
+// Decode-step weights: wt [out N, in K] (fp16/bf16) rearranged for the skinny
+// GEMM (the operands of one wave instruction contiguous), and x [M <= 16, K]
+// times it: out [M, N] = epilogue(x @ wt^T).
+TensorP pack_weight(const TensorP& wt);
+TensorP matmul_packed(const TensorP& x, const TensorP& packed, int64_t N, const Epilogue* epi = nullptr);
 // int8 weights with per-row scales (out = x @ (q * scale[:,None])^T)
 TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
 
@@ -83,8 +93,10 @@ TensorP attention(const TensorP& q, const TensorP& k, const TensorP& v, bool cau
 // (lens int32 [B] on the device; the queries' own keys are the last Tq of
 // them); the output is logically [B, H, Tq, D], stored as [B, Tq, H, D].
 TensorP decode_attention(const TensorP& q, const TensorP& k_cache, const TensorP& v_cache, const TensorP& lens);
-// cache[b, h, pos[b] + t, :] = rows[b, h, t, :] (pos int32 [B] on the device).
-void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos);
+// cache[b, h, pos[b] + t, :] = rows[b, h, t, :] (pos int32 [B] on the device);
+// an optional second cache/rows pair of the same shape in the same launch.
+void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos, const TensorP& cache2 = nullptr,
+              const TensorP& rows2 = nullptr);
 
 }  // namespace ops
 }  // namespace agpu

@@ -388,6 +388,11 @@ def decode_section(timed, line, randn):
         copies = max(2, int(320e6 // (K * N * 2)) + 1)
         ws = [randn((N, K) if bk else (K, N), np.float16, 0.02) for _ in range(copies)]
         x = randn((M, K), np.float16)
+        pks = [E.op("pack_weight", [w]) for w in ws]
+        ms, _ = timed(lambda pk: E.op("matmul_packed", [x, pk], i=(N,)), pks, 4 * copies)
+        line(f"gemm_decode {name} f16 M={M} (skinny, packed weights)", [M, K, N], 2 * (K * N + M * K + M * N),
+             ms, 2.0 * M * N * K, BF16_MFMA_PEAK_TFLOPS)
+        del pks
         for skinny in (1, 0):
             prev = lib.applegpu_ffi_gemm_skinny(skinny)
             plan = ctypes.create_string_buffer(96)

@@ -208,6 +208,11 @@ float applegpu_ffi_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
  * row i of sequence b attends to cache rows j <= lens[b] - Tq + i.
  * Returns 0, or -1 with the error set. */
 int32_t applegpu_kv_write(uint64_t cache_id, uint64_t rows_id, uint64_t pos_id);
+/* The K and V appends of one layer in one launch: same contract as
+ * applegpu_kv_write for (k_cache, k_rows) and (v_cache, v_rows), which must
+ * have the same shapes and dtype. */
+int32_t applegpu_kv_write_pair(uint64_t k_cache_id, uint64_t v_cache_id, uint64_t k_rows_id, uint64_t v_rows_id,
+                               uint64_t pos_id);
 
 int32_t applegpu_capture_begin(void);
 int64_t applegpu_capture_end(void);

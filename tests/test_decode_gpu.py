@@ -77,6 +77,30 @@ def test_kv_write_ragged_positions_bit_exact(gpu, dtype):
     np.testing.assert_array_equal(_host(cache), want)
 
 
+def test_kv_write_pair_bit_exact(gpu):
+    """K and V rows of a fused QKV projection into two caches in one launch."""
+    B, H, Tmax, D, T = 3, 4, 9, 64, 2
+    kc0 = RNG.standard_normal((B, H, Tmax, D)).astype(np.float16)
+    vc0 = RNG.standard_normal((B, H, Tmax, D)).astype(np.float16)
+    qkv = RNG.standard_normal((B, T, 3, H, D)).astype(np.float16)
+    pos = np.array([0, 4, 8], np.int32)
+    kc, vc = gpu.from_numpy(kc0), gpu.from_numpy(vc0)
+    qd = gpu.reshape(gpu.from_numpy(qkv), [B, T, 3 * H * D])
+    rows = [gpu.transpose_dims(gpu.reshape(gpu.slice(qd, 2, j * H * D, (j + 1) * H * D), [B, T, H, D]), 1, 2)
+            for j in (1, 2)]
+    gpu.kv_write_pair(kc, vc, rows[0], rows[1], gpu.from_numpy(pos))
+    wk, wv = kc0.copy(), vc0.copy()
+    for b in range(B):
+        for t in range(T):
+            if pos[b] + t < Tmax:
+                wk[b, :, pos[b] + t] = qkv[b, t, 1]
+                wv[b, :, pos[b] + t] = qkv[b, t, 2]
+    np.testing.assert_array_equal(kc.to_numpy(), wk)
+    np.testing.assert_array_equal(vc.to_numpy(), wv)
+    with pytest.raises(ValueError, match="kv_write"):
+        gpu.kv_write_pair(kc, gpu.zeros([B, H, Tmax + 1, D], "float16"), rows[0], rows[1], gpu.from_numpy(pos))
+
+
 def test_kv_write_rejects_bad_operands(gpu):
     cache = gpu.zeros([2, 2, 8, 32], "float16")
     rows = gpu.zeros([2, 2, 1, 32], "float32")
@@ -124,6 +148,22 @@ def test_decode_attention_vs_oracle(gpu, dtype, tol, D, Tmax, Tq):
     assert got.shape == [B, H, Tq, D]
     ref = _decode_ref(q, kc, vc, lens)
     assert rel_err(_host(got), ref) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [("float32", 1e-3), ("float16", 1e-2)])
+@pytest.mark.parametrize("B,H,Tq,Tmax,D", [(8, 20, 1, 640, 64), (4, 16, 2, 300, 128), (2, 64, 1, 97, 32)])
+def test_decode_attention_whole_row_blocks_vs_oracle(gpu, dtype, tol, B, H, Tq, Tmax, D):
+    """At least 128 (batch, head, query) rows: one 16-wave block per row over
+    the whole context (the C4 decode shape is the first case)."""
+    q = _round(RNG.standard_normal((B, H, Tq, D)).astype(np.float32), dtype)
+    kc = _round(RNG.standard_normal((B, H, Tmax, D)).astype(np.float32), dtype)
+    vc = _round(RNG.standard_normal((B, H, Tmax, D)).astype(np.float32), dtype)
+    lens = np.linspace(Tq, Tmax, B).astype(np.int32)
+    lens[0] = 0 if Tq == 1 else Tq   # an empty row (zeros) when allowed
+    lens[-1] = Tmax
+    got = gpu.decode_attention(_dev(gpu, q, dtype), _dev(gpu, kc, dtype), _dev(gpu, vc, dtype),
+                               gpu.from_numpy(lens))
+    assert rel_err(_host(got), _decode_ref(q, kc, vc, lens)) < tol
 
 
 def test_decode_attention_empty_and_clamped_lengths(gpu):

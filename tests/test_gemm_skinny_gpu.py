@@ -164,3 +164,104 @@ def test_skinny_graph_replay(gpu):
             _np(xd @ wt)
     finally:
         g.destroy()
+
+
+@pytest.mark.parametrize("dt", ["float16", "bfloat16"])
+@pytest.mark.parametrize("M,K,N", [(8, 1280, 3840), (1, 1280, 5120), (16, 4096, 64), (5, 8, 24)])
+def test_layer_norm_folded_into_skinny_gemm(gpu, dt, M, K, N):
+    """add_bias(layer_norm(x) @ W^T) with the layer_norm output used once:
+    the graph folds the normalisation into the skinny kernel's A loads."""
+    x = _round((RNG.standard_normal((M, K)) * 3 + 1).astype(np.float32), dt)
+    gam = _round((RNG.standard_normal(K) * 0.5 + 1).astype(np.float32), dt)
+    bet = _round((RNG.standard_normal(K) * 0.1).astype(np.float32), dt)
+    w = _round((RNG.standard_normal((N, K)) * 0.03).astype(np.float32), dt)
+    bias = _round(RNG.standard_normal(N).astype(np.float32), dt)
+    xd, gd, bd, wd, biasd = (_dev(gpu, a, dt) for a in (x, gam, bet, w, bias))
+    wt = gpu.transpose(wd)
+    before = gpu.graph_stats()["fused_gemm_epilogues"]
+    fused = _np(gpu.add_bias(gpu.layer_norm(xd, gd, bd) @ wt, biasd))
+    assert gpu.graph_stats()["fused_gemm_epilogues"] == before + 1
+    h = gpu.layer_norm(xd, gd, bd)           # a live handle: no folding
+    plain = _np(gpu.add_bias(h @ wt, biasd))
+    ln = _round(O.layer_norm(x, gam, bet), dt)   # the layer_norm output as the device stores it
+    ref = O.matmul(ln.astype(np.float64), w.T.astype(np.float64)) + bias
+    assert rel_err(fused, ref) < TOL[dt]
+    assert rel_err(fused, plain) < TOL[dt]
+
+
+@pytest.mark.parametrize("dt,M,bk", [("float32", 8, True), ("float16", 32, True), ("float16", 8, False)])
+def test_layer_norm_fold_falls_back(gpu, dt, M, bk):
+    """Where the skinny kernel does not run (fp32, M > 16, W n-contiguous) the
+    folded layer_norm is computed explicitly first: same result."""
+    K, N = 256, 96
+    x = _round(RNG.standard_normal((M, K)).astype(np.float32), dt)
+    gam = _round((RNG.standard_normal(K) * 0.5 + 1).astype(np.float32), dt)
+    bet = _round((RNG.standard_normal(K) * 0.1).astype(np.float32), dt)
+    w = _round((RNG.standard_normal((N, K) if bk else (K, N)) * 0.05).astype(np.float32), dt)
+    bias = _round(RNG.standard_normal(N).astype(np.float32), dt)
+    xd, gd, bd, wd, biasd = (_dev(gpu, a, dt) for a in (x, gam, bet, w, bias))
+    got = _np(gpu.add_bias(gpu.layer_norm(xd, gd, bd) @ (gpu.transpose(wd) if bk else wd), biasd))
+    ln = _round(O.layer_norm(x, gam, bet), dt)
+    ref = O.matmul(ln.astype(np.float64), (w.T if bk else w).astype(np.float64)) + bias
+    assert rel_err(got, ref) < TOL[dt]
+
+
+@pytest.mark.parametrize("dt", ["float16", "bfloat16"])
+@pytest.mark.parametrize("M,K,N", [(8, 1280, 3840), (8, 5120, 1280), (1, 1280, 50257), (16, 4096, 64), (3, 40, 21),
+                                   (13, 776, 1001)])
+def test_packed_weights_vs_oracle_and_unpacked(gpu, dt, M, K, N):
+    """pack_weight + matmul_packed: zero-padded tiles for ragged N and K; the
+    same MFMA sequence as the unpacked skinny kernel, so the same bits."""
+    x = _round(RNG.standard_normal((M, K)).astype(np.float32), dt)
+    w = _round((RNG.standard_normal((N, K)) * 0.05).astype(np.float32), dt)
+    xd, wd = _dev(gpu, x, dt), _dev(gpu, w, dt)
+    pk = gpu.pack_weight(wd)
+    assert pk.shape == [(N + 15) // 16, (K + 31) // 32, 64, 8]
+    got = _np(gpu.matmul_packed(xd, pk, N))
+    assert rel_err(got, O.matmul(x.astype(np.float64), w.T.astype(np.float64))) < TOL[dt]
+    np.testing.assert_array_equal(got, _np(xd @ gpu.transpose(wd)))
+
+
+def test_packed_layout_matches_definition(gpu):
+    """packed[t][s][l][e] = W^T[16t + l%16][32s + 8(l/16) + e], zero outside."""
+    N, K = 37, 72
+    w = RNG.standard_normal((N, K)).astype(np.float16)
+    pk = gpu.pack_weight(gpu.from_numpy(w)).to_numpy()
+    want = np.zeros(pk.shape, np.float16)
+    for t in range(pk.shape[0]):
+        for s in range(pk.shape[1]):
+            for l in range(64):
+                n, k0 = 16 * t + l % 16, 32 * s + 8 * (l // 16)
+                for e in range(8):
+                    if n < N and k0 + e < K:
+                        want[t, s, l, e] = w[n, k0 + e]
+    np.testing.assert_array_equal(pk, want)
+
+
+def test_packed_fused_epilogue_and_layer_norm(gpu):
+    """layer_norm -> matmul_packed -> add_bias -> gelu: one fused kernel."""
+    M, K, N, dt = 8, 1280, 5120, "float16"
+    x = _round((RNG.standard_normal((M, K)) * 2 + 0.5).astype(np.float32), dt)
+    gam = _round((RNG.standard_normal(K) * 0.5 + 1).astype(np.float32), dt)
+    bet = _round((RNG.standard_normal(K) * 0.1).astype(np.float32), dt)
+    w = _round((RNG.standard_normal((N, K)) * 0.03).astype(np.float32), dt)
+    bias = _round(RNG.standard_normal(N).astype(np.float32), dt)
+    xd, gd, bd, wd, biasd = (_dev(gpu, a, dt) for a in (x, gam, bet, w, bias))
+    pk = gpu.pack_weight(wd)
+    before = gpu.graph_stats()["fused_gemm_epilogues"]
+    got = _np(gpu.gelu(gpu.add_bias(gpu.matmul_packed(gpu.layer_norm(xd, gd, bd), pk, N), biasd)))
+    assert gpu.graph_stats()["fused_gemm_epilogues"] == before + 1
+    ln = _round(O.layer_norm(x, gam, bet), dt)
+    ref = O.gelu_tanh(O.matmul(ln.astype(np.float64), w.T.astype(np.float64)) + bias)
+    assert rel_err(got, ref) < 1e-2
+
+
+def test_packed_rejects_bad_use(gpu):
+    w = gpu.cast(gpu.from_numpy(RNG.standard_normal((64, 128)).astype(np.float32)), "float16")
+    pk = gpu.pack_weight(w)
+    with pytest.raises(ValueError):  # 17 rows: the packed layout is for decode steps
+        gpu.matmul_packed(gpu.zeros([17, 128], "float16"), pk, 64).eval()
+    with pytest.raises(ValueError):  # wrong output width for these tiles
+        gpu.matmul_packed(gpu.zeros([4, 128], "float16"), pk, 100).eval()
+    with pytest.raises(ValueError):
+        gpu.pack_weight(gpu.zeros([4, 8], "float32")).eval()
