@@ -23,6 +23,10 @@
 // gets zeros (the fused attention kernel uses the same convention).
 #include "device.hpp"
 
+#include <cstdlib>
+#include <type_traits>
+#include <cstring>
+
 namespace agpu {
 namespace k {
 using namespace dev;
@@ -34,7 +38,7 @@ namespace {
 // no merge launch); with few rows, 4-wave blocks split the context and
 // decode_merge combines their partials.
 constexpr int kDRowsWhole = 128;          // rows at which a block takes a whole row
-constexpr int kDWavesWhole = 16, kDUnrollWhole = 4;
+constexpr int kDWavesWhole = 16, kDUnrollWhole = 4, kDUnrollWhole6 = 6;
 constexpr int kDWavesSplit = 4, kDUnrollSplit = 2;
 
 struct DArgs {
@@ -47,22 +51,95 @@ struct DArgs {
   int splits, chunk;
 };
 
+// 8 consecutive elements, raw: one 16-byte load (two for fp32) when VEC.
+// Loads are issued into raw registers and converted where they are used, so
+// a wave's loads of one iteration are all in flight together (converting at
+// the load makes the compiler wait for each load before the next).
+template <typename T, bool VEC>
+struct Raw8 {
+  static constexpr int NV = VEC ? (int)sizeof(T) / 2 : 1;  // uint4s per 8 elements
+  uint4 v[NV];
+  T s[VEC ? 1 : 8];
+  __device__ __forceinline__ void load(const T* p) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) v[i] = ((const uint4*)p)[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s[i] = p[i];
+    }
+  }
+  __device__ __forceinline__ void to_float(float (&x)[8]) const {
+    if constexpr (VEC) {
+      T e[8];
+      __builtin_memcpy(e, v, 16 * NV);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = to_f(e[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = to_f(s[i]);
+    }
+  }
+};
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+
+// q . k over 8 elements with fp32 accumulation: four v_dot2_f32_{f16,bf16}
+// on raw 16-bit pairs (products exact in fp32, no conversions), else FMAs.
+template <typename T, bool VEC>
+__device__ __forceinline__ float dot8(const Raw8<T, VEC>& q, const Raw8<T, VEC>& k) {
+  if constexpr (VEC && std::is_same<T, half_t>::value) {
+    h2_t a[4], b[4];
+    __builtin_memcpy(a, q.v, 16);
+    __builtin_memcpy(b, k.v, 16);
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d = __builtin_amdgcn_fdot2(a[i], b[i], d, false);
+    return d;
+  } else if constexpr (VEC && std::is_same<T, bf16_t>::value) {
+    b2_t a[4], b[4];
+    __builtin_memcpy(a, q.v, 16);
+    __builtin_memcpy(b, k.v, 16);
+    float d = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d = __builtin_amdgcn_fdot2_f32_bf16(a[i], b[i], d, false);
+    return d;
+  } else {
+    float x[8], y[8];
+    q.to_float(x);
+    k.to_float(y);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d += x[e] * y[e];
+    return d;
+  }
+}
+
+// Sum over aligned groups of G lanes (G = 2, 4, 8, 16) with DPP lane moves
+// (VALU operand modifiers, no LDS round trip): quad_perm swaps for lane
+// distance 1 and 2, row_half_mirror (lane i <-> 7-i in each 8) and
+// row_mirror (i <-> 15-i in each 16) for the halves of 8- and 16-lane
+// groups, each applied once the smaller groups already hold their sums.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (G >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+  if constexpr (G >= 16) v += dpp_mov<0x140>(v); // row_mirror
+  return v;
+}
+
 template <typename T, bool VEC>
 __device__ __forceinline__ void load8(const T* p, float (&x)[8]) {
-  if constexpr (VEC && sizeof(T) == 2) {
-    uint4 u = *(const uint4*)p;
-    T e[8];
-    __builtin_memcpy(e, &u, 16);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = to_f(e[i]);
-  } else if constexpr (VEC && sizeof(T) == 4) {
-    const float4 a = ((const float4*)p)[0], b = ((const float4*)p)[1];
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = to_f(p[i]);
-  }
+  Raw8<T, VEC> r;
+  r.load(p);
+  r.to_float(x);
 }
 
 // Number of keys visible to query row i of a sequence holding `len` keys
@@ -74,13 +151,14 @@ __device__ __forceinline__ int64_t visible_keys(const DArgs& p, int64_t b, int64
   return vis < 0 ? 0 : (vis > len ? len : vis);
 }
 
-// Merges online-softmax state (om, ol, oa) into (m, l, a).
+// Merges online-softmax state (om, ol, oa) into (m, l, a); maxima are in the
+// log2 domain.
 __device__ __forceinline__ void merge_state(float& m, float& l, float (&a)[8], float om, float ol,
                                             const float (&oa)[8]) {
   const float M = fmaxf(m, om);
   if (M == -INFINITY) return;  // both empty
-  const float f1 = m == -INFINITY ? 0.f : expf(m - M);
-  const float f2 = om == -INFINITY ? 0.f : expf(om - M);
+  const float f1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+  const float f2 = om == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(om - M);
   l = l * f1 + ol * f2;
 #pragma unroll
   for (int e = 0; e < 8; ++e) a[e] = a[e] * f1 + oa[e] * f2;
@@ -102,51 +180,64 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
   const int64_t row = blockIdx.y;
   const int64_t i = row % p.Tq, bh = row / p.Tq;
   const int64_t h = bh % p.H, b = bh / p.H;
-  const int64_t vis = visible_keys(p, b, i);
   const int64_t j_lo = (int64_t)s * p.chunk;
-  const int64_t j_hi = j_lo + p.chunk < vis ? j_lo + p.chunk : vis;
 
-  float q[8];
-  load8<T, VEC>((const T*)p.q + b * p.q_sb + h * p.q_sh + i * p.q_st + sub * 8, q);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) q[e] *= p.scale;
+  // Scores are kept in the log2 domain (scale * log2(e) folded into one
+  // multiply) so every exponential is one v_exp_f32.
+  Raw8<T, VEC> qr;
+  qr.load((const T*)p.q + b * p.q_sb + h * p.q_sh + i * p.q_st + sub * 8);
+  const float c2 = p.scale * 1.4426950408889634f;
   const T* K = (const T*)p.k + b * p.k_sb + h * p.k_sh + sub * 8;
   const T* V = (const T*)p.v + b * p.v_sb + h * p.v_sh + sub * 8;
+  const int tmax = (int)p.Tmax, kst = (int)p.k_st, vst = (int)p.v_st;
+
+  // Raw K/V rows of one iteration, clamped into the cache (always legal) and
+  // masked when scored.  The first iteration's loads go out before the
+  // sequence length is read, so the two latencies overlap.
+  Raw8<T, VEC> kr[UN], vr[UN];
+  auto load_iter = [&](int64_t base) {
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int j = (int)base + (u * NW + w) * KPS + g;
+      const int jc = j < tmax ? j : tmax - 1;
+      kr[u].load(K + jc * kst);   // 32-bit offsets: Tmax * stride < 2^31 (checked on the host)
+      vr[u].load(V + jc * vst);
+    }
+  };
+  load_iter(j_lo);
+  const int64_t vis = visible_keys(p, b, i);
+  const int64_t j_hi = j_lo + p.chunk < vis ? j_lo + p.chunk : vis;
 
   float m = -INFINITY, l = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 
   for (int64_t base = j_lo; base < j_hi; base += BS) {
-    // all loads of the iteration first (rows clamped into the cache, masked
-    // below), then the arithmetic
-    float kx[UN][8], vx[UN][8];
-    int64_t jj[UN];
+    // the iteration's scores, then one online-softmax rescale for all of them
+    const int64_t lim = j_hi - base;
+    float sc[UN];
+    float mx = m;
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int64_t j = base + (int64_t)(u * NW + w) * KPS + g;
-      jj[u] = j;
-      const int64_t jc = j < p.Tmax ? j : p.Tmax - 1;
-      load8<T, VEC>(K + jc * p.k_st, kx[u]);
-      load8<T, VEC>(V + jc * p.v_st, vx[u]);
+      const float d = group_sum<LPK>(dot8(qr, kr[u]));
+      sc[u] = (u * NW + w) * KPS + g < lim ? d * c2 : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
     }
+    const float alpha = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+    l *= alpha;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      float dot = 0.f;
+      const float pe = sc[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[u] - mx);
+      l += pe;
+      float vx[8];
+      vr[u].to_float(vx);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dot += q[e] * kx[u][e];
-#pragma unroll
-      for (int x = 1; x < LPK; x <<= 1) dot += __shfl_xor(dot, x, 64);
-      const bool ok = jj[u] < j_hi;
-      const float sc = ok ? dot : -INFINITY;
-      const float m_new = fmaxf(m, sc);
-      const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
-      const float pe = ok ? expf(sc - m_new) : 0.f;
-      l = l * alpha + pe;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = acc[e] * alpha + pe * vx[u][e];
-      m = m_new;
+      for (int e = 0; e < 8; ++e) acc[e] += pe * vx[e];
     }
+    m = mx;
+    if (base + BS < j_hi) load_iter(base + BS);
   }
 
   // the wave's KPS key groups meet by xor shuffles over the group bits of
@@ -175,7 +266,7 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
 #pragma unroll
     for (int x = 0; x < NW; ++x) {
       const float mx = sm_m[x];
-      const float f = mx == -INFINITY ? 0.f : expf(mx - M);
+      const float f = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - M);
       L += sm_l[x] * f;
       A += sm_acc[x][tid] * f;
     }
@@ -204,7 +295,7 @@ __global__ void __launch_bounds__(128) decode_merge(DArgs p) {
   if (M != -INFINITY) {
     for (int s = 0; s < p.splits; ++s) {
       const float ms = P[s * (D + 2) + D];
-      const float f = ms == -INFINITY ? 0.f : expf(ms - M);
+      const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
       L += P[s * (D + 2) + D + 1] * f;
       A += P[s * (D + 2) + t] * f;
     }
@@ -246,7 +337,13 @@ template <typename T, int D>
 void launch_decode(const DArgs& p, bool vec, int64_t rows, bool whole, hipStream_t s) {
   const dim3 grid((unsigned)p.splits, (unsigned)rows);
   constexpr int NWW = kDWavesWhole, UW = kDUnrollWhole, NWS = kDWavesSplit, US = kDUnrollSplit;
-  if (whole) {
+  // 6 key steps per wave when that covers the whole cache in one iteration
+  constexpr int UW6 = kDUnrollWhole6;
+  const bool one_pass = p.Tmax <= (int64_t)NWW * (64 / (D / 8)) * UW6;
+  if (whole && one_pass) {
+    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW6>), grid, dim3(64 * NWW), 0, s, p);
+    else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW6>), grid, dim3(64 * NWW), 0, s, p);
+  } else if (whole) {
     if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW>), grid, dim3(64 * NWW), 0, s, p);
     else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW>), grid, dim3(64 * NWW), 0, s, p);
   } else {
@@ -286,9 +383,29 @@ bool decode_attention_supported(const DecodeAttn& a) {
          (a.dt == DType::F32 || a.dt == DType::F16 || a.dt == DType::BF16);
 }
 
+// Launch-shape override for tuning sweeps: APPLEGPU_DECODE_ATTN=whole, or
+// split:<n> (n key splits of 4-wave blocks); unset = the heuristic below.
+static int decode_forced_splits() {
+  static int v = [] {
+    const char* e = getenv("APPLEGPU_DECODE_ATTN");
+    if (!e) return 0;
+    if (!strcmp(e, "whole")) return -1;
+    if (!strncmp(e, "split:", 6)) return atoi(e + 6) > 0 ? atoi(e + 6) : 0;
+    return 0;
+  }();
+  return v;
+}
+
+static bool decode_whole(const DecodeAttn& a) {
+  const int f = decode_forced_splits();
+  if (f == -1) return true;
+  if (f > 0) return false;
+  return a.B * a.H * a.Tq >= kDRowsWhole;
+}
+
 int decode_attention_splits(const DecodeAttn& a, int64_t* chunk) {
   const int64_t rows = a.B * a.H * a.Tq;
-  if (rows >= kDRowsWhole) {
+  if (decode_whole(a)) {
     *chunk = a.Tmax;
     return 1;
   }
@@ -297,6 +414,7 @@ int decode_attention_splits(const DecodeAttn& a, int64_t* chunk) {
   // aim for >= 2048 blocks over the 256 CUs, with at least one block
   // iteration per split
   int64_t want = rows >= 2048 ? 1 : (2048 + rows - 1) / rows;
+  if (decode_forced_splits() > 0) want = decode_forced_splits();
   const int64_t max_splits = (a.Tmax + bs - 1) / bs;
   if (want > max_splits) want = max_splits;
   if (want < 1) want = 1;
@@ -316,6 +434,8 @@ size_t decode_attention_ws_bytes(const DecodeAttn& a) {
 void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s) {
   if (!decode_attention_supported(a)) fail("decode_attention: head dim %lld not supported", (long long)a.D);
   if (a.Tmax <= 0) fail("decode_attention: empty cache");
+  if (a.Tmax * (a.k_st > a.v_st ? a.k_st : a.v_st) >= (int64_t)1 << 31)
+    fail("decode_attention: cache rows of one head span more than 2^31 elements");
   const int64_t rows = a.B * a.H * a.Tq;
   if (rows == 0) return;
   if (rows > 0x7fffffffLL) fail("decode_attention: too many rows");
@@ -343,7 +463,7 @@ void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s) {
   const bool vec = al(a.q, a.q_sb, a.q_sh, a.q_st) && al(a.k, a.k_sb, a.k_sh, a.k_st) &&
                    al(a.v, a.v_sb, a.v_sh, a.v_st);
   AGPU_FLOAT_SWITCH(a.dt, {
-    const bool whole = rows >= kDRowsWhole;
+    const bool whole = decode_whole(a);
     if (a.D == 32) launch_decode<T, 32>(p, vec, rows, whole, s);
     else if (a.D == 64) launch_decode<T, 64>(p, vec, rows, whole, s);
     else launch_decode<T, 128>(p, vec, rows, whole, s);

@@ -23,8 +23,10 @@
 // columns x 64 bytes of W^T, 5.2 us for contiguous 1 KB runs).  So:
 //  - PACKED: B comes in the layout [N/16][K/32][64 lanes][8]: the operands of
 //    one wave instruction are 1 KB contiguous; padding is zero;
-//  - XLDS: the M rows of A (M*K <= 16384 elements) are staged in LDS once
-//    per block, so A operands come from LDS instead of global memory.  With
+//  - XLDS: the M rows of A (M*K <= 16384 elements, K <= 2048) are staged in
+//    LDS once per block, so A operands come from LDS instead of global
+//    memory (an 80 KB variant for the long-K projection measured slower: one
+//    block per CU).  With
 //    a layer-norm prologue (A = layer_norm(x) over K: the GPT-2 ln_1/ln_2 ->
 //    projection pairs) wave w computes mean and 1/std of row w by two passes
 //    over the row in registers (the reference's formula,
@@ -49,7 +51,7 @@ namespace {
 constexpr int kSkWaves = 16;        // waves per block, splitting K
 constexpr int kSkMaxM = 16;
 constexpr int kSkXlds = 16384;      // A elements staged in LDS (32 KB)
-constexpr int kSkRowMaxK = 4096;    // row a wave holds in registers while staging
+constexpr int kSkRowMaxK = 2048;    // row a wave holds in registers for the LN statistics
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -68,13 +70,14 @@ template <> struct Mfma16<bf16_t> {
 };
 
 // UN: steps in flight per wave; LN: layer-norm the A rows (needs XLDS);
-// PACKED: B in the packed layout; XLDS: A rows staged in LDS.
-template <typename T, int UN, bool LN, bool PACKED, bool XLDS>
+// PACKED: B in the packed layout; XS > 0: A rows staged in LDS (XS elements).
+template <typename T, int UN, bool LN, bool PACKED, int XS>
 __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
+  constexpr bool XLDS = XS > 0;
   static_assert(!LN || XLDS, "the layer-norm prologue stages A in LDS");
   typedef typename Mfma16<T>::vec V8;
   __shared__ float red[kSkWaves][16 * 16];
-  __shared__ __attribute__((aligned(16))) T xs[XLDS ? kSkXlds : 8];
+  __shared__ __attribute__((aligned(16))) T xs[XLDS ? XS : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const int64_t row = (lane & 15) < p.M ? (lane & 15) : p.M - 1;
@@ -115,11 +118,19 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
     if (w < p.M) {
       const T* xr = (const T*)p.A + w * p.a_sm;
       constexpr int R = kSkRowMaxK / 512;  // 8-runs per lane
-      V8 run[R];
+      // the row, and for a layer-norm prologue gamma and beta, all loaded up
+      // front: one round trip
+      V8 run[R], lg[LN ? R : 1], lb[LN ? R : 1];
 #pragma unroll
       for (int c = 0; c < R; ++c) {
         const int64_t kk = (int64_t)(lane + 64 * c) * 8;
-        if (kk < p.K) run[c] = *(const V8*)(xr + kk);
+        if (kk < p.K) {
+          run[c] = *(const V8*)(xr + kk);
+          if constexpr (LN) {
+            lg[c] = *(const V8*)((const T*)p.ln_g + kk);
+            lb[c] = *(const V8*)((const T*)p.ln_b + kk);
+          }
+        }
       }
       if constexpr (LN) {
         float sum = 0.f;
@@ -143,13 +154,10 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
         const float rs = 1.f / sqrtf(wave_sum(sq) / (float)p.K + p.ln_eps);
 #pragma unroll
         for (int c = 0; c < R; ++c) {
-          const int64_t kk = (int64_t)(lane + 64 * c) * 8;
-          if (kk < p.K) {
-            const V8 g = *(const V8*)((const T*)p.ln_g + kk);
-            const V8 bb = *(const V8*)((const T*)p.ln_b + kk);
+          if ((int64_t)(lane + 64 * c) * 8 < p.K) {
 #pragma unroll
             for (int e = 0; e < 8; ++e)
-              run[c][e] = T((float)g[e] * ((float)run[c][e] - mean) * rs + (float)bb[e]);
+              run[c][e] = T((float)lg[c][e] * ((float)run[c][e] - mean) * rs + (float)lb[c][e]);
           }
         }
       }
@@ -242,12 +250,16 @@ static bool skinny_a_ok(const Gemm& g) {
          gemm_tune().cfg < 0 && gemm_tune().splits == 0;
 }
 
-static bool skinny_xlds(const Gemm& g) { return g.M * g.K <= kSkXlds && g.K <= kSkRowMaxK; }
+// LDS staging of A: 0 = none, else the array size the launch uses.
+static int skinny_xlds(const Gemm& g) {
+  if (g.M * g.K <= kSkXlds && g.K <= kSkRowMaxK) return kSkXlds;
+  return 0;
+}
 
 bool gemm_skinny_ln_ok(const Gemm& g) {
   Gemm probe = g;
   probe.ln_gamma = probe.ln_beta = nullptr;
-  return skinny_plan(probe, 0).use && skinny_xlds(g) && g.ln_gamma && g.ln_beta && al16(g.ln_gamma) &&
+  return skinny_plan(probe, 0).use && skinny_xlds(g) == kSkXlds && g.ln_gamma && g.ln_beta && al16(g.ln_gamma) &&
          al16(g.ln_beta);
 }
 
@@ -264,15 +276,15 @@ SkinnyPlan skinny_plan(const Gemm& g, int cus) {
 }
 
 template <typename T, bool PK>
-static void launch_skinny(const GArgs& p, dim3 grid, bool deep, bool ln, bool xlds, hipStream_t s) {
+static void launch_skinny(const GArgs& p, dim3 grid, bool deep, bool ln, int xs, hipStream_t s) {
   const dim3 blk(64 * kSkWaves);
-  if (ln) hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, true, PK, true>), grid, blk, 0, s, p);
-  else if (xlds) {
-    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, true>), grid, blk, 0, s, p);
-    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, true>), grid, blk, 0, s, p);
+  if (ln) hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, true, PK, kSkXlds>), grid, blk, 0, s, p);
+  else if (xs) {
+    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, kSkXlds>), grid, blk, 0, s, p);
+    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, kSkXlds>), grid, blk, 0, s, p);
   } else {
-    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, false>), grid, blk, 0, s, p);
-    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, false>), grid, blk, 0, s, p);
+    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, 0>), grid, blk, 0, s, p);
+    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, 0>), grid, blk, 0, s, p);
   }
 }
 
@@ -283,7 +295,7 @@ void gemm_skinny(const Gemm& g, const SkinnyPlan& pl, const GArgs& p, hipStream_
   if (g.b_packed && !al16(g.B)) fail("gemm: packed weights must be 16-byte aligned");
   // 4 steps in flight when each wave has at most 4 (K <= 2048), else 12
   const bool deep = (g.K + 32 * kSkWaves - 1) / (32 * kSkWaves) > 4;
-  const bool xlds = skinny_xlds(g);
+  const int xlds = skinny_xlds(g);
   if (g.dt == DType::F16) {
     if (g.b_packed) launch_skinny<half_t, true>(p, grid, deep, ln, xlds, s);
     else launch_skinny<half_t, false>(p, grid, deep, ln, xlds, s);

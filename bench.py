@@ -308,6 +308,8 @@ def kernel_suite(only=""):
         c4_section(timed, line, randn)
     if want("decode"):
         decode_section(timed, line, randn)
+    if want("decode") or want("dattn"):
+        decode_attention_line(timed, line, randn)
 
 
 def rows_section(timed, line, randn):
@@ -372,6 +374,21 @@ def c4_section(timed, line, randn):
     q1 = randn((BH, 1, hd), np.float16)
     ms, _ = timed(lambda k: E.op("attention", [q1, k, kc[1]]), [kc[0]], 20)
     line("attention decode f16 (q_len 1, ctx 640)", [BH, 640, hd], 2 * (2 * BH * 640 * hd + 2 * BH * hd), ms)
+
+
+def decode_attention_line(timed, line, randn):
+    """decode_attention at the C4 decode shape: 8 x 20 heads, one query row,
+    contexts 513..640 (the average of the 128 steps, 576), fp16 cache of 640."""
+    from applegpu_runtime import eager as E
+    B, H, Tmax, D = 8, 20, 640, 64
+    layers = 12   # rotating caches: 12 x 2 x 26 MB beyond the Infinity Cache
+    kc = [randn((B, H, Tmax, D), np.float16) for _ in range(layers)]
+    vc = [randn((B, H, Tmax, D), np.float16) for _ in range(layers)]
+    q = randn((B, H, 1, D), np.float16)
+    lens = E.from_numpy(np.full(B, 576, np.int32))
+    ms, _ = timed(lambda i: E.op("decode_attention", [q, kc[i], vc[i], lens]), list(range(layers)), 4 * layers)
+    mode = os.environ.get("APPLEGPU_DECODE_ATTN", "auto")
+    line(f"decode_attention f16 ({mode}) B=8 H=20 ctx 576 of 640", [B, H, 576, D], 2 * B * H * 576 * D * 2, ms)
 
 
 def decode_section(timed, line, randn):
