@@ -37,6 +37,41 @@ struct GArgs {
   const void* ln_g; const void* ln_b; float ln_eps;
 };
 
+// Epilogue operands of one output, loadable ahead of the product (they do
+// not depend on it), so that their latency hides under the main loop; kept
+// raw until the epilogue (converting at the load would make the compiler
+// wait for them right there).
+template <typename T>
+struct EpiIn {
+  T bias = T(0), res = T(0), mask = T(1);
+};
+// Branch-free: an absent operand reads the output element itself (a legal
+// address; the value is not used), so no load sits behind a branch that the
+// compiler would close with a wait.
+template <typename T>
+__device__ __forceinline__ EpiIn<T> epilogue_load(const GArgs& p, int64_t b, int64_t row, int64_t col) {
+  const T* out = (const T*)p.C + b * p.c_sb + row * p.c_sm + col;
+  const T* bp = p.bias ? (const T*)p.bias + col : out;
+  const T* rp = p.res ? (const T*)p.res + b * p.r_sb + row * p.r_sm + col : out;
+  const T* mp = p.mask ? (const T*)p.mask + b * p.k_sb + row * p.k_sm + col : out;
+  EpiIn<T> e;
+  e.bias = *bp;
+  e.res = *rp;
+  e.mask = *mp;
+  return e;
+}
+template <typename T>
+__device__ __forceinline__ void epilogue_finish(const GArgs& p, int64_t b, int64_t row, int64_t col, float acc,
+                                                const EpiIn<T>& e) {
+  float v = p.alpha * acc + (p.bias ? to_f(e.bias) : 0.f);
+  if (p.act == kActRelu) v = fmaxf(v, 0.f);
+  else if (p.act == kActGelu) v = gelu_tanh(v);
+  else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+  v += p.res ? to_f(e.res) : 0.f;
+  if (p.mask) v = to_f(e.mask) > 0.f ? v : 0.f;
+  ((T*)p.C)[b * p.c_sb + row * p.c_sm + col] = from_f<T>(v);
+}
+
 template <typename T>
 __device__ __forceinline__ void epilogue_store(const GArgs& p, int64_t b, int64_t row, int64_t col, float acc) {
   float v = p.alpha * acc;

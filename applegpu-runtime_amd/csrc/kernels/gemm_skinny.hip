@@ -113,6 +113,12 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
 
   V8 b[UN];
   load_b(b, w);  // in flight during the staging below
+  // threads 0..255 each finish one output (m, n0 + c): its bias/residual now
+  // (every thread loads, from a clamped legal element: no divergent branch
+  // around the loads)
+  const int om = (tid >> 4) & 15, oc = tid & 15;
+  const bool owns = tid < 256 && om < p.M && n0 + oc < p.N;
+  const EpiIn<T> ein = epilogue_load<T>(p, 0, om < p.M ? om : p.M - 1, n0 + oc < p.N ? n0 + oc : p.N - 1);
 
   if constexpr (XLDS) {
     if (w < p.M) {
@@ -195,14 +201,11 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[w][(4 * (lane >> 4) + r) * 16 + (lane & 15)] = acc[r];
   __syncthreads();
-  if (tid >= 256) return;
-  const int m = tid >> 4, c = tid & 15;
-  const int64_t n = n0 + c;
-  if (m >= p.M || n >= p.N) return;
+  if (!owns) return;
   float v = 0.f;
 #pragma unroll
   for (int ww = 0; ww < kSkWaves; ++ww) v += red[ww][tid];
-  epilogue_store<T>(p, 0, m, n, v);
+  epilogue_finish<T>(p, 0, om, n0 + oc, v, ein);
 }
 
 // out[t][s][l][e] = W^T[16t + l%16][32s + 8(l/16) + e], zero outside [N, K).
