@@ -54,15 +54,32 @@ def compile_one(src: str) -> tuple[str, int, str]:
     return src, p.returncode, msg
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
+def stale(src: str) -> bool:
+    """True when the object is missing or older than its source or any header
+    under csrc/ (a conservative stand-in for dependency tracking)."""
+    obj = obj_for(src)
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    if os.path.getmtime(src) > t:
+        return True
+    for root, _, files in os.walk(CSRC):
+        for f in files:
+            if f.endswith(".hpp") and os.path.getmtime(os.path.join(root, f)) > t:
+                return True
+    return False
+
+
+def build(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> str:
     if not os.path.exists(HIPCC):
         raise RuntimeError(f"hipcc not found at {HIPCC}")
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
+    todo = [s for s in srcs if stale(s)] if incremental else srcs
     jobs = jobs or min(8, os.cpu_count() or 4)
     failed = []
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        for src, rc, msg in ex.map(compile_one, srcs):
+        for src, rc, msg in ex.map(compile_one, todo):
             if msg.strip() and (rc != 0 or verbose):
                 print(f"--- {os.path.relpath(src, HERE)}\n{msg}", file=sys.stderr)
             if rc != 0:
@@ -108,6 +125,8 @@ def build_torch_shim(verbose: bool = True) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only sources older than their object (or than any header)")
     a = ap.parse_args()
-    print(build(a.j))
+    print(build(a.j, incremental=a.incremental))
     print(build_torch_shim())

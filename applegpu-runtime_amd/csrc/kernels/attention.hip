@@ -17,7 +17,12 @@
 // Q, K, V and O are read/written through their own (batch, head, token)
 // strides with unit stride along d, so head splits of a fused QKV projection
 // and the head-merge transpose cost nothing.
+//
+// 16-bit inputs with d = 64 or 128 and 16-byte aligned rows take the MFMA
+// kernel (flash_attn_mfma below); other cases take the scalar kernel.
 #include "device.hpp"
+
+#include <type_traits>
 
 namespace agpu {
 namespace k {
@@ -31,7 +36,7 @@ constexpr int kTPR = 16; // threads per query row
 
 struct AArgs {
   const void* q; const void* k; const void* v; void* o;
-  int64_t H, Tq, Tk;
+  int64_t B, H, Tq, Tk;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
   float scale;
   int causal;
@@ -161,7 +166,308 @@ __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
   for (int i = 0; i < DPT; ++i) O[sub * DPT + i] = from_f<T>(o[i] * inv);
 }
 
+
+// ── MFMA flash attention (16-bit Q/K/V) ─────────────────────────────────────
+// One block of 4 wavefronts owns QB = 64*QG query rows of one (batch, head);
+// each wavefront owns QG groups of 16 rows.  K/V tiles of 64 keys are staged
+// in LDS (double-buffered: the next tile's global loads are in flight while
+// the current one is multiplied) and shared by the 4 wavefronts.
+//
+// Both products use v_mfma_f32_16x16x32 (lane l: A row l%16 and B column
+// l%16, each at k = 8*(l/16)..+8; C register r of lane l is row 4*(l/16)+r,
+// column l%16), oriented so that softmax needs no data movement:
+//  - S^T = K Q^T: A = 16 keys x 32 dims of K (a 16-byte LDS read), B = this
+//    lane's query row, held in registers for the whole kernel.  C then gives
+//    every lane 16 scores of ONE query (l%16) for keys 16t + 4*(l/16) + r;
+//  - the online softmax of a query is lane-local plus two xor shuffles (the
+//    four lanes sharing l%16) for the tile max; the running sum stays
+//    lane-partial until the end;
+//  - O^T += V^T P^T: B = the lane's own probabilities (converted to the input
+//    type), A = V^T.  The k index of an MFMA may be any permutation of the
+//    keys as long as A and B agree, so V is stored in LDS transposed, [d][key],
+//    with each 32-key group permuted so that the 8 keys lane group g holds
+//    (4g..4g+3 and 16+4g..16+4g+3) are 8 consecutive elements: A is one
+//    16-byte LDS read too;
+//  - O^T's C layout gives lane l query l%16 and dims 16u + 4*(l/16) + r, so
+//    the per-query rescale is one multiply per register.
+// Scores are scaled by scale*log2(e) and exponentiated with exp2, which is
+// exp of the scaled score.  Causal (key j visible to query i iff j <= i):
+// a block stops at its last query's key; a wavefront skips tiles entirely
+// after its queries, masks only the tiles that cross them, and blocks run
+// heaviest query tiles first.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <typename E> struct FaMfma;
+template <> struct FaMfma<half_t> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x4 run(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct FaMfma<bf16_t> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ f32x4 run(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kFaWaves = 4;
+constexpr int kFaKeys = 64;  // keys per LDS tile
+
+// Position of key k (0..63) of a tile inside its V^T row: within each group
+// of 32, key 16h + 4g + r goes to 8g + 4h + r.
+__device__ __forceinline__ int fa_vpos(int k) {
+  return (k & 32) | ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3);
+}
+
+// One K/V tile in registers: K as KU 16-byte chunks, V as VU pairs of chunks
+// of two consecutive keys (they become 32-bit pairs in the transposed tile).
+// Named registers rather than arrays: with arrays the compiler kept the tile
+// in scratch memory across the products.
+template <typename T, int D>
+struct FaTile {
+  static constexpr int CH = D / 8;
+  static constexpr int KU = kFaKeys * CH / (64 * kFaWaves);
+  static constexpr int VU = (kFaKeys / 2) * CH / (64 * kFaWaves);
+  static_assert(KU <= 4 && VU <= 2, "tile registers");
+  uint4 k0, k1, k2, k3, va0, vb0, va1, vb1;
+
+  __device__ __forceinline__ static uint4 ld(const T* base, int64_t row, int64_t stride, int64_t Tk, int col) {
+    const int64_t j = row < Tk ? row : Tk - 1;  // rows past Tk repeat row Tk-1
+    return *(const uint4*)(base + j * stride + col);
+  }
+  __device__ __forceinline__ void load(const T* K, const T* V, const AArgs& p, int64_t j0, int tid) {
+    constexpr int NT = 64 * kFaWaves;
+    k0 = ld(K, j0 + tid / CH, p.k_st, p.Tk, 8 * (tid % CH));
+    if constexpr (KU > 1) k1 = ld(K, j0 + (tid + NT) / CH, p.k_st, p.Tk, 8 * (tid % CH));
+    if constexpr (KU > 2) k2 = ld(K, j0 + (tid + 2 * NT) / CH, p.k_st, p.Tk, 8 * (tid % CH));
+    if constexpr (KU > 3) k3 = ld(K, j0 + (tid + 3 * NT) / CH, p.k_st, p.Tk, 8 * (tid % CH));
+    va0 = ld(V, j0 + 2 * (tid / CH), p.v_st, p.Tk, 8 * (tid % CH));
+    vb0 = ld(V, j0 + 2 * (tid / CH) + 1, p.v_st, p.Tk, 8 * (tid % CH));
+    if constexpr (VU > 1) {
+      va1 = ld(V, j0 + 2 * ((tid + NT) / CH), p.v_st, p.Tk, 8 * (tid % CH));
+      vb1 = ld(V, j0 + 2 * ((tid + NT) / CH) + 1, p.v_st, p.Tk, 8 * (tid % CH));
+    }
+  }
+  template <int VP>
+  __device__ __forceinline__ static void put_v(T* Vt, int e, uint4 a4, uint4 c4) {
+    const int d0 = 8 * (e % CH);
+    const int pos = fa_vpos(2 * (e / CH));  // even: keys 2m and 2m+1 land side by side
+    const uint32_t a[4] = {a4.x, a4.y, a4.z, a4.w};
+    const uint32_t c[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      *(uint32_t*)&Vt[(d0 + 2 * x) * VP + pos] = (a[x] & 0xffffu) | (c[x] << 16);
+      *(uint32_t*)&Vt[(d0 + 2 * x + 1) * VP + pos] = (a[x] >> 16) | (c[x] & 0xffff0000u);
+    }
+  }
+  template <int KP, int VP>
+  __device__ __forceinline__ void store(T* Ks, T* Vt, int tid) const {
+    constexpr int NT = 64 * kFaWaves;
+    const int col = 8 * (tid % CH);
+    *(uint4*)&Ks[(tid / CH) * KP + col] = k0;
+    if constexpr (KU > 1) *(uint4*)&Ks[((tid + NT) / CH) * KP + col] = k1;
+    if constexpr (KU > 2) *(uint4*)&Ks[((tid + 2 * NT) / CH) * KP + col] = k2;
+    if constexpr (KU > 3) *(uint4*)&Ks[((tid + 3 * NT) / CH) * KP + col] = k3;
+    put_v<VP>(Vt, tid, va0, vb0);
+    if constexpr (VU > 1) put_v<VP>(Vt, tid + NT, va1, vb1);
+  }
+};
+
+template <typename T, int D, int QG>
+__global__ void __launch_bounds__(64 * kFaWaves) flash_attn_mfma(AArgs p) {
+  static_assert(D % 64 == 0, "d must be a multiple of 64");
+  typedef typename FaMfma<T>::vec V8;
+  constexpr int QB = kFaWaves * QG * 16;  // query rows per block
+  constexpr int KP = D + 8;               // K tile row pitch (elements)
+  constexpr int VP = kFaKeys + 8;         // V^T row pitch (elements)
+  constexpr int DS = D / 32;              // 32-deep steps of Q K^T
+  constexpr int DT = D / 16;              // 16-dim tiles of O^T
+  __shared__ __attribute__((aligned(16))) T Ks[2][kFaKeys * KP];
+  __shared__ __attribute__((aligned(16))) T Vt[2][D * VP];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t BH = p.B * p.H;
+  const int64_t bh = blockIdx.x % BH;
+  const int64_t tq = blockIdx.x / BH;
+  const int64_t qt = p.causal ? p.q_tiles - 1 - tq : tq;
+  const int64_t b = bh / p.H, h = bh % p.H;
+  const int64_t q0 = qt * QB;
+  const int64_t qw = q0 + (int64_t)w * QG * 16;  // this wavefront's first query
+
+  const T* Q = (const T*)p.q + b * p.q_sb + h * p.q_sh;
+  const T* K = (const T*)p.k + b * p.k_sb + h * p.k_sh;
+  const T* V = (const T*)p.v + b * p.v_sb + h * p.v_sh;
+
+  int64_t kv_end = p.Tk;
+  if (p.causal) {
+    const int64_t qe = q0 + QB < p.Tq ? q0 + QB : p.Tq;
+    kv_end = qe < p.Tk ? qe : p.Tk;
+  }
+  const int ntiles = (int)((kv_end + kFaKeys - 1) / kFaKeys);
+
+
+  // Q operands: column l%16 of each group, dims 32s + 8g .. +8
+  V8 qf[QG][DS];
+  int lim[QG];  // keys < lim are visible to this lane's query
+#pragma unroll
+  for (int gi = 0; gi < QG; ++gi) {
+    const int64_t qi = qw + 16 * gi + l16;
+    const int64_t qr = qi < p.Tq ? qi : p.Tq - 1;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qf[gi][s] = *(const V8*)(Q + qr * p.q_st + 32 * s + 8 * g);
+    lim[gi] = (int)(p.causal ? (qi + 1 < p.Tk ? qi + 1 : p.Tk) : p.Tk);
+  }
+
+  f32x4 acc[QG][DT];
+  float m[QG], ls[QG];
+#pragma unroll
+  for (int gi = 0; gi < QG; ++gi) {
+    m[gi] = -INFINITY;
+    ls[gi] = 0.f;
+#pragma unroll
+    for (int u = 0; u < DT; ++u) acc[gi][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const float c2 = p.scale * 1.4426950408889634f;
+
+  if (ntiles > 0) {
+    FaTile<T, D> t0;
+    t0.load(K, V, p, 0, tid);
+    t0.template store<KP, VP>(Ks[0], Vt[0], tid);
+  }
+  __syncthreads();
+
+  // One tile: S^T, online softmax, O^T update, then the next tile's LDS
+  // stores.  MASK applies the visibility test to every score; tiles wholly
+  // visible to all of the block's queries skip it.  Both loop bodies are
+  // branch-free, so the next tile's global loads stay at the top and are
+  // in flight during the products.
+  auto tile = [&](int it, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int buf = it & 1;
+    const int j0 = it * kFaKeys;
+    // the next tile's loads (unconditional: past the end they reread row Tk-1)
+    FaTile<T, D> nx;
+    nx.load(K, V, p, (int64_t)j0 + kFaKeys, tid);
+
+    const T* Kb = Ks[buf];
+    const T* Vb = Vt[buf];
+    f32x4 st[QG][4];
+#pragma unroll
+    for (int gi = 0; gi < QG; ++gi)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) st[gi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        const V8 a = *(const V8*)&Kb[(16 * t + l16) * KP + 32 * s + 8 * g];
+#pragma unroll
+        for (int gi = 0; gi < QG; ++gi) st[gi][t] = FaMfma<T>::run(a, qf[gi][s], st[gi][t]);
+      }
+    V8 pf[QG][2];
+#pragma unroll
+    for (int gi = 0; gi < QG; ++gi) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = st[gi][t][r] * c2;
+          if constexpr (MASK) v = j0 + 16 * t + 4 * g + r < lim[gi] ? v : -INFINITY;
+          st[gi][t][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mn = fmaxf(m[gi], mx);
+      const float mu = mn == -INFINITY ? 0.f : mn;
+      const float alpha = __builtin_amdgcn_exp2f(m[gi] - mu);
+      m[gi] = mn;
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pv = __builtin_amdgcn_exp2f(st[gi][t][r] - mu);
+          ps += pv;
+          pf[gi][t >> 1][4 * (t & 1) + r] = (T)pv;
+        }
+      ls[gi] = ls[gi] * alpha + ps;
+#pragma unroll
+      for (int u = 0; u < DT; ++u) acc[gi][u] *= alpha;
+    }
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const V8 a = *(const V8*)&Vb[(16 * u + l16) * VP + 32 * s + 8 * g];
+#pragma unroll
+        for (int gi = 0; gi < QG; ++gi) acc[gi][u] = FaMfma<T>::run(a, pf[gi][s], acc[gi][u]);
+      }
+    // the LDS stores into the other buffer stay after this tile's LDS reads
+    asm volatile("" ::: "memory");
+    nx.template store<KP, VP>(Ks[buf ^ 1], Vt[buf ^ 1], tid);
+    __syncthreads();
+  };
+
+  // leading tiles visible in full to every query of the block
+  int nfull = (int)(p.Tk / kFaKeys);
+  if (p.causal && (q0 + 1) / kFaKeys < nfull) nfull = (int)((q0 + 1) / kFaKeys);
+  if (nfull > ntiles) nfull = ntiles;
+  int it = 0;
+  for (; it < nfull; ++it) tile(it, std::integral_constant<bool, false>());
+  for (; it < ntiles; ++it) tile(it, std::integral_constant<bool, true>());
+
+  T* O = (T*)p.o + b * p.o_sb + h * p.o_sh;
+#pragma unroll
+  for (int gi = 0; gi < QG; ++gi) {
+    float l = ls[gi] + __shfl_xor(ls[gi], 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int64_t qi = qw + 16 * gi + l16;
+    if (qi >= p.Tq) continue;
+#pragma unroll
+    for (int u = 0; u < DT; ++u) {
+      T o4[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o4[r] = from_f<T>(acc[gi][u][r] * inv);
+      uint2 pk;
+      __builtin_memcpy(&pk, o4, 8);
+      *(uint2*)(O + qi * p.o_st + 16 * u + 4 * g) = pk;
+    }
+  }
+}
+
 }  // namespace
+
+// 16-byte loads of every Q/K/V row and 8-byte stores of O need aligned bases
+// and row/head/batch strides that are multiples of 8 elements.
+static bool attention_mfma_ok(const Attn& a) {
+  if (!(a.dt == DType::F16 || a.dt == DType::BF16) || !(a.D == 64 || a.D == 128)) return false;
+  if (a.Tk >= (int64_t(1) << 30)) return false;  // key indices are 32-bit in the kernel
+  if (((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v) % 16 != 0 || (uintptr_t)a.o % 8 != 0) return false;
+  const int64_t st[12] = {a.q_sb, a.q_sh, a.q_st, a.k_sb, a.k_sh, a.k_st,
+                          a.v_sb, a.v_sh, a.v_st, a.o_sb, a.o_sh, a.o_st};
+  for (int64_t x : st)
+    if (x % 8 != 0) return false;
+  return true;
+}
+
+template <typename T>
+static void launch_fa_mfma(const AArgs& p, int64_t D, bool wide, unsigned blocks, hipStream_t s) {
+  const dim3 grid(blocks), block(64 * kFaWaves);
+  if (D == 64) {
+    if (wide) hipLaunchKernelGGL((flash_attn_mfma<T, 64, 2>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((flash_attn_mfma<T, 64, 1>), grid, block, 0, s, p);
+  } else {
+    if (wide) hipLaunchKernelGGL((flash_attn_mfma<T, 128, 2>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((flash_attn_mfma<T, 128, 1>), grid, block, 0, s, p);
+  }
+}
 
 bool attention_supported(const Attn& a) {
   return (a.D == 64 || a.D == 128 || a.D == 32) && (a.dt == DType::F32 || a.dt == DType::F16 || a.dt == DType::BF16);
@@ -172,13 +478,26 @@ void attention(const Attn& a, hipStream_t s) {
   if (a.B * a.H * a.Tq == 0) return;
   AArgs p{};
   p.q = a.q; p.k = a.k; p.v = a.v; p.o = a.o;
-  p.H = a.H; p.Tq = a.Tq; p.Tk = a.Tk;
+  p.B = a.B; p.H = a.H; p.Tq = a.Tq; p.Tk = a.Tk;
   p.q_sb = a.q_sb; p.q_sh = a.q_sh; p.q_st = a.q_st;
   p.k_sb = a.k_sb; p.k_sh = a.k_sh; p.k_st = a.k_st;
   p.v_sb = a.v_sb; p.v_sh = a.v_sh; p.v_st = a.v_st;
   p.o_sb = a.o_sb; p.o_sh = a.o_sh; p.o_st = a.o_st;
   p.scale = a.scale;
   p.causal = a.causal ? 1 : 0;
+  if (attention_mfma_ok(a)) {
+    // 128 query rows per block when that still gives every CU a block
+    const int64_t bh = a.B * a.H;
+    const bool wide = bh * ((a.Tq + 127) / 128) >= 256;
+    const int qb = wide ? 128 : 64;
+    p.q_tiles = (int)((a.Tq + qb - 1) / qb);
+    const int64_t blocks = bh * p.q_tiles;
+    if (blocks > 0x7fffffff) fail("fused attention: grid too large");
+    if (a.dt == DType::F16) launch_fa_mfma<half_t>(p, a.D, wide, (unsigned)blocks, s);
+    else launch_fa_mfma<bf16_t>(p, a.D, wide, (unsigned)blocks, s);
+    check_launch("attention");
+    return;
+  }
   p.q_tiles = (int)((a.Tq + kQT - 1) / kQT);
   int64_t blocks = a.B * a.H * p.q_tiles;
   if (blocks > 0x7fffffff) fail("fused attention: grid too large");
