@@ -369,112 +369,251 @@ __global__ void __launch_bounds__(256) gemm_mf(GArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  GLoad<TI, BM, BK, AK> ga;
-  GLoad<TB, BN, BK, BKC> gb;
-  auto put = [&](auto masked, int stage) {
-    constexpr bool MK = decltype(masked)::value;
-    E* s = lds + stage * STAGE;
-    if constexpr (X3) {
-      ga.template store_split<MK>(s, s + AE, LD);
-      gb.template store_split<MK>(s + 2 * AE, s + 2 * AE + BE, LD, bscale);
-    } else {
-      ga.template store_plain<MK>(s, LD);
-      gb.template store_plain<MK>(s + AE, LD);
-    }
-  };
-  auto fetch_edge = [&](int64_t k, int64_t kmax) {
-    ga.load_edge(A, p.a_sm, p.a_sk, m0, p.M, k, kmax);
-    gb.load_edge(B, p.b_sn, p.b_sk, n0, p.N, k, kmax);
-  };
-  auto fetch_fast = [&](int64_t k) {
-    ga.load_fast(A, p.a_sm, p.a_sk, m0, p.M, k);
-    gb.load_fast(B, p.b_sn, p.b_sk, n0, p.N, k);
-  };
-
-  typedef typename Mfma32<E>::vec V8;
-  auto compute = [&](int buf) {
-    const E* s = lds + buf * STAGE;
-    const E* a_hi = s;
-    const E* b_hi = s + NA * AE;
-#pragma unroll
-    for (int ks = 0; ks < KW; ks += 16) {
-      const int ko = wk * KW + ks + 8 * (lane >> 5);
-      V8 ah[TM], bh[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) ah[i] = *(const V8*)&a_hi[(wm + i * 32 + (lane & 31)) * LD + ko];
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bh[j] = *(const V8*)&b_hi[(wn + j * 32 + (lane & 31)) * LD + ko];
+  // PD = 2 for fp32 operands on the fast path (below); 16-bit operands and
+  // the masked-load variant keep the one-set loop in the else branch (with
+  // two sets the compiler put their loaders' arrays in scratch memory).
+  constexpr int PD = X3 && FAST ? 2 : 1;
+  if constexpr (PD == 2) {
+    // Two register sets of operand slices: slice s is fetched into set s % 2
+    // two slices before it is multiplied, so while slice kt is multiplied the
+    // loads of slices kt+1 and kt+2 are both in flight (at the fp32 shapes of
+    // the workloads the loop is bound by load latency, not by the MFMAs).
+    GLoad<TI, BM, BK, AK> ga0, ga1;
+    GLoad<TB, BN, BK, BKC> gb0, gb1;
+    auto put = [&](auto masked, int stage, const auto& la, const auto& lb) __attribute__((always_inline)) {
+      constexpr bool MK = decltype(masked)::value;
+      E* s = lds + stage * STAGE;
       if constexpr (X3) {
-        const E* a_lo = s + AE;
-        const E* b_lo = s + 2 * AE + BE;
-        V8 al[TM], bl[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) al[i] = *(const V8*)&a_lo[(wm + i * 32 + (lane & 31)) * LD + ko];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bl[j] = *(const V8*)&b_lo[(wn + j * 32 + (lane & 31)) * LD + ko];
-        // small terms first, then hi*hi
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(al[i], bh[j], acc[i][j]);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(ah[i], bl[j], acc[i][j]);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(ah[i], bh[j], acc[i][j]);
-    }
-  };
-
-  // Slice schedule.  FAST: an optional masked remainder slice first, then
-  // full slices from k_full.  !FAST: every slice masked.
-  const int64_t span = kend > kbeg ? kend - kbeg : 0;
-  const int64_t tail = FAST ? span % BK : 0;
-  const int64_t k_full = kbeg + tail;
-  const int64_t nk = FAST ? span / BK + (tail ? 1 : 0) : (span + BK - 1) / BK;
-  std::integral_constant<bool, true> masked;
-  std::integral_constant<bool, false> plain;
-  if (nk > 0) {
-    if constexpr (FAST) {
-      if (tail) {
-        fetch_edge(kbeg, k_full);
-        put(masked, 0);
+        la.template store_split<MK>(s, s + AE, LD);
+        lb.template store_split<MK>(s + 2 * AE, s + 2 * AE + BE, LD, bscale);
       } else {
-        fetch_fast(k_full);
-        put(plain, 0);
+        la.template store_plain<MK>(s, LD);
+        lb.template store_plain<MK>(s + AE, LD);
       }
-    } else {
-      fetch_edge(kbeg, kend);
-      put(masked, 0);
-    }
-  }
-  __syncthreads();
+    };
+    auto fetch_edge = [&](auto& la, auto& lb, int64_t k, int64_t kmax) __attribute__((always_inline)) {
+      la.load_edge(A, p.a_sm, p.a_sk, m0, p.M, k, kmax);
+      lb.load_edge(B, p.b_sn, p.b_sk, n0, p.N, k, kmax);
+    };
+    auto fetch_fast = [&](auto& la, auto& lb, int64_t k) __attribute__((always_inline)) {
+      la.load_fast(A, p.a_sm, p.a_sk, m0, p.M, k);
+      lb.load_fast(B, p.b_sn, p.b_sk, n0, p.N, k);
+    };
 
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = ST == 2 ? (int)(kt & 1) : 0;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      if constexpr (FAST) fetch_fast(k_full + (kt + 1 - (tail ? 1 : 0)) * BK);
-      else fetch_edge(kbeg + (kt + 1) * BK, kend);
-    }
-    compute(buf);
-    if constexpr (ST == 2) {
-      if (more) {
-        if constexpr (FAST) put(plain, buf ^ 1);
-        else put(masked, buf ^ 1);
+    typedef typename Mfma32<E>::vec V8;
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+      const E* s = lds + buf * STAGE;
+      const E* a_hi = s;
+      const E* b_hi = s + NA * AE;
+  #pragma unroll
+      for (int ks = 0; ks < KW; ks += 16) {
+        const int ko = wk * KW + ks + 8 * (lane >> 5);
+        V8 ah[TM], bh[TN];
+  #pragma unroll
+        for (int i = 0; i < TM; ++i) ah[i] = *(const V8*)&a_hi[(wm + i * 32 + (lane & 31)) * LD + ko];
+  #pragma unroll
+        for (int j = 0; j < TN; ++j) bh[j] = *(const V8*)&b_hi[(wn + j * 32 + (lane & 31)) * LD + ko];
+        if constexpr (X3) {
+          const E* a_lo = s + AE;
+          const E* b_lo = s + 2 * AE + BE;
+          V8 al[TM], bl[TN];
+  #pragma unroll
+          for (int i = 0; i < TM; ++i) al[i] = *(const V8*)&a_lo[(wm + i * 32 + (lane & 31)) * LD + ko];
+  #pragma unroll
+          for (int j = 0; j < TN; ++j) bl[j] = *(const V8*)&b_lo[(wn + j * 32 + (lane & 31)) * LD + ko];
+          // small terms first, then hi*hi
+  #pragma unroll
+          for (int i = 0; i < TM; ++i)
+  #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(al[i], bh[j], acc[i][j]);
+  #pragma unroll
+          for (int i = 0; i < TM; ++i)
+  #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(ah[i], bl[j], acc[i][j]);
+        }
+  #pragma unroll
+        for (int i = 0; i < TM; ++i)
+  #pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(ah[i], bh[j], acc[i][j]);
       }
-      __syncthreads();
-    } else {
-      __syncthreads();
-      if (more) {
-        if constexpr (FAST) put(plain, 0);
-        else put(masked, 0);
+    };
+
+    // Slice schedule.  FAST: an optional masked remainder slice 0, then full
+    // slices from k_full.  !FAST: every slice masked.
+    const int64_t span = kend > kbeg ? kend - kbeg : 0;
+    const int64_t tail = FAST ? span % BK : 0;
+    const int64_t k_full = kbeg + tail;
+    const int64_t nk = FAST ? span / BK + (tail ? 1 : 0) : (span + BK - 1) / BK;
+    std::integral_constant<bool, true> masked;
+    std::integral_constant<bool, false> plain;
+    // k of full slice s >= 1 (FAST).  Fetches past the last slice re-read the
+    // last one (legal addresses, no branch around the loads); what they bring
+    // is never multiplied.
+    auto slice_k = [&](int64_t s) __attribute__((always_inline)) {
+      const int64_t c = s < nk ? s : nk - 1;
+      return FAST ? k_full + (c - (tail ? 1 : 0)) * BK : kbeg + c * BK;
+    };
+    auto fetch_main = [&](auto& la, auto& lb, int64_t s) __attribute__((always_inline)) {
+      if constexpr (FAST) fetch_fast(la, lb, slice_k(s));
+      else fetch_edge(la, lb, slice_k(s), kend);
+    };
+    auto put_main = [&](int stage, const auto& la, const auto& lb) __attribute__((always_inline)) {
+      if constexpr (FAST) put(plain, stage, la, lb);
+      else put(masked, stage, la, lb);
+    };
+    if (nk > 0) {
+      if constexpr (FAST) {
+        if (tail) {
+          fetch_edge(ga0, gb0, kbeg, k_full);
+          put(masked, 0, ga0, gb0);
+        } else {
+          fetch_fast(ga0, gb0, k_full);
+          put(plain, 0, ga0, gb0);
+        }
+        if (PD == 2 && nk > 1) fetch_fast(ga1, gb1, slice_k(1));
+      } else {
+        fetch_edge(ga0, gb0, kbeg, kend);
+        put(masked, 0, ga0, gb0);
+        if (PD == 2 && nk > 1) fetch_edge(ga1, gb1, slice_k(1), kend);
+      }
+    }
+    __syncthreads();
+
+    // One slice: fetch slice kt+PD into set F, multiply slice kt, then store
+    // slice kt+1 (set P) into the other LDS stage.  The loop is unrolled by two
+    // so that stages and register sets are compile-time choices.
+    auto iter = [&](int64_t kt, int stage, auto& fa, auto& fb, const auto& pa, const auto& pb) __attribute__((always_inline)) {
+      fetch_main(fa, fb, kt + PD);
+      compute(stage);
+      if constexpr (ST == 2) {
+        put_main(stage ^ 1, pa, pb);
+        __syncthreads();
+      } else {
+        __syncthreads();
+        put_main(0, pa, pb);
         __syncthreads();
       }
+    };
+    {
+      int64_t kt = 0;
+      for (; kt + 1 < nk; kt += 2) {
+        iter(kt, 0, ga0, gb0, ga1, gb1);
+        iter(kt + 1, ST == 2 ? 1 : 0, ga1, gb1, ga0, gb0);
+      }
+      if (kt < nk) {  // odd slice count: the last slice sits in stage 0
+        compute(0);
+        __syncthreads();  // the in-block split-K reduction reuses the stages
+      }
     }
+  } else {
+    GLoad<TI, BM, BK, AK> ga;
+    GLoad<TB, BN, BK, BKC> gb;
+    auto put = [&](auto masked, int stage) {
+      constexpr bool MK = decltype(masked)::value;
+      E* s = lds + stage * STAGE;
+      if constexpr (X3) {
+        ga.template store_split<MK>(s, s + AE, LD);
+        gb.template store_split<MK>(s + 2 * AE, s + 2 * AE + BE, LD, bscale);
+      } else {
+        ga.template store_plain<MK>(s, LD);
+        gb.template store_plain<MK>(s + AE, LD);
+      }
+    };
+    auto fetch_edge = [&](int64_t k, int64_t kmax) {
+      ga.load_edge(A, p.a_sm, p.a_sk, m0, p.M, k, kmax);
+      gb.load_edge(B, p.b_sn, p.b_sk, n0, p.N, k, kmax);
+    };
+    auto fetch_fast = [&](int64_t k) {
+      ga.load_fast(A, p.a_sm, p.a_sk, m0, p.M, k);
+      gb.load_fast(B, p.b_sn, p.b_sk, n0, p.N, k);
+    };
+
+    typedef typename Mfma32<E>::vec V8;
+    auto compute = [&](int buf) {
+      const E* s = lds + buf * STAGE;
+      const E* a_hi = s;
+      const E* b_hi = s + NA * AE;
+  #pragma unroll
+      for (int ks = 0; ks < KW; ks += 16) {
+        const int ko = wk * KW + ks + 8 * (lane >> 5);
+        V8 ah[TM], bh[TN];
+  #pragma unroll
+        for (int i = 0; i < TM; ++i) ah[i] = *(const V8*)&a_hi[(wm + i * 32 + (lane & 31)) * LD + ko];
+  #pragma unroll
+        for (int j = 0; j < TN; ++j) bh[j] = *(const V8*)&b_hi[(wn + j * 32 + (lane & 31)) * LD + ko];
+        if constexpr (X3) {
+          const E* a_lo = s + AE;
+          const E* b_lo = s + 2 * AE + BE;
+          V8 al[TM], bl[TN];
+  #pragma unroll
+          for (int i = 0; i < TM; ++i) al[i] = *(const V8*)&a_lo[(wm + i * 32 + (lane & 31)) * LD + ko];
+  #pragma unroll
+          for (int j = 0; j < TN; ++j) bl[j] = *(const V8*)&b_lo[(wn + j * 32 + (lane & 31)) * LD + ko];
+          // small terms first, then hi*hi
+  #pragma unroll
+          for (int i = 0; i < TM; ++i)
+  #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(al[i], bh[j], acc[i][j]);
+  #pragma unroll
+          for (int i = 0; i < TM; ++i)
+  #pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(ah[i], bl[j], acc[i][j]);
+        }
+  #pragma unroll
+        for (int i = 0; i < TM; ++i)
+  #pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = Mfma32<E>::run(ah[i], bh[j], acc[i][j]);
+      }
+    };
+
+    // Slice schedule.  FAST: an optional masked remainder slice first, then
+    // full slices from k_full.  !FAST: every slice masked.
+    const int64_t span = kend > kbeg ? kend - kbeg : 0;
+    const int64_t tail = FAST ? span % BK : 0;
+    const int64_t k_full = kbeg + tail;
+    const int64_t nk = FAST ? span / BK + (tail ? 1 : 0) : (span + BK - 1) / BK;
+    std::integral_constant<bool, true> masked;
+    std::integral_constant<bool, false> plain;
+    if (nk > 0) {
+      if constexpr (FAST) {
+        if (tail) {
+          fetch_edge(kbeg, k_full);
+          put(masked, 0);
+        } else {
+          fetch_fast(k_full);
+          put(plain, 0);
+        }
+      } else {
+        fetch_edge(kbeg, kend);
+        put(masked, 0);
+      }
+    }
+    __syncthreads();
+
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int buf = ST == 2 ? (int)(kt & 1) : 0;
+      const bool more = kt + 1 < nk;
+      if (more) {
+        if constexpr (FAST) fetch_fast(k_full + (kt + 1 - (tail ? 1 : 0)) * BK);
+        else fetch_edge(kbeg + (kt + 1) * BK, kend);
+      }
+      compute(buf);
+      if constexpr (ST == 2) {
+        if (more) {
+          if constexpr (FAST) put(plain, buf ^ 1);
+          else put(masked, buf ^ 1);
+        }
+        __syncthreads();
+      } else {
+        __syncthreads();
+        if (more) {
+          if constexpr (FAST) put(plain, 0);
+          else put(masked, 0);
+          __syncthreads();
+        }
+      }
+    }
+
   }
 
   // In-block split-K: waves wk > 0 hand their partial sums to wave wk = 0
