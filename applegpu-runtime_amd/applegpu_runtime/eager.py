@@ -157,5 +157,22 @@ def op(name: str, tensors, f=(), i=(), nout=1):
     return res[0] if nout == 1 else tuple(res)
 
 
+def sgd_matmul_(w, a, b, ta=False, tb=False, alpha=1.0):
+    """w += alpha * op(a) @ op(b) in place: an SGD weight step fused with its
+    gradient GEMM (the update runs in the GEMM's epilogue)."""
+    op("sgd_matmul_", [w, a, b], f=(float(alpha),), i=(int(ta), int(tb)))
+
+
+def sgd_sum_rows_(bias, g, alpha=1.0):
+    """bias += alpha * g.sum(0) in place: an SGD bias step fused with its
+    gradient reduction."""
+    op("sgd_sum_rows_", [bias, g], f=(float(alpha),))
+
+
+def mse_loss_grad(out, y):
+    """(mean((out - y)^2), d loss / d out) in one launch."""
+    return op("mse_loss_grad", [out, y], nout=2)
+
+
 def synchronize():
     lib.applegpu_eager_flush_and_wait()

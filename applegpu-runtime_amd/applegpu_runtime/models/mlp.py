@@ -10,10 +10,14 @@ weight and input gradients, threshold_backward (relu'), sum over the batch
 through the eager C ABI, with the fusions the MI355X backend offers:
 
   forward   h = relu(x W^T + b)        one GEMM, bias + relu in the epilogue
+  loss      mse and dL/dout             one launch
   backward  dh = (g W) * (h > 0)        one GEMM, relu' mask in the epilogue
-            dW = g^T h                  one GEMM, transposed A read in place
-            db = sum(g, 0)              column reduction
-  SGD       p += -lr * grad             one axpy per parameter
+  + SGD     W += -lr * g^T h            one GEMM, the update in its epilogue
+            b += -lr * sum(g, 0)        one column reduction
+(the output layer's 4096 -> 1 products run on the unit-extent GEMM kernels).
+Every gradient is formed from the step's starting parameters, as autograd
+does: layer i's input gradient (which reads W_i) is computed before W_i is
+updated in place.
 
 Parameters follow torch.nn.Linear's layout (W [out, in], b [out]).
 """
@@ -57,6 +61,21 @@ class EagerMLP:
     def train_step(self, x, y, lr=0.01):
         """One forward + MSE + backward + SGD step; returns the loss tensor (on device)."""
         out, acts = self.forward(x)
+        loss, g = E.mse_loss_grad(out, y)
+        for i in range(len(self.params) - 1, -1, -1):
+            w, b = self.params[i]
+            # dL/d(input of layer i) masked by relu' of the previous layer's
+            # output, from W_i before its update
+            g_in = E.matmul_masked(g, w, False, False, acts[i]) if i > 0 else None
+            E.sgd_matmul_(w, g, acts[i], True, False, -lr)   # W_i -= lr * g^T a_i
+            E.sgd_sum_rows_(b, g, -lr)                        # b_i -= lr * sum(g, 0)
+            g = g_in
+        return loss
+
+    def train_step_unfused(self, x, y, lr=0.01):
+        """The same step with every gradient materialised and one axpy per
+        parameter (the reference's aten sequence); kept for comparison."""
+        out, acts = self.forward(x)
         loss = E.mse_loss(out, y)
         g = E.mse_loss_backward(self._one, out, y)
         grads = [None] * len(self.params)
@@ -67,7 +86,6 @@ class EagerMLP:
             db = E.sum_dim(g, 0, False)
             grads[i] = (dw, db)
             if i > 0:
-                # dL/d(input of layer i) masked by relu' of the previous layer's output
                 g = E.matmul_masked(g, w, False, False, acts[i])
         for (w, b), (dw, db) in zip(self.params, grads):
             E.add_(w, dw, -lr)

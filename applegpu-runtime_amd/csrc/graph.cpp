@@ -31,6 +31,7 @@ enum Op : int {
   OP_WHERE, OP_MASKED_FILL, OP_TRIU, OP_TRIL,
   OP_QUANTIZE_PER_ROW, OP_DEQUANTIZE_PER_ROW, OP_LINEAR_INT8, OP_CONTIGUOUS, OP_FULL,
   OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
+  OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD,
   OP_COUNT
 };
 
@@ -48,6 +49,7 @@ static const char* kNames[OP_COUNT] = {
     "where", "masked_fill", "triu", "tril",
     "quantize_per_row", "dequantize_per_row", "linear_int8", "contiguous", "full",
     "decode_attention", "pack_weight", "matmul_packed",
+    "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad",
 };
 
 int op_code(const char* name) {
@@ -65,7 +67,7 @@ int op_code(const char* name) {
   return it == m.end() ? -1 : it->second;
 }
 const char* op_name(int code) { return code >= 0 && code < OP_COUNT ? kNames[code] : "?"; }
-int op_outputs(int code) { return code == OP_QUANTIZE_PER_ROW ? 2 : 1; }
+int op_outputs(int code) { return code == OP_QUANTIZE_PER_ROW || code == OP_MSE_LOSS_GRAD ? 2 : 1; }
 
 static void need(const std::vector<TensorP>& in, size_t n, int code) {
   if (in.size() != n) fail("%s expects %zu tensor inputs, got %zu", op_name(code), n, in.size());
@@ -195,6 +197,15 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
     case OP_DECODE_ATTENTION: need(in, 4, code); return {decode_attention(in[0], in[1], in[2], in[3])};
     case OP_PACK_WEIGHT: need(in, 1, code); return {pack_weight(in[0])};
     case OP_MATMUL_PACKED: need(in, 2, code); return {matmul_packed(in[0], in[1], ip(iv, 0, code))};
+    case OP_SGD_MATMUL:
+      need(in, 3, code);
+      return {sgd_matmul_(in[0], in[1], in[2], iv.size() > 0 && iv[0], iv.size() > 1 && iv[1], (float)fp(f, 0, code))};
+    case OP_SGD_SUM_ROWS: need(in, 2, code); return {sgd_sum_rows_(in[0], in[1], (float)fp(f, 0, code))};
+    case OP_MSE_LOSS_GRAD: {
+      need(in, 2, code);
+      auto lg = mse_loss_grad(in[0], in[1]);
+      return {lg.first, lg.second};
+    }
     case OP_CONTIGUOUS: {
       need(in, 1, code);
       TensorP c = contiguous(in[0]);
@@ -220,6 +231,8 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
 // ── lazy recording ─────────────────────────────────────────────────────────
 std::vector<TensorP> record_op(int code, const std::vector<TensorP>& in, const std::vector<double>& f,
                                const std::vector<int64_t>& iv) {
+  if (code == OP_SGD_MATMUL || code == OP_SGD_SUM_ROWS)
+    fail("%s updates its first operand in place: eager only", op_name(code));
   std::vector<TensorP> metas;
   {
     MetaScope ms;

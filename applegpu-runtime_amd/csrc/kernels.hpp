@@ -84,6 +84,11 @@ void reduce_all(int kind, DType dt, const void* a, const void* b, int64_t n, flo
 // MSE backward: dx = (a - b) * (2/n) * g[0]   (g: one element of dtype dt)
 void mse_backward(DType dt, const void* a, const void* b, const void* g, void* dx, int64_t n,
                   hipStream_t s);
+// y[c] += alpha * sum_r x[r, c] over a contiguous [rows, cols] x (SGD bias step).
+void sum_rows_axpy(DType dt, const void* x, void* y, int64_t rows, int64_t cols, float alpha, hipStream_t s);
+// MSE loss and gradient (upstream gradient 1) in one launch, n <= 65536.
+bool mse_fused_ok(int64_t n);
+void mse_loss_grad(DType dt, const void* a, const void* b, void* loss, void* grad, int64_t n, hipStream_t s);
 
 // ── indexing ──────────────────────────────────────────────────────────────
 void embedding(DType dt, const void* w, int64_t vocab, int64_t dim, DType idx_dt,

@@ -314,10 +314,14 @@ Plan make_plan(const Gemm& g, int cus) {
     } else {
       // Measured on MI355X (fp32 via bf16x3 and fp16, shapes of the GPT-2,
       // MLP and int8 workloads): 128x128 tiles win once they alone give every
-      // CU a block (fp16: with 64-deep K slices); below that, 64x64 tiles
-      // with 64-deep K slices, split across blocks until about two blocks
-      // per CU.
-      pl.cfg = tiles_for(g, 128, 128) >= cus ? (is16 ? 5 : 0) : 6;
+      // CU a block (fp16: with 64-deep K slices), and for fp32 with M >= 256
+      // and K >= 2048 when up to 8 K splits make two blocks per CU (the MLP
+      // layers); otherwise 64x64 tiles with 64-deep K slices, split across
+      // blocks until about two blocks per CU.
+      const int64_t t128 = tiles_for(g, 128, 128);
+      if (t128 >= cus) pl.cfg = is16 ? 5 : 0;
+      else if (!is16 && g.M >= 256 && g.K >= 2048 && t128 * 8 >= 2LL * cus) pl.cfg = 0;
+      else pl.cfg = 6;
     }
     pl.bm = kMfShape[pl.cfg].bm;
     pl.bn = kMfShape[pl.cfg].bn;
@@ -330,8 +334,12 @@ Plan make_plan(const Gemm& g, int cus) {
     splits = tu.splits;
   } else if (pl.kind == kMf) {
     // Split K across blocks while the grid is short of two blocks per CU and
-    // every split keeps at least 3 K slices (at most 8 splits).
-    while (tiles * splits < 2LL * cus && nk / (splits * 2) >= 3 && splits < 8) splits *= 2;
+    // every split keeps at least 3 K slices (at most 8 splits).  A grid that
+    // already gives every CU a block is not split: the reduction pass over
+    // the whole output costs more than the second block per CU gains (LM
+    // head 128 x 50257: 62 us unsplit, 88 us in two splits).
+    if (tiles < cus)
+      while (tiles * splits < 2LL * cus && nk / (splits * 2) >= 3 && splits < 8) splits *= 2;
   } else {
     while (tiles * splits * 2 <= cus && nk / (splits * 2) >= 8 && splits < 32) splits *= 2;
   }
@@ -414,6 +422,10 @@ const char* gemm_plan_name(const Gemm& g) {
     snprintf(buf, sizeof buf, "skinny mfma16 blocks=%lld", (long long)sp.blocks);
     return buf;
   }
+  if (const int tk = thin_kind(g)) {
+    snprintf(buf, sizeof buf, "thin %s", tk == kThinN1 ? "n1" : tk == kThinM1 ? "m1" : "k1");
+    return buf;
+  }
   Plan pl = make_plan(g, cu_count());
   const char* kind = pl.kind == kGeneric ? "generic" : pl.kind == kNative32 ? "f32-native" : "mf";
   snprintf(buf, sizeof buf, "%s cfg%d %dx%dx%d splits=%d", kind, pl.kind == kMf ? pl.cfg : -1, pl.bm, pl.bn, pl.bk,
@@ -423,7 +435,7 @@ const char* gemm_plan_name(const Gemm& g) {
 
 size_t gemm_workspace_bytes(const Gemm& g) {
   const SkinnyPlan sp = skinny_plan(g, cu_count());
-  if (sp.use) return 0;
+  if (sp.use || thin_kind(g)) return 0;
   Plan pl = make_plan(g, cu_count());
   if (pl.splits <= 1) return 0;
   return (size_t)pl.splits * g.batch * g.M * g.N * sizeof(float);
@@ -438,6 +450,14 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     one.splits = 1;
     one.kps = g.K;
     gemm_skinny(g, sp, make_args(g, one), s);
+    return;
+  }
+  if (const int tk = thin_kind(g)) {
+    Plan one{};
+    one.bm = one.bn = 1;
+    one.splits = 1;
+    one.kps = g.K;
+    gemm_thin(tk, g.dt, make_args(g, one), s);
     return;
   }
   if (g.ln_gamma) fail("gemm: a layer-norm prologue needs the skinny kernel");

@@ -727,6 +727,12 @@ struct SkinnyPlan {
 SkinnyPlan skinny_plan(const Gemm& g, int cus);
 void gemm_skinny(const Gemm& g, const SkinnyPlan& pl, const GArgs& p, hipStream_t s);
 
+// GEMMs with a unit extent (gemm_thin.hip): N == 1, M == 1 (fp32, B rows
+// contiguous along n) or K == 1; kThinNone when the problem is not one.
+enum { kThinNone = 0, kThinN1, kThinM1, kThinK1 };
+int thin_kind(const Gemm& g);
+void gemm_thin(int kind, DType dt, const GArgs& p, hipStream_t s);
+
 // Defined in gemm_mf_{f32,f16,bf16}_{fast,edge}.hip.
 void launch_mf_f32(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);
 void launch_mf_f16(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);

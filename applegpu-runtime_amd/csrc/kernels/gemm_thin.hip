@@ -1,0 +1,108 @@
+// GEMMs with a unit extent, where MFMA tiles would be almost all padding:
+//   N == 1: matrix-vector, C[b, m] = sum_k A[b, m, k] B[b, k]  (one wavefront
+//           per output row, a shuffle reduction);
+//   M == 1: vector-matrix with B rows contiguous along n, C[b, n] =
+//           sum_k A[b, k] B[b, k, n]  (a 1024-thread block per 64 columns,
+//           16 k slices reduced through LDS in slice order);
+//   K == 1: outer product, C[b, m, n] = A[b, m] B[b, n]  (elementwise).
+// Same arithmetic as the reference's matmul/linear (fp32 accumulation,
+// crates/core/src/kernel_templates.rs:987-1072) and the same fused epilogue
+// as the tiled kernels (alpha, bias, activation, residual, mask).  In the
+// C3 MLP step these are the forward and both backward products of the
+// 4096 -> 1 output layer.
+#include "gemm_kernels.hpp"
+
+namespace agpu {
+namespace k {
+using namespace dev;
+
+namespace {
+
+template <typename T>
+__global__ void __launch_bounds__(256) gemv_n1(GArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t b = blockIdx.y;
+  if (m >= p.M) return;  // a whole wavefront; the kernel has no barrier
+  const T* A = (const T*)p.A + b * p.a_sb + m * p.a_sm;
+  const T* B = (const T*)p.B + b * p.b_sb;
+  float acc = 0.f;
+#pragma unroll 8
+  for (int64_t k = lane; k < p.K; k += 64) acc += to_f(A[k * p.a_sk]) * to_f(B[k * p.b_sk]);
+  acc = wave_sum(acc);
+  if (lane == 0) epilogue_store<T>(p, b, m, 0, acc);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(1024) gevm_m1(GArgs p) {
+  __shared__ float sh[16][64];
+  const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t b = blockIdx.y;
+  const T* A = (const T*)p.A + b * p.a_sb;
+  const T* B = (const T*)p.B + b * p.b_sb;
+  float s = 0.f;
+  if (n < p.N) {
+#pragma unroll 8
+    for (int64_t k = slice; k < p.K; k += 16) s += to_f(A[k * p.a_sk]) * to_f(B[k * p.b_sk + n]);
+  }
+  sh[slice][lane] = s;
+  __syncthreads();
+  if (slice == 0 && n < p.N) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += sh[i][lane];
+    epilogue_store<T>(p, b, 0, n, t);
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) outer_k1(GArgs p) {
+  const int64_t b = blockIdx.y;
+  const int64_t total = p.M * p.N;
+  const T* A = (const T*)p.A + b * p.a_sb;
+  const T* B = (const T*)p.B + b * p.b_sb;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / p.N, n = i % p.N;
+    epilogue_store<T>(p, b, m, n, to_f(A[m * p.a_sm]) * to_f(B[n * p.b_sn]));
+  }
+}
+
+}  // namespace
+
+int thin_kind(const Gemm& g) {
+  const bool fl = g.dt == DType::F32 || g.dt == DType::F16 || g.dt == DType::BF16;
+  if (!fl || g.b_dt != g.dt || g.b_scale || g.ln_gamma || g.b_packed || g.batch > 65535) return kThinNone;
+  if (g.K == 1) return kThinK1;
+  if (g.N == 1) return kThinN1;
+  if (g.M == 1 && g.dt == DType::F32 && g.b_sn == 1) return kThinM1;
+  return kThinNone;
+}
+
+void gemm_thin(int kind, DType dt, const GArgs& p, hipStream_t s) {
+  const unsigned nb = (unsigned)p.batch;
+  switch (kind) {
+    case kThinN1: {
+      dim3 grid((unsigned)((p.M + 3) / 4), nb);
+      AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((gemv_n1<T>), grid, dim3(256), 0, s, p));
+      break;
+    }
+    case kThinM1: {
+      dim3 grid((unsigned)((p.N + 63) / 64), nb);
+      AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((gevm_m1<T>), grid, dim3(1024), 0, s, p));
+      break;
+    }
+    case kThinK1: {
+      int64_t blocks = (p.M * p.N + 255) / 256;
+      if (blocks > 4096) blocks = 4096;
+      dim3 grid((unsigned)blocks, nb);
+      AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((outer_k1<T>), grid, dim3(256), 0, s, p));
+      break;
+    }
+    default: fail("gemm_thin: not a thin shape");
+  }
+  check_launch("gemm_thin");
+}
+
+}  // namespace k
+}  // namespace agpu

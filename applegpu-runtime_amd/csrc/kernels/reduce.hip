@@ -31,24 +31,34 @@ __global__ void __launch_bounds__(256) sum_last(const T* __restrict__ x, T* __re
   if (lane == 0) y[row] = from_f<T>(s * scale);
 }
 
-// Column sums: a 256-thread block covers 64 columns x 4 row-slices, then the
-// four partial sums meet in LDS.
+// Column sums: a 1024-thread block covers 64 columns x 16 row slices (each
+// thread's loads are independent, so they are all in flight), then the 16
+// partial sums meet in LDS and are added in slice order.  acc != 0 adds the
+// scaled sum to y instead of storing it (y += scale * sum: the bias update
+// of an SGD step fused with its gradient).
 template <typename T>
-__global__ void __launch_bounds__(256) sum_cols(const T* __restrict__ x, T* __restrict__ y, int64_t outer,
-                                                int64_t red, int64_t inner, float scale) {
-  __shared__ float sh[4][64];
+__global__ void __launch_bounds__(1024) sum_cols(const T* __restrict__ x, T* __restrict__ y, int64_t outer,
+                                                 int64_t red, int64_t inner, float scale, int acc) {
+  __shared__ float sh[16][64];
   const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
   const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   const int64_t o = blockIdx.y;
   float s = 0.f;
   if (col < inner) {
     const T* base = x + o * red * inner + col;
-    for (int64_t r = slice; r < red; r += 4) s += to_f(base[r * inner]);
+#pragma unroll 8
+    for (int64_t r = slice; r < red; r += 16) s += to_f(base[r * inner]);
   }
   sh[slice][lane] = s;
   __syncthreads();
-  if (slice == 0 && col < inner)
-    y[o * inner + col] = from_f<T>((sh[0][lane] + sh[1][lane] + sh[2][lane] + sh[3][lane]) * scale);
+  if (slice == 0 && col < inner) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += sh[i][lane];
+    float v = t * scale;
+    if (acc) v += to_f(y[o * inner + col]);
+    y[o * inner + col] = from_f<T>(v);
+  }
 }
 
 template <typename T>
@@ -103,6 +113,34 @@ __global__ void __launch_bounds__(256) mse_bwd_kernel(const T* __restrict__ a, c
   const float gs = to_f(g[0]);
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
     dx[i] = from_f<T>((to_f(a[i]) - to_f(b[i])) * two_over_n * gs);
+}
+
+// MSE loss and its gradient (upstream gradient 1) in one single-block
+// launch, for the small outputs of a training step: loss = sum((a-b)^2) / n
+// (the 1024 per-thread partial sums are reduced in a fixed order) and
+// grad = (a - b) * 2/n, the expressions of reduce_stage1/2 and
+// mse_bwd_kernel.
+constexpr int kMseFusedMax = 1 << 16;
+template <typename T>
+__global__ void __launch_bounds__(1024) mse_fused_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                         T* __restrict__ loss, T* __restrict__ grad, int64_t n,
+                                                         float inv_n, float two_over_n) {
+  __shared__ float sh[16];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+    const float d = to_f(a[i]) - to_f(b[i]);
+    s += d * d;
+    grad[i] = from_f<T>(d * two_over_n * 1.f);
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += sh[i];
+    loss[0] = from_f<T>(t * inv_n);
+  }
 }
 
 // Rows with an index outside [0, vocab) come out as zeros.
@@ -163,8 +201,8 @@ void sum_dim(DType dt, const void* x, void* y, int64_t outer, int64_t red, int64
   } else {
     if (outer > 65535) fail("sum_dim: outer extent %lld too large", (long long)outer);
     dim3 grid((unsigned)((inner + 63) / 64), (unsigned)outer);
-    AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((sum_cols<T>), grid, dim3(256), 0, s, (const T*)x, (T*)y, outer,
-                                             red, inner, scale));
+    AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((sum_cols<T>), grid, dim3(1024), 0, s, (const T*)x, (T*)y, outer,
+                                             red, inner, scale, 0));
   }
   check_launch("sum_dim");
 }
@@ -191,6 +229,24 @@ void mse_backward(DType dt, const void* a, const void* b, const void* g, void* d
   AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((mse_bwd_kernel<T>), dim3(grid_for(n)), dim3(256), 0, s, (const T*)a,
                                            (const T*)b, (const T*)g, (T*)dx, n, two_over_n));
   check_launch("mse_backward");
+}
+
+void sum_rows_axpy(DType dt, const void* x, void* y, int64_t rows, int64_t cols, float alpha, hipStream_t s) {
+  if (cols == 0) return;
+  dim3 grid((unsigned)((cols + 63) / 64), 1);
+  AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((sum_cols<T>), grid, dim3(1024), 0, s, (const T*)x, (T*)y, (int64_t)1,
+                                           rows, cols, alpha, 1));
+  check_launch("sum_rows_axpy");
+}
+
+bool mse_fused_ok(int64_t n) { return n > 0 && n <= kMseFusedMax; }
+
+void mse_loss_grad(DType dt, const void* a, const void* b, void* loss, void* grad, int64_t n, hipStream_t s) {
+  if (!mse_fused_ok(n)) fail("mse_loss_grad: %lld elements (one block handles at most %d)", (long long)n,
+                             kMseFusedMax);
+  AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((mse_fused_kernel<T>), dim3(1), dim3(1024), 0, s, (const T*)a,
+                                           (const T*)b, (T*)loss, (T*)grad, n, 1.f / (float)n, 2.f / (float)n));
+  check_launch("mse_loss_grad");
 }
 
 void embedding(DType dt, const void* w, int64_t vocab, int64_t dim, DType idx_dt, const void* idx, int64_t n,

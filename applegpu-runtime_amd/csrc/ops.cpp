@@ -596,6 +596,41 @@ TensorP mse_loss_backward(const TensorP& g, const TensorP& a, const TensorP& b) 
   return out;
 }
 
+std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b) {
+  if (a->dims() != b->dims()) fail("mse_loss_grad: shape mismatch %s vs %s", shape_str(a->dims()).c_str(),
+                                   shape_str(b->dims()).c_str());
+  if (a->dtype != b->dtype) fail("mse_loss_grad: dtype mismatch");
+  check_dtype("mse_loss_grad", kFloatOnly, a->dtype);
+  const int64_t n = a->numel();
+  if (!k::mse_fused_ok(n)) {
+    TensorP one = full(a->dtype, {1}, 1.f);
+    return {mse_loss(a, b), mse_loss_backward(one, a, b)};
+  }
+  TensorP ac = contiguous(a), bc = contiguous(b);
+  TensorP loss = alloc_out(a->dtype, {1});
+  TensorP grad = alloc_out(a->dtype, a->dims());
+  LAUNCH k::mse_loss_grad(a->dtype, ac->data(), bc->data(), loss->data(), grad->data(), n, rt().stream());
+  return {loss, grad};
+}
+
+TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha) {
+  if (w->ndim != 2) fail("sgd_matmul_: the parameter must be 2-D");
+  Epilogue e;
+  e.alpha = alpha;
+  e.residual = w;
+  return matmul(a, b, ta, tb, &e, w);
+}
+
+TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha) {
+  check_dtype("sgd_sum_rows_", kFloatOnly, g->dtype);
+  if (g->ndim != 2 || bias->dtype != g->dtype || bias->numel() != g->shape[1] || !bias->is_contiguous())
+    fail("sgd_sum_rows_: bias must be a contiguous [%lld] tensor of the gradient's dtype",
+         (long long)(g->ndim == 2 ? g->shape[1] : -1));
+  TensorP gc = contiguous(g);
+  LAUNCH k::sum_rows_axpy(g->dtype, gc->data(), bias->data(), gc->shape[0], gc->shape[1], alpha, rt().stream());
+  return bias;
+}
+
 // ── indexing ───────────────────────────────────────────────────────────────
 TensorP embedding(const TensorP& w, const TensorP& idx) {
   if (w->ndim != 2) fail("embedding weights must be 2D [vocab_size, embed_dim]");
@@ -754,7 +789,7 @@ static void set_epilogue(k::Gemm& g, const Epilogue* epi, const std::vector<int6
   if (epi->mask) side(epi->mask, &g.mask, &g.k_sm, &g.k_sb, &keep->mask);
 }
 
-TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi) {
+TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi, const TensorP& into) {
   TensorP a = ta ? transpose_dims(a_in, a_in->ndim - 2, a_in->ndim - 1) : a_in;
   TensorP b = tb ? transpose_dims(b_in, b_in->ndim - 2, b_in->ndim - 1) : b_in;
   if (a_in->ndim < 2 || b_in->ndim < 2) fail("matmul requires at least 2D tensors, got %s and %s",
@@ -794,7 +829,16 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
     b = ex;
     batch_stride(*b, bdims, &b_sb);
   }
-  TensorP out = alloc_out(a->dtype, od);
+  TensorP out;
+  if (into) {
+    // caller-provided output (may also be the residual: each output element
+    // is read and written by the same thread of the epilogue)
+    if (into->dtype != a->dtype || into->dims() != od || !into->is_contiguous())
+      fail("matmul: output must be a contiguous %s tensor of shape %s", dtype_name(a->dtype), shape_str(od).c_str());
+    out = into;
+  } else {
+    out = alloc_out(a->dtype, od);
+  }
 
   k::Gemm g;
   g.dt = a->dtype;
@@ -820,7 +864,7 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
     if (!ok) {
       Epilogue plain = *epi;
       plain.ln_gamma = plain.ln_beta = nullptr;
-      return matmul(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), b_in, ta, tb, &plain);
+      return matmul(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), b_in, ta, tb, &plain, into);
     }
   }
   EpiKeep keep;

@@ -75,7 +75,14 @@ struct Epilogue {
   float ln_eps = 1e-5f;
 };
 TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = false,
-               const Epilogue* epi = nullptr);
+               const Epilogue* epi = nullptr, const TensorP& into = nullptr);
+// SGD steps fused with their gradients, in place:
+//   w += alpha * op(a) op(b)   (the weight gradient GEMM; w contiguous 2-D)
+//   bias += alpha * sum(g, 0)  (g contiguous [rows, N])
+TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha);
+TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha);
+// MSE loss and its gradient (upstream gradient 1): {loss [1], grad like a}.
+std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b);
 // Decode-step weights: wt [out N, in K] (fp16/bf16) rearranged for the skinny
 // GEMM (the operands of one wave instruction contiguous), and x [M <= 16, K]
 // times it: out [M, N] = epilogue(x @ wt^T).

@@ -1,0 +1,156 @@
+"""The fused pieces of the MLP training step and the unit-extent GEMM kernels
+against the oracle and against the unfused sequence they replace:
+
+  - GEMMs with N == 1, M == 1 or K == 1 (matrix-vector, vector-matrix, outer
+    product) with the fused epilogue (bias, relu, residual, mask), fp32 and
+    16-bit, batched;
+  - w += alpha * op(a) op(b) in the GEMM epilogue (sgd_matmul_), also with
+    split-K and in the MLP's transposed-A layout;
+  - bias += alpha * sum(g, 0) (sgd_sum_rows_);
+  - MSE loss and gradient in one launch (mse_loss_grad);
+  - the fused MLP step against the unfused one (materialised gradients, one
+    axpy per parameter: the reference's aten sequence,
+    backend_cpp/applegpu_backend.cpp:533-566, 801-895)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(9090)
+
+
+def f32(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def _plan(M, N, K, a_kcontig=True, b_kcontig=False, dt=0):
+    from applegpu_runtime._native import lib
+    buf = ctypes.create_string_buffer(96)
+    assert lib.applegpu_ffi_gemm_plan(M, N, K, 1, dt, a_kcontig, b_kcontig, buf, 96) == 0
+    return buf.value.decode()
+
+
+def test_thin_plans():
+    assert _plan(256, 1, 4096) == "thin n1"
+    assert _plan(1, 4096, 256, b_kcontig=False) == "thin m1"
+    assert _plan(256, 4096, 1) == "thin k1"
+    assert not _plan(1, 4096, 768, b_kcontig=True).startswith("thin")  # B not contiguous along n
+    assert not _plan(2, 4096, 256).startswith("thin")
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 4096, 1), (7, 33, 1), (1, 256, 4096), (1, 5, 70), (256, 1, 4096),
+                                   (3, 1, 5), (1, 1, 1), (130, 1, 1)])
+def test_thin_matmul_matches_oracle(gpu, m, k, n):
+    a, b = f32(m, k), f32(k, n)
+    got = (gpu.from_numpy(a) @ gpu.from_numpy(b)).to_numpy()
+    assert rel_err(got, O.matmul(a, b)) < 1e-5
+
+
+@pytest.mark.parametrize("dt,tol", [("float16", 1e-2), ("bfloat16", 1e-2)])
+@pytest.mark.parametrize("m,k,n", [(64, 300, 1), (64, 1, 300)])
+def test_thin_matmul_16bit(gpu, dt, tol, m, k, n):
+    a, b = f32(m, k), f32(k, n)
+    ta, tb = (gpu.cast(gpu.from_numpy(x), dt) for x in (a, b))
+    got = (ta @ tb).to_numpy().astype(np.float32)
+    ref = O.matmul(ta.to_numpy().astype(np.float32), tb.to_numpy().astype(np.float32))
+    assert rel_err(got, ref) < tol
+
+
+def test_thin_batched(gpu):
+    a, b = f32(3, 40, 50), f32(3, 50, 1)
+    got = (gpu.from_numpy(a) @ gpu.from_numpy(b)).to_numpy()
+    assert rel_err(got, O.matmul(a, b)) < 1e-5
+    a, b = f32(3, 40, 1), f32(3, 1, 70)
+    got = (gpu.from_numpy(a) @ gpu.from_numpy(b)).to_numpy()
+    assert rel_err(got, O.matmul(a, b)) < 1e-5
+
+
+def test_thin_epilogues(gpu):
+    """Bias + relu on the matrix-vector kernel (the MLP output layer's forward
+    with a hidden activation) and the relu' mask on the outer product (its
+    input gradient)."""
+    from applegpu_runtime import eager as E
+    x, w, bias = f32(256, 512), f32(1, 512, scale=0.05), f32(1)
+    got = E.linear(E.from_numpy(x), E.from_numpy(w), E.from_numpy(bias), act=1).numpy()
+    ref = np.maximum(x.astype(np.float64) @ w.T.astype(np.float64) + bias, 0)
+    assert rel_err(got, ref) < 1e-5
+    g, w3, h = f32(256, 1), f32(1, 512), f32(256, 512)
+    got = E.matmul_masked(E.from_numpy(g), E.from_numpy(w3), False, False, E.from_numpy(h)).numpy()
+    ref = (g.astype(np.float64) @ w3.astype(np.float64)) * (h > 0)
+    assert rel_err(got, ref) < 1e-6
+    assert (got[h <= 0] == 0).all()
+
+
+@pytest.mark.parametrize("rows,cols,inner", [(4096, 4096, 256), (10, 128, 32), (1, 4096, 256), (300, 70, 1000)])
+def test_sgd_matmul_matches_unfused(gpu, rows, cols, inner):
+    """W -= lr * g^T a, fused into the GEMM epilogue, equals the materialised
+    gradient followed by the axpy (and the float64 oracle)."""
+    from applegpu_runtime import eager as E
+    w0, g, a = f32(rows, cols), f32(inner, rows, scale=0.1), f32(inner, cols)
+    lr = 0.01
+    wf = E.from_numpy(w0)
+    E.sgd_matmul_(wf, E.from_numpy(g), E.from_numpy(a), True, False, -lr)
+    wu = E.from_numpy(w0)
+    E.add_(wu, E.matmul_ex(E.from_numpy(g), E.from_numpy(a), True, False), -lr)
+    fused, unfused = wf.numpy(), wu.numpy()
+    ref = w0.astype(np.float64) - lr * (g.astype(np.float64).T @ a.astype(np.float64))
+    assert rel_err(fused, ref) < 1e-5
+    assert rel_err(fused - w0, ref - w0) < 1e-3  # the update itself: fp32 GEMM bar
+    np.testing.assert_allclose(fused, unfused, rtol=1e-6, atol=1e-6)
+
+
+def test_sgd_matmul_rejects_bad_parameter(gpu):
+    from applegpu_runtime import eager as E
+    w = E.from_numpy(f32(8, 8))
+    with pytest.raises(RuntimeError):
+        E.sgd_matmul_(w, E.from_numpy(f32(4, 9)), E.from_numpy(f32(4, 8)), True, False, -0.1)
+    with pytest.raises(RuntimeError):
+        E.sgd_matmul_(E.from_numpy(f32(4, 2, 2)), E.from_numpy(f32(4, 4)), E.from_numpy(f32(4, 4)), True, False, 1.)
+
+
+@pytest.mark.parametrize("rows,cols", [(256, 4096), (32, 10), (1000, 3), (1, 1)])
+def test_sgd_sum_rows(gpu, rows, cols):
+    from applegpu_runtime import eager as E
+    b0, g = f32(cols), f32(rows, cols)
+    bt = E.from_numpy(b0)
+    E.sgd_sum_rows_(bt, E.from_numpy(g), -0.01)
+    ref = b0.astype(np.float64) - 0.01 * g.astype(np.float64).sum(0)
+    np.testing.assert_allclose(bt.numpy(), ref, rtol=1e-5, atol=1e-6)
+    # the plain column sum (same kernel, store mode) still matches
+    np.testing.assert_allclose(E.sum_dim(E.from_numpy(g), 0).numpy(), g.astype(np.float64).sum(0), rtol=1e-5,
+                               atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [(256, 1), (32, 10), (70000,)])
+def test_mse_loss_grad(gpu, n):
+    from applegpu_runtime import eager as E
+    a, b = f32(*n), f32(*n)
+    loss, grad = E.mse_loss_grad(E.from_numpy(a), E.from_numpy(b))
+    d = a.astype(np.float64) - b
+    np.testing.assert_allclose(loss.numpy(), [np.mean(d * d)], rtol=1e-5)
+    np.testing.assert_allclose(grad.numpy(), 2.0 * d / a.size, rtol=1e-6, atol=1e-9)
+    one = E.from_numpy(np.ones(1, np.float32))
+    np.testing.assert_array_equal(grad.numpy(), E.mse_loss_backward(one, E.from_numpy(a), E.from_numpy(b)).numpy())
+
+
+@pytest.mark.parametrize("sizes,batch", [([64, 128, 10], 32), ([4096, 4096, 4096, 1], 256)])
+def test_fused_mlp_step_matches_unfused(gpu, sizes, batch):
+    from applegpu_runtime import eager as E
+    from applegpu_runtime.models.mlp import EagerMLP, torch_default_init
+    params = torch_default_init(sizes, seed=7)
+    x = RNG.standard_normal((batch, sizes[0]), dtype=np.float32)
+    y = RNG.standard_normal((batch, sizes[-1]), dtype=np.float32)
+    fused, unfused = EagerMLP(params), EagerMLP(params)
+    tx, ty = E.from_numpy(x), E.from_numpy(y)
+    lf = fused.train_step(tx, ty, lr=0.01).numpy()
+    lu = unfused.train_step_unfused(tx, ty, lr=0.01).numpy()
+    np.testing.assert_allclose(lf, lu, rtol=1e-6)
+    for (wf, bf), (wu, bu), (w0, b0) in zip(fused.numpy_params(), unfused.numpy_params(), params):
+        np.testing.assert_allclose(wf, wu, rtol=1e-6, atol=1e-7)
+        np.testing.assert_allclose(bf, bu, rtol=1e-6, atol=1e-7)
+        assert rel_err(wf - w0, wu - w0) < 1e-4
