@@ -352,9 +352,11 @@ void eval(const TensorP& root) {
     for (auto& c : t->node->in)
       if (c->pending()) uses[c.get()]++;
 
-  // GEMM epilogue fusion: matmul -> [add_bias (2-D)] -> [gelu|gelu_exact|relu] -> [add residual].
+  // GEMM epilogue fusion: matmul -> [add_bias (2-D)] -> [gelu|gelu_exact|relu] -> [add residual],
+  // plus a layer_norm of the group's output computed by its split-K reduction.
   std::unordered_map<Tensor*, Group> groups;  // keyed by the group's current final node
   std::unordered_set<Tensor*> absorbed;
+  std::unordered_map<Tensor*, TensorP> post_ln;  // group final node -> layer_norm node reading it
   for (auto& t : order) {
     Node* n = t->node.get();
     if (n->code == OP_ADD_BIAS && t->ndim == 2) {
@@ -367,7 +369,16 @@ void eval(const TensorP& root) {
         // layer_norm -> matmul: the GEMM normalises its A rows itself when
         // its kernel can (ops::matmul falls back to an explicit layer_norm)
         const TensorP& la = x->node->in[0];
-        if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 && is_single_internal_use(la, uses)) {
+        // (only 16-bit GEMMs of <= 16 rows can: the skinny kernel; otherwise
+        // the layer_norm stays a node, which the producing GEMM's split-K
+        // reduction may compute)
+        if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 && la->dtype != DType::F32 &&
+            la->shape[0] <= 16 && is_single_internal_use(la, uses)) {
+          for (auto pit = post_ln.begin(); pit != post_ln.end(); ++pit)
+            if (pit->second.get() == la.get()) {  // normalised in this GEMM's prologue instead
+              post_ln.erase(pit);
+              break;
+            }
           g.ln_gamma = la->node->in[1];
           g.ln_beta = la->node->in[2];
           g.ln_eps = la->node->f.empty() ? 1e-5f : (float)la->node->f[0];
@@ -393,6 +404,10 @@ void eval(const TensorP& root) {
         absorbed.insert(x.get());
         groups[t.get()] = g;
       }
+    } else if (n->code == OP_LAYER_NORM && t->ndim == 2) {
+      const TensorP& x = n->in[0];
+      if (groups.count(x.get()) && !post_ln.count(x.get()) && n->in[1]->ndim == 1 && n->in[2]->ndim == 1)
+        post_ln[x.get()] = t;
     } else if (n->code == OP_ADD) {
       for (int side = 0; side < 2; ++side) {
         const TensorP& x = n->in[side];
@@ -430,7 +445,19 @@ void eval(const TensorP& root) {
       e.ln_gamma = g.ln_gamma;
       e.ln_beta = g.ln_beta;
       e.ln_eps = g.ln_eps;
-      res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e) : ops::matmul(g.a, g.b, false, false, &e)};
+      auto pit = post_ln.find(t.get());
+      TensorP lnt = pit != post_ln.end() && pit->second->pending() ? pit->second : nullptr;
+      if (lnt && g.packed_n == 0) {
+        ops::PostLn pl;
+        pl.gamma = lnt->node->in[1];
+        pl.beta = lnt->node->in[2];
+        pl.eps = lnt->node->f.empty() ? 1e-5f : (float)lnt->node->f[0];
+        res = {ops::matmul(g.a, g.b, false, false, &e, nullptr, &pl)};
+        assign(lnt, pl.y);
+        g_stats.launches_saved++;
+      } else {
+        res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e) : ops::matmul(g.a, g.b, false, false, &e)};
+      }
       g_stats.fused_gemm_epilogues++;
       g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0);
     } else if (n->code < 0) {

@@ -125,7 +125,16 @@ struct Gemm {
   float ln_eps = 1e-5f;
   // B in the skinny kernel's packed layout (pack_weights), 16-bit, M <= 16
   bool b_packed = false;
+  // Y = layer_norm(C) over N (gamma, beta [N]) computed by the split-K
+  // reduction while it writes C (gemm_post_ln_fused); Y is [M, N] contiguous
+  const void* pln_gamma = nullptr;
+  const void* pln_beta = nullptr;
+  void* pln_y = nullptr;
+  float pln_eps = 1e-5f;
 };
+// Whether the launch ends in a split-K reduction that can also produce
+// layer_norm(C) (one batch, N <= 2048); otherwise the caller runs layer_norm.
+bool gemm_post_ln_fused(const Gemm& g);
 // Whether the skinny decode kernel takes this problem, and whether it can
 // also normalise the A rows (layer norm over K, K <= 4096) while loading them.
 bool gemm_is_skinny(const Gemm& g);

@@ -220,6 +220,140 @@ __global__ void __launch_bounds__(256) splitk_reduce(GArgs p) {
   }
 }
 
+// Split-K reduction that also layer-normalises each output row (one batch,
+// N <= 256*NV, N % 4 == 0): one wavefront per row sums the partials in split order and
+// applies the epilogue as splitk_reduce does, stores C, then computes
+// Y = layer_norm(C) from the stored values with layer_norm_wave's element
+// mapping (element (64 i + lane) * 4 + j), two-pass statistics and
+// reduction order, so Y equals what a separate layer_norm of C would give.
+// GPT-2 runs it for the projection and fc2 GEMMs, whose outputs (residual
+// stream) feed ln_2 / the next layer's ln_1 (models/gpt2.py:84-178).
+// 4 consecutive elements as floats (16-byte or 8-byte load; 16-byte aligned
+// for fp32, 8-byte for 16-bit types).
+template <typename T>
+__device__ __forceinline__ void ld4f(const T* src, float (&o)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 v = *(const float4*)src;
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else {
+    T t[4];
+    *(uint2*)t = *(const uint2*)src;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = to_f(t[j]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st4(T* dst, const float (&v)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    *(float4*)dst = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    T t[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t[j] = from_f<T>(v[j]);
+    *(uint2*)dst = *(const uint2*)t;
+  }
+}
+
+template <typename T, int NV>
+__global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
+  constexpr int MS = 8;  // partials loaded up front; more are added afterwards
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.M) return;  // whole wavefront; no barriers below
+  const int64_t N = p.N, total = p.M * p.N;
+  const int ns = p.splits;
+  // Every load first, from clamped legal addresses (chunks past N read
+  // chunk 0 and are discarded), so that they are all in flight together.
+  float part[NV][MS][4], bias[NV][4], res[NV][4], msk[NV][4], gam[NV][4], bet[NV][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    const int64_t cc = c < N ? c : 0;
+#pragma unroll
+    for (int sp = 0; sp < MS; ++sp) {
+      const float4 w = *(const float4*)(p.ws + (int64_t)(sp < ns ? sp : 0) * total + row * N + cc);
+      part[i][sp][0] = w.x; part[i][sp][1] = w.y; part[i][sp][2] = w.z; part[i][sp][3] = w.w;
+    }
+    const T* out = (const T*)p.C + row * p.c_sm + cc;
+    ld4f<T>(p.bias ? (const T*)p.bias + cc : out, bias[i]);
+    ld4f<T>(p.res ? (const T*)p.res + row * p.r_sm + cc : out, res[i]);
+    ld4f<T>(p.mask ? (const T*)p.mask + row * p.k_sm + cc : out, msk[i]);
+    ld4f<T>((const T*)p.pln_g + cc, gam[i]);
+    ld4f<T>((const T*)p.pln_b + cc, bet[i]);
+  }
+  float v[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < MS; ++sp)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += sp < ns ? part[i][sp][j] : 0.f;
+    for (int sp = MS; sp < ns; ++sp)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += c < N ? p.ws[(int64_t)sp * total + row * N + c + j] : 0.f;
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // epilogue_store's arithmetic
+      float x = p.alpha * acc[j];
+      if (p.bias) x += bias[i][j];
+      if (p.act == kActRelu) x = fmaxf(x, 0.f);
+      else if (p.act == kActGelu) x = gelu_tanh(x);
+      else if (p.act == kActGeluExact) x = 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+      if (p.res) x += res[i][j];
+      if (p.mask) x = msk[i][j] > 0.f ? x : 0.f;
+      o[j] = to_f(from_f<T>(x));  // the value as stored
+    }
+    if (c < N) st4<T>((T*)p.C + row * p.c_sm + c, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i][j] = c < N ? o[j] : 0.f;
+      s += v[i][j];
+    }
+  }
+  const float mean = wave_sum(s) / (float)N;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float d = c < N ? v[i][j] - mean : 0.f;
+      q += d * d;
+    }
+  }
+  const float var = wave_sum(q) / (float)N;
+  const float inv = 1.f / sqrtf(var + p.pln_eps);
+  T* y = (T*)p.pln_y + row * N;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = gam[i][j] * (v[i][j] - mean) * inv + bet[i][j];
+    if (c < N) st4<T>(y + c, o);
+  }
+}
+
+template <typename T>
+void launch_reduce_ln(const GArgs& p, hipStream_t s) {
+  const dim3 grid((unsigned)((p.M + 3) / 4)), block(256);
+  switch ((p.N + 255) / 256) {
+    case 1: hipLaunchKernelGGL((splitk_reduce_ln<T, 1>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((splitk_reduce_ln<T, 2>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((splitk_reduce_ln<T, 3>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((splitk_reduce_ln<T, 4>), grid, block, 0, s, p); break;
+    case 5: hipLaunchKernelGGL((splitk_reduce_ln<T, 5>), grid, block, 0, s, p); break;
+    case 6: hipLaunchKernelGGL((splitk_reduce_ln<T, 6>), grid, block, 0, s, p); break;
+    case 7: hipLaunchKernelGGL((splitk_reduce_ln<T, 7>), grid, block, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((splitk_reduce_ln<T, 8>), grid, block, 0, s, p); break;
+    default: fail("gemm: fused layer_norm needs N <= 2048");
+  }
+}
+
 // Any strides, any float dtype, and int8 B with per-n scales: a plain tiled
 // kernel (16x16 threads, 4x4 outputs each) used for layouts the MFMA kernels
 // do not take.
@@ -371,6 +505,10 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   p.ln_g = g.ln_gamma;
   p.ln_b = g.ln_beta;
   p.ln_eps = g.ln_eps;
+  p.pln_g = g.pln_gamma;
+  p.pln_b = g.pln_beta;
+  p.pln_y = g.pln_y;
+  p.pln_eps = g.pln_eps;
   const size_t esz = dtype_size(g.dt);
   const int vw = (int)(16 / esz);  // elements per 16-byte vector
   // Vector loads need 16-byte aligned runs along the contiguous axis.
@@ -402,6 +540,19 @@ int cu_count() {
 }  // namespace
 
 bool gemm_is_skinny(const Gemm& g) { return skinny_plan(g, cu_count()).use; }
+
+bool gemm_post_ln_fused(const Gemm& g) {
+  if (skinny_plan(g, cu_count()).use || thin_kind(g)) return false;
+  if (g.batch != 1 || g.N > 2048 || g.N % 4 != 0 || g.c_sm != g.N) return false;
+  // four-element vector accesses of C, Y and the epilogue operands
+  const uintptr_t al = 4 * dtype_size(g.dt) - 1;
+  auto ok = [&](const void* q) { return q == nullptr || ((uintptr_t)q & al) == 0; };
+  if (!ok(g.C) || !ok(g.bias) || !ok(g.residual) || !ok(g.mask) || !ok(g.pln_gamma) || !ok(g.pln_beta) ||
+      !ok(g.pln_y) || (g.residual && g.r_sm % 4 != 0) || (g.mask && g.k_sm % 4 != 0))
+    return false;
+  const Plan pl = make_plan(g, cu_count());
+  return pl.kind == kMf && pl.splits > 1;
+}
 
 GemmTune& gemm_tune() {
   static GemmTune t = [] {
@@ -443,6 +594,7 @@ size_t gemm_workspace_bytes(const Gemm& g) {
 
 void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
+  if (g.pln_y && !gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
   const SkinnyPlan sp = skinny_plan(g, cu_count());
   if (sp.use) {
     Plan one{};
@@ -504,11 +656,19 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   }
   check_launch("gemm_mfma");
   if (pl.splits > 1) {
+    if (g.pln_y) {
+      if (!gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
+      AGPU_FLOAT_SWITCH(g.dt, launch_reduce_ln<T>(p, s));
+      check_launch("splitk_reduce_ln");
+      return;
+    }
     int64_t total = g.batch * g.M * g.N;
     int64_t blocks = (total + 1023) / 1024;
     if (blocks > 65536) blocks = 65536;
     AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce<T>), dim3((unsigned)blocks), dim3(256), 0, s, p));
     check_launch("splitk_reduce");
+  } else if (g.pln_y) {
+    fail("gemm: layer_norm fusion needs a split-K launch");
   }
 }
 

@@ -35,6 +35,7 @@ struct GArgs {
   bool vec_a, vec_b;
   const float* b_scale;
   const void* ln_g; const void* ln_b; float ln_eps;
+  const void* pln_g; const void* pln_b; void* pln_y; float pln_eps;
 };
 
 // Epilogue operands of one output, loadable ahead of the product (they do
@@ -82,6 +83,21 @@ __device__ __forceinline__ void epilogue_store(const GArgs& p, int64_t b, int64_
   if (p.res) v += to_f(((const T*)p.res)[b * p.r_sb + row * p.r_sm + col]);
   if (p.mask) v = to_f(((const T*)p.mask)[b * p.k_sb + row * p.k_sm + col]) > 0.f ? v : 0.f;
   ((T*)p.C)[b * p.c_sb + row * p.c_sm + col] = from_f<T>(v);
+}
+
+// epilogue_store's arithmetic, returning the value as stored (rounded to T).
+template <typename T>
+__device__ __forceinline__ float epilogue_apply(const GArgs& p, int64_t b, int64_t row, int64_t col, float acc) {
+  float v = p.alpha * acc;
+  if (p.bias) v += to_f(((const T*)p.bias)[col]);
+  if (p.act == kActRelu) v = fmaxf(v, 0.f);
+  else if (p.act == kActGelu) v = gelu_tanh(v);
+  else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+  if (p.res) v += to_f(((const T*)p.res)[b * p.r_sb + row * p.r_sm + col]);
+  if (p.mask) v = to_f(((const T*)p.mask)[b * p.k_sb + row * p.k_sm + col]) > 0.f ? v : 0.f;
+  const T o = from_f<T>(v);
+  ((T*)p.C)[b * p.c_sb + row * p.c_sm + col] = o;
+  return to_f(o);
 }
 
 // Tile scheduling: XCD-aware remap, then 8-row tile groups.

@@ -789,7 +789,8 @@ static void set_epilogue(k::Gemm& g, const Epilogue* epi, const std::vector<int6
   if (epi->mask) side(epi->mask, &g.mask, &g.k_sm, &g.k_sb, &keep->mask);
 }
 
-TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi, const TensorP& into) {
+TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi, const TensorP& into,
+               PostLn* post_ln) {
   TensorP a = ta ? transpose_dims(a_in, a_in->ndim - 2, a_in->ndim - 1) : a_in;
   TensorP b = tb ? transpose_dims(b_in, b_in->ndim - 2, b_in->ndim - 1) : b_in;
   if (a_in->ndim < 2 || b_in->ndim < 2) fail("matmul requires at least 2D tensors, got %s and %s",
@@ -864,15 +865,38 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
     if (!ok) {
       Epilogue plain = *epi;
       plain.ln_gamma = plain.ln_beta = nullptr;
-      return matmul(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), b_in, ta, tb, &plain, into);
+      return matmul(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), b_in, ta, tb, &plain, into, post_ln);
     }
   }
   EpiKeep keep;
   set_epilogue(g, epi, od, bdims, &keep);
+  TensorP pl_g, pl_b;
+  bool pln_fused = false;
+  if (post_ln) {
+    if (!post_ln->gamma || !post_ln->beta || post_ln->gamma->dtype != g.dt || post_ln->beta->dtype != g.dt ||
+        post_ln->gamma->numel() != N || post_ln->beta->numel() != N)
+      fail("matmul: layer_norm gamma and beta must be [%lld] of the output dtype", (long long)N);
+    pl_g = contiguous(post_ln->gamma);
+    pl_b = contiguous(post_ln->beta);
+    if (!meta_mode()) {
+      TensorP y = alloc_out(g.dt, od);
+      k::Gemm probe = g;
+      probe.pln_gamma = pl_g->data();
+      probe.pln_beta = pl_b->data();
+      probe.pln_y = y->data();
+      probe.pln_eps = post_ln->eps;
+      pln_fused = k::gemm_post_ln_fused(probe);
+      if (pln_fused) {
+        g = probe;
+        post_ln->y = y;
+      }
+    }
+  }
   size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
   BufferP ws;
   if (wsb) ws = scratch(wsb);
   LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
+  if (post_ln && !pln_fused) post_ln->y = layer_norm(out, pl_g, pl_b, post_ln->eps);
   return out;
 }
 

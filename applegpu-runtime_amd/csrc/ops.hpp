@@ -74,8 +74,15 @@ struct Epilogue {
   TensorP ln_gamma, ln_beta;
   float ln_eps = 1e-5f;
 };
+// Also y = layer_norm(out, gamma, beta, eps) over the last dim; computed by
+// the GEMM's split-K reduction when its plan has one, else by layer_norm.
+struct PostLn {
+  TensorP gamma, beta;
+  float eps = 1e-5f;
+  TensorP y;  // result
+};
 TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = false,
-               const Epilogue* epi = nullptr, const TensorP& into = nullptr);
+               const Epilogue* epi = nullptr, const TensorP& into = nullptr, PostLn* post_ln = nullptr);
 // SGD steps fused with their gradients, in place:
 //   w += alpha * op(a) op(b)   (the weight gradient GEMM; w contiguous 2-D)
 //   bias += alpha * sum(g, 0)  (g contiguous [rows, N])
