@@ -18,8 +18,9 @@
 // strides with unit stride along d, so head splits of a fused QKV projection
 // and the head-merge transpose cost nothing.
 //
-// 16-bit inputs with d = 64 or 128 and 16-byte aligned rows take the MFMA
-// kernel (flash_attn_mfma below); other cases take the scalar kernel.
+// Inputs with d = 64 or 128 and 16-byte aligned rows take the MFMA kernels
+// (flash_attn_mfma for 16-bit, flash_attn_f32 below); other cases take the
+// scalar kernel.
 #include "device.hpp"
 
 #include <type_traits>
@@ -442,18 +443,302 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_mfma(AArgs p) {
   }
 }
 
+
+// ── MFMA flash attention, fp32 ─────────────────────────────────────────────
+// The 16-bit kernel's structure with v_mfma_f32_16x16x4_f32 (exact fp32
+// products, fp32 accumulation): lane l's A operand is row l%16 and B operand
+// column l%16 at k = l/16; C register r of lane l is row 4*(l/16)+r,
+// column l%16.  The k index of each product is permuted (A and B agree), so
+// that every operand a lane needs is a run of consecutive floats:
+//  - S^T = K Q^T: step s gives lane group g = l/16 the dimension
+//    d = g*D/4 + s, so a lane's K operands are D/4 consecutive floats of
+//    one key row (16-byte LDS reads) and its query row is held the same way;
+//  - O^T += V^T P^T: one product per key (t, r) of the lane's scores, B =
+//    the lane's own probability; O^T row rho of 16-row tile u is dimension
+//    d = (D/16)*rho + u, so a lane's V operands are D/16 consecutive floats
+//    of one key row and its outputs are runs of D/16 consecutive floats.
+// Both K and V tiles sit in LDS untransposed, rows padded by 4 floats.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct FaTile32 {
+  static constexpr int C4 = D / 4;                           // float4 chunks per row
+  static constexpr int NU = kFaKeys * C4 / (64 * kFaWaves);  // chunks per thread per operand
+  static_assert(NU <= 8, "tile registers");
+  // named registers (with arrays the compiler kept the tile in scratch memory)
+  float4 k0, k1, k2, k3, k4, k5, k6, k7, v0, v1, v2, v3, v4, v5, v6, v7;
+
+  template <int I>
+  __device__ __forceinline__ void ld1(const float* K, const float* V, const AArgs& p, int64_t j0, int tid,
+                                      float4& k, float4& v) {
+    if constexpr (I < NU) {
+      const int e = tid + 64 * kFaWaves * I;
+      const int64_t j = j0 + e / C4 < p.Tk ? j0 + e / C4 : p.Tk - 1;  // rows past Tk repeat row Tk-1
+      k = *(const float4*)(K + j * p.k_st + 4 * (e % C4));
+      v = *(const float4*)(V + j * p.v_st + 4 * (e % C4));
+    }
+  }
+  template <int KP, int I>
+  __device__ __forceinline__ void st1(float* Ks, float* Vs, int tid, const float4& k, const float4& v) const {
+    if constexpr (I < NU) {
+      const int e = tid + 64 * kFaWaves * I;
+      *(float4*)&Ks[(e / C4) * KP + 4 * (e % C4)] = k;
+      *(float4*)&Vs[(e / C4) * KP + 4 * (e % C4)] = v;
+    }
+  }
+  __device__ __forceinline__ void load(const float* K, const float* V, const AArgs& p, int64_t j0, int tid) {
+    ld1<0>(K, V, p, j0, tid, k0, v0); ld1<1>(K, V, p, j0, tid, k1, v1);
+    ld1<2>(K, V, p, j0, tid, k2, v2); ld1<3>(K, V, p, j0, tid, k3, v3);
+    ld1<4>(K, V, p, j0, tid, k4, v4); ld1<5>(K, V, p, j0, tid, k5, v5);
+    ld1<6>(K, V, p, j0, tid, k6, v6); ld1<7>(K, V, p, j0, tid, k7, v7);
+  }
+  template <int KP>
+  __device__ __forceinline__ void store(float* Ks, float* Vs, int tid) const {
+    st1<KP, 0>(Ks, Vs, tid, k0, v0); st1<KP, 1>(Ks, Vs, tid, k1, v1);
+    st1<KP, 2>(Ks, Vs, tid, k2, v2); st1<KP, 3>(Ks, Vs, tid, k3, v3);
+    st1<KP, 4>(Ks, Vs, tid, k4, v4); st1<KP, 5>(Ks, Vs, tid, k5, v5);
+    st1<KP, 6>(Ks, Vs, tid, k6, v6); st1<KP, 7>(Ks, Vs, tid, k7, v7);
+  }
+};
+
+// KSPLIT: the block's 4 wavefronts share one group of 16 queries and split
+// every key tile four ways (wavefront w takes its keys 16w..16w+15), then
+// merge their running maxima, sums and outputs through LDS.  Used when there
+// are too few 64-query blocks to fill the GPU (GPT-2 at 128 tokens: 24):
+// each wavefront then does a quarter of the serial work.
+template <int D, bool KSPLIT>
+__global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
+  static_assert(D % 64 == 0, "d must be a multiple of 64");
+  constexpr int QB = KSPLIT ? 16 : kFaWaves * 16;  // query rows per block
+  constexpr int NT = KSPLIT ? 1 : 4;  // 16-key sub-tiles per wavefront and tile (KSPLIT: sub-tile w)
+  constexpr int KP = D + 4;          // K and V tile row pitch (floats)
+  constexpr int DS = D / 4;          // 4-deep steps of Q K^T
+  constexpr int DT = D / 16;         // 16-row tiles of O^T
+  __shared__ __attribute__((aligned(16))) float Ks[2][kFaKeys * KP];
+  __shared__ __attribute__((aligned(16))) float Vs[2][kFaKeys * KP];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t BH = p.B * p.H;
+  const int64_t bh = blockIdx.x % BH;
+  const int64_t tq = blockIdx.x / BH;
+  const int64_t qt = p.causal ? p.q_tiles - 1 - tq : tq;
+  const int64_t b = bh / p.H, h = bh % p.H;
+  const int64_t q0 = qt * QB;
+  const int64_t qw = KSPLIT ? q0 : q0 + (int64_t)w * 16;
+  const int tw = KSPLIT ? w : 0;  // first key sub-tile of this wavefront
+
+  const float* Q = (const float*)p.q + b * p.q_sb + h * p.q_sh;
+  const float* K = (const float*)p.k + b * p.k_sb + h * p.k_sh;
+  const float* V = (const float*)p.v + b * p.v_sb + h * p.v_sh;
+
+  int64_t kv_end = p.Tk;
+  if (p.causal) {
+    const int64_t qe = q0 + QB < p.Tq ? q0 + QB : p.Tq;
+    kv_end = qe < p.Tk ? qe : p.Tk;
+  }
+  const int ntiles = (int)((kv_end + kFaKeys - 1) / kFaKeys);
+
+  // query row l16 of this wavefront, dims g*DS .. g*DS + DS-1
+  const int64_t qi = qw + l16;
+  const int64_t qr = qi < p.Tq ? qi : p.Tq - 1;
+  float qf[DS];
+#pragma unroll
+  for (int s = 0; s < DS; s += 4) {
+    const float4 x = *(const float4*)(Q + qr * p.q_st + g * DS + s);
+    qf[s] = x.x; qf[s + 1] = x.y; qf[s + 2] = x.z; qf[s + 3] = x.w;
+  }
+  const int lim = (int)(p.causal ? (qi + 1 < p.Tk ? qi + 1 : p.Tk) : p.Tk);
+
+  f32x4v acc[DT];
+#pragma unroll
+  for (int u = 0; u < DT; ++u) acc[u] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, ls = 0.f;
+  const float c2 = p.scale * 1.4426950408889634f;
+
+  if (ntiles > 0) {
+    FaTile32<D> t0;
+    t0.load(K, V, p, 0, tid);
+    t0.template store<KP>(Ks[0], Vs[0], tid);
+  }
+  __syncthreads();
+
+  auto tile = [&](int it, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int buf = it & 1;
+    const int j0 = it * kFaKeys;
+    // the next tile, in plain local registers (held in a struct, the tile
+    // went to scratch memory once a scheduling barrier followed its loads)
+    constexpr int NU = FaTile32<D>::NU;
+    float4 k0, k1, k2, k3, k4, k5, k6, k7, v0, v1, v2, v3, v4, v5, v6, v7;
+#define AGPU_FA32_LD(I)                                                                    \
+    if constexpr (I < NU) {                                                                \
+      const int e = tid + 64 * kFaWaves * I;                                               \
+      const int64_t jn = (int64_t)j0 + kFaKeys + e / (D / 4);                              \
+      const int64_t jc = jn < p.Tk ? jn : p.Tk - 1;                                        \
+      k##I = *(const float4*)(K + jc * p.k_st + 4 * (e % (D / 4)));                        \
+      v##I = *(const float4*)(V + jc * p.v_st + 4 * (e % (D / 4)));                        \
+    }
+    AGPU_FA32_LD(0) AGPU_FA32_LD(1) AGPU_FA32_LD(2) AGPU_FA32_LD(3)
+    AGPU_FA32_LD(4) AGPU_FA32_LD(5) AGPU_FA32_LD(6) AGPU_FA32_LD(7)
+#undef AGPU_FA32_LD
+    // keep the loads here, ahead of the products (the scheduler otherwise
+    // sinks them next to the LDS stores, where they are waited for at once)
+    __builtin_amdgcn_sched_barrier(0);
+
+    const float* Kb = Ks[buf];
+    const float* Vb = Vs[buf];
+    f32x4v st[NT];
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti) {
+      const int t = tw + ti;
+      st[ti] = f32x4v{0.f, 0.f, 0.f, 0.f};
+      const float* kr = Kb + (16 * t + l16) * KP + g * DS;
+#pragma unroll
+      for (int s = 0; s < DS; s += 4) {
+        const float4 a = *(const float4*)(kr + s);
+        st[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, qf[s], st[ti], 0, 0, 0);
+        st[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, qf[s + 1], st[ti], 0, 0, 0);
+        st[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, qf[s + 2], st[ti], 0, 0, 0);
+        st[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, qf[s + 3], st[ti], 0, 0, 0);
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = st[ti][r] * c2;
+        if constexpr (MASK) v = j0 + 16 * (tw + ti) + 4 * g + r < lim ? v : -INFINITY;
+        st[ti][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - mu);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = __builtin_amdgcn_exp2f(st[ti][r] - mu);
+        ps += pv;
+        st[ti][r] = pv;
+      }
+    ls = ls * alpha + ps;
+#pragma unroll
+    for (int u = 0; u < DT; ++u) acc[u] *= alpha;
+#pragma unroll
+    for (int ti = 0; ti < NT; ++ti)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vr = Vb + (16 * (tw + ti) + 4 * g + r) * KP + DT * l16;
+        float a[DT];
+#pragma unroll
+        for (int u = 0; u < DT; u += 4) {
+          const float4 x = *(const float4*)(vr + u);
+          a[u] = x.x; a[u + 1] = x.y; a[u + 2] = x.z; a[u + 3] = x.w;
+        }
+#pragma unroll
+        for (int u = 0; u < DT; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], st[ti][r], acc[u], 0, 0, 0);
+      }
+#define AGPU_FA32_ST(I)                                                                    \
+    if constexpr (I < NU) {                                                                \
+      const int e = tid + 64 * kFaWaves * I;                                               \
+      *(float4*)&Ks[buf ^ 1][(e / (D / 4)) * KP + 4 * (e % (D / 4))] = k##I;               \
+      *(float4*)&Vs[buf ^ 1][(e / (D / 4)) * KP + 4 * (e % (D / 4))] = v##I;               \
+    }
+    AGPU_FA32_ST(0) AGPU_FA32_ST(1) AGPU_FA32_ST(2) AGPU_FA32_ST(3)
+    AGPU_FA32_ST(4) AGPU_FA32_ST(5) AGPU_FA32_ST(6) AGPU_FA32_ST(7)
+#undef AGPU_FA32_ST
+    __syncthreads();
+  };
+
+  int nfull = (int)(p.Tk / kFaKeys);
+  if (p.causal && (q0 + 1) / kFaKeys < nfull) nfull = (int)((q0 + 1) / kFaKeys);
+  if (nfull > ntiles) nfull = ntiles;
+  int it = 0;
+  for (; it < nfull; ++it) tile(it, std::integral_constant<bool, false>());
+  for (; it < ntiles; ++it) tile(it, std::integral_constant<bool, true>());
+
+  float l = ls + __shfl_xor(ls, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if constexpr (KSPLIT) {
+    // merge the four wavefronts' states (the tile buffers are free after the
+    // loop's last barrier): wave w > 0 hands (m, l, acc) to wave 0
+    float* red = &Ks[0][0];
+    constexpr int PER = DT * 4 + 2;
+    if (w > 0) {
+      float* dst = red + ((w - 1) * 64 + lane) * PER;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[u * 4 + r] = acc[u][r];
+      dst[DT * 4] = m;
+      dst[DT * 4 + 1] = l;
+    }
+    __syncthreads();
+    if (w > 0) return;
+    float mw[kFaWaves], lw[kFaWaves];
+    mw[0] = m;
+    lw[0] = l;
+#pragma unroll
+    for (int v = 1; v < kFaWaves; ++v) {
+      const float* src = red + ((v - 1) * 64 + lane) * PER;
+      mw[v] = src[DT * 4];
+      lw[v] = src[DT * 4 + 1];
+    }
+    float M = mw[0];
+#pragma unroll
+    for (int v = 1; v < kFaWaves; ++v) M = fmaxf(M, mw[v]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float sc[kFaWaves];
+    l = 0.f;
+#pragma unroll
+    for (int v = 0; v < kFaWaves; ++v) {
+      sc[v] = __builtin_amdgcn_exp2f(mw[v] - Mu);
+      l += lw[v] * sc[v];
+    }
+#pragma unroll
+    for (int u = 0; u < DT; ++u) acc[u] *= sc[0];
+#pragma unroll
+    for (int v = 1; v < kFaWaves; ++v) {
+      const float* src = red + ((v - 1) * 64 + lane) * PER;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[u][r] += src[u * 4 + r] * sc[v];
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qi >= p.Tq) return;
+  float* O = (float*)p.o + b * p.o_sb + h * p.o_sh + qi * p.o_st;
+  // register r of O^T tile u: dimension DT*(4g + r) + u
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float o[DT];
+#pragma unroll
+    for (int u = 0; u < DT; ++u) o[u] = acc[u][r] * inv;
+#pragma unroll
+    for (int u = 0; u < DT; u += 4)
+      *(float4*)(O + DT * (4 * g + r) + u) = make_float4(o[u], o[u + 1], o[u + 2], o[u + 3]);
+  }
+}
 }  // namespace
 
 // 16-byte loads of every Q/K/V row and 8-byte stores of O need aligned bases
 // and row/head/batch strides that are multiples of 8 elements.
 static bool attention_mfma_ok(const Attn& a) {
-  if (!(a.dt == DType::F16 || a.dt == DType::BF16) || !(a.D == 64 || a.D == 128)) return false;
+  if (!(a.dt == DType::F16 || a.dt == DType::BF16 || a.dt == DType::F32) || !(a.D == 64 || a.D == 128)) return false;
   if (a.Tk >= (int64_t(1) << 30)) return false;  // key indices are 32-bit in the kernel
   if (((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v) % 16 != 0 || (uintptr_t)a.o % 8 != 0) return false;
   const int64_t st[12] = {a.q_sb, a.q_sh, a.q_st, a.k_sb, a.k_sh, a.k_st,
                           a.v_sb, a.v_sh, a.v_st, a.o_sb, a.o_sh, a.o_st};
   for (int64_t x : st)
-    if (x % 8 != 0) return false;
+    if (x % 8 != 0) return false;  // fp32: 4 would do; 8 keeps one rule
   return true;
 }
 
@@ -485,6 +770,24 @@ void attention(const Attn& a, hipStream_t s) {
   p.o_sb = a.o_sb; p.o_sh = a.o_sh; p.o_st = a.o_st;
   p.scale = a.scale;
   p.causal = a.causal ? 1 : 0;
+  if (attention_mfma_ok(a) && a.dt == DType::F32) {
+    // 64 queries per block when that gives every CU a block; else 16 per
+    // block with the key tiles split across the block's wavefronts
+    const bool ksplit = a.B * a.H * ((a.Tq + 63) / 64) < 256;
+    p.q_tiles = (int)((a.Tq + (ksplit ? 15 : 63)) / (ksplit ? 16 : 64));
+    const int64_t blocks = a.B * a.H * p.q_tiles;
+    if (blocks > 0x7fffffff) fail("fused attention: grid too large");
+    if (ksplit) {
+      if (a.D == 64) hipLaunchKernelGGL((flash_attn_f32<64, true>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
+      else hipLaunchKernelGGL((flash_attn_f32<128, true>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
+      check_launch("attention");
+      return;
+    }
+    if (a.D == 64) hipLaunchKernelGGL((flash_attn_f32<64, false>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
+    else hipLaunchKernelGGL((flash_attn_f32<128, false>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
+    check_launch("attention");
+    return;
+  }
   if (attention_mfma_ok(a)) {
     // 128 query rows per block when that still gives every CU a block
     const int64_t bh = a.B * a.H;
