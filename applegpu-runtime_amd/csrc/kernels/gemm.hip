@@ -354,6 +354,50 @@ void launch_reduce_ln(const GArgs& p, hipStream_t s) {
   }
 }
 
+// splitk_reduce for one batch with N % 4 == 0 and 4-element aligned
+// epilogue operands: each thread owns 4 consecutive outputs, issues every
+// load first (up to 8 partials from clamped split indices, then bias,
+// residual and mask as vectors, all branch-free) and stores one vector.
+// Same sums in the same split order and the same epilogue arithmetic as
+// splitk_reduce.
+template <typename T>
+__global__ void __launch_bounds__(256) splitk_reduce_vec(GArgs p) {
+  constexpr int MS = 8;
+  const int64_t total = p.M * p.N;
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= total) return;
+  const int ns = p.splits;
+  const int64_t row = i / p.N, col = i % p.N;
+  float part[MS][4];
+#pragma unroll
+  for (int sp = 0; sp < MS; ++sp) {
+    const float4 w = *(const float4*)(p.ws + (int64_t)(sp < ns ? sp : 0) * total + i);
+    part[sp][0] = w.x; part[sp][1] = w.y; part[sp][2] = w.z; part[sp][3] = w.w;
+  }
+  const T* out = (const T*)p.C + row * p.c_sm + col;
+  float bias[4], res[4], msk[4];
+  ld4f<T>(p.bias ? (const T*)p.bias + col : out, bias);
+  ld4f<T>(p.res ? (const T*)p.res + row * p.r_sm + col : out, res);
+  ld4f<T>(p.mask ? (const T*)p.mask + row * p.k_sm + col : out, msk);
+  float o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float acc = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < MS; ++sp) acc += sp < ns ? part[sp][j] : 0.f;
+    for (int sp = MS; sp < ns; ++sp) acc += p.ws[(int64_t)sp * total + i + j];
+    float x = p.alpha * acc;
+    if (p.bias) x += bias[j];
+    if (p.act == kActRelu) x = fmaxf(x, 0.f);
+    else if (p.act == kActGelu) x = gelu_tanh(x);
+    else if (p.act == kActGeluExact) x = 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+    if (p.res) x += res[j];
+    if (p.mask) x = msk[j] > 0.f ? x : 0.f;
+    o[j] = x;
+  }
+  st4<T>((T*)p.C + row * p.c_sm + col, o);
+}
+
 // Any strides, any float dtype, and int8 B with per-n scales: a plain tiled
 // kernel (16x16 threads, 4x4 outputs each) used for layouts the MFMA kernels
 // do not take.
@@ -541,6 +585,16 @@ int cu_count() {
 
 bool gemm_is_skinny(const Gemm& g) { return skinny_plan(g, cu_count()).use; }
 
+// splitk_reduce_vec's conditions: one batch, rows of whole 4-vectors and
+// 4-element aligned output and epilogue operands.
+static bool reduce_vec_ok(const Gemm& g) {
+  if (g.batch != 1 || g.N % 4 != 0 || g.c_sm % 4 != 0) return false;
+  const uintptr_t al = 4 * dtype_size(g.dt) - 1;
+  auto ok = [&](const void* q) { return q == nullptr || ((uintptr_t)q & al) == 0; };
+  return ok(g.C) && ok(g.bias) && ok(g.residual) && ok(g.mask) && (!g.residual || g.r_sm % 4 == 0) &&
+         (!g.mask || g.k_sm % 4 == 0);
+}
+
 bool gemm_post_ln_fused(const Gemm& g) {
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return false;
   if (g.batch != 1 || g.N > 2048 || g.N % 4 != 0 || g.c_sm != g.N) return false;
@@ -663,6 +717,12 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
       return;
     }
     int64_t total = g.batch * g.M * g.N;
+    if (reduce_vec_ok(g) && (total + 1023) / 1024 <= 0x7fffffff) {
+      AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce_vec<T>), dim3((unsigned)((total + 1023) / 1024)),
+                                                 dim3(256), 0, s, p));
+      check_launch("splitk_reduce");
+      return;
+    }
     int64_t blocks = (total + 1023) / 1024;
     if (blocks > 65536) blocks = 65536;
     AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce<T>), dim3((unsigned)blocks), dim3(256), 0, s, p));
