@@ -682,7 +682,46 @@ __global__ void __launch_bounds__(256) gemm_mf(GArgs p) {
       }
   };
   if (p.splits == 1) {
-    if (owner) for_each_out([&](int64_t row, int64_t col, float v) { epilogue_store<TC>(p, b, row, col, v); });
+    if (!owner) return;
+    // epilogue_store's arithmetic, with each 32x32 block's operands loaded
+    // together first (uniform branches, clamped rows and columns) instead of
+    // one dependent load per output: the residual of an in-place update
+    // (w += alpha * A B) is a full tile read.
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t col = n0 + wn + j * 32 + (lane & 31);
+        const int64_t cc = col < p.N ? col : p.N - 1;
+        const int64_t r0 = m0 + wm + i * 32 + 4 * (lane >> 5);
+        float bias = 0.f, res[16], msk[16];
+        if (p.bias) bias = to_f(((const TC*)p.bias)[cc]);
+        if (p.res) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = r0 + 8 * (r >> 2) + (r & 3);
+            res[r] = to_f(((const TC*)p.res)[b * p.r_sb + (row < p.M ? row : p.M - 1) * p.r_sm + cc]);
+          }
+        }
+        if (p.mask) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = r0 + 8 * (r >> 2) + (r & 3);
+            msk[r] = to_f(((const TC*)p.mask)[b * p.k_sb + (row < p.M ? row : p.M - 1) * p.k_sm + cc]);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = r0 + 8 * (r >> 2) + (r & 3);
+          float v = p.alpha * acc[i][j][r] + bias;
+          if (p.act == kActRelu) v = fmaxf(v, 0.f);
+          else if (p.act == kActGelu) v = gelu_tanh(v);
+          else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+          if (p.res) v += res[r];
+          if (p.mask) v = msk[r] > 0.f ? v : 0.f;
+          if (row < p.M && col < p.N) ((TC*)p.C)[b * p.c_sb + row * p.c_sm + col] = from_f<TC>(v);
+        }
+      }
     return;
   }
   // Split K across blocks: every split stores its partial tile and
