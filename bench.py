@@ -190,19 +190,19 @@ def main():
     if not (np.isfinite(logits).all() and np.isfinite(loss)):
         raise RuntimeError("non-finite results")
 
-    # ── roofline: the MLP weight-gradient GEMM dW = g^T h ────────────────────
+    # ── roofline: the MLP weight-gradient GEMM with its SGD update, as the
+    # step runs it: W += -lr * g^T h (bias-free; W a scratch copy) ──────────
     K_, M_, N_ = MLP_BATCH, MLP_SIZES[1], MLP_SIZES[0]
     g_act = E.from_numpy(rng.standard_normal((K_, M_), dtype=np.float32) * np.float32(1e-3))
     h_act = E.from_numpy(np.maximum(rng.standard_normal((K_, N_), dtype=np.float32), 0))
+    w_scr = E.from_numpy(params[1][0])
     for _ in range(3):
-        E.matmul_ex(g_act, h_act, True, False)
+        E.sgd_matmul_(w_scr, g_act, h_act, True, False, -0.01)
     lib.applegpu_ffi_synchronize()
     reps = 50
     lib.applegpu_ffi_event_record(0)
-    out = None
     for _ in range(reps):
-        out = None
-        out = E.matmul_ex(g_act, h_act, True, False)
+        E.sgd_matmul_(w_scr, g_act, h_act, True, False, -0.01)
     lib.applegpu_ffi_event_record(1)
     gemm_ms = lib.applegpu_ffi_event_elapsed_ms(0, 1) / reps
     gemm_flop = 2.0 * M_ * N_ * K_
@@ -239,7 +239,8 @@ def main():
             "device": dev,
         },
         "roofline": {
-            "kernel": "gemm_mf dW = g^T h (M=4096 N=4096 K=256, fp32 via bf16x3), plan " + plan.value.decode(),
+            "kernel": "gemm_mf W += -lr * g^T h (MLP weight gradient with its SGD step in the epilogue; "
+                      "M=4096 N=4096 K=256, fp32 via bf16x3), plan " + plan.value.decode(),
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": FP32_MFMA_PEAK_TFLOPS,
