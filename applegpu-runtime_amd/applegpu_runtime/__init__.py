@@ -457,6 +457,16 @@ def sum_dim(t, dim, keepdim=False): return _op(b"sum_dim", [_t(t)], i=(int(dim),
 def embedding(weights, indices): return _op(b"embedding", [_t(weights), _t(indices)])
 def add_bias(input, bias): return _op(b"add_bias", [_t(input), _t(bias)])
 def attention(q, k, v): return _op(b"attention", [_t(q), _t(k), _t(v)])
+
+
+def qkv_attention(x, w, b, n_head, causal=True, batch=1, read_partials=False):
+    """Attention of a fused QKV projection: heads of (x @ w + b) split into Q,
+    K, V (w [K, 3d] row-major, as GPT-2's c_attn), (causal) attention, heads
+    merged back: [batch*T, d].  read_partials (fp32): the attention kernel
+    reads the projection's split-K partial sums plus the bias itself, with no
+    reduction launch (same values; slower at GPT-2 small's shape)."""
+    return _op(b"qkv_attention", [_t(x), _t(w), _t(b)],
+               i=(int(n_head), int(bool(causal)), int(batch), int(bool(read_partials))))
 def attention_causal(q, k, v): return _op(b"attention_causal", [_t(q), _t(k), _t(v)])
 def gather(input, dim, index): return _op(b"gather", [_t(input), _t(index)], i=(int(dim),))
 def index_select(input, dim, index): return _op(b"index_select", [_t(input), _t(index)], i=(int(dim),))

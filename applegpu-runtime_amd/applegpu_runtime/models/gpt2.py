@@ -118,14 +118,16 @@ def _mm(model: dict, x, name: str, rows: int = None):
     return x @ (gpu.transpose(w) if model.get("kmajor") else w)
 
 
-def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
+def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cache=True):
     """Returns (logits [seq, vocab], new_kv_cache) for one sequence.
 
     input_ids: list/array of token ids, or an int32 GpuTensor [T] already on
     the device (then `positions`, an int32 GpuTensor [T], may be given too;
     both device-resident inputs let the forward run under `gpu.capture`).
     With kv_cache (list of (k, v) per layer, each [n_head, past, d_head]) only
-    the last token is processed.
+    the last token is processed.  need_cache=False (a full forward whose K/V
+    are not kept; new_kv_cache is then None) lets each layer run its QKV
+    projection and attention as one `qkv_attention` op.
     """
     w = model["weights"]
     cfg = model["config"]
@@ -151,20 +153,25 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
     for i in range(L):
         p = f"transformer.h.{i}"
         h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
-        qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
+        if not cached and not need_cache and not model.get("kmajor"):
+            # projection + head split + causal attention in one op: the
+            # attention kernel reads the projection's partial sums directly
+            a = gpu.qkv_attention(h, w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"], H, causal=True)
+        else:
+            qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
 
-        def heads(lo):
-            part = gpu.slice(qkv, 1, lo, lo + d)
-            return gpu.transpose_dims(gpu.reshape(part, [T, H, hd]), 0, 1)
+            def heads(lo):
+                part = gpu.slice(qkv, 1, lo, lo + d)
+                return gpu.transpose_dims(gpu.reshape(part, [T, H, hd]), 0, 1)
 
-        q, k, v = heads(0), heads(d), heads(2 * d)
-        if cached:
-            pk, pv = kv_cache[i]
-            k = gpu.concat(pk, k, 1)
-            v = gpu.concat(pv, v, 1)
-        new_cache.append((k, v))
-        a = gpu.attention(q, k, v) if cached else gpu.attention_causal(q, k, v)
-        a = gpu.reshape(gpu.transpose_dims(a, 0, 1), [T, d])
+            q, k, v = heads(0), heads(d), heads(2 * d)
+            if cached:
+                pk, pv = kv_cache[i]
+                k = gpu.concat(pk, k, 1)
+                v = gpu.concat(pv, v, 1)
+            new_cache.append((k, v))
+            a = gpu.attention(q, k, v) if cached else gpu.attention_causal(q, k, v)
+            a = gpu.reshape(gpu.transpose_dims(a, 0, 1), [T, d])
         x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
 
         h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
@@ -173,7 +180,7 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None):
 
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
     logits = x @ gpu.transpose(w["transformer.wte.weight"])
-    return logits, new_cache
+    return logits, (new_cache if need_cache or cached else None)
 
 
 # ── batched prefill + greedy decode over a preallocated KV cache ────────────

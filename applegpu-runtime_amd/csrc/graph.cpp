@@ -31,7 +31,7 @@ enum Op : int {
   OP_WHERE, OP_MASKED_FILL, OP_TRIU, OP_TRIL,
   OP_QUANTIZE_PER_ROW, OP_DEQUANTIZE_PER_ROW, OP_LINEAR_INT8, OP_CONTIGUOUS, OP_FULL,
   OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
-  OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD,
+  OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD, OP_QKV_ATTENTION,
   OP_COUNT
 };
 
@@ -49,7 +49,7 @@ static const char* kNames[OP_COUNT] = {
     "where", "masked_fill", "triu", "tril",
     "quantize_per_row", "dequantize_per_row", "linear_int8", "contiguous", "full",
     "decode_attention", "pack_weight", "matmul_packed",
-    "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad",
+    "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad", "qkv_attention",
 };
 
 int op_code(const char* name) {
@@ -201,6 +201,10 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       need(in, 3, code);
       return {sgd_matmul_(in[0], in[1], in[2], iv.size() > 0 && iv[0], iv.size() > 1 && iv[1], (float)fp(f, 0, code))};
     case OP_SGD_SUM_ROWS: need(in, 2, code); return {sgd_sum_rows_(in[0], in[1], (float)fp(f, 0, code))};
+    case OP_QKV_ATTENTION:
+      need(in, 3, code);
+      return {qkv_attention(in[0], in[1], in[2], ip(iv, 0, code), iv.size() > 1 ? iv[1] != 0 : true,
+                            iv.size() > 2 ? iv[2] : 1, iv.size() > 3 && iv[3] != 0)};
     case OP_MSE_LOSS_GRAD: {
       need(in, 2, code);
       auto lg = mse_loss_grad(in[0], in[1]);

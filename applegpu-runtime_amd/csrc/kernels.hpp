@@ -125,6 +125,9 @@ struct Gemm {
   float ln_eps = 1e-5f;
   // B in the skinny kernel's packed layout (pack_weights), 16-bit, M <= 16
   bool b_packed = false;
+  // split-K launches leave the partial sums in the workspace (the caller
+  // consumes them) instead of reducing them into C
+  bool no_reduce = false;
   // Y = layer_norm(C) over N (gamma, beta [N]) computed by the split-K
   // reduction while it writes C (gemm_post_ln_fused); Y is [M, N] contiguous
   const void* pln_gamma = nullptr;
@@ -135,6 +138,8 @@ struct Gemm {
 // Whether the launch ends in a split-K reduction that can also produce
 // layer_norm(C) (one batch, N <= 2048); otherwise the caller runs layer_norm.
 bool gemm_post_ln_fused(const Gemm& g);
+// K splits of the launch's plan (1 when it has no split-K reduction).
+int gemm_splits(const Gemm& g);
 // Whether the skinny decode kernel takes this problem, and whether it can
 // also normalise the A rows (layer norm over K, K <= 4096) while loading them.
 bool gemm_is_skinny(const Gemm& g);
@@ -175,8 +180,17 @@ struct Attn {
   void* o = nullptr; int64_t o_sb = 0, o_sh = 0, o_st = 0;
   bool causal = false;   // key j visible to query i iff j <= i (diagonal at (0,0))
   float scale = 1.f;
+  // nsplit > 0 (2, 4 or 8; fp32): q, k, v point at split 0 of a split-K GEMM
+  // workspace whose partial sums are `plane` elements apart; each value is
+  // their sum (in split order) plus qb/kb/vb[h * b_sh + dim]
+  int nsplit = 0;
+  int64_t plane = 0, b_sh = 0;
+  const void* qb = nullptr; const void* kb = nullptr; const void* vb = nullptr;
 };
 bool attention_supported(const Attn& a);
+// Whether attention can read Q/K/V as projection partials (fp32 MFMA kernel:
+// d = 64 or 128, 16-byte aligned rows).
+bool attention_partials_ok(const Attn& a);
 void attention(const Attn& a, hipStream_t s);
 
 // ── KV-cache decode ───────────────────────────────────────────────────────

@@ -42,7 +42,29 @@ struct AArgs {
   float scale;
   int causal;
   int q_tiles;
+  // Q/K/V given as split-K partial sums of their projection (fp32 kernel,
+  // NSP > 0 partials `plane` elements apart) plus a bias, b_sh per head
+  const float* qb; const float* kb; const float* vb;
+  int64_t b_sh, plane;
 };
+
+// Four consecutive fp32 values: a plain load, or (NSP > 0) the sum of NSP
+// split-K partials in split order plus the bias: the split-K reduction's
+// arithmetic, so the values equal the materialised projection's.
+template <int NSP>
+__device__ __forceinline__ float4 ld_part4(const float* ptr, int64_t plane, const float* bias) {
+  float4 a = *(const float4*)ptr;
+  if constexpr (NSP > 0) {
+#pragma unroll
+    for (int sp = 1; sp < NSP; ++sp) {
+      const float4 b = *(const float4*)(ptr + sp * plane);
+      a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+    }
+    const float4 c = *(const float4*)bias;
+    a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+  }
+  return a;
+}
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) flash_attn(AArgs p) {
@@ -460,7 +482,7 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_mfma(AArgs p) {
 // Both K and V tiles sit in LDS untransposed, rows padded by 4 floats.
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
-template <int D>
+template <int D, int NSP>
 struct FaTile32 {
   static constexpr int C4 = D / 4;                           // float4 chunks per row
   static constexpr int NU = kFaKeys * C4 / (64 * kFaWaves);  // chunks per thread per operand
@@ -469,13 +491,13 @@ struct FaTile32 {
   float4 k0, k1, k2, k3, k4, k5, k6, k7, v0, v1, v2, v3, v4, v5, v6, v7;
 
   template <int I>
-  __device__ __forceinline__ void ld1(const float* K, const float* V, const AArgs& p, int64_t j0, int tid,
-                                      float4& k, float4& v) {
+  __device__ __forceinline__ void ld1(const float* K, const float* V, const float* KB, const float* VB,
+                                      const AArgs& p, int64_t j0, int tid, float4& k, float4& v) {
     if constexpr (I < NU) {
       const int e = tid + 64 * kFaWaves * I;
       const int64_t j = j0 + e / C4 < p.Tk ? j0 + e / C4 : p.Tk - 1;  // rows past Tk repeat row Tk-1
-      k = *(const float4*)(K + j * p.k_st + 4 * (e % C4));
-      v = *(const float4*)(V + j * p.v_st + 4 * (e % C4));
+      k = ld_part4<NSP>(K + j * p.k_st + 4 * (e % C4), p.plane, KB + 4 * (e % C4));
+      v = ld_part4<NSP>(V + j * p.v_st + 4 * (e % C4), p.plane, VB + 4 * (e % C4));
     }
   }
   template <int KP, int I>
@@ -486,11 +508,12 @@ struct FaTile32 {
       *(float4*)&Vs[(e / C4) * KP + 4 * (e % C4)] = v;
     }
   }
-  __device__ __forceinline__ void load(const float* K, const float* V, const AArgs& p, int64_t j0, int tid) {
-    ld1<0>(K, V, p, j0, tid, k0, v0); ld1<1>(K, V, p, j0, tid, k1, v1);
-    ld1<2>(K, V, p, j0, tid, k2, v2); ld1<3>(K, V, p, j0, tid, k3, v3);
-    ld1<4>(K, V, p, j0, tid, k4, v4); ld1<5>(K, V, p, j0, tid, k5, v5);
-    ld1<6>(K, V, p, j0, tid, k6, v6); ld1<7>(K, V, p, j0, tid, k7, v7);
+  __device__ __forceinline__ void load(const float* K, const float* V, const float* KB, const float* VB,
+                                       const AArgs& p, int64_t j0, int tid) {
+    ld1<0>(K, V, KB, VB, p, j0, tid, k0, v0); ld1<1>(K, V, KB, VB, p, j0, tid, k1, v1);
+    ld1<2>(K, V, KB, VB, p, j0, tid, k2, v2); ld1<3>(K, V, KB, VB, p, j0, tid, k3, v3);
+    ld1<4>(K, V, KB, VB, p, j0, tid, k4, v4); ld1<5>(K, V, KB, VB, p, j0, tid, k5, v5);
+    ld1<6>(K, V, KB, VB, p, j0, tid, k6, v6); ld1<7>(K, V, KB, VB, p, j0, tid, k7, v7);
   }
   template <int KP>
   __device__ __forceinline__ void store(float* Ks, float* Vs, int tid) const {
@@ -506,10 +529,11 @@ struct FaTile32 {
 // merge their running maxima, sums and outputs through LDS.  Used when there
 // are too few 64-query blocks to fill the GPU (GPT-2 at 128 tokens: 24):
 // each wavefront then does a quarter of the serial work.
-template <int D, bool KSPLIT>
+// NSP > 0: Q, K and V are read as split-K partials plus bias (ld_part4).
+template <int D, bool KSPLIT, int NSP>
 __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
   static_assert(D % 64 == 0, "d must be a multiple of 64");
-  constexpr int QB = KSPLIT ? 16 : kFaWaves * 16;  // query rows per block
+  constexpr int QB_ROWS = KSPLIT ? 16 : kFaWaves * 16;  // query rows per block
   constexpr int NT = KSPLIT ? 1 : 4;  // 16-key sub-tiles per wavefront and tile (KSPLIT: sub-tile w)
   constexpr int KP = D + 4;          // K and V tile row pitch (floats)
   constexpr int DS = D / 4;          // 4-deep steps of Q K^T
@@ -524,17 +548,21 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
   const int64_t tq = blockIdx.x / BH;
   const int64_t qt = p.causal ? p.q_tiles - 1 - tq : tq;
   const int64_t b = bh / p.H, h = bh % p.H;
-  const int64_t q0 = qt * QB;
+  const int64_t q0 = qt * QB_ROWS;
   const int64_t qw = KSPLIT ? q0 : q0 + (int64_t)w * 16;
   const int tw = KSPLIT ? w : 0;  // first key sub-tile of this wavefront
 
   const float* Q = (const float*)p.q + b * p.q_sb + h * p.q_sh;
   const float* K = (const float*)p.k + b * p.k_sb + h * p.k_sh;
   const float* V = (const float*)p.v + b * p.v_sb + h * p.v_sh;
+  // per-head bias (NSP > 0 only; otherwise unused, any legal address)
+  const float* QB = NSP > 0 ? p.qb + h * p.b_sh : Q;
+  const float* KB = NSP > 0 ? p.kb + h * p.b_sh : K;
+  const float* VB = NSP > 0 ? p.vb + h * p.b_sh : V;
 
   int64_t kv_end = p.Tk;
   if (p.causal) {
-    const int64_t qe = q0 + QB < p.Tq ? q0 + QB : p.Tq;
+    const int64_t qe = q0 + QB_ROWS < p.Tq ? q0 + QB_ROWS : p.Tq;
     kv_end = qe < p.Tk ? qe : p.Tk;
   }
   const int ntiles = (int)((kv_end + kFaKeys - 1) / kFaKeys);
@@ -545,7 +573,7 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
   float qf[DS];
 #pragma unroll
   for (int s = 0; s < DS; s += 4) {
-    const float4 x = *(const float4*)(Q + qr * p.q_st + g * DS + s);
+    const float4 x = ld_part4<NSP>(Q + qr * p.q_st + g * DS + s, p.plane, QB + g * DS + s);
     qf[s] = x.x; qf[s + 1] = x.y; qf[s + 2] = x.z; qf[s + 3] = x.w;
   }
   const int lim = (int)(p.causal ? (qi + 1 < p.Tk ? qi + 1 : p.Tk) : p.Tk);
@@ -557,8 +585,8 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
   const float c2 = p.scale * 1.4426950408889634f;
 
   if (ntiles > 0) {
-    FaTile32<D> t0;
-    t0.load(K, V, p, 0, tid);
+    FaTile32<D, NSP> t0;
+    t0.load(K, V, KB, VB, p, 0, tid);
     t0.template store<KP>(Ks[0], Vs[0], tid);
   }
   __syncthreads();
@@ -569,15 +597,15 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
     const int j0 = it * kFaKeys;
     // the next tile, in plain local registers (held in a struct, the tile
     // went to scratch memory once a scheduling barrier followed its loads)
-    constexpr int NU = FaTile32<D>::NU;
+    constexpr int NU = FaTile32<D, NSP>::NU;
     float4 k0, k1, k2, k3, k4, k5, k6, k7, v0, v1, v2, v3, v4, v5, v6, v7;
 #define AGPU_FA32_LD(I)                                                                    \
     if constexpr (I < NU) {                                                                \
       const int e = tid + 64 * kFaWaves * I;                                               \
       const int64_t jn = (int64_t)j0 + kFaKeys + e / (D / 4);                              \
       const int64_t jc = jn < p.Tk ? jn : p.Tk - 1;                                        \
-      k##I = *(const float4*)(K + jc * p.k_st + 4 * (e % (D / 4)));                        \
-      v##I = *(const float4*)(V + jc * p.v_st + 4 * (e % (D / 4)));                        \
+      k##I = ld_part4<NSP>(K + jc * p.k_st + 4 * (e % (D / 4)), p.plane, KB + 4 * (e % (D / 4))); \
+      v##I = ld_part4<NSP>(V + jc * p.v_st + 4 * (e % (D / 4)), p.plane, VB + 4 * (e % (D / 4))); \
     }
     AGPU_FA32_LD(0) AGPU_FA32_LD(1) AGPU_FA32_LD(2) AGPU_FA32_LD(3)
     AGPU_FA32_LD(4) AGPU_FA32_LD(5) AGPU_FA32_LD(6) AGPU_FA32_LD(7)
@@ -754,6 +782,26 @@ static void launch_fa_mfma(const AArgs& p, int64_t D, bool wide, unsigned blocks
   }
 }
 
+template <bool KS, int D>
+static void launch_fa32_d(const AArgs& p, int nsp, unsigned blocks, hipStream_t s) {
+  const dim3 grid(blocks), block(64 * kFaWaves);
+  switch (nsp) {
+    case 0: hipLaunchKernelGGL((flash_attn_f32<D, KS, 0>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((flash_attn_f32<D, KS, 2>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((flash_attn_f32<D, KS, 4>), grid, block, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((flash_attn_f32<D, KS, 8>), grid, block, 0, s, p); break;
+    default: fail("fused attention: %d projection partials (2, 4 or 8 supported)", nsp);
+  }
+}
+
+template <bool KS>
+static void launch_fa32(const AArgs& p, const Attn& a, unsigned blocks, hipStream_t s) {
+  if (a.D == 64) launch_fa32_d<KS, 64>(p, a.nsplit, blocks, s);
+  else launch_fa32_d<KS, 128>(p, a.nsplit, blocks, s);
+}
+
+bool attention_partials_ok(const Attn& a) { return a.dt == DType::F32 && attention_mfma_ok(a); }
+
 bool attention_supported(const Attn& a) {
   return (a.D == 64 || a.D == 128 || a.D == 32) && (a.dt == DType::F32 || a.dt == DType::F16 || a.dt == DType::BF16);
 }
@@ -770,6 +818,9 @@ void attention(const Attn& a, hipStream_t s) {
   p.o_sb = a.o_sb; p.o_sh = a.o_sh; p.o_st = a.o_st;
   p.scale = a.scale;
   p.causal = a.causal ? 1 : 0;
+  p.qb = (const float*)a.qb; p.kb = (const float*)a.kb; p.vb = (const float*)a.vb;
+  p.b_sh = a.b_sh; p.plane = a.plane;
+  if (a.nsplit > 0 && !attention_partials_ok(a)) fail("fused attention: projection partials need the fp32 MFMA kernel");
   if (attention_mfma_ok(a) && a.dt == DType::F32) {
     // 64 queries per block when that gives every CU a block; else 16 per
     // block with the key tiles split across the block's wavefronts
@@ -778,13 +829,11 @@ void attention(const Attn& a, hipStream_t s) {
     const int64_t blocks = a.B * a.H * p.q_tiles;
     if (blocks > 0x7fffffff) fail("fused attention: grid too large");
     if (ksplit) {
-      if (a.D == 64) hipLaunchKernelGGL((flash_attn_f32<64, true>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
-      else hipLaunchKernelGGL((flash_attn_f32<128, true>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
+      launch_fa32<true>(p, a, (unsigned)blocks, s);
       check_launch("attention");
       return;
     }
-    if (a.D == 64) hipLaunchKernelGGL((flash_attn_f32<64, false>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
-    else hipLaunchKernelGGL((flash_attn_f32<128, false>), dim3((unsigned)blocks), dim3(64 * kFaWaves), 0, s, p);
+    launch_fa32<false>(p, a, (unsigned)blocks, s);
     check_launch("attention");
     return;
   }

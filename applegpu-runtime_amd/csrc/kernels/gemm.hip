@@ -595,6 +595,12 @@ static bool reduce_vec_ok(const Gemm& g) {
          (!g.mask || g.k_sm % 4 == 0);
 }
 
+int gemm_splits(const Gemm& g) {
+  if (skinny_plan(g, cu_count()).use || thin_kind(g)) return 1;
+  const Plan pl = make_plan(g, cu_count());
+  return pl.kind == kMf ? pl.splits : 1;
+}
+
 bool gemm_post_ln_fused(const Gemm& g) {
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return false;
   if (g.batch != 1 || g.N > 2048 || g.N % 4 != 0 || g.c_sm != g.N) return false;
@@ -649,6 +655,7 @@ size_t gemm_workspace_bytes(const Gemm& g) {
 void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   if (g.pln_y && !gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
+  if (g.no_reduce && gemm_splits(g) < 2) fail("gemm: partial sums requested from a launch without a K split");
   const SkinnyPlan sp = skinny_plan(g, cu_count());
   if (sp.use) {
     Plan one{};
@@ -710,6 +717,7 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   }
   check_launch("gemm_mfma");
   if (pl.splits > 1) {
+    if (g.no_reduce) return;
     if (g.pln_y) {
       if (!gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
       AGPU_FLOAT_SWITCH(g.dt, launch_reduce_ln<T>(p, s));

@@ -1040,6 +1040,71 @@ TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool ca
   return out;
 }
 
+TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int64_t n_head, bool causal,
+                      int64_t batch, bool read_partials) {
+  const char* name = "qkv_attention";
+  if (x->ndim != 2 || w->ndim != 2 || b->ndim != 1) fail("%s: x [B*T, K], w [K, 3d] and b [3d] expected", name);
+  check_dtype(name, kFloatOnly, x->dtype);
+  if (w->dtype != x->dtype || b->dtype != x->dtype) fail("%s: dtypes differ", name);
+  const int64_t R = x->shape[0], K = x->shape[1], N = w->shape[1];
+  if (w->shape[0] != K || b->numel() != N || N % 3 != 0) fail("%s: w must be [%lld, 3d] and b [3d]", name, (long long)K);
+  const int64_t d = N / 3;
+  if (n_head <= 0 || d % n_head != 0) fail("%s: %lld columns do not split into %lld heads", name, (long long)d,
+                                           (long long)n_head);
+  if (batch <= 0 || R % batch != 0) fail("%s: %lld rows do not split into %lld sequences", name, (long long)R,
+                                         (long long)batch);
+  const int64_t T = R / batch, hd = d / n_head;
+
+  // The composed path: one GEMM with the bias, head views, attention.
+  auto composed = [&]() {
+    Epilogue e;
+    e.bias = b;
+    TensorP qkv = matmul(x, w, false, false, &e);
+    auto heads = [&](int64_t lo) {
+      TensorP part = slice(qkv, 1, lo, lo + d);
+      return transpose_dims(reshape(part, {batch, T, n_head, hd}), 1, 2);
+    };
+    TensorP a = attention(heads(0), heads(d), heads(2 * d), causal, true);
+    return reshape(transpose_dims(a, 1, 2), {R, d});
+  };
+  if (meta_mode() || !read_partials || x->dtype != DType::F32) return composed();
+
+  TensorP xc = x->strides[1] == 1 ? x : contiguous(x);
+  TensorP wc = w->strides[1] == 1 ? w : contiguous(w);
+  TensorP bc = contiguous(b);
+  k::Gemm g;
+  g.dt = g.b_dt = DType::F32;
+  g.M = R; g.N = N; g.K = K; g.batch = 1;
+  g.A = xc->data(); g.a_sm = xc->strides[0]; g.a_sk = 1; g.a_sb = R * K;
+  g.B = wc->data(); g.b_sk = wc->strides[0]; g.b_sn = 1; g.b_sb = K * N;
+  g.C = nullptr; g.c_sm = N; g.c_sb = R * N;
+  g.no_reduce = true;
+  const int splits = k::gemm_splits(g);
+  k::Attn a;
+  a.dt = DType::F32;
+  a.B = batch; a.H = n_head; a.Tq = T; a.Tk = T; a.D = hd;
+  a.causal = causal;
+  a.scale = 1.0f / std::sqrt((float)hd);
+  a.q_sb = a.k_sb = a.v_sb = T * N;
+  a.q_sh = a.k_sh = a.v_sh = hd;
+  a.q_st = a.k_st = a.v_st = N;
+  a.nsplit = splits;
+  a.plane = R * N;
+  a.b_sh = hd;
+  if (!(splits == 2 || splits == 4 || splits == 8)) return composed();
+  BufferP ws = scratch(k::gemm_workspace_bytes(g));
+  float* w0 = (float*)ws->ptr;
+  a.q = w0; a.k = w0 + d; a.v = w0 + 2 * d;
+  a.qb = bc->data(); a.kb = (const float*)bc->data() + d; a.vb = (const float*)bc->data() + 2 * d;
+  TensorP out = alloc_out(DType::F32, {batch, T, n_head, hd});
+  a.o = out->data();
+  a.o_sb = T * d; a.o_sh = hd; a.o_st = d;
+  if (!k::attention_partials_ok(a)) return composed();
+  LAUNCH k::gemm(g, ws->ptr, rt().stream());
+  LAUNCH k::attention(a, rt().stream());
+  return reshape(out, {R, d});
+}
+
 // ── KV-cache decode ────────────────────────────────────────────────────────
 // Shape checks shared by kv_write and decode_attention: 4-D [B, H, T, D]
 // operands with a unit stride along D.

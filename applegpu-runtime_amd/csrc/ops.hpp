@@ -98,6 +98,16 @@ TensorP matmul_packed(const TensorP& x, const TensorP& packed, int64_t N, const 
 // int8 weights with per-row scales (out = x @ (q * scale[:,None])^T)
 TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
 
+// GPT-2's attention block input side in one op: qkv = x w + b (x [B*T, K],
+// w [K, 3d] row-major, b [3d]), split into n_head heads of Q, K, V, then
+// (causal) attention; returns the head-merged output [B*T, d].  By default
+// the projection (with its split-K reduction) and the attention run one after
+// another.  read_partials (fp32, split-K plan): the attention kernel reads
+// the projection's partial sums plus the bias instead, one launch fewer; at
+// GPT-2 small's 128 tokens that measured slower (each head's K/V partials
+// are re-read by all 8 of its query blocks).  Same values either way.
+TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int64_t n_head, bool causal,
+                      int64_t batch, bool read_partials = false);
 // Attention over [..., T, D] operands (leading dims shared by q, k, v).
 // out_layout_thd: store the output physically as [..., T, H, D] (the result
 // is still logically [..., H, T, D]) so a following head merge is free.

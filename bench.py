@@ -142,7 +142,7 @@ def main():
 
     # ── op-by-op (uncaptured) reference timing ──────────────────────────────
     def gpt2_eager():
-        G.gpt2_forward(model, idx, positions=pos)[0].eval()
+        G.gpt2_forward(model, idx, positions=pos, need_cache=False)[0].eval()
 
     eager_mlp = EagerMLP(params)
     for _ in range(2):
@@ -164,7 +164,7 @@ def main():
     del eager_mlp
 
     # ── captured graphs ──────────────────────────────────────────────────────
-    g_fwd = gpu.capture(lambda: G.gpt2_forward(model, idx, positions=pos)[0])
+    g_fwd = gpu.capture(lambda: G.gpt2_forward(model, idx, positions=pos, need_cache=False)[0])
     g_train = gpu.capture(lambda: mlp.train_step(x, y, lr=0.01))
     for _ in range(args.warmup):
         g_fwd.replay()
