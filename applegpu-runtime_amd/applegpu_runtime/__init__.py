@@ -555,13 +555,21 @@ def kv_write_pair(k_cache, v_cache, k_rows, v_rows, pos):
         raise ValueError(ffi_error())
 
 
-def decode_attention(q, k_cache, v_cache, lens):
+def decode_attention(q, k_cache, v_cache, lens, k_new=None, v_new=None):
     """softmax(q K^T / sqrt(D)) V of q [B, H, Tq, D] over the first lens[b]
     rows of the [B, H, Tmax, D] caches (lens: int32 device tensor [B]); query
     row i of sequence b sees cache rows j <= lens[b] - Tq + i.  With Tq = 1
     this is the reference's decode step, non-causal attention of the new
-    token over the whole cache (python/applegpu_runtime/models/gpt2.py:132-135)."""
-    return _op(b"decode_attention", [_t(q), _t(k_cache), _t(v_cache), _t(lens)])
+    token over the whole cache (python/applegpu_runtime/models/gpt2.py:132-135).
+
+    k_new, v_new ([B, H, 1, D], Tq = 1): the step's own K and V rows, written
+    into the caches as row lens[b] - 1 by the same kernel when the result is
+    evaluated (the kv_write of the step, without a launch of its own); the
+    caches must not be read by anything else of the same graph."""
+    ins = [_t(q), _t(k_cache), _t(v_cache), _t(lens)]
+    if k_new is not None or v_new is not None:
+        ins += [_t(k_new), _t(v_new)]
+    return _op(b"decode_attention", ins)
 
 
 # ── graph capture ────────────────────────────────────────────────────────────

@@ -311,8 +311,8 @@ def gpt2_decode_step(model: dict, tokens, cache: KVCache):
     lens = cache.pos + cache.one
 
     def attend(i, q, k, v):
-        gpu.kv_write_pair(cache.k[i], cache.v[i], k, v, cache.pos)
-        return gpu.decode_attention(q, cache.k[i], cache.v[i], lens)
+        # the attention kernel stores k, v as cache row pos (= lens - 1)
+        return gpu.decode_attention(q, cache.k[i], cache.v[i], lens, k_new=k, v_new=v)
 
     for i in range(cfg["n_layer"]):
         x = _block(model, i, x, B, 1, attend)

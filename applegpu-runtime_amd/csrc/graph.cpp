@@ -194,7 +194,10 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       need(in, 2, code);
       return {dequantize_per_row(in[0], in[1], iv.empty() ? DType::F32 : dt_param(iv[0]))};
     case OP_LINEAR_INT8: need(in, 3, code); return {linear_int8(in[0], in[1], in[2])};
-    case OP_DECODE_ATTENTION: need(in, 4, code); return {decode_attention(in[0], in[1], in[2], in[3])};
+    case OP_DECODE_ATTENTION:
+      if (in.size() == 6) return {decode_attention(in[0], in[1], in[2], in[3], in[4], in[5])};
+      need(in, 4, code);
+      return {decode_attention(in[0], in[1], in[2], in[3])};
     case OP_PACK_WEIGHT: need(in, 1, code); return {pack_weight(in[0])};
     case OP_MATMUL_PACKED: need(in, 2, code); return {matmul_packed(in[0], in[1], ip(iv, 0, code))};
     case OP_SGD_MATMUL:

@@ -207,6 +207,10 @@ struct DecodeAttn {
   void* o = nullptr; int64_t o_sb = 0, o_sh = 0, o_st = 0;
   const int32_t* lens = nullptr;
   float scale = 1.f;
+  // optional (Tq == 1): the step's new K and V rows [B, H, 1, D], stored as
+  // cache row lens[b] - 1 by the same launch (and scored from registers)
+  const void* kn = nullptr; int64_t kn_sb = 0, kn_sh = 0;
+  const void* vn = nullptr; int64_t vn_sb = 0, vn_sh = 0;
 };
 bool decode_attention_supported(const DecodeAttn& a);
 int decode_attention_splits(const DecodeAttn& a, int64_t* chunk);

@@ -49,6 +49,10 @@ struct DArgs {
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st;
   float scale;
   int splits, chunk;
+  // append (Tq == 1): the new K and V rows [B, H, 1, D] (strides per batch
+  // and head); they become cache row lens[b] - 1
+  const void* kn; const void* vn;
+  int64_t kn_sb, kn_sh, vn_sb, vn_sh;
 };
 
 // 8 consecutive elements, raw: one 16-byte load (two for fp32) when VEC.
@@ -67,6 +71,15 @@ struct Raw8 {
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) s[i] = p[i];
+    }
+  }
+  __device__ __forceinline__ void store(T* p) const {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) ((uint4*)p)[i] = v[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p[i] = s[i];
     }
   }
   __device__ __forceinline__ void to_float(float (&x)[8]) const {
@@ -165,8 +178,11 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float (&a)[8], f
   m = M;
 }
 
-// NW waves per block, UN key steps in flight per wave.
-template <typename T, int D, bool VEC, int NW, int UN>
+// NW waves per block, UN key steps in flight per wave.  NEW (Tq == 1): the
+// step's own K/V row comes in beside the cache as key lens[b] - 1; the block
+// whose key range holds that key scores it from the new rows and stores it
+// into the cache, so the append costs no launch of its own.
+template <typename T, int D, bool VEC, int NW, int UN, bool NEW>
 __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
   constexpr int LPK = D / 8;           // lanes per key
   constexpr int KPS = 64 / LPK;        // keys per wave step
@@ -190,6 +206,7 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
   const T* K = (const T*)p.k + b * p.k_sb + h * p.k_sh + sub * 8;
   const T* V = (const T*)p.v + b * p.v_sb + h * p.v_sh + sub * 8;
   const int tmax = (int)p.Tmax, kst = (int)p.k_st, vst = (int)p.v_st;
+  int jnew = -1;  // NEW: cache row of the new K/V row, -1 for none
 
   // Raw K/V rows of one iteration, clamped into the cache (always legal) and
   // masked when scored.  The first iteration's loads go out before the
@@ -206,8 +223,16 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
   };
   load_iter(j_lo);
   const int64_t vis = visible_keys(p, b, i);
-  const int64_t j_hi = j_lo + p.chunk < vis ? j_lo + p.chunk : vis;
-
+  int64_t j_hi = j_lo + p.chunk < vis ? j_lo + p.chunk : vis;
+  if constexpr (NEW) {
+    // The new row is key lens[b] - 1, the last visible one.  A length
+    // outside [1, Tmax] names no cache row: the new row is then neither
+    // scored nor stored (kv_write drops such rows) and attention sees the
+    // cache as it is.  Otherwise the loop stops short of it.
+    const int64_t lb = p.lens[b];
+    jnew = (lb >= 1 && lb <= p.Tmax) ? (int)lb - 1 : -1;
+    if (jnew >= 0 && j_hi > jnew) j_hi = jnew;
+  }
   float m = -INFINITY, l = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
@@ -238,6 +263,32 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
     }
     m = mx;
     if (base + BS < j_hi) load_iter(base + BS);
+  }
+
+  if constexpr (NEW) {
+    // The block whose key range holds the new row: key group 0 of wave 0
+    // adds it as one more online-softmax term, and its lanes (8 dims each)
+    // store it into the cache.  No wave reads cache row jnew unmasked, so
+    // the store races with nothing that counts.
+    if (w == 0 && jnew >= j_lo && jnew < j_lo + p.chunk) {
+      Raw8<T, VEC> knr, vnr;
+      knr.load((const T*)p.kn + b * p.kn_sb + h * p.kn_sh + sub * 8);
+      vnr.load((const T*)p.vn + b * p.vn_sb + h * p.vn_sh + sub * 8);
+      const float d = group_sum<LPK>(dot8(qr, knr)) * c2;
+      if (g == 0) {
+        const float M = fmaxf(m, d);
+        const float f1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+        const float f2 = __builtin_amdgcn_exp2f(d - M);
+        float vx[8];
+        vnr.to_float(vx);
+        l = l * f1 + f2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] * f1 + f2 * vx[e];
+        m = M;
+        knr.store((T*)K + (int64_t)jnew * kst);
+        vnr.store((T*)V + (int64_t)jnew * vst);
+      }
+    }
   }
 
   // the wave's KPS key groups meet by xor shuffles over the group bits of
@@ -333,24 +384,30 @@ __global__ void __launch_bounds__(256) kv_write_kernel(KvArgs<E> a) {
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
-template <typename T, int D>
-void launch_decode(const DArgs& p, bool vec, int64_t rows, bool whole, hipStream_t s) {
+template <typename T, int D, bool NEW>
+void launch_decode_n(const DArgs& p, bool vec, int64_t rows, bool whole, hipStream_t s) {
   const dim3 grid((unsigned)p.splits, (unsigned)rows);
   constexpr int NWW = kDWavesWhole, UW = kDUnrollWhole, NWS = kDWavesSplit, US = kDUnrollSplit;
   // 6 key steps per wave when that covers the whole cache in one iteration
   constexpr int UW6 = kDUnrollWhole6;
   const bool one_pass = p.Tmax <= (int64_t)NWW * (64 / (D / 8)) * UW6;
   if (whole && one_pass) {
-    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW6>), grid, dim3(64 * NWW), 0, s, p);
-    else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW6>), grid, dim3(64 * NWW), 0, s, p);
+    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW6, NEW>), grid, dim3(64 * NWW), 0, s, p);
+    else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW6, NEW>), grid, dim3(64 * NWW), 0, s, p);
   } else if (whole) {
-    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW>), grid, dim3(64 * NWW), 0, s, p);
-    else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW>), grid, dim3(64 * NWW), 0, s, p);
+    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWW, UW, NEW>), grid, dim3(64 * NWW), 0, s, p);
+    else hipLaunchKernelGGL((decode_attn<T, D, false, NWW, UW, NEW>), grid, dim3(64 * NWW), 0, s, p);
   } else {
-    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWS, US>), grid, dim3(64 * NWS), 0, s, p);
-    else hipLaunchKernelGGL((decode_attn<T, D, false, NWS, US>), grid, dim3(64 * NWS), 0, s, p);
+    if (vec) hipLaunchKernelGGL((decode_attn<T, D, true, NWS, US, NEW>), grid, dim3(64 * NWS), 0, s, p);
+    else hipLaunchKernelGGL((decode_attn<T, D, false, NWS, US, NEW>), grid, dim3(64 * NWS), 0, s, p);
   }
   if (p.splits > 1) hipLaunchKernelGGL((decode_merge<T, D>), dim3((unsigned)rows), dim3(D), 0, s, p);
+}
+
+template <typename T, int D>
+void launch_decode(const DArgs& p, bool vec, int64_t rows, bool whole, hipStream_t s) {
+  if (p.kn) launch_decode_n<T, D, true>(p, vec, rows, whole, s);
+  else launch_decode_n<T, D, false>(p, vec, rows, whole, s);
 }
 
 template <typename E>
@@ -448,6 +505,11 @@ void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s) {
   p.v_sb = a.v_sb; p.v_sh = a.v_sh; p.v_st = a.v_st;
   p.o_sb = a.o_sb; p.o_sh = a.o_sh; p.o_st = a.o_st;
   p.scale = a.scale;
+  if (a.kn) {
+    if (a.Tq != 1 || !a.vn) fail("decode_attention: appending new K/V rows needs one query row per sequence");
+    p.kn = a.kn; p.vn = a.vn;
+    p.kn_sb = a.kn_sb; p.kn_sh = a.kn_sh; p.vn_sb = a.vn_sb; p.vn_sh = a.vn_sh;
+  }
   int64_t chunk;
   p.splits = decode_attention_splits(a, &chunk);
   p.chunk = (int)chunk;
@@ -461,7 +523,8 @@ void decode_attention(const DecodeAttn& a, void* ws, hipStream_t s) {
     return al16(ptr) && (s0 * es) % 16 == 0 && (s1 * es) % 16 == 0 && (s2 * es) % 16 == 0;
   };
   const bool vec = al(a.q, a.q_sb, a.q_sh, a.q_st) && al(a.k, a.k_sb, a.k_sh, a.k_st) &&
-                   al(a.v, a.v_sb, a.v_sh, a.v_st);
+                   al(a.v, a.v_sb, a.v_sh, a.v_st) &&
+                   (!a.kn || (al(a.kn, a.kn_sb, a.kn_sh, 0) && al(a.vn, a.vn_sb, a.vn_sh, 0)));
   AGPU_FLOAT_SWITCH(a.dt, {
     const bool whole = decode_whole(a);
     if (a.D == 32) launch_decode<T, 32>(p, vec, rows, whole, s);

@@ -1121,7 +1121,8 @@ static TensorP check_lens(const char* name, const char* what, const TensorP& len
   return contiguous(lens);
 }
 
-TensorP decode_attention(const TensorP& q, const TensorP& kc, const TensorP& vc, const TensorP& lens) {
+TensorP decode_attention(const TensorP& q, const TensorP& kc, const TensorP& vc, const TensorP& lens,
+                         const TensorP& k_new, const TensorP& v_new) {
   const char* name = "decode_attention";
   check_dtype(name, kFloatOnly, q->dtype);
   if (kc->dtype != q->dtype || vc->dtype != q->dtype) fail("%s: q and the caches must share a dtype", name);
@@ -1147,6 +1148,18 @@ TensorP decode_attention(const TensorP& q, const TensorP& kc, const TensorP& vc,
   a.k = kc->data(); a.k_sb = kc->strides[0]; a.k_sh = kc->strides[1]; a.k_st = kc->strides[2];
   a.v = vc->data(); a.v_sb = vc->strides[0]; a.v_sh = vc->strides[1]; a.v_st = vc->strides[2];
   a.lens = (const int32_t*)lc->data();
+  if (k_new || v_new) {
+    if (!k_new || !v_new) fail("%s: new K and V rows come together", name);
+    if (Tq != 1) fail("%s: appending new rows needs one query row per sequence, got %lld", name, (long long)Tq);
+    for (const TensorP& t : {k_new, v_new}) {
+      if (t->dtype != q->dtype) fail("%s: new rows must share q's dtype", name);
+      check_bhtd(name, "new rows", *t);
+      if (t->shape[0] != B || t->shape[1] != H || t->shape[2] != 1 || t->shape[3] != D)
+        fail("%s: new rows must be [%lld, %lld, 1, %lld]", name, (long long)B, (long long)H, (long long)D);
+    }
+    a.kn = k_new->data(); a.kn_sb = k_new->strides[0]; a.kn_sh = k_new->strides[1];
+    a.vn = v_new->data(); a.vn_sb = v_new->strides[0]; a.vn_sh = v_new->strides[1];
+  }
   // physical [B, Tq, H, D], logical [B, H, Tq, D]
   TensorP base = alloc_out(q->dtype, {B, Tq, H, D});
   TensorP out = make_meta(q->dtype, q->dims());

@@ -116,7 +116,11 @@ TensorP attention(const TensorP& q, const TensorP& k, const TensorP& v, bool cau
 // q [B, H, Tq, D] against the first lens[b] rows of the [B, H, Tmax, D] caches
 // (lens int32 [B] on the device; the queries' own keys are the last Tq of
 // them); the output is logically [B, H, Tq, D], stored as [B, Tq, H, D].
-TensorP decode_attention(const TensorP& q, const TensorP& k_cache, const TensorP& v_cache, const TensorP& lens);
+// With k_new / v_new ([B, H, 1, D], Tq == 1) the step's own K and V rows are
+// appended by the same launch: they become cache row lens[b] - 1 (dropped
+// when lens[b] exceeds the cache), so the caches are updated in place.
+TensorP decode_attention(const TensorP& q, const TensorP& k_cache, const TensorP& v_cache, const TensorP& lens,
+                         const TensorP& k_new = nullptr, const TensorP& v_new = nullptr);
 // cache[b, h, pos[b] + t, :] = rows[b, h, t, :] (pos int32 [B] on the device);
 // an optional second cache/rows pair of the same shape in the same launch.
 void kv_write(const TensorP& cache, const TensorP& rows, const TensorP& pos, const TensorP& cache2 = nullptr,

@@ -166,6 +166,74 @@ def test_decode_attention_whole_row_blocks_vs_oracle(gpu, dtype, tol, B, H, Tq, 
     assert rel_err(_host(got), _decode_ref(q, kc, vc, lens)) < tol
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("B,H,Tmax,D", [(8, 20, 640, 64), (2, 3, 300, 64), (4, 2, 97, 128), (8, 20, 97, 32)])
+def test_decode_attention_appending_new_rows(gpu, dtype, B, H, Tmax, D):
+    """k_new/v_new: the launch appends the step's K/V rows (as cache row
+    lens - 1) and attends over them.  Both caches equal kv_write_pair's bit
+    for bit; the output equals kv_write_pair followed by decode_attention up
+    to summation order (the new key is the last online-softmax term of its
+    block) and the float64 oracle within the attention bar, in whole-row
+    (B*H >= 128) and split-KV blocks, for lengths that put the new row in
+    the first key block, the middle and the last cache row."""
+    q = _round(RNG.standard_normal((B, H, 1, D)).astype(np.float32), dtype)
+    kc = _round(RNG.standard_normal((B, H, Tmax, D)).astype(np.float32), dtype)
+    vc = _round(RNG.standard_normal((B, H, Tmax, D)).astype(np.float32), dtype)
+    kn = _round(RNG.standard_normal((B, H, 1, D)).astype(np.float32), dtype)
+    vn = _round(RNG.standard_normal((B, H, 1, D)).astype(np.float32), dtype)
+    lens = np.linspace(1, Tmax, B).astype(np.int32)
+    lens[-1] = Tmax
+    pos = (lens - 1).astype(np.int32)
+    # fused
+    k1, v1 = _dev(gpu, kc, dtype), _dev(gpu, vc, dtype)
+    got = gpu.decode_attention(_dev(gpu, q, dtype), k1, v1, gpu.from_numpy(lens),
+                               k_new=_dev(gpu, kn, dtype), v_new=_dev(gpu, vn, dtype))
+    got_h = _host(got)
+    # two launches
+    k2, v2 = _dev(gpu, kc, dtype), _dev(gpu, vc, dtype)
+    gpu.kv_write_pair(k2, v2, _dev(gpu, kn, dtype), _dev(gpu, vn, dtype), gpu.from_numpy(pos))
+    want = _host(gpu.decode_attention(_dev(gpu, q, dtype), k2, v2, gpu.from_numpy(lens)))
+    if dtype == "float32":
+        np.testing.assert_allclose(got_h, want, rtol=1e-5, atol=1e-6)
+    else:  # one rounding of the 16-bit output apart
+        np.testing.assert_allclose(got_h, want, rtol=1e-2, atol=1e-3)
+    np.testing.assert_array_equal(_host(k1), _host(k2))
+    np.testing.assert_array_equal(_host(v1), _host(v2))
+    kref, vref = kc.copy(), vc.copy()
+    for bi in range(B):
+        kref[bi, :, pos[bi]] = kn[bi, :, 0]
+        vref[bi, :, pos[bi]] = vn[bi, :, 0]
+    tol = 1e-3 if dtype == "float32" else 2e-2
+    assert rel_err(got_h, _decode_ref(q, kref, vref, lens)) < tol
+
+
+def test_decode_attention_new_rows_past_the_cache_are_dropped(gpu):
+    """A length past Tmax: the cache keeps its rows (kv_write drops such rows
+    too) and attention covers the whole cache."""
+    B, H, Tmax, D = 2, 2, 40, 64
+    q = RNG.standard_normal((B, H, 1, D)).astype(np.float32)
+    kc = RNG.standard_normal((B, H, Tmax, D)).astype(np.float32)
+    vc = RNG.standard_normal((B, H, Tmax, D)).astype(np.float32)
+    kn = RNG.standard_normal((B, H, 1, D)).astype(np.float32)
+    kd, vd = gpu.from_numpy(kc), gpu.from_numpy(vc)
+    lens = np.array([Tmax + 1, 5], np.int32)
+    gpu.decode_attention(gpu.from_numpy(q), kd, vd, gpu.from_numpy(lens), k_new=gpu.from_numpy(kn),
+                         v_new=gpu.from_numpy(kn)).eval()
+    np.testing.assert_array_equal(_host(kd)[0], kc[0])      # nothing stored for sequence 0
+    np.testing.assert_array_equal(_host(kd)[1, :, 4], kn[1, :, 0])
+
+
+def test_decode_attention_new_rows_reject_bad_shapes(gpu):
+    q = gpu.from_numpy(RNG.standard_normal((1, 2, 2, 64)).astype(np.float32))
+    kc = gpu.from_numpy(RNG.standard_normal((1, 2, 8, 64)).astype(np.float32))
+    kn = gpu.from_numpy(RNG.standard_normal((1, 2, 1, 64)).astype(np.float32))
+    lens = gpu.from_numpy(np.array([4], np.int32))
+    with pytest.raises(ValueError):   # two query rows
+        gpu.decode_attention(q, kc, kc, lens, k_new=kn, v_new=kn).eval()
+    with pytest.raises(ValueError):   # V row missing
+        gpu.decode_attention(gpu.slice(q, 2, 0, 1), kc, kc, lens, k_new=kn).eval()
+
+
 def test_decode_attention_empty_and_clamped_lengths(gpu):
     """len 0 gives zeros; lengths past the cache are clamped to it."""
     B, H, Tmax, D = 3, 2, 70, 64
