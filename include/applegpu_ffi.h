@@ -205,7 +205,10 @@ float applegpu_ffi_event_elapsed_ms(uint32_t start_slot, uint32_t end_slot);
  * a captured graph that is replayed with advancing positions.  The matching
  * reader is the lazy op "decode_attention" (applegpu_graph_op): inputs q
  * [B, H, Tq, D], k_cache, v_cache [B, H, Tmax, D] and lens int32 [B]; query
- * row i of sequence b attends to cache rows j <= lens[b] - Tq + i.
+ * row i of sequence b attends to cache rows j <= lens[b] - Tq + i.  With
+ * Tq == 1 it takes two more inputs, k_new and v_new [B, H, 1, D]: the step's
+ * own rows, which the same launch stores as cache row lens[b] - 1 (when
+ * 1 <= lens[b] <= Tmax) and attends to, in place of this call.
  * Returns 0, or -1 with the error set. */
 int32_t applegpu_kv_write(uint64_t cache_id, uint64_t rows_id, uint64_t pos_id);
 /* The K and V appends of one layer in one launch: same contract as
