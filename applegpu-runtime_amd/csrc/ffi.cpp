@@ -758,10 +758,20 @@ uint64_t applegpu_eager_find_by_data_ptr(const uint8_t* ptr) {
   return rt().find_by_data_ptr(ptr);
 }
 
-int32_t applegpu_eager_execute_graph(const uint8_t*, uint32_t, const uint64_t*, uint32_t, const uint16_t*, uint32_t,
-                                     uint64_t*, uint8_t**) {
+int32_t applegpu_eager_execute_graph(const uint8_t* ops_data, uint32_t ops_len, const uint64_t* input_tids,
+                                     uint32_t n_inputs, const uint16_t* output_indices, uint32_t n_outputs,
+                                     uint64_t* out_tids, uint8_t** out_ptrs) {
+  // crates/core/src/eager_ffi.rs:661-708: returns the number of outputs, or
+  // -1 with "compiled graph failed: ..." set
   std::lock_guard<std::recursive_mutex> g(big_lock());
-  set_eager_err("unsupported: the torch.compile bytecode executor is not part of the MI355X backend");
+  try {
+    execute_compiled(ops_data, ops_len, input_tids, n_inputs, output_indices, n_outputs, out_tids, out_ptrs);
+    return (int32_t)n_outputs;
+  } catch (const std::exception& e) {
+    set_eager_err(std::string("compiled graph failed: ") + e.what());
+  } catch (...) {
+    set_eager_err("compiled graph failed: unknown error");
+  }
   return -1;
 }
 

@@ -328,28 +328,34 @@ void assign(const TensorP& dst, const TensorP& src) {
 
 }  // namespace
 
-void eval(const TensorP& root) {
-  if (!root->pending()) return;
-  // Post-order walk over pending ancestors (iterative).
+void eval(const TensorP& root) { eval_all({root}); }
+
+void eval_all(const std::vector<TensorP>& roots) {
+  // Post-order walk over the roots' pending ancestors (iterative), so the
+  // fusion plan below sees every root's subgraph at once.
   std::vector<TensorP> order;
   std::unordered_set<Tensor*> seen;
   std::vector<std::pair<TensorP, size_t>> stack;
-  stack.push_back({root, 0});
-  seen.insert(root.get());
-  while (!stack.empty()) {
-    auto& top = stack.back();
-    Node* n = top.first->node.get();
-    if (top.second < n->in.size()) {
-      TensorP c = n->in[top.second++];
-      if (c->pending() && !seen.count(c.get())) {
-        seen.insert(c.get());
-        stack.push_back({c, 0});
+  for (const TensorP& root : roots) {
+    if (!root || !root->pending() || seen.count(root.get())) continue;
+    stack.push_back({root, 0});
+    seen.insert(root.get());
+    while (!stack.empty()) {
+      auto& top = stack.back();
+      Node* n = top.first->node.get();
+      if (top.second < n->in.size()) {
+        TensorP c = n->in[top.second++];
+        if (c->pending() && !seen.count(c.get())) {
+          seen.insert(c.get());
+          stack.push_back({c, 0});
+        }
+      } else {
+        order.push_back(top.first);
+        stack.pop_back();
       }
-    } else {
-      order.push_back(top.first);
-      stack.pop_back();
     }
   }
+  if (order.empty()) return;
   g_stats.evals++;
   g_stats.nodes += order.size();
 

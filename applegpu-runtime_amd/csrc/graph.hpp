@@ -49,6 +49,16 @@ std::vector<TensorP> record_op(int code, const std::vector<TensorP>& in, const s
 
 // Materialise a pending tensor (no-op when it already has storage).
 void eval(const TensorP& t);
+// Materialise several pending tensors with one fusion plan over all their
+// pending ancestors (a node shared by two roots runs once).
+void eval_all(const std::vector<TensorP>& roots);
+
+// torch.compile bytecode executor (crates/core/src/compiled_graph.rs:61-193):
+// runs a serialized FX graph over the eager tensors `inputs` and returns
+// the ids and data pointers of the nodes `out_idx` names.  Throws on a
+// malformed graph or a failing op; nothing is written to the outputs then.
+void execute_compiled(const uint8_t* ops, size_t len, const uint64_t* inputs, uint32_t n_in, const uint16_t* out_idx,
+                      uint32_t n_out, uint64_t* out_ids, uint8_t** out_ptrs);
 
 struct GraphStats {
   uint64_t evals = 0, nodes = 0, fused_gemm_epilogues = 0, launches_saved = 0;

@@ -162,6 +162,31 @@ at::Tensor wrap(uint64_t id) {
   return make_tensor(std::move(storage), st, sizes, c10::contiguous_strides(sizes));
 }
 
+// Wraps any eager id, a strided view included, as a tensor that owns the id
+// (freed with the storage).  The storage starts at the id's first element
+// and spans the bytes its strides reach.  torch.compile graph outputs come
+// back this way without a copy.
+at::Tensor wrap_eager(int64_t id) {
+  ensure_init();
+  uint64_t dims[8];
+  int64_t strides[8];
+  uint32_t nd = 0, nd2 = 0;
+  if (applegpu_eager_shape((uint64_t)id, dims, &nd) != 0) fail_last("shape");
+  if (applegpu_eager_strides((uint64_t)id, strides, &nd2) != 0 || nd2 != nd) fail_last("strides");
+  const auto st = st_of(applegpu_eager_dtype((uint64_t)id));
+  std::vector<int64_t> sizes(dims, dims + nd), str(strides, strides + nd);
+  int64_t numel = 1, last = 0;
+  for (uint32_t i = 0; i < nd; ++i) {
+    numel *= sizes[i];
+    last += (sizes[i] - 1) * str[i];
+  }
+  void* p = applegpu_eager_data_ptr((uint64_t)id);
+  if (!p && numel > 0) fail_last("data_ptr");
+  const size_t bytes = numel > 0 ? (size_t)(last + 1) * c10::elementSize(st) : 0;
+  c10::Storage storage(c10::Storage::use_byte_size_t(), bytes, data_ptr_for(p, (uint64_t)id), &g_allocator, false);
+  return make_tensor(std::move(storage), st, sizes, str);
+}
+
 // Wraps an output as `like`'s shape when the runtime returned a [1] scalar.
 at::Tensor wrap_as(uint64_t id, c10::IntArrayRef sizes) {
   at::Tensor t = wrap(id);
@@ -595,6 +620,9 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("cat", ag_cat);
   m.impl("_local_scalar_dense", ag_local_scalar_dense);
 }
+
+// torch.ops.applegpu.wrap_eager(id): see wrap_eager above.
+TORCH_LIBRARY(applegpu, m) { m.def("wrap_eager(int id) -> Tensor", &wrap_eager); }
 
 TORCH_LIBRARY_IMPL(_, PrivateUse1, m) { m.fallback(torch::CppFunction::makeFromBoxedFunction<&cpu_fallback>()); }
 

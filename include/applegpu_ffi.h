@@ -123,9 +123,20 @@ uint8_t* applegpu_eager_softmax(uint64_t input_id, uint64_t* out_id);
 uint64_t applegpu_eager_find_by_data_ptr(const uint8_t* ptr);
 
 /* Exported but undeclared in the reference (eager_ffi.rs:661-708; bound via
- * ctypes in python/applegpu_runtime/compile_backend.py:961-1030).  The
- * torch.compile bytecode executor is not part of this backend: returns -1
- * with an "unsupported" error. */
+ * ctypes in python/applegpu_runtime/compile_backend.py:961-1030): runs a
+ * serialized torch.compile FX graph.  ops_data is the op list of
+ * crates/core/src/compiled_graph.rs:7-9 (per op: code u8, n_inputs u8,
+ * inputs u16[n], out_ndim u8, out_dims u64[ndim], out_dtype u8,
+ * params_len u8, params f32[plen]; codes 0-13 and 255 of
+ * compiled_graph.rs:43-57); node i < n_inputs is input_tids[i], each op
+ * appends one node.  Writes the id and data pointer of node
+ * output_indices[i] to out_tids[i] / out_ptrs[i]: an input (or its
+ * identity) comes back as its own id, every other returned node as a new id
+ * the caller frees, one id per node.  The ops are queued on the library
+ * stream (addmm + relu and other GEMM epilogues fuse); contents are valid
+ * after flush_and_wait or to any later op.  Returns n_outputs, or -1 with
+ * "compiled graph failed: ..." set (a malformed op list is rejected before
+ * anything runs). */
 int32_t applegpu_eager_execute_graph(const uint8_t* ops_data, uint32_t ops_len,
                                      const uint64_t* input_tids, uint32_t n_inputs,
                                      const uint16_t* output_indices, uint32_t n_outputs,

@@ -93,7 +93,7 @@ def test_init_without_gpu_reports_an_error():
         assert out.startswith("ERR:") and "device" in out.lower(), out
 
 
-def test_execute_graph_reports_unsupported_without_device():
+def test_execute_graph_reports_missing_device():
     code = (
         "import ctypes,sys; lib=ctypes.CDLL(sys.argv[1]);"
         "lib.applegpu_eager_last_error.restype=ctypes.c_char_p;"
@@ -101,4 +101,5 @@ def test_execute_graph_reports_unsupported_without_device():
         "print(r, lib.applegpu_eager_last_error().decode())"
     )
     out = subprocess.run(["python", "-c", code, LIB], capture_output=True, text=True, timeout=120).stdout.strip()
-    assert out.startswith("-1") and "unsupported" in out
+    if not _gpu_visible():
+        assert out.startswith("-1") and "device" in out, out
