@@ -489,6 +489,39 @@ def threshold_backward(grad_output, input, threshold):
 
 
 def softmax_backward(grad_output, output): return _op(b"softmax_backward", [_t(grad_output), _t(output)])
+
+
+# backward ops of the transformer blocks (crates/python/src/lib.rs:1153-1229)
+def layer_norm_backward(grad_output, input, gamma, eps=1e-5):
+    """dL/dx of layer_norm over the last dim (statistics recomputed from the
+    input); ops.rs:690-728."""
+    return _op(b"layer_norm_backward", [_t(grad_output), _t(input), _t(gamma)], f=(float(eps),))
+
+
+def layer_norm_grads(grad_output, input, gamma, eps=1e-5):
+    """(dx, dgamma, dbeta) of layer_norm: dx as layer_norm_backward, dgamma =
+    sum over rows of dy * xhat, dbeta = sum over rows of dy."""
+    return _op(b"layer_norm_grads", [_t(grad_output), _t(input), _t(gamma)], f=(float(eps),), nout=3)
+
+
+def gelu_backward(grad_output, input):
+    """grad * d/dx gelu_tanh(x) (ops.rs:1090-1111)."""
+    return _op(b"gelu_backward", [_t(grad_output), _t(input)])
+
+
+def gelu_tanh_backward(grad_output, input):
+    return _op(b"gelu_tanh_backward", [_t(grad_output), _t(input)])
+
+
+def gelu_exact_backward(grad_output, input):
+    """grad * (Phi(x) + x phi(x)) (ops.rs:1136-1158)."""
+    return _op(b"gelu_exact_backward", [_t(grad_output), _t(input)])
+
+
+def embedding_backward(grad_output, indices, num_weights):
+    """[num_weights, D] with row w = sum of the grad rows whose index is w,
+    added in token order (ops.rs:915-960)."""
+    return _op(b"embedding_backward", [_t(grad_output), _t(indices)], i=(int(num_weights),))
 def mse_loss(a, b): return _op(b"mse_loss", [_t(a), _t(b)])
 def mse_loss_backward(grad, a, b): return _op(b"mse_loss_backward", [_t(grad), _t(a), _t(b)])
 

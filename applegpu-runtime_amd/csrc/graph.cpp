@@ -32,6 +32,8 @@ enum Op : int {
   OP_QUANTIZE_PER_ROW, OP_DEQUANTIZE_PER_ROW, OP_LINEAR_INT8, OP_CONTIGUOUS, OP_FULL,
   OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
   OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD, OP_QKV_ATTENTION,
+  OP_LAYER_NORM_BACKWARD, OP_LAYER_NORM_GRADS, OP_GELU_BACKWARD, OP_GELU_TANH_BACKWARD, OP_GELU_EXACT_BACKWARD,
+  OP_EMBEDDING_BACKWARD,
   OP_COUNT
 };
 
@@ -50,6 +52,8 @@ static const char* kNames[OP_COUNT] = {
     "quantize_per_row", "dequantize_per_row", "linear_int8", "contiguous", "full",
     "decode_attention", "pack_weight", "matmul_packed",
     "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad", "qkv_attention",
+    "layer_norm_backward", "layer_norm_grads", "gelu_backward", "gelu_tanh_backward", "gelu_exact_backward",
+    "embedding_backward",
 };
 
 int op_code(const char* name) {
@@ -67,7 +71,10 @@ int op_code(const char* name) {
   return it == m.end() ? -1 : it->second;
 }
 const char* op_name(int code) { return code >= 0 && code < OP_COUNT ? kNames[code] : "?"; }
-int op_outputs(int code) { return code == OP_QUANTIZE_PER_ROW || code == OP_MSE_LOSS_GRAD ? 2 : 1; }
+int op_outputs(int code) {
+  if (code == OP_LAYER_NORM_GRADS) return 3;
+  return code == OP_QUANTIZE_PER_ROW || code == OP_MSE_LOSS_GRAD ? 2 : 1;
+}
 
 static void need(const std::vector<TensorP>& in, size_t n, int code) {
   if (in.size() != n) fail("%s expects %zu tensor inputs, got %zu", op_name(code), n, in.size());
@@ -145,6 +152,17 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
     case OP_MSE_LOSS: need(in, 2, code); return {mse_loss(in[0], in[1])};
     case OP_MSE_LOSS_BACKWARD: need(in, 3, code); return {mse_loss_backward(in[0], in[1], in[2])};
     case OP_SOFTMAX_BACKWARD: need(in, 2, code); return {softmax_backward(in[0], in[1])};
+    case OP_LAYER_NORM_BACKWARD:
+    case OP_LAYER_NORM_GRADS:
+      // (grad_output, input, gamma[, saved mean, saved rstd]), eps (default
+      // 1e-5, crates/python/src/lib.rs:1159)
+      if (in.size() != 3 && in.size() != 5) fail("%s expects 3 or 5 tensor inputs", op_name(code));
+      return layer_norm_grads(in[0], in[1], in[2], f.empty() ? 1e-5f : (float)f[0], code == OP_LAYER_NORM_GRADS,
+                              in.size() == 5 ? in[3] : nullptr, in.size() == 5 ? in[4] : nullptr);
+    case OP_GELU_BACKWARD:
+    case OP_GELU_TANH_BACKWARD: need(in, 2, code); return {gelu_backward(in[0], in[1], false)};
+    case OP_GELU_EXACT_BACKWARD: need(in, 2, code); return {gelu_backward(in[0], in[1], true)};
+    case OP_EMBEDDING_BACKWARD: need(in, 2, code); return {embedding_backward(in[0], in[1], ip(iv, 0, code))};
     case OP_THRESHOLD_BACKWARD:
       need(in, 2, code);
       return {threshold_backward(in[0], in[1], f.empty() ? 0.f : (float)f[0])};

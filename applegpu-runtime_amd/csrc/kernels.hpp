@@ -26,6 +26,8 @@ enum Bin : int {
   kLt, kGt, kLe, kGe, kEq, kNe,
   kThresholdBwd,  // out = b > p0 ? a : 0   (a = grad, b = input)
   kSoftmaxBwd,    // unused by the binary launcher (row kernel)
+  kGeluBwd,       // out = a * gelu_tanh'(b)  (a = grad, b = input)
+  kGeluExactBwd,  // out = a * gelu_erf'(b)
 };
 enum Un : int {
   kNeg, kRelu, kExp, kLog, kSqrt, kAbs, kSign, kTanh, kSin, kCos, kSigmoid,
@@ -63,6 +65,18 @@ void layer_norm(DType dt, const void* x, int64_t ldx, const void* gamma, const v
 enum RedOp : int { kRSum, kRMean, kRAmax, kRArgmax, kRVar };
 void row_reduce(int op, DType in, DType out, const void* x, int64_t ldx, void* y, int64_t rows,
                 int64_t cols, int correction, hipStream_t s);
+// layer_norm backward over contiguous [rows, cols] dy and x: dx with the
+// statistics recomputed from x, or taken from mean_in/rstd_in ([rows], the
+// input dtype) when given; stats (nullable) gets [rows][2] = (mean,
+// 1/sqrt(var + eps)).  layer_norm_param_grads then forms dgamma and dbeta
+// (column sums, fixed order) from dy, x and stats; `ws` holds
+// layer_norm_param_ws_bytes(rows, cols).
+void layer_norm_backward(DType dt, const void* dy, const void* x, const void* gamma, void* dx, float* stats,
+                         const void* mean_in, const void* rstd_in, int64_t rows, int64_t cols, float eps,
+                         hipStream_t s);
+size_t layer_norm_param_ws_bytes(int64_t rows, int64_t cols);
+void layer_norm_param_grads(DType dt, const void* dy, const void* x, const float* stats, void* dgamma, void* dbeta,
+                            float* ws, int64_t rows, int64_t cols, hipStream_t s);
 // Softmax backward: dx = y * (dy - sum(dy * y)) per row.
 void softmax_backward(DType dt, const void* dy, const void* y, void* dx, int64_t rows,
                       int64_t cols, hipStream_t s);
@@ -93,6 +107,10 @@ void mse_loss_grad(DType dt, const void* a, const void* b, void* loss, void* gra
 // ── indexing ──────────────────────────────────────────────────────────────
 void embedding(DType dt, const void* w, int64_t vocab, int64_t dim, DType idx_dt,
                const void* idx, int64_t n, void* out, hipStream_t s);
+// dw [nw, dim] = per-row sums of the dy [n, dim] rows each index names, in
+// token order (zeros elsewhere; indices outside [0, nw) add nothing).
+void embedding_backward(DType dt, const void* dy, DType idx_dt, const void* idx, int64_t n, int64_t dim,
+                        int64_t nw, void* dw, hipStream_t s);
 // Gathers along `dim` of a contiguous [outer, size, inner] tensor.
 // index_select: out[o, j, i] = x[o, idx[j], i]            (idx 1-D, length m)
 // gather:       out[o, j, i] = x[o, idx[o, j, i], i]      (idx shaped like out)

@@ -33,6 +33,23 @@ template <> __device__ __forceinline__ bool is_float_t<float>() { return true; }
 // +-10 before tanh (kernel_templates.rs:300-301), a no-op for fp32 tanh.
 __device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.f + erff(x * 0.70710678118654752f)); }
 
+// d/dx of gelu_tanh, with the forward's clamp of the inner term to +-10
+// (kernel_templates.rs:2074-2096 and :2100-2122 compute the same):
+// 0.5 (1 + t) + 0.5 x (1 - t^2) k (1 + 3 * 0.044715 x^2), t = tanh(k (x + 0.044715 x^3)).
+__device__ __forceinline__ float gelu_tanh_grad(float x) {
+  const float k = 0.7978845608028654f;
+  const float u = fminf(fmaxf(k * (x + 0.044715f * x * x * x), -10.f), 10.f);
+  const float t = tanhf(u);
+  return 0.5f * (1.f + t) + 0.5f * x * (1.f - t * t) * k * (1.f + 3.f * 0.044715f * x * x);
+}
+
+// d/dx of x * Phi(x): Phi(x) + x * phi(x) (kernel_templates.rs:2126-2152).
+__device__ __forceinline__ float gelu_erf_grad(float x) {
+  const float cdf = 0.5f * (1.f + erff(x * 0.70710678118654752f));
+  const float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
+  return cdf + x * pdf;
+}
+
 template <typename C>
 __device__ __forceinline__ C bin_apply(int op, C a, C b, float p0) {
   switch (op) {
@@ -57,6 +74,12 @@ __device__ __forceinline__ C bin_apply(int op, C a, C b, float p0) {
     case kEq: return a == b;
     case kNe: return a != b;
     case kThresholdBwd: return (float)b > p0 ? a : C(0);
+    case kGeluBwd:
+      if constexpr (std::is_floating_point<C>::value) return a * gelu_tanh_grad(b);
+      else return C(0);
+    case kGeluExactBwd:
+      if constexpr (std::is_floating_point<C>::value) return a * gelu_erf_grad(b);
+      else return C(0);
   }
   return C(0);
 }

@@ -157,6 +157,78 @@ __global__ void __launch_bounds__(256) embedding_kernel(const T* __restrict__ w,
   }
 }
 
+// ── embedding backward ────────────────────────────────────────────────────
+// dw[w, :] = sum of dy[i, :] over the tokens i with idx[i] == w, added in
+// token order; rows no token names are zero (filled first).  One 256-thread
+// block per token: the first token naming w collects every token naming w,
+// in ascending order, into an LDS list (wavefront ballots keep the order)
+// and writes the row, so each row has one writer and one summation order.
+// The reference scatters with float atomics (kernel_templates.rs:1867-1913),
+// whose order varies from run to run.  Tokens whose index is outside
+// [0, nw) add nothing.
+constexpr int kEbList = 1024;  // tokens gathered per round
+constexpr int kEbCols = 4;     // columns per thread: a pass covers 1024 columns
+
+template <typename T>
+__global__ void __launch_bounds__(256) fill_zero_kernel(T* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = T(0);
+}
+
+template <typename T, typename I>
+__global__ void __launch_bounds__(256) embedding_bwd_kernel(const T* __restrict__ dy, const I* __restrict__ idx,
+                                                            T* __restrict__ dw, int64_t n, int64_t dim,
+                                                            int64_t nw) {
+  __shared__ int64_t list[kEbList];
+  __shared__ int wave_cnt[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t i = blockIdx.x;
+  const int64_t w = (int64_t)idx[i];
+  if (w < 0 || w >= nw) return;  // uniform over the block
+  int dup = 0;
+#pragma unroll 8
+  for (int64_t j = tid; j < i; j += 256) dup |= (int64_t)idx[j] == w;
+  if (__syncthreads_or(dup)) return;  // an earlier token's block writes row w
+
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  for (int64_t c0 = 0; c0 < dim; c0 += 256 * kEbCols) {
+    float acc[kEbCols];
+#pragma unroll
+    for (int k = 0; k < kEbCols; ++k) acc[k] = 0.f;
+    int64_t t0 = i;
+    while (t0 < n) {
+      // gather the next round of matching tokens (ascending) into the list
+      int cnt = 0;
+      while (t0 < n && cnt <= kEbList - 256) {
+        const int64_t j = t0 + tid;
+        const bool m = j < n && (int64_t)idx[j] == w;
+        const uint64_t mask = __ballot(m);
+        if (lane == 0) wave_cnt[wv] = __popcll(mask);
+        __syncthreads();
+        int off = cnt;
+        for (int x = 0; x < wv; ++x) off += wave_cnt[x];
+        if (m) list[off + __popcll(mask & below)] = j;
+        cnt += wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+        __syncthreads();
+        t0 += 256;
+      }
+      for (int e = 0; e < cnt; ++e) {
+        const T* row = dy + list[e] * dim;
+#pragma unroll
+        for (int k = 0; k < kEbCols; ++k) {
+          const int64_t c = c0 + k * 256 + tid;
+          if (c < dim) acc[k] += to_f(row[c]);
+        }
+      }
+      __syncthreads();  // the list is refilled next round
+    }
+#pragma unroll
+    for (int k = 0; k < kEbCols; ++k) {
+      const int64_t c = c0 + k * 256 + tid;
+      if (c < dim) dw[w * dim + c] = from_f<T>(acc[k]);
+    }
+  }
+}
+
 template <typename T, typename I>
 __global__ void __launch_bounds__(256) index_select_kernel(const T* __restrict__ x, int64_t outer, int64_t size,
                                                            int64_t inner, const I* __restrict__ idx, int64_t m,
@@ -259,6 +331,23 @@ void embedding(DType dt, const void* w, int64_t vocab, int64_t dim, DType idx_dt
                                                vocab, dim, (const I*)idx, n, (TV*)out));
   });
   check_launch("embedding");
+}
+
+void embedding_backward(DType dt, const void* dy, DType idx_dt, const void* idx, int64_t n, int64_t dim,
+                        int64_t nw, void* dw, hipStream_t s) {
+  if (nw == 0 || dim == 0) return;
+  if (n > 0x7fffffffLL) fail("embedding_backward: %lld tokens exceed the grid", (long long)n);
+  AGPU_FLOAT_SWITCH(dt, {
+    typedef T TV;
+    const int64_t total = nw * dim;
+    const int64_t fb = (total + 255) / 256;
+    hipLaunchKernelGGL((fill_zero_kernel<TV>), dim3((unsigned)(fb < 8192 ? fb : 8192)), dim3(256), 0, s, (TV*)dw,
+                       total);
+    if (n > 0)
+      AGPU_INT_SWITCH(idx_dt, hipLaunchKernelGGL((embedding_bwd_kernel<TV, I>), dim3((unsigned)n), dim3(256), 0, s,
+                                                 (const TV*)dy, (const I*)idx, (TV*)dw, n, dim, nw));
+  });
+  check_launch("embedding_backward");
 }
 
 void index_select(DType dt, const void* x, int64_t outer, int64_t size, int64_t inner, DType idx_dt,

@@ -249,6 +249,178 @@ __global__ void __launch_bounds__(256) layer_norm_block(const T* __restrict__ x,
     yr[c] = from_f<T>(to_f(g[c]) * (to_f(xr[c]) - mean) * inv + to_f(b[c]));
 }
 
+// ── layer_norm backward ───────────────────────────────────────────────────
+// dx = inv * (dy*g - mean_j(dy*g) - xhat * mean_j(dy*g * xhat)) with the
+// row's mean and inv = 1/sqrt(var + eps) recomputed from x by the forward
+// kernel's own two-pass arithmetic (kernel_templates.rs:1601-1659).  stats
+// (optional) receives [rows][2] = (mean, inv) for the parameter gradients.
+// mean_in/rstd_in (optional, [rows]): the forward's saved statistics, used
+// instead of recomputing them (torch's layer_norm backward carries no eps).
+template <typename T, int NV, bool FULL>
+__global__ void __launch_bounds__(256) layer_norm_bwd_wave(const T* __restrict__ dy, const T* __restrict__ x,
+                                                           const T* __restrict__ g, T* __restrict__ dx,
+                                                           float* __restrict__ stats, const T* __restrict__ mean_in,
+                                                           const T* __restrict__ rstd_in, int64_t rows,
+                                                           int64_t cols, float eps, bool vec) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  const T* dr = dy + row * cols;
+  float v[NV][4], d[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    load4<T, FULL>(xr, c, cols, vec, 0.f, v[i]);
+    load4<T, FULL>(dr, c, cols, vec, 0.f, d[i]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s += v[i][j];
+  }
+  float mean, inv;
+  if (mean_in) {
+    mean = to_f(mean_in[row]);
+    inv = to_f(rstd_in[row]);
+  } else {
+    mean = wave_sum(s) / (float)cols;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = (c + j < cols) ? v[i][j] - mean : 0.f;
+        q += e * e;
+      }
+    }
+    inv = 1.f / sqrtf(wave_sum(q) / (float)cols + eps);
+  }
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float gv[4];
+    load4<T, FULL>(g, c, cols, vec, 0.f, gv);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float xh = (c + j < cols) ? (v[i][j] - mean) * inv : 0.f;
+      const float dg = d[i][j] * gv[j];  // 0 past the row (both loads fill 0)
+      v[i][j] = xh;
+      d[i][j] = dg;
+      s1 += dg;
+      s2 += dg * xh;
+    }
+  }
+  const float m1 = wave_sum(s1) / (float)cols, m2 = wave_sum(s2) / (float)cols;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = inv * (d[i][j] - m1 - v[i][j] * m2);
+    store4<T, FULL>(dx + row * cols, c, cols, vec, o);
+  }
+  if (stats && lane == 0) {
+    stats[2 * row] = mean;
+    stats[2 * row + 1] = inv;
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) layer_norm_bwd_block(const T* __restrict__ dy, const T* __restrict__ x,
+                                                            const T* __restrict__ g, T* __restrict__ dx,
+                                                            float* __restrict__ stats, const T* __restrict__ mean_in,
+                                                            const T* __restrict__ rstd_in, int64_t cols, float eps) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * cols;
+  const T* dr = dy + row * cols;
+  float mean, inv;
+  if (mean_in) {
+    mean = to_f(mean_in[row]);
+    inv = to_f(rstd_in[row]);
+  } else {
+    float s = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) s += to_f(xr[c]);
+    mean = block_sum(s, sh) / (float)cols;
+    float q = 0.f;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const float e = to_f(xr[c]) - mean;
+      q += e * e;
+    }
+    inv = 1.f / sqrtf(block_sum(q, sh) / (float)cols + eps);
+  }
+  float s1 = 0.f, s2 = 0.f;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float dg = to_f(dr[c]) * to_f(g[c]);
+    s1 += dg;
+    s2 += dg * (to_f(xr[c]) - mean) * inv;
+  }
+  const float m1 = block_sum(s1, sh) / (float)cols;
+  const float m2 = block_sum(s2, sh) / (float)cols;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) {
+    const float xh = (to_f(xr[c]) - mean) * inv;
+    dx[row * cols + c] = from_f<T>(inv * (to_f(dr[c]) * to_f(g[c]) - m1 - xh * m2));
+  }
+  if (stats && threadIdx.x == 0) {
+    stats[2 * row] = mean;
+    stats[2 * row + 1] = inv;
+  }
+}
+
+// dgamma[c] = sum_r dy[r,c] * (x[r,c] - mean_r) * inv_r, dbeta[c] = sum_r dy[r,c].
+// Stage 1: a 1024-thread block owns 64 columns of a chunk of kLnChunk rows
+// (16 row slices, merged through LDS) and writes fp32 partials
+// part[chunk][2][cols]; stage 2 adds the chunks in order (deterministic).
+constexpr int kLnChunk = 256;
+
+template <typename T>
+__global__ void __launch_bounds__(1024) ln_param_partials(const T* __restrict__ dy, const T* __restrict__ x,
+                                                          const float* __restrict__ stats, float* __restrict__ part,
+                                                          int64_t rows, int64_t cols) {
+  __shared__ float shg[16][64], shb[16][64];
+  const int lane = threadIdx.x & 63, slice = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t chunk = blockIdx.y;
+  const int64_t r1 = (chunk + 1) * kLnChunk < rows ? (chunk + 1) * kLnChunk : rows;
+  float sg = 0.f, sb = 0.f;
+  if (col < cols) {
+#pragma unroll 4
+    for (int64_t r = chunk * kLnChunk + slice; r < r1; r += 16) {
+      const float d = to_f(dy[r * cols + col]);
+      sb += d;
+      sg += d * (to_f(x[r * cols + col]) - stats[2 * r]) * stats[2 * r + 1];
+    }
+  }
+  shg[slice][lane] = sg;
+  shb[slice][lane] = sb;
+  __syncthreads();
+  if (slice == 0 && col < cols) {
+    float tg = 0.f, tb = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      tg += shg[i][lane];
+      tb += shb[i][lane];
+    }
+    part[(chunk * 2) * cols + col] = tg;
+    part[(chunk * 2 + 1) * cols + col] = tb;
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) ln_param_final(const float* __restrict__ part, T* __restrict__ dg,
+                                                      T* __restrict__ db, int64_t chunks, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float sg = 0.f, sb = 0.f;
+  for (int64_t k = 0; k < chunks; ++k) {
+    sg += part[(k * 2) * cols + c];
+    sb += part[(k * 2 + 1) * cols + c];
+  }
+  dg[c] = from_f<T>(sg);
+  db[c] = from_f<T>(sb);
+}
+
 // ── row reductions (one wavefront per row) ───────────────────────────────
 template <typename TI, typename TO>
 __global__ void __launch_bounds__(256) row_reduce_wave(int op, const TI* __restrict__ x, int64_t ldx,
@@ -599,6 +771,46 @@ void ln_launch(const void* x, int64_t ldx, const void* g, const void* b, void* y
   }
 }
 
+struct LnbArgs {
+  const void *dy, *x, *g, *mean_in, *rstd_in;
+  void* dx;
+  float* stats;
+  int64_t rows, cols;
+  float eps;
+};
+
+template <typename T, int NV>
+void lnb_nv(const LnbArgs& a, bool vec, hipStream_t s) {
+  if (vec && a.cols == NV * 256)
+    hipLaunchKernelGGL((layer_norm_bwd_wave<T, NV, true>), dim3(rows_grid(a.rows)), dim3(256), 0, s, (const T*)a.dy,
+                       (const T*)a.x, (const T*)a.g, (T*)a.dx, a.stats, (const T*)a.mean_in, (const T*)a.rstd_in,
+                       a.rows, a.cols, a.eps, vec);
+  else
+    hipLaunchKernelGGL((layer_norm_bwd_wave<T, NV, false>), dim3(rows_grid(a.rows)), dim3(256), 0, s,
+                       (const T*)a.dy, (const T*)a.x, (const T*)a.g, (T*)a.dx, a.stats, (const T*)a.mean_in,
+                       (const T*)a.rstd_in, a.rows, a.cols, a.eps, vec);
+}
+
+template <typename T>
+void lnb_launch(const LnbArgs& a, hipStream_t s) {
+  const bool vec = vec_ok(a.x, a.cols, sizeof(T)) && vec_ok(a.dy, a.cols, sizeof(T)) &&
+                   vec_ok(a.dx, a.cols, sizeof(T)) && vec_ok(a.g, 0, sizeof(T));
+  switch ((a.cols + 255) / 256) {
+    case 1: lnb_nv<T, 1>(a, vec, s); break;
+    case 2: lnb_nv<T, 2>(a, vec, s); break;
+    case 3: lnb_nv<T, 3>(a, vec, s); break;
+    case 4: lnb_nv<T, 4>(a, vec, s); break;
+    case 5: lnb_nv<T, 5>(a, vec, s); break;
+    case 6: lnb_nv<T, 6>(a, vec, s); break;
+    case 7: lnb_nv<T, 7>(a, vec, s); break;
+    case 8: lnb_nv<T, 8>(a, vec, s); break;
+    default:
+      hipLaunchKernelGGL((layer_norm_bwd_block<T>), dim3((unsigned)a.rows), dim3(256), 0, s, (const T*)a.dy,
+                         (const T*)a.x, (const T*)a.g, (T*)a.dx, a.stats, (const T*)a.mean_in, (const T*)a.rstd_in,
+                         a.cols, a.eps);
+  }
+}
+
 template <typename T>
 void q_launch(const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols, hipStream_t s) {
   bool vec = vec_ok(x, cols, sizeof(T)) && vec_ok(q, cols, 1);
@@ -688,6 +900,36 @@ void softmax_backward(DType dt, const void* dy, const void* y, void* dx, int64_t
   AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((softmax_bwd_wave<T>), dim3(rows_grid(rows)), dim3(256), 0, s,
                                            (const T*)dy, (const T*)y, (T*)dx, rows, cols));
   check_launch("softmax_backward");
+}
+
+void layer_norm_backward(DType dt, const void* dy, const void* x, const void* gamma, void* dx, float* stats,
+                         const void* mean_in, const void* rstd_in, int64_t rows, int64_t cols, float eps,
+                         hipStream_t s) {
+  if (rows == 0 || cols == 0) return;
+  if (rows > 0x7fffffffLL) fail("layer_norm_backward: too many rows");
+  if ((mean_in == nullptr) != (rstd_in == nullptr)) fail("layer_norm_backward: saved mean without rstd");
+  const LnbArgs a{dy, x, gamma, mean_in, rstd_in, dx, stats, rows, cols, eps};
+  AGPU_FLOAT_SWITCH(dt, lnb_launch<T>(a, s));
+  check_launch("layer_norm_backward");
+}
+
+size_t layer_norm_param_ws_bytes(int64_t rows, int64_t cols) {
+  return (size_t)((rows + kLnChunk - 1) / kLnChunk) * 2 * (size_t)cols * sizeof(float);
+}
+
+void layer_norm_param_grads(DType dt, const void* dy, const void* x, const float* stats, void* dgamma, void* dbeta,
+                            float* ws, int64_t rows, int64_t cols, hipStream_t s) {
+  if (cols == 0) return;
+  const int64_t chunks = (rows + kLnChunk - 1) / kLnChunk;
+  if (chunks > 65535) fail("layer_norm_backward: %lld rows exceed the parameter-gradient grid", (long long)rows);
+  AGPU_FLOAT_SWITCH(dt, {
+    if (chunks > 0)
+      hipLaunchKernelGGL((ln_param_partials<T>), dim3((unsigned)((cols + 63) / 64), (unsigned)chunks), dim3(1024), 0,
+                         s, (const T*)dy, (const T*)x, stats, ws, rows, cols);
+    hipLaunchKernelGGL((ln_param_final<T>), dim3((unsigned)((cols + 255) / 256)), dim3(256), 0, s, (const float*)ws,
+                       (T*)dgamma, (T*)dbeta, chunks, cols);
+  });
+  check_launch("layer_norm_param_grads");
 }
 
 void quantize_rows(DType in, const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols,

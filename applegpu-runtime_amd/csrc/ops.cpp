@@ -66,8 +66,8 @@ static void check_dtype(const char* op, Cls c, DType d) {
 static const char* bin_name(int op) {
   static const char* n[] = {"add", "sub", "mul", "div", "elem_min", "elem_max", "mod", "bitwise_and",
                             "bitwise_or", "bitwise_xor", "lt", "gt", "le", "ge", "eq", "ne",
-                            "threshold_backward"};
-  return op >= 0 && op <= k::kThresholdBwd ? n[op] : "binary";
+                            "threshold_backward", "softmax_backward", "gelu_backward", "gelu_exact_backward"};
+  return op >= 0 && op <= k::kGeluExactBwd ? n[op] : "binary";
 }
 
 static Cls bin_class(int op) {
@@ -77,7 +77,7 @@ static Cls bin_class(int op) {
     case k::kAnd: case k::kOr: case k::kXor: return kIntOrBool;
     case k::kLt: case k::kGt: case k::kLe: case k::kGe: return kOrdered;
     case k::kEq: case k::kNe: return kEquality;
-    case k::kThresholdBwd: return kFloatOnly;
+    case k::kThresholdBwd: case k::kGeluBwd: case k::kGeluExactBwd: return kFloatOnly;
   }
   return kAny;
 }
@@ -510,6 +510,82 @@ TensorP softmax_backward(const TensorP& dy, const TensorP& y) {
   TensorP out = alloc_out(a->dtype, a->dims());
   LAUNCH k::softmax_backward(a->dtype, a->data(), b->data(), out->data(), a->numel() / std::max<int64_t>(cols, 1), cols,
                       rt().stream());
+  return out;
+}
+
+// layer_norm backward (ops.rs:690-728 validates the same shapes): dx, and
+// with `params` also dgamma = sum_r dy * xhat and dbeta = sum_r dy, each
+// formed from statistics recomputed from x, or from the forward's saved
+// mean and rstd (one value per row) when given.
+std::vector<TensorP> layer_norm_grads(const TensorP& dy, const TensorP& x, const TensorP& g, float eps, bool params,
+                                      const TensorP& mean, const TensorP& rstd) {
+  check_dtype("layer_norm_backward", kFloatOnly, dy->dtype);
+  if (dy->dims() != x->dims())
+    fail("layer_norm_backward: grad_output shape %s != input shape %s", shape_str(dy->dims()).c_str(),
+         shape_str(x->dims()).c_str());
+  if (dy->dtype != x->dtype || g->dtype != x->dtype) fail("layer_norm_backward: dtypes of grad, input and gamma differ");
+  if (x->ndim < 1) fail("layer_norm_backward requires at least 1D tensor");
+  const int64_t cols = x->shape[x->ndim - 1];
+  if (!(g->ndim == 1 && g->shape[0] == cols))
+    fail("layer_norm_backward: gamma shape %s must be [%lld]", shape_str(g->dims()).c_str(), (long long)cols);
+  TensorP a = contiguous(dy), b = contiguous(x), gc = contiguous(g);
+  const int64_t rows = cols ? b->numel() / cols : 0;
+  TensorP mc, rc;
+  if (mean || rstd) {
+    if (!mean || !rstd) fail("layer_norm_backward: saved mean and rstd go together");
+    if (mean->numel() != rows || rstd->numel() != rows || mean->dtype != x->dtype || rstd->dtype != x->dtype)
+      fail("layer_norm_backward: saved mean/rstd must hold one %s per row (%lld rows)", dtype_name(x->dtype),
+           (long long)rows);
+    mc = contiguous(mean);
+    rc = contiguous(rstd);
+  }
+  const void* mp = mc ? mc->data() : nullptr;
+  const void* rp = rc ? rc->data() : nullptr;
+  TensorP dx = alloc_out(x->dtype, x->dims());
+  if (!params) {
+    LAUNCH k::layer_norm_backward(x->dtype, a->data(), b->data(), gc->data(), dx->data(), nullptr, mp, rp, rows, cols,
+                                  eps, rt().stream());
+    return {dx};
+  }
+  TensorP dg = alloc_out(x->dtype, {cols}), db = alloc_out(x->dtype, {cols});
+  if (!meta_mode()) {
+    BufferP st = scratch((size_t)std::max<int64_t>(rows, 1) * 2 * sizeof(float));
+    BufferP ws = scratch(std::max<size_t>(k::layer_norm_param_ws_bytes(rows, cols), 4));
+    k::layer_norm_backward(x->dtype, a->data(), b->data(), gc->data(), dx->data(), (float*)st->ptr, mp, rp, rows,
+                           cols, eps, rt().stream());
+    k::layer_norm_param_grads(x->dtype, a->data(), b->data(), (const float*)st->ptr, dg->data(), db->data(),
+                              (float*)ws->ptr, rows, cols, rt().stream());
+  }
+  return {dx, dg, db};
+}
+
+TensorP gelu_backward(const TensorP& grad, const TensorP& x, bool exact) {
+  // ops.rs:1090-1158: same shapes and dtype; the tanh form is gelu_backward
+  // and gelu_tanh_backward, the erf form gelu_exact_backward
+  if (grad->dims() != x->dims())
+    fail("gelu_backward shape mismatch: grad %s vs input %s", shape_str(grad->dims()).c_str(),
+         shape_str(x->dims()).c_str());
+  return binary(exact ? k::kGeluExactBwd : k::kGeluBwd, grad, x);
+}
+
+TensorP embedding_backward(const TensorP& grad, const TensorP& idx, int64_t num_weights) {
+  // ops.rs:915-960: int indices, grad [..., D] whose leading extent is the
+  // number of indices; the result is [num_weights, D] in grad's dtype
+  check_dtype("embedding_backward", kFloatOnly, grad->dtype);
+  if (idx->dtype != DType::I32 && idx->dtype != DType::I64)
+    fail("embedding_backward indices must be Int32, got %s", dtype_name(idx->dtype));
+  if (grad->ndim < 1) fail("embedding_backward grad_output must have at least 1 dimension");
+  if (idx->ndim < 1) fail("embedding_backward indices must have at least 1 dimension");
+  if (num_weights < 0) fail("embedding_backward: negative num_weights");
+  const int64_t dim = grad->shape[grad->ndim - 1];
+  const int64_t n = idx->numel();
+  const int64_t prefix = dim ? grad->numel() / dim : 0;
+  if (dim && prefix != n)
+    fail("embedding_backward: grad_output prefix %lld != indices numel %lld", (long long)prefix, (long long)n);
+  TensorP gc = contiguous(grad), ic = contiguous(idx);
+  TensorP out = alloc_out(grad->dtype, {num_weights, dim});
+  LAUNCH k::embedding_backward(grad->dtype, gc->data(), ic->dtype, ic->data(), n, dim, num_weights, out->data(),
+                               rt().stream());
   return out;
 }
 

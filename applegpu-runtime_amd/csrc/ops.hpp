@@ -45,6 +45,11 @@ TensorP softmax(const TensorP& x, int mode /* k::RowOp */);
 TensorP layer_norm(const TensorP& x, const TensorP& g, const TensorP& b, float eps);
 TensorP row_reduce(int op /* k::RedOp */, const TensorP& x, int correction = 0);
 TensorP softmax_backward(const TensorP& dy, const TensorP& y);
+// layer_norm backward: {dx} or, with params, {dx, dgamma, dbeta}.
+std::vector<TensorP> layer_norm_grads(const TensorP& dy, const TensorP& x, const TensorP& g, float eps, bool params,
+                                      const TensorP& mean = nullptr, const TensorP& rstd = nullptr);
+TensorP gelu_backward(const TensorP& grad, const TensorP& x, bool exact);
+TensorP embedding_backward(const TensorP& grad, const TensorP& idx, int64_t num_weights);
 std::pair<TensorP, TensorP> quantize_per_row(const TensorP& x);             // (int8 codes, f32 scales)
 TensorP dequantize_per_row(const TensorP& q, const TensorP& scale, DType dt);
 

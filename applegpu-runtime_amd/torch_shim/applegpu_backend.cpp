@@ -525,6 +525,53 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> ag_native_layer_norm(const at::Te
   return {y, mean, rstd};
 }
 
+// dx (and dgamma, dbeta) from the forward's saved mean and rstd, so the
+// forward's eps carries over; the reference recomputes with eps = 1e-5 and
+// forms dgamma/dbeta on the CPU (python/applegpu_runtime/torch_backend.py:1652-1692).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> ag_native_layer_norm_backward(
+    const at::Tensor& grad_out, const at::Tensor& input, c10::SymIntArrayRef nshape, const at::Tensor& mean,
+    const at::Tensor& rstd, const std::optional<at::Tensor>& weight, const std::optional<at::Tensor>& bias,
+    std::array<bool, 3> mask) {
+  TORCH_CHECK(nshape.size() == 1, "applegpu native_layer_norm_backward: normalized over the last dim only");
+  const int64_t cols = input.size(-1);
+  const bool has_w = weight.has_value() && weight->defined();
+  at::Tensor g = has_w ? *weight : at::ones({cols}, input.options());
+  Views v;
+  uint64_t ins[5] = {v.of(grad_out), v.of(input), v.of(g), v.of(mean.to(input.scalar_type())),
+                     v.of(rstd.to(input.scalar_type()))};
+  uint64_t out[3] = {0, 0, 0};
+  const double eps = 1e-5;  // unused: the saved statistics are used
+  if (applegpu_eager_op("layer_norm_grads", ins, 5, &eps, 1, nullptr, 0, out, 3) != 3) fail_last("layer_norm_grads");
+  at::Tensor dx = wrap(out[0]), dg = wrap(out[1]), db = wrap(out[2]);
+  return {mask[0] ? dx.view(input.sizes()) : at::Tensor(), mask[1] && has_w ? dg : at::Tensor(),
+          mask[2] && bias.has_value() && bias->defined() ? db : at::Tensor()};
+}
+
+at::Tensor ag_gelu_backward(const at::Tensor& grad, const at::Tensor& self, c10::string_view approximate) {
+  return run_t(approximate == "tanh" ? "gelu_backward" : "gelu_exact_backward", {grad, self});
+}
+
+// Rows summed in token order on the device (deterministic); padding_idx's
+// row stays zero as torch defines it.
+at::Tensor ag_embedding_dense_backward(const at::Tensor& grad, const at::Tensor& indices, c10::SymInt num_weights,
+                                       c10::SymInt padding_idx, bool scale_grad_by_freq) {
+  TORCH_CHECK(!scale_grad_by_freq, "applegpu embedding backward: scale_grad_by_freq is not supported");
+  const int64_t nw = num_weights.expect_int(), pad = padding_idx.expect_int();
+  at::Tensor idx = indices.reshape({-1});
+  at::Tensor g = grad.reshape({idx.numel(), grad.size(-1)});
+  at::Tensor dw = run_t("embedding_backward", {g, idx}, {}, {nw});
+  if (pad >= 0 && pad < nw) dw.select(0, pad).zero_();
+  return dw;
+}
+
+at::Tensor ag_softmax_backward_data(const at::Tensor& grad, const at::Tensor& out, int64_t dim,
+                                    at::ScalarType input_dtype) {
+  TORCH_CHECK(input_dtype == grad.scalar_type(), "applegpu _softmax_backward_data: mixed dtypes are not supported");
+  const int64_t d = c10::maybe_wrap_dim(dim, grad.dim());
+  if (d == grad.dim() - 1) return run_t("softmax_backward", {grad, out});
+  return run_t("softmax_backward", {grad.transpose(d, -1), out.transpose(d, -1)}).transpose(d, -1);
+}
+
 at::Tensor ag_softmax(const at::Tensor& self, int64_t dim, bool half_to_float) {
   TORCH_CHECK(!half_to_float, "applegpu _softmax: half_to_float is not supported");
   const int64_t d = c10::maybe_wrap_dim(dim, self.dim());
@@ -615,6 +662,10 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("sum", ag_sum);
   m.impl("embedding", ag_embedding);
   m.impl("native_layer_norm", ag_native_layer_norm);
+  m.impl("native_layer_norm_backward", ag_native_layer_norm_backward);
+  m.impl("gelu_backward", ag_gelu_backward);
+  m.impl("embedding_dense_backward", ag_embedding_dense_backward);
+  m.impl("_softmax_backward_data", ag_softmax_backward_data);
   m.impl("_softmax", ag_softmax);
   m.impl("_log_softmax", ag_log_softmax);
   m.impl("cat", ag_cat);

@@ -138,6 +138,62 @@ def mse_loss_backward(g, a, b):
     return ((a.astype(np.float64) - b.astype(np.float64)) * (2.0 / n) * float(g.reshape(-1)[0])).astype(a.dtype)
 
 
+# ── backward ops of the transformer blocks ────────────────────────────────
+def softmax_backward(dy, y):
+    """y * (dy - sum(dy * y)) per row — crates/core/src/kernel_templates.rs:1562-1597."""
+    dy64, y64 = dy.astype(np.float64), y.astype(np.float64)
+    return (y64 * (dy64 - (dy64 * y64).sum(-1, keepdims=True))).astype(dy.dtype)
+
+
+def layer_norm_backward(dy, x, gamma, eps=1e-5, params=False):
+    """dx = inv (dy g - mean(dy g) - xhat mean(dy g xhat)), statistics from x
+    (two-pass mean, population variance) — kernel_templates.rs:1601-1659;
+    with params also dgamma = sum_rows(dy xhat), dbeta = sum_rows(dy)
+    (python/applegpu_runtime/torch_backend.py:1652-1692 computes those)."""
+    x64, dy64, g64 = x.astype(np.float64), dy.astype(np.float64), gamma.astype(np.float64)
+    mean = x64.mean(-1, keepdims=True)
+    inv = 1.0 / np.sqrt(((x64 - mean) ** 2).mean(-1, keepdims=True) + eps)
+    xh = (x64 - mean) * inv
+    dg = dy64 * g64
+    dx = inv * (dg - dg.mean(-1, keepdims=True) - xh * (dg * xh).mean(-1, keepdims=True))
+    if not params:
+        return dx.astype(x.dtype)
+    flat = (-1, x.shape[-1])
+    return (dx.astype(x.dtype), (dy64 * xh).reshape(flat).sum(0).astype(x.dtype),
+            dy64.reshape(flat).sum(0).astype(x.dtype))
+
+
+def gelu_tanh_backward(dy, x):
+    """dy * d/dx gelu_tanh(x), inner term clamped to +-10 — kernel_templates.rs:2074-2122."""
+    x64 = x.astype(np.float64)
+    k = math.sqrt(2.0 / math.pi)
+    t = np.tanh(np.clip(k * (x64 + 0.044715 * x64 ** 3), -10.0, 10.0))
+    d = 0.5 * (1.0 + t) + 0.5 * x64 * (1.0 - t * t) * k * (1.0 + 3.0 * 0.044715 * x64 * x64)
+    return (dy.astype(np.float64) * d).astype(dy.dtype)
+
+
+def gelu_erf_backward(dy, x):
+    """dy * (Phi(x) + x phi(x)) — kernel_templates.rs:2126-2152 (erf from math.erf)."""
+    x64 = x.astype(np.float64)
+    cdf = 0.5 * (1.0 + np.vectorize(math.erf)(x64 / math.sqrt(2.0)))
+    pdf = np.exp(-0.5 * x64 * x64) / math.sqrt(2.0 * math.pi)
+    return (dy.astype(np.float64) * (cdf + x64 * pdf)).astype(dy.dtype)
+
+
+def embedding_backward(dy, idx, num_weights):
+    """Row w = sum of dy rows whose index is w — ops.rs:915-960,
+    kernel_templates.rs:1867-1913.  Added in token order in float32, the
+    order the device kernel uses, so results compare bit for bit; indices
+    outside [0, num_weights) add nothing."""
+    idx = np.asarray(idx).reshape(-1)
+    rows = dy.reshape(idx.size, -1).astype(np.float32)
+    out = np.zeros((num_weights, rows.shape[1]), np.float32)
+    for i, w in enumerate(idx):
+        if 0 <= w < num_weights:
+            out[w] = out[w] + rows[i]
+    return out.astype(dy.dtype)
+
+
 # ── GEMM / attention ───────────────────────────────────────────────────────
 def matmul(a, b):
     """Batched row-major C = A @ B with fp32 results; batch dims broadcast and a

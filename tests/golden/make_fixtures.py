@@ -52,6 +52,17 @@ KNOWN = [
     {"src": "python/tests/test_transformer_ops.py:102-120", "op": "embedding",
      "w": [[0.1, 0.2, 0.3], [1.1, 1.2, 1.3], [2.1, 2.2, 2.3], [3.1, 3.2, 3.3], [4.1, 4.2, 4.3]],
      "idx": [0, 3, 1], "expect": [[0.1, 0.2, 0.3], [3.1, 3.2, 3.3], [1.1, 1.2, 1.3]], "atol": 0.0},
+    {"src": "crates/core/src/ops.rs:4573-4611", "op": "softmax_backward", "y": [[0.2, 0.3, 0.5], [0.1, 0.7, 0.2]],
+     "dy": [[1.0, 0.0, 0.0], [0.0, 1.0, 0.0]], "expect": [[0.16, -0.06, -0.10], [-0.07, 0.21, -0.14]], "atol": 1e-5},
+    {"src": "crates/core/src/ops.rs:4618-4647", "op": "softmax_backward_ones", "x": [[1.0, 2.0, 3.0], [4.0, 1.0, 2.0]],
+     "expect_abs_max": 0.0, "atol": 1e-5},
+    {"src": "crates/core/src/ops.rs:4699-4730", "op": "layer_norm_backward_row_sums",
+     "x": [[1, 2, 3, 4], [5, 6, 7, 8]], "gamma": [1, 1, 1, 1], "dy": [[1] * 4] * 2, "expect_row_sums": [0.0, 0.0],
+     "atol": 1e-4},
+    {"src": "crates/core/src/ops.rs:4973-4998", "op": "embedding_backward", "dy": [[1, 2], [3, 4], [5, 6]],
+     "idx": [0, 1, 0], "num_weights": 3, "expect": [[6, 8], [3, 4], [0, 0]], "atol": 1e-4},
+    {"src": "crates/core/src/ops.rs:5000-5021", "op": "embedding_backward", "dy": [[10, 20], [30, 40], [50, 60]],
+     "idx": [0, 1, 2], "num_weights": 3, "expect": [[10, 20], [30, 40], [50, 60]], "atol": 1e-4},
 ]
 
 

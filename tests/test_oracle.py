@@ -48,6 +48,21 @@ def test_known_answers(known):
         elif op == "embedding":
             np.testing.assert_array_equal(O.embedding(np.array(k["w"], np.float32), k["idx"]),
                                           np.array(k["expect"], np.float32))
+        elif op == "softmax_backward":
+            got = O.softmax_backward(np.array(k["dy"], np.float32), np.array(k["y"], np.float32))
+            np.testing.assert_allclose(got, k["expect"], atol=k["atol"], err_msg=k["src"])
+            np.testing.assert_allclose(got.sum(-1), 0.0, atol=k["atol"])
+        elif op == "softmax_backward_ones":
+            y = O.softmax(np.array(k["x"], np.float32))
+            got = O.softmax_backward(np.ones_like(y), y)
+            assert np.abs(got).max() <= k["expect_abs_max"] + k["atol"], k["src"]
+        elif op == "layer_norm_backward_row_sums":
+            got = O.layer_norm_backward(np.array(k["dy"], np.float32), np.array(k["x"], np.float32),
+                                        np.array(k["gamma"], np.float32))
+            np.testing.assert_allclose(got.sum(-1), k["expect_row_sums"], atol=k["atol"], err_msg=k["src"])
+        elif op == "embedding_backward":
+            got = O.embedding_backward(np.array(k["dy"], np.float32), k["idx"], k["num_weights"])
+            np.testing.assert_allclose(got, k["expect"], atol=k["atol"], err_msg=k["src"])
         else:
             raise AssertionError(f"unhandled known answer {op}")
 
@@ -257,6 +272,43 @@ def test_torch_cpu_kv_decoder_matches_full_recompute():
         ref, _ = M.gpt2_forward_np(w, cfg, np.concatenate([ids[b], toks[b, :-1]]))
         np.testing.assert_allclose(np.stack([s[b] for s in steps]), ref[T - 1:], rtol=1e-4, atol=1e-4)
         np.testing.assert_allclose(lg[b].numpy(), ref[:T], rtol=1e-4, atol=1e-4)
+
+
+def _torch_grads(fn, dy, *xs):
+    ts = [torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in xs]
+    fn(*ts).backward(torch.tensor(dy, dtype=torch.float64))
+    return [t.grad.numpy() for t in ts]
+
+
+def test_backward_ops_vs_torch_autograd():
+    """The backward restatements against torch's autograd of the forward op
+    in float64, at ragged and GPT-2 widths (a dropped term or wrong sign in
+    any of them moves the result far past these bounds)."""
+    rng = np.random.default_rng(44)
+    for rows, cols in [(3, 7), (16, 768), (5, 2500)]:
+        x = rng.standard_normal((rows, cols)).astype(np.float32) * 2 + 0.5
+        g = rng.standard_normal(cols).astype(np.float32)
+        b = rng.standard_normal(cols).astype(np.float32)
+        dy = rng.standard_normal((rows, cols)).astype(np.float32)
+        tx, tg, tb = _torch_grads(lambda a, w, c: F.layer_norm(a, (cols,), w, c, 1e-5), dy, x, g, b)
+        dx, dg, db = O.layer_norm_backward(dy, x, g, 1e-5, params=True)
+        np.testing.assert_allclose(dx, tx, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(dg, tg, rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(db, tb, rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(O.layer_norm_backward(dy, x, g), dx)
+        (ts,) = _torch_grads(lambda a: torch.softmax(a, -1), dy, x)
+        np.testing.assert_allclose(O.softmax_backward(dy, O.softmax(x)), ts, rtol=1e-4, atol=1e-6)
+        for approx, fn in (("tanh", O.gelu_tanh_backward), ("none", O.gelu_erf_backward)):
+            (tgl,) = _torch_grads(lambda a: F.gelu(a, approximate=approx), dy, x)
+            np.testing.assert_allclose(fn(dy, x), tgl, rtol=1e-5, atol=1e-6)
+    # embedding: repeated, unused and every-row indices
+    w = rng.standard_normal((50, 24)).astype(np.float32)
+    idx = np.concatenate([rng.integers(0, 50, 300), [7] * 40, [49, 0]]).astype(np.int64)
+    dy = rng.standard_normal((idx.size, 24)).astype(np.float32)
+    tw = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    F.embedding(torch.tensor(idx), tw).backward(torch.tensor(dy, dtype=torch.float64))
+    np.testing.assert_allclose(O.embedding_backward(dy, idx, 50), tw.grad.numpy(), rtol=1e-5, atol=1e-5)
+    assert (O.embedding_backward(dy, idx, 60)[50:] == 0).all()
 
 
 def test_oracle_catches_planted_mistakes():
