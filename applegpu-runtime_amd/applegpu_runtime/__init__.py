@@ -456,7 +456,9 @@ def sum_dim(t, dim, keepdim=False): return _op(b"sum_dim", [_t(t)], i=(int(dim),
 # transformer ops
 def embedding(weights, indices): return _op(b"embedding", [_t(weights), _t(indices)])
 def add_bias(input, bias): return _op(b"add_bias", [_t(input), _t(bias)])
-def attention(q, k, v): return _op(b"attention", [_t(q), _t(k), _t(v)])
+def attention(q, k, v, scale=None):
+    """softmax(q k^T * scale) v, scale 1/sqrt(d_k) by default (lib.rs:932)."""
+    return _op(b"attention", [_t(q), _t(k), _t(v)], f=() if scale is None else (float(scale),))
 
 
 def qkv_attention(x, w, b, n_head, causal=True, batch=1, read_partials=False):
@@ -467,7 +469,9 @@ def qkv_attention(x, w, b, n_head, causal=True, batch=1, read_partials=False):
     reduction launch (same values; slower at GPT-2 small's shape)."""
     return _op(b"qkv_attention", [_t(x), _t(w), _t(b)],
                i=(int(n_head), int(bool(causal)), int(batch), int(bool(read_partials))))
-def attention_causal(q, k, v): return _op(b"attention_causal", [_t(q), _t(k), _t(v)])
+def attention_causal(q, k, v, scale=None):
+    """Causal attention, query i seeing keys j <= i (lib.rs:1026)."""
+    return _op(b"attention_causal", [_t(q), _t(k), _t(v)], f=() if scale is None else (float(scale),))
 def gather(input, dim, index): return _op(b"gather", [_t(input), _t(index)], i=(int(dim),))
 def index_select(input, dim, index): return _op(b"index_select", [_t(input), _t(index)], i=(int(dim),))
 def where_cond(cond, x, y): return _op(b"where", [_t(cond), _t(x), _t(y)])

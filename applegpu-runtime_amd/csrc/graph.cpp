@@ -197,8 +197,11 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       return {matmul(in[0], in[1], false, true, &e)};
     }
     case OP_ADD_BIAS: need(in, 2, code); return {add_bias(in[0], in[1])};
-    case OP_ATTENTION: need(in, 3, code); return {attention(in[0], in[1], in[2], false)};
-    case OP_ATTENTION_CAUSAL: need(in, 3, code); return {attention(in[0], in[1], in[2], true)};
+    case OP_ATTENTION:
+    case OP_ATTENTION_CAUSAL:
+      // optional f[0]: the softmax scale (default 1/sqrt(D))
+      need(in, 3, code);
+      return {attention(in[0], in[1], in[2], code == OP_ATTENTION_CAUSAL, false, f.empty() ? 0.f : (float)f[0])};
     case OP_WHERE: need(in, 3, code); return {where(in[0], in[1], in[2])};
     case OP_MASKED_FILL: need(in, 2, code); return {masked_fill(in[0], in[1], (float)fp(f, 0, code))};
     case OP_TRIU: need(in, 1, code); return {tri(in[0], true, iv.empty() ? 0 : iv[0])};
@@ -510,7 +513,8 @@ void eval_all(const std::vector<TensorP>& roots) {
       continue;
     } else if (n->code == OP_ATTENTION || n->code == OP_ATTENTION_CAUSAL) {
       // Head-interleaved output: a following transpose(0,1)+reshape is free.
-      res = {ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true)};
+      res = {ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true,
+                            n->f.empty() ? 0.f : (float)n->f[0])};
     } else {
       res = run_op(n->code, n->in, n->f, n->iv);
     }

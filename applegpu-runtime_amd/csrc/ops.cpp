@@ -1045,7 +1045,8 @@ TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale) {
 }
 
 // ── attention ──────────────────────────────────────────────────────────────
-TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool causal, bool out_layout_thd) {
+TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool causal, bool out_layout_thd,
+                  float scale_arg) {
   const char* name = causal ? "attention_causal" : "attention";
   if (q->ndim < 2 || kk->ndim < 2 || v->ndim < 2) fail("%s requires at least 2D tensors for Q, K, V", name);
   check_dtype(name, kFloatOnly, q->dtype);
@@ -1058,7 +1059,8 @@ TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool ca
     fail("K and V must have same kv_len: %lld vs %lld", (long long)Tk, (long long)v->shape[v->ndim - 2]);
   const int64_t Dv = v->shape[v->ndim - 1];
   const int64_t Tq = q->shape[q->ndim - 2];
-  const float scale = 1.0f / std::sqrt((float)D);
+  if (scale_arg < 0.f || !std::isfinite(scale_arg)) fail("%s: scale must be finite and >= 0", name);
+  const float scale = scale_arg > 0.f ? scale_arg : 1.0f / std::sqrt((float)D);
   std::vector<int64_t> lead(q->shape, q->shape + q->ndim - 2);
   bool same_lead = q->ndim == kk->ndim && q->ndim == v->ndim;
   for (int i = 0; same_lead && i < q->ndim - 2; ++i)

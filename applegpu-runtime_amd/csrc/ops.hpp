@@ -116,8 +116,10 @@ TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int6
 // Attention over [..., T, D] operands (leading dims shared by q, k, v).
 // out_layout_thd: store the output physically as [..., T, H, D] (the result
 // is still logically [..., H, T, D]) so a following head merge is free.
+// scale: the softmax scale; 0 means 1/sqrt(D), the reference's
+// (crates/core/src/ops.rs:1531-1620).
 TensorP attention(const TensorP& q, const TensorP& k, const TensorP& v, bool causal,
-                  bool out_layout_thd = false);
+                  bool out_layout_thd = false, float scale = 0.f);
 // q [B, H, Tq, D] against the first lens[b] rows of the [B, H, Tmax, D] caches
 // (lens int32 [B] on the device; the queries' own keys are the last Tq of
 // them); the output is logically [B, H, Tq, D], stored as [B, Tq, H, D].

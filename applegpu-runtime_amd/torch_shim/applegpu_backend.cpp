@@ -20,11 +20,13 @@
 #include <ATen/core/op_registration/adaption.h>
 #include <ATen/detail/PrivateUse1HooksInterface.h>
 #include <ATen/native/CPUFallback.h>
+#include <ATen/native/transformers/attention.h>
 #include <c10/core/impl/DeviceGuardImplInterface.h>
 #include <torch/library.h>
 #include <torch/torch.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
@@ -572,6 +574,78 @@ at::Tensor ag_softmax_backward_data(const at::Tensor& grad, const at::Tensor& ou
   return run_t("softmax_backward", {grad.transpose(d, -1), out.transpose(d, -1)}).transpose(d, -1);
 }
 
+// ── masks ───────────────────────────────────────────────────────────────────
+at::Tensor ag_masked_fill(const at::Tensor& self, const at::Tensor& mask, const at::Scalar& value) {
+  return run_t("masked_fill", {self, to_dev(mask, at::kBool)}, {value.toDouble()});
+}
+at::Tensor& ag_masked_fill_(at::Tensor& self, const at::Tensor& mask, const at::Scalar& value) {
+  self.copy_(ag_masked_fill(self, mask, value));
+  return self;
+}
+at::Tensor ag_where(const at::Tensor& cond, const at::Tensor& self, const at::Tensor& other) {
+  const auto st = at::result_type(self, other);
+  return run_t("where", {to_dev(cond, at::kBool), to_dev(self, st), to_dev(other, st)});
+}
+at::Tensor ag_triu(const at::Tensor& self, int64_t diagonal) { return run_t("triu", {self}, {}, {diagonal}); }
+at::Tensor ag_tril(const at::Tensor& self, int64_t diagonal) { return run_t("tril", {self}, {}, {diagonal}); }
+
+// ── scaled_dot_product_attention ────────────────────────────────────────────
+// torch asks _fused_sdp_choice which backend serves SDPA on this device.
+// Calls without a mask, dropout or grouped K/V go to the fused attention
+// kernel through the overrideable backend; anything else takes torch's math
+// path, whose ops are device kernels too.  The reference registers neither
+// and runs SDPA through its CPU fallback.
+int64_t ag_fused_sdp_choice(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                            const std::optional<at::Tensor>& mask, double dropout, bool, std::optional<double>,
+                            bool enable_gqa) {
+  const bool fused = !(mask.has_value() && mask->defined()) && dropout == 0.0 && !enable_gqa && q.dim() >= 2 &&
+                     q.dim() <= 4 && k.dim() == q.dim() && v.dim() == q.dim() && q.size(-1) == k.size(-1) &&
+                     v.size(-1) == q.size(-1) && k.size(-2) == v.size(-2) && q.scalar_type() == k.scalar_type() &&
+                     q.scalar_type() == v.scalar_type() && at::isFloatingType(q.scalar_type()) &&
+                     q.scalar_type() != at::kDouble;
+  bool same_lead = fused;
+  for (int64_t i = 0; same_lead && i < q.dim() - 2; ++i) same_lead = k.size(i) == q.size(i) && v.size(i) == q.size(i);
+  return same_lead ? 4 /* SDPBackend::overrideable */ : 0 /* SDPBackend::math */;
+}
+
+double sdp_scale(const at::Tensor& q, std::optional<double> scale) {
+  return scale.has_value() ? *scale : 1.0 / std::sqrt((double)q.size(-1));
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, c10::SymInt, c10::SymInt, at::Tensor, at::Tensor, at::Tensor>
+ag_sdpa_overrideable(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                     const std::optional<at::Tensor>& bias, double dropout, bool is_causal, bool,
+                     std::optional<double> scale) {
+  TORCH_CHECK(!(bias.has_value() && bias->defined()) && dropout == 0.0,
+              "applegpu fused attention: no attention bias or dropout");
+  at::Tensor out = run_t(is_causal ? "attention_causal" : "attention", {q, k, v}, {sdp_scale(q, scale)});
+  // logsumexp is not formed (the backward recomputes the probabilities); an
+  // empty [..., Tq] float tensor stands in for it
+  std::vector<int64_t> ls(q.sizes().begin(), q.sizes().end() - 1);
+  at::Tensor lse = at::empty(ls, q.options().dtype(at::kFloat));
+  return {out, lse, at::Tensor(), at::Tensor(), c10::SymInt(q.size(-2)), c10::SymInt(k.size(-2)), at::Tensor(),
+          at::Tensor(), at::Tensor()};
+}
+
+// P = softmax(q k^T s) recomputed (top-left causal mask, as torch's
+// is_causal), then dV = P^T dO, dS = softmax_backward(dO V^T, P),
+// dQ = s dS K, dK = s dS^T Q; every product on the device GEMM.
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> ag_sdpa_overrideable_backward(
+    const at::Tensor& go, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor&,
+    std::array<bool, 4> mask, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+    c10::SymInt, c10::SymInt, double dropout, bool is_causal, const at::Tensor&, const at::Tensor&,
+    std::optional<double> scale) {
+  TORCH_CHECK(dropout == 0.0, "applegpu fused attention backward: no dropout");
+  const double s = sdp_scale(q, scale);
+  at::Tensor sc = run_t("scalar_mul", {run_t("matmul_ex", {q, k}, {}, {0, 1})}, {s});
+  at::Tensor p = run_t(is_causal ? "softmax_causal" : "softmax", {sc});
+  at::Tensor dv = mask[2] ? run_t("matmul_ex", {p, go}, {}, {1, 0}) : at::Tensor();
+  at::Tensor ds = run_t("softmax_backward", {run_t("matmul_ex", {go, v}, {}, {0, 1}), p});
+  at::Tensor dq = mask[0] ? run_t("scalar_mul", {run_t("matmul_ex", {ds, k}, {}, {0, 0})}, {s}) : at::Tensor();
+  at::Tensor dk = mask[1] ? run_t("scalar_mul", {run_t("matmul_ex", {ds, q}, {}, {1, 0})}, {s}) : at::Tensor();
+  return {dq, dk, dv, at::Tensor()};
+}
+
 at::Tensor ag_softmax(const at::Tensor& self, int64_t dim, bool half_to_float) {
   TORCH_CHECK(!half_to_float, "applegpu _softmax: half_to_float is not supported");
   const int64_t d = c10::maybe_wrap_dim(dim, self.dim());
@@ -666,6 +740,14 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
   m.impl("gelu_backward", ag_gelu_backward);
   m.impl("embedding_dense_backward", ag_embedding_dense_backward);
   m.impl("_softmax_backward_data", ag_softmax_backward_data);
+  m.impl("masked_fill.Scalar", ag_masked_fill);
+  m.impl("masked_fill_.Scalar", ag_masked_fill_);
+  m.impl("where.self", ag_where);
+  m.impl("triu", ag_triu);
+  m.impl("tril", ag_tril);
+  m.impl("_fused_sdp_choice", ag_fused_sdp_choice);
+  m.impl("_scaled_dot_product_fused_attention_overrideable", ag_sdpa_overrideable);
+  m.impl("_scaled_dot_product_fused_attention_overrideable_backward", ag_sdpa_overrideable_backward);
   m.impl("_softmax", ag_softmax);
   m.impl("_log_softmax", ag_log_softmax);
   m.impl("cat", ag_cat);
@@ -676,6 +758,12 @@ TORCH_LIBRARY_IMPL(aten, PrivateUse1, m) {
 TORCH_LIBRARY(applegpu, m) { m.def("wrap_eager(int id) -> Tensor", &wrap_eager); }
 
 TORCH_LIBRARY_IMPL(_, PrivateUse1, m) { m.fallback(torch::CppFunction::makeFromBoxedFunction<&cpu_fallback>()); }
+
+// scaled_dot_product_attention reads its backend choice from this stub
+// (the _fused_sdp_choice op above answers the same question when called).
+namespace at::native {
+REGISTER_PRIVATEUSE1_DISPATCH(_fused_sdp_choice_stub, &ag_fused_sdp_choice);
+}
 
 // ── DeviceGuard, hooks, allocator registration ──────────────────────────────
 namespace {
