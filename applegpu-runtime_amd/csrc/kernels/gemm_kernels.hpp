@@ -158,6 +158,20 @@ __device__ __forceinline__ void split_bf16(float x, bf16_t& hi, bf16_t& lo) {
   lo = (bf16_t)(__builtin_isfinite(x) ? r : 0.f);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// split_bf16 of two values at once: each rounding is one v_cvt_pk_bf16_f32
+// for the pair (the scalar form converts one value per instruction).
+__device__ __forceinline__ void split_bf16x2(float x0, float x1, bf16x2_t& hi, bf16x2_t& lo) {
+  const f32x2_t x = {x0, x1};
+  hi = __builtin_convertvector(x, bf16x2_t);
+  f32x2_t r = x - __builtin_convertvector(hi, f32x2_t);
+  r.x = __builtin_isfinite(x0) ? r.x : 0.f;
+  r.y = __builtin_isfinite(x1) ? r.y : 0.f;
+  lo = __builtin_convertvector(r, bf16x2_t);
+}
+
 // Per-thread share of a ROWS x BK operand slice.  KCONT: the operand is
 // contiguous along k (A row-major, or B = W^T with W [n][k]); the thread owns
 // one row and EPT consecutive k.  !KCONT: contiguous along rows (A column-
@@ -264,15 +278,35 @@ struct GLoad {
       for (int i = 0; i < EPT; i += 8) {
         bf16x8_t h, l;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          bf16_t a, b;
-          const float x = std::is_same<TI, int8_t>::value ? (float)at<MASKED>(i + e) * rs : (float)at<MASKED>(i + e);
-          split_bf16(x, a, b);
-          h[e] = a;
-          l[e] = b;
+        for (int e = 0; e < 8; e += 2) {
+          const float x0 = std::is_same<TI, int8_t>::value ? (float)at<MASKED>(i + e) * rs : (float)at<MASKED>(i + e);
+          const float x1 =
+              std::is_same<TI, int8_t>::value ? (float)at<MASKED>(i + e + 1) * rs : (float)at<MASKED>(i + e + 1);
+          bf16x2_t a, b;
+          split_bf16x2(x0, x1, a, b);
+          h[e] = a.x;
+          h[e + 1] = a.y;
+          l[e] = b.x;
+          l[e + 1] = b.y;
         }
         *(bf16x8_t*)&hi[r * LD + kk + i] = h;
         *(bf16x8_t*)&lo[r * LD + kk + i] = l;
+      }
+    } else if constexpr (KP % 2 == 0) {
+#pragma unroll
+      for (int c = 0; c < VW; ++c) {
+        bf16_t h[KP], l[KP];
+#pragma unroll
+        for (int j = 0; j < KP; j += 2) {
+          bf16x2_t a, b;
+          split_bf16x2((float)at<MASKED>(j * VW + c), (float)at<MASKED>((j + 1) * VW + c), a, b);
+          h[j] = a.x;
+          h[j + 1] = a.y;
+          l[j] = b.x;
+          l[j + 1] = b.y;
+        }
+        store_run(&hi[(r + c) * LD + kk], h);
+        store_run(&lo[(r + c) * LD + kk], l);
       }
     } else {
 #pragma unroll
