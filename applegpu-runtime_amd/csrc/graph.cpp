@@ -317,12 +317,13 @@ struct Group {
   int64_t packed_n = 0;       // b is packed decode weights of this many columns
 };
 
-bool is_single_internal_use(const TensorP& t, const std::unordered_map<Tensor*, int>& uses) {
+bool is_single_internal_use(const TensorP& t, const std::unordered_map<Tensor*, int>& uses, int planner_refs = 0) {
   if (!t->pending() || t->ext_refs != 0) return false;
   auto it = uses.find(t.get());
   if (it == uses.end() || it->second != 1) return false;
-  // holders: the consumer's node input + the eval order list
-  return t.use_count() == 2 + 0;
+  // holders: the consumer's node input + the eval order list (+ references
+  // the fusion planner itself keeps)
+  return t.use_count() == 2 + planner_refs;
 }
 
 void assign(const TensorP& dst, const TensorP& src) {
@@ -406,8 +407,12 @@ void eval_all(const std::vector<TensorP>& roots) {
         // (only 16-bit GEMMs of <= 16 rows can: the skinny kernel; otherwise
         // the layer_norm stays a node, which the producing GEMM's split-K
         // reduction may compute)
+        // (a pairing in post_ln, made when the layer_norm was visited as the
+        // reader of an earlier group, holds one more reference to it)
+        int paired = 0;
+        for (auto& kv : post_ln) paired += kv.second.get() == la.get();
         if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 && la->dtype != DType::F32 &&
-            la->shape[0] <= 16 && is_single_internal_use(la, uses)) {
+            la->shape[0] <= 16 && is_single_internal_use(la, uses, paired)) {
           for (auto pit = post_ln.begin(); pit != post_ln.end(); ++pit)
             if (pit->second.get() == la.get()) {  // normalised in this GEMM's prologue instead
               post_ln.erase(pit);
@@ -493,7 +498,7 @@ void eval_all(const std::vector<TensorP>& roots) {
         res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e) : ops::matmul(g.a, g.b, false, false, &e)};
       }
       g_stats.fused_gemm_epilogues++;
-      g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0);
+      g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0) + (g.ln_gamma ? 1 : 0);
     } else if (n->code < 0) {
       fail("internal: multi-output selector reached without its producer");
     } else if (op_outputs(n->code) > 1) {

@@ -234,6 +234,26 @@ def test_decode_attention_new_rows_reject_bad_shapes(gpu):
         gpu.decode_attention(gpu.slice(q, 2, 0, 1), kc, kc, lens, k_new=kn).eval()
 
 
+def test_decode_step_folds_every_layer_norm(gpu):
+    """One decode step is one lazy graph (the K/V append rides in the
+    attention launch), in which every ln_1/ln_2 feeds a skinny GEMM that
+    normalises its rows itself, even where the same layer_norm also reads
+    the previous GEMM group's output: per layer 2 folded layer_norms plus
+    the bias/residual/gelu epilogues: 9 launches saved per layer."""
+    from applegpu_runtime.models import gpt2 as G
+    cfg = {"vocab_size": 300, "n_positions": 64, "n_embd": 128, "n_layer": 3, "n_head": 2}
+    model = G.load_model(G.random_weights(cfg, seed=9), cfg, dtype="float16")
+    cache = G.KVCache(cfg, batch=4, max_len=32, dtype="float16")
+    prompt = RNG.integers(0, cfg["vocab_size"], (4, 8)).astype(np.int32)
+    _, tok = G.gpt2_prefill(model, gpu.from_numpy(prompt), cache)
+    gpu.blit_copy(gpu.from_numpy(np.full(4, 8, np.int32)), cache.pos)
+    before = gpu.graph_stats()["launches_saved"]
+    logits, nxt, lens = G.gpt2_decode_step(model, tok, cache)
+    nxt.eval()
+    saved = gpu.graph_stats()["launches_saved"] - before
+    assert saved >= 9 * cfg["n_layer"], saved
+
+
 def test_decode_attention_empty_and_clamped_lengths(gpu):
     """len 0 gives zeros; lengths past the cache are clamped to it."""
     B, H, Tmax, D = 3, 2, 70, 64
