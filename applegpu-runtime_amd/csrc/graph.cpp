@@ -391,7 +391,8 @@ void eval_all(const std::vector<TensorP>& roots) {
   // plus a layer_norm of the group's output computed by its split-K reduction.
   std::unordered_map<Tensor*, Group> groups;  // keyed by the group's current final node
   std::unordered_set<Tensor*> absorbed;
-  std::unordered_map<Tensor*, TensorP> post_ln;  // group final node -> layer_norm node reading it
+  std::unordered_map<Tensor*, TensorP> post_ln;  // group final node (or embedding sum) -> layer_norm reading it
+  std::unordered_set<Tensor*> emb_adds;            // embedding + embedding nodes run as one kernel
   for (auto& t : order) {
     Node* n = t->node.get();
     if (n->code == OP_ADD_BIAS && t->ndim == 2) {
@@ -445,8 +446,22 @@ void eval_all(const std::vector<TensorP>& roots) {
       }
     } else if (n->code == OP_LAYER_NORM && t->ndim == 2) {
       const TensorP& x = n->in[0];
-      if (groups.count(x.get()) && !post_ln.count(x.get()) && n->in[1]->ndim == 1 && n->in[2]->ndim == 1)
+      // (computed where x is, which comes before gamma and beta in the walk:
+      // they must already hold their values)
+      if ((groups.count(x.get()) || emb_adds.count(x.get())) && !post_ln.count(x.get()) && n->in[1]->ndim == 1 &&
+          n->in[2]->ndim == 1 && !n->in[1]->pending() && !n->in[2]->pending())
         post_ln[x.get()] = t;
+    } else if (n->code == OP_ADD && n->in[0]->pending() && n->in[1]->pending() &&
+               n->in[0]->node->code == OP_EMBEDDING && n->in[1]->node->code == OP_EMBEDDING &&
+               n->in[0]->dims() == t->dims() && n->in[1]->dims() == t->dims() &&
+               is_single_internal_use(n->in[0], uses) && is_single_internal_use(n->in[1], uses) &&
+               ops::embedding_add_fusable(n->in[0]->node->in[0], n->in[0]->node->in[1], n->in[1]->node->in[0],
+                                          n->in[1]->node->in[1])) {
+      // token + position embedding: one launch (and the layer_norm reading
+      // the sum, when one does, below)
+      emb_adds.insert(t.get());
+      absorbed.insert(n->in[0].get());
+      absorbed.insert(n->in[1].get());
     } else if (n->code == OP_ADD) {
       for (int side = 0; side < 2; ++side) {
         const TensorP& x = n->in[side];
@@ -516,6 +531,23 @@ void eval_all(const std::vector<TensorP>& roots) {
       t->node.reset();
       order[i].reset();
       continue;
+    } else if (emb_adds.count(t.get())) {
+      const Node* e1 = n->in[0]->node.get();
+      const Node* e2 = n->in[1]->node.get();
+      auto pit = post_ln.find(t.get());
+      TensorP lnt = pit != post_ln.end() && pit->second->pending() ? pit->second : nullptr;
+      if (lnt && lnt->dtype == t->dtype && lnt->dims() == t->dims()) {
+        ops::PostLn pl;
+        pl.gamma = lnt->node->in[1];
+        pl.beta = lnt->node->in[2];
+        pl.eps = lnt->node->f.empty() ? 1e-5f : (float)lnt->node->f[0];
+        res = {ops::embedding_add(e1->in[0], e1->in[1], e2->in[0], e2->in[1], &pl)};
+        assign(lnt, pl.y);
+        g_stats.launches_saved += 3;
+      } else {
+        res = {ops::embedding_add(e1->in[0], e1->in[1], e2->in[0], e2->in[1], nullptr)};
+        g_stats.launches_saved += 2;
+      }
     } else if (n->code == OP_ATTENTION || n->code == OP_ATTENTION_CAUSAL) {
       // Head-interleaved output: a following transpose(0,1)+reshape is free.
       res = {ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true,

@@ -77,6 +77,12 @@ void layer_norm_backward(DType dt, const void* dy, const void* x, const void* ga
 size_t layer_norm_param_ws_bytes(int64_t rows, int64_t cols);
 void layer_norm_param_grads(DType dt, const void* dy, const void* x, const float* stats, void* dgamma, void* dbeta,
                             float* ws, int64_t rows, int64_t cols, hipStream_t s);
+// x[r] = w1[i1[r]] + w2[i2[r]] over [rows, cols] (cols <= 2048; contiguous
+// [vocab, cols] tables), and when gamma is given also y = layer_norm(x).
+bool embedding_add_ok(int64_t cols);
+void embedding_add(DType dt, const void* w1, DType i1_dt, const void* i1, int64_t v1, const void* w2, DType i2_dt,
+                   const void* i2, int64_t v2, void* x, const void* gamma, const void* beta, void* y, int64_t rows,
+                   int64_t cols, float eps, hipStream_t s);
 // Softmax backward: dx = y * (dy - sum(dy * y)) per row.
 void softmax_backward(DType dt, const void* dy, const void* y, void* dx, int64_t rows,
                       int64_t cols, hipStream_t s);

@@ -421,6 +421,68 @@ __global__ void __launch_bounds__(256) ln_param_final(const float* __restrict__ 
   db[c] = from_f<T>(sb);
 }
 
+// ── token + position embedding, optionally with the layer_norm after it ───
+// x[r] = w1[i1[r]] + w2[i2[r]] (fp32 sum, rounded once, as embedding +
+// embedding + add store it; an index outside its table gives a zero row, as
+// the embedding kernel does), and with LN also y[r] = layer_norm(x[r]) from
+// the stored (rounded) x by layer_norm_wave's own arithmetic.  GPT-2's
+// wte[ids] + wpe[pos] -> ln_1 (python/applegpu_runtime/models/gpt2.py:84-178)
+// in one launch instead of four.
+template <typename T, typename I, int NV, bool LN>
+__global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, const I* __restrict__ i1, int64_t v1,
+                                                      const T* __restrict__ w2, const I* __restrict__ i2, int64_t v2,
+                                                      T* __restrict__ x, const T* __restrict__ g,
+                                                      const T* __restrict__ b, T* __restrict__ y, int64_t rows,
+                                                      int64_t cols, float eps, bool vec) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t a = (int64_t)i1[row], c = (int64_t)i2[row];
+  const bool oka = a >= 0 && a < v1, okc = c >= 0 && c < v2;
+  const T* ra = w1 + (oka ? a : 0) * cols;
+  const T* rc = w2 + (okc ? c : 0) * cols;
+  float v[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t col = ((int64_t)i * 64 + lane) * 4;
+    float p[4], q[4];
+    load4<T>(ra, col, cols, vec, 0.f, p);
+    load4<T>(rc, col, cols, vec, 0.f, q);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // the sum as stored (rounded to T), which is what layer_norm reads
+      v[i][j] = to_f(from_f<T>((oka ? p[j] : 0.f) + (okc ? q[j] : 0.f)));
+      s += col + j < cols ? v[i][j] : 0.f;
+    }
+    store4<T>(x + row * cols, col, cols, vec, v[i]);
+  }
+  if constexpr (LN) {
+    const float mean = wave_sum(s) / (float)cols;
+    float qs = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t col = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float d = col + j < cols ? v[i][j] - mean : 0.f;
+        qs += d * d;
+      }
+    }
+    const float inv = 1.f / sqrtf(wave_sum(qs) / (float)cols + eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t col = ((int64_t)i * 64 + lane) * 4;
+      float gv[4], bv[4];
+      load4<T>(g, col, cols, vec, 0.f, gv);
+      load4<T>(b, col, cols, vec, 0.f, bv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[i][j] = gv[j] * (v[i][j] - mean) * inv + bv[j];
+      store4<T>(y + row * cols, col, cols, vec, v[i]);
+    }
+  }
+}
+
 // ── row reductions (one wavefront per row) ───────────────────────────────
 template <typename TI, typename TO>
 __global__ void __launch_bounds__(256) row_reduce_wave(int op, const TI* __restrict__ x, int64_t ldx,
@@ -930,6 +992,62 @@ void layer_norm_param_grads(DType dt, const void* dy, const void* x, const float
                        (T*)dgamma, (T*)dbeta, chunks, cols);
   });
   check_launch("layer_norm_param_grads");
+}
+
+bool embedding_add_ok(int64_t cols) { return cols > 0 && cols <= 2048; }
+
+namespace {
+struct EaArgs {
+  const void *w1, *i1, *w2, *i2, *g, *b;
+  void *x, *y;
+  int64_t v1, v2, rows, cols;
+  float eps;
+  bool vec;
+};
+
+template <typename T, typename I, int NV>
+void ea_nv(const EaArgs& a, hipStream_t s) {
+  if (a.g)
+    hipLaunchKernelGGL((embed_add_wave<T, I, NV, true>), dim3(rows_grid(a.rows)), dim3(256), 0, s, (const T*)a.w1,
+                       (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)a.g,
+                       (const T*)a.b, (T*)a.y, a.rows, a.cols, a.eps, a.vec);
+  else
+    hipLaunchKernelGGL((embed_add_wave<T, I, NV, false>), dim3(rows_grid(a.rows)), dim3(256), 0, s, (const T*)a.w1,
+                       (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)nullptr,
+                       (const T*)nullptr, (T*)nullptr, a.rows, a.cols, a.eps, a.vec);
+}
+
+template <typename T, typename I>
+void ea_launch(const EaArgs& a, hipStream_t s) {
+  switch ((a.cols + 255) / 256) {
+    case 1: ea_nv<T, I, 1>(a, s); break;
+    case 2: ea_nv<T, I, 2>(a, s); break;
+    case 3: ea_nv<T, I, 3>(a, s); break;
+    case 4: ea_nv<T, I, 4>(a, s); break;
+    case 5: ea_nv<T, I, 5>(a, s); break;
+    case 6: ea_nv<T, I, 6>(a, s); break;
+    default: ea_nv<T, I, 8>(a, s);
+  }
+}
+}  // namespace
+
+void embedding_add(DType dt, const void* w1, DType i1_dt, const void* i1, int64_t v1, const void* w2, DType i2_dt,
+                   const void* i2, int64_t v2, void* x, const void* gamma, const void* beta, void* y, int64_t rows,
+                   int64_t cols, float eps, hipStream_t s) {
+  if (rows == 0) return;
+  if (!embedding_add_ok(cols)) fail("embedding_add: %lld columns (at most 2048)", (long long)cols);
+  if (i1_dt != i2_dt) fail("embedding_add: index dtypes differ");
+  if (rows > 0x7fffffffLL) fail("embedding_add: too many rows");
+  const size_t es = dtype_size(dt);
+  const bool ln = gamma != nullptr;
+  EaArgs a{w1, i1, w2, i2, gamma, beta, x, y, v1, v2, rows, cols, eps, false};
+  a.vec = vec_ok(w1, cols, es) && vec_ok(w2, cols, es) && vec_ok(x, cols, es) &&
+          (!ln || (vec_ok(y, cols, es) && vec_ok(gamma, 0, es) && vec_ok(beta, 0, es)));
+  AGPU_FLOAT_SWITCH(dt, {
+    typedef T TV;
+    AGPU_INT_SWITCH(i1_dt, ea_launch<TV, I>(a, s));
+  });
+  check_launch("embedding_add");
 }
 
 void quantize_rows(DType in, const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols,

@@ -722,6 +722,35 @@ TensorP embedding(const TensorP& w, const TensorP& idx) {
   return out;
 }
 
+bool embedding_add_fusable(const TensorP& w1, const TensorP& i1, const TensorP& w2, const TensorP& i2) {
+  return w1->ndim == 2 && w2->ndim == 2 && w1->dtype == w2->dtype && dtype_is_float(w1->dtype) &&
+         w1->dtype != DType::F64 && w1->shape[1] == w2->shape[1] && k::embedding_add_ok(w1->shape[1]) &&
+         i1->dtype == i2->dtype && (i1->dtype == DType::I32 || i1->dtype == DType::I64) && i1->dims() == i2->dims() &&
+         w1->is_contiguous() && w2->is_contiguous();
+}
+
+TensorP embedding_add(const TensorP& w1, const TensorP& i1, const TensorP& w2, const TensorP& i2, PostLn* ln) {
+  if (!embedding_add_fusable(w1, i1, w2, i2)) fail("embedding_add: operands do not fit the fused kernel");
+  TensorP a = contiguous(i1), c = contiguous(i2);
+  std::vector<int64_t> od = i1->dims();
+  od.push_back(w1->shape[1]);
+  TensorP x = alloc_out(w1->dtype, od);
+  const int64_t rows = a->numel(), cols = w1->shape[1];
+  TensorP gc, bc;
+  if (ln) {
+    if (!(ln->gamma->ndim == 1 && ln->gamma->shape[0] == cols && ln->beta->ndim == 1 && ln->beta->shape[0] == cols &&
+          ln->gamma->dtype == w1->dtype && ln->beta->dtype == w1->dtype))
+      fail("embedding_add: layer_norm gamma/beta must be [%lld] of the table dtype", (long long)cols);
+    gc = contiguous(ln->gamma);
+    bc = contiguous(ln->beta);
+    ln->y = alloc_out(w1->dtype, od);
+  }
+  LAUNCH k::embedding_add(w1->dtype, w1->data(), a->dtype, a->data(), w1->shape[0], w2->data(), c->dtype, c->data(),
+                          w2->shape[0], x->data(), ln ? gc->data() : nullptr, ln ? bc->data() : nullptr,
+                          ln ? ln->y->data() : nullptr, rows, cols, ln ? ln->eps : 1e-5f, rt().stream());
+  return x;
+}
+
 TensorP index_select(const TensorP& x, int dim, const TensorP& idx) {
   check_dtype("index_select", kNotBool, x->dtype);
   if (idx->ndim != 1) fail("index_select index must be 1D");

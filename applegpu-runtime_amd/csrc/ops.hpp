@@ -88,6 +88,11 @@ struct PostLn {
 };
 TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = false,
                const Epilogue* epi = nullptr, const TensorP& into = nullptr, PostLn* post_ln = nullptr);
+// w1[i1] + w2[i2] in one launch (token + position embedding), and with ln
+// also ln->y = layer_norm of the sum; embedding_add_fusable says whether the
+// operands fit the kernel.
+bool embedding_add_fusable(const TensorP& w1, const TensorP& i1, const TensorP& w2, const TensorP& i2);
+TensorP embedding_add(const TensorP& w1, const TensorP& i1, const TensorP& w2, const TensorP& i2, PostLn* ln);
 // SGD steps fused with their gradients, in place:
 //   w += alpha * op(a) op(b)   (the weight gradient GEMM; w contiguous 2-D)
 //   bias += alpha * sum(g, 0)  (g contiguous [rows, N])
