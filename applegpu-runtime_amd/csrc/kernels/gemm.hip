@@ -254,9 +254,8 @@ __device__ __forceinline__ void st4(T* dst, const float (&v)[4]) {
   }
 }
 
-template <typename T, int NV>
+template <typename T, int NV, int MS>  // MS: partials loaded up front; more are added afterwards
 __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
-  constexpr int MS = 8;  // partials loaded up front; more are added afterwards
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= p.M) return;  // whole wavefront; no barriers below
@@ -338,18 +337,25 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
   }
 }
 
+template <typename T, int NV>
+void launch_reduce_ln_nv(const GArgs& p, dim3 grid, dim3 block, hipStream_t s) {
+  if (p.splits <= 2) hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 2>), grid, block, 0, s, p);
+  else if (p.splits <= 4) hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 4>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 8>), grid, block, 0, s, p);
+}
+
 template <typename T>
 void launch_reduce_ln(const GArgs& p, hipStream_t s) {
   const dim3 grid((unsigned)((p.M + 3) / 4)), block(256);
   switch ((p.N + 255) / 256) {
-    case 1: hipLaunchKernelGGL((splitk_reduce_ln<T, 1>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((splitk_reduce_ln<T, 2>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((splitk_reduce_ln<T, 3>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((splitk_reduce_ln<T, 4>), grid, block, 0, s, p); break;
-    case 5: hipLaunchKernelGGL((splitk_reduce_ln<T, 5>), grid, block, 0, s, p); break;
-    case 6: hipLaunchKernelGGL((splitk_reduce_ln<T, 6>), grid, block, 0, s, p); break;
-    case 7: hipLaunchKernelGGL((splitk_reduce_ln<T, 7>), grid, block, 0, s, p); break;
-    case 8: hipLaunchKernelGGL((splitk_reduce_ln<T, 8>), grid, block, 0, s, p); break;
+    case 1: launch_reduce_ln_nv<T, 1>(p, grid, block, s); break;
+    case 2: launch_reduce_ln_nv<T, 2>(p, grid, block, s); break;
+    case 3: launch_reduce_ln_nv<T, 3>(p, grid, block, s); break;
+    case 4: launch_reduce_ln_nv<T, 4>(p, grid, block, s); break;
+    case 5: launch_reduce_ln_nv<T, 5>(p, grid, block, s); break;
+    case 6: launch_reduce_ln_nv<T, 6>(p, grid, block, s); break;
+    case 7: launch_reduce_ln_nv<T, 7>(p, grid, block, s); break;
+    case 8: launch_reduce_ln_nv<T, 8>(p, grid, block, s); break;
     default: fail("gemm: fused layer_norm needs N <= 2048");
   }
 }
@@ -360,9 +366,8 @@ void launch_reduce_ln(const GArgs& p, hipStream_t s) {
 // residual and mask as vectors, all branch-free) and stores one vector.
 // Same sums in the same split order and the same epilogue arithmetic as
 // splitk_reduce.
-template <typename T>
+template <typename T, int MS>  // MS: partials loaded up front (the split count rounded up to 2, 4 or 8)
 __global__ void __launch_bounds__(256) splitk_reduce_vec(GArgs p) {
-  constexpr int MS = 8;
   const int64_t total = p.M * p.N;
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i >= total) return;
@@ -726,8 +731,12 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     }
     int64_t total = g.batch * g.M * g.N;
     if (reduce_vec_ok(g) && (total + 1023) / 1024 <= 0x7fffffff) {
-      AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce_vec<T>), dim3((unsigned)((total + 1023) / 1024)),
-                                                 dim3(256), 0, s, p));
+      const dim3 rgrid((unsigned)((total + 1023) / 1024));
+      AGPU_FLOAT_SWITCH(g.dt, {
+        if (p.splits <= 2) hipLaunchKernelGGL((splitk_reduce_vec<T, 2>), rgrid, dim3(256), 0, s, p);
+        else if (p.splits <= 4) hipLaunchKernelGGL((splitk_reduce_vec<T, 4>), rgrid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((splitk_reduce_vec<T, 8>), rgrid, dim3(256), 0, s, p);
+      });
       check_launch("splitk_reduce");
       return;
     }
