@@ -257,7 +257,8 @@ __device__ __forceinline__ void st4(T* dst, const float (&v)[4]) {
 template <typename T, int NV, int MS>  // MS: partials loaded up front; more are added afterwards
 __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // one wavefront per row; a block holds blockDim.x / 64 rows
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= p.M) return;  // whole wavefront; no barriers below
   const int64_t N = p.N, total = p.M * p.N;
   const int ns = p.splits;
@@ -346,7 +347,10 @@ void launch_reduce_ln_nv(const GArgs& p, dim3 grid, dim3 block, hipStream_t s) {
 
 template <typename T>
 void launch_reduce_ln(const GArgs& p, hipStream_t s) {
-  const dim3 grid((unsigned)((p.M + 3) / 4)), block(256);
+  // Up to 1024 rows, one row per block: the rows then spread over as many
+  // CUs as there are rows (GPT-2's 128 rows: 128 CUs, not 32).
+  const int rpb = p.M <= 1024 ? 1 : 4;
+  const dim3 grid((unsigned)((p.M + rpb - 1) / rpb)), block(64 * rpb);
   switch ((p.N + 255) / 256) {
     case 1: launch_reduce_ln_nv<T, 1>(p, grid, block, s); break;
     case 2: launch_reduce_ln_nv<T, 2>(p, grid, block, s); break;
