@@ -106,7 +106,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is described in DESIGN.md, not built).", file=sys.stderr)
+              "(multi-GPU sharding is designed, not built).", file=sys.stderr)
         sys.exit(2)
 
     import applegpu_runtime as gpu
