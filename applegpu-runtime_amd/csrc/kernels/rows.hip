@@ -435,7 +435,7 @@ __global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, 
                                                       const T* __restrict__ b, T* __restrict__ y, int64_t rows,
                                                       int64_t cols, float eps, bool vec) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // one wavefront per row
   if (row >= rows) return;
   const int64_t a = (int64_t)i1[row], c = (int64_t)i2[row];
   const bool oka = a >= 0 && a < v1, okc = c >= 0 && c < v2;
@@ -1007,12 +1007,15 @@ struct EaArgs {
 
 template <typename T, typename I, int NV>
 void ea_nv(const EaArgs& a, hipStream_t s) {
+  // up to 1024 rows, one row per block: the rows reach as many CUs
+  const int rpb = a.rows <= 1024 ? 1 : kRowsPerBlock;
+  const dim3 grid((unsigned)((a.rows + rpb - 1) / rpb)), block(64 * rpb);
   if (a.g)
-    hipLaunchKernelGGL((embed_add_wave<T, I, NV, true>), dim3(rows_grid(a.rows)), dim3(256), 0, s, (const T*)a.w1,
+    hipLaunchKernelGGL((embed_add_wave<T, I, NV, true>), grid, block, 0, s, (const T*)a.w1,
                        (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)a.g,
                        (const T*)a.b, (T*)a.y, a.rows, a.cols, a.eps, a.vec);
   else
-    hipLaunchKernelGGL((embed_add_wave<T, I, NV, false>), dim3(rows_grid(a.rows)), dim3(256), 0, s, (const T*)a.w1,
+    hipLaunchKernelGGL((embed_add_wave<T, I, NV, false>), grid, block, 0, s, (const T*)a.w1,
                        (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)nullptr,
                        (const T*)nullptr, (T*)nullptr, a.rows, a.cols, a.eps, a.vec);
 }
