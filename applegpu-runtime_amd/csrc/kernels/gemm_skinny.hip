@@ -33,8 +33,9 @@
 //    crates/core/src/kernel_templates.rs:1075-1116) and stages the row
 //    normalised, g * (x - mean) * rstd + b rounded to the operand type, as
 //    the layer_norm kernel would have stored it.
-// The first steps' B loads are issued before the staging, so they are in
-// flight while it runs.  The k-reduction happens inside the MFMA
+// The staged rows are loaded first and the first steps' B loads right after,
+// so the weights are in flight while the staging (and its layer-norm
+// statistics) runs.  The k-reduction happens inside the MFMA
 // accumulators: no cross-lane reduction, no split-K workspace and no second
 // launch.  (A scalar-FMA variant that staged A in LDS and a split-K variant
 // that finished in the last block were both slower than the MFMA tiles: the
@@ -111,22 +112,15 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
     }
   };
 
-  V8 b[UN];
-  load_b(b, w);  // in flight during the staging below
-  // threads 0..255 each finish one output (m, n0 + c): its bias/residual now
-  // (every thread loads, from a clamped legal element: no divergent branch
-  // around the loads)
-  const int om = (tid >> 4) & 15, oc = tid & 15;
-  const bool owns = tid < 256 && om < p.M && n0 + oc < p.N;
-  const EpiIn<T> ein = epilogue_load<T>(p, 0, om < p.M ? om : p.M - 1, n0 + oc < p.N ? n0 + oc : p.N - 1);
-
+  // The staged A row (and gamma, beta) is loaded first, then this wave's
+  // first B steps, then the epilogue operands: a wave's loads complete in
+  // issue order, so the staging below waits for its row only, while the
+  // weight stream is still in flight.
+  constexpr int R = kSkRowMaxK / 512;  // 8-runs per lane of a staged row
+  V8 run[XLDS ? R : 1], lg[LN ? R : 1], lb[LN ? R : 1];
   if constexpr (XLDS) {
     if (w < p.M) {
       const T* xr = (const T*)p.A + w * p.a_sm;
-      constexpr int R = kSkRowMaxK / 512;  // 8-runs per lane
-      // the row, and for a layer-norm prologue gamma and beta, all loaded up
-      // front: one round trip
-      V8 run[R], lg[LN ? R : 1], lb[LN ? R : 1];
 #pragma unroll
       for (int c = 0; c < R; ++c) {
         const int64_t kk = (int64_t)(lane + 64 * c) * 8;
@@ -138,6 +132,19 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
           }
         }
       }
+    }
+  }
+  V8 b[UN];
+  load_b(b, w);  // in flight during the staging below
+  // threads 0..255 each finish one output (m, n0 + c): its bias/residual now
+  // (every thread loads, from a clamped legal element: no divergent branch
+  // around the loads)
+  const int om = (tid >> 4) & 15, oc = tid & 15;
+  const bool owns = tid < 256 && om < p.M && n0 + oc < p.N;
+  const EpiIn<T> ein = epilogue_load<T>(p, 0, om < p.M ? om : p.M - 1, n0 + oc < p.N ? n0 + oc : p.N - 1);
+
+  if constexpr (XLDS) {
+    if (w < p.M) {
       if constexpr (LN) {
         float sum = 0.f;
 #pragma unroll
