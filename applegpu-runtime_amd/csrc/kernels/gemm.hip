@@ -263,8 +263,11 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
   const int64_t N = p.N, total = p.M * p.N;
   const int ns = p.splits;
   // Every load first, from clamped legal addresses (chunks past N read
-  // chunk 0 and are discarded), so that they are all in flight together.
-  float part[NV][MS][4], bias[NV][4], res[NV][4], msk[NV][4], gam[NV][4], bet[NV][4];
+  // chunk 0 and are discarded), so that they are all in flight together;
+  // gamma and beta, needed last, go out last (a wavefront's loads complete
+  // in issue order).  Absent epilogue operands are not loaded (the tests
+  // are uniform across the wavefront).
+  float part[NV][MS][4], bias[NV][4] = {}, res[NV][4] = {}, msk[NV][4] = {}, gam[NV][4], bet[NV][4];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t c = ((int64_t)i * 64 + lane) * 4;
@@ -274,10 +277,14 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
       const float4 w = *(const float4*)(p.ws + (int64_t)(sp < ns ? sp : 0) * total + row * N + cc);
       part[i][sp][0] = w.x; part[i][sp][1] = w.y; part[i][sp][2] = w.z; part[i][sp][3] = w.w;
     }
-    const T* out = (const T*)p.C + row * p.c_sm + cc;
-    ld4f<T>(p.bias ? (const T*)p.bias + cc : out, bias[i]);
-    ld4f<T>(p.res ? (const T*)p.res + row * p.r_sm + cc : out, res[i]);
-    ld4f<T>(p.mask ? (const T*)p.mask + row * p.k_sm + cc : out, msk[i]);
+    if (p.bias) ld4f<T>((const T*)p.bias + cc, bias[i]);
+    if (p.res) ld4f<T>((const T*)p.res + row * p.r_sm + cc, res[i]);
+    if (p.mask) ld4f<T>((const T*)p.mask + row * p.k_sm + cc, msk[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    const int64_t cc = c < N ? c : 0;
     ld4f<T>((const T*)p.pln_g + cc, gam[i]);
     ld4f<T>((const T*)p.pln_b + cc, bet[i]);
   }
