@@ -468,7 +468,13 @@ void eval_all(const std::vector<TensorP>& roots) {
         const TensorP& other = n->in[1 - side];
         auto it = groups.find(x.get());
         if (it == groups.end() || it->second.residual || !is_single_internal_use(x, uses)) continue;
-        if (other->dims() != t->dims() || other.get() == x.get()) continue;
+        // Only a same-shape, same-dtype add folds into the epilogue: the GEMM
+        // writes its own output shape, so an add that broadcasts the GEMM
+        // output (a [1, N] product plus an [M, N] residual, or a 2-D product
+        // plus a 3-D one) stays a node of its own.
+        if (other->dims() != t->dims() || x->dims() != t->dims() || other->dtype != x->dtype ||
+            other.get() == x.get())
+          continue;
         Group g = it->second;
         g.residual = other;
         groups.erase(it);

@@ -254,12 +254,16 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
     for (int e = 0; e < 8; ++e) acc[e] *= alpha;
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const float pe = sc[u] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[u] - mx);
+      // A masked key (past the visible length, or a clamped address) adds
+      // nothing, whatever its cache row holds: a NaN or Inf left in an
+      // unused row must not reach the output through 0 * v.
+      const bool live = sc[u] != -INFINITY;
+      const float pe = live ? __builtin_amdgcn_exp2f(sc[u] - mx) : 0.f;
       l += pe;
       float vx[8];
       vr[u].to_float(vx);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += pe * vx[e];
+      for (int e = 0; e < 8; ++e) acc[e] = live ? fmaf(pe, vx[e], acc[e]) : acc[e];
     }
     m = mx;
     if (base + BS < j_hi) load_iter(base + BS);

@@ -109,11 +109,6 @@ def argmax(x):
     return out.reshape(shp)
 
 
-def row_sum(x): return x.astype(np.float64).sum(axis=-1).astype(x.dtype)
-def row_mean(x): return x.astype(np.float64).mean(axis=-1).astype(x.dtype)
-def row_amax(x): return x.max(axis=-1)
-
-
 # ── reductions / loss ──────────────────────────────────────────────────────
 def sum_dim(x, dim, keepdim=False):
     """crates/core/src/eager.rs:827-855 (output shape; a 0-D result becomes [1])."""

@@ -268,6 +268,42 @@ def test_decode_attention_empty_and_clamped_lengths(gpu):
     assert rel_err(_host(got), ref) < 1e-3
 
 
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+@pytest.mark.parametrize("B,H", [(8, 20), (2, 2)])
+def test_decode_attention_ignores_nan_in_unused_cache_rows(gpu, dtype, B, H):
+    """Rows past each sequence's length hold NaN and Inf: masked keys add
+    nothing, so the output equals attention over the valid rows alone, in
+    whole-row and split-KV blocks, with and without the appended new row."""
+    Tmax, D = 200, 64
+    q = _round(RNG.standard_normal((B, H, 1, D)).astype(np.float32), dtype)
+    kc = _round(RNG.standard_normal((B, H, Tmax, D)).astype(np.float32), dtype)
+    vc = _round(RNG.standard_normal((B, H, Tmax, D)).astype(np.float32), dtype)
+    lens = np.linspace(3, Tmax - 5, B).astype(np.int32)
+    kbad, vbad = kc.copy(), vc.copy()
+    for b in range(B):
+        kbad[b, :, lens[b]:] = np.nan
+        vbad[b, :, lens[b]:] = np.inf
+        vbad[b, :, lens[b]::2] = np.nan
+    got = gpu.decode_attention(_dev(gpu, q, dtype), _dev(gpu, kbad, dtype), _dev(gpu, vbad, dtype),
+                               gpu.from_numpy(lens))
+    got_h = _host(got)
+    assert np.isfinite(got_h).all()
+    tol = 1e-3 if dtype == "float32" else 1e-2
+    assert rel_err(got_h, _decode_ref(q, kc, vc, lens)) < tol
+    # the step's own row appended at lens - 1, NaN beyond it
+    kn = _round(RNG.standard_normal((B, H, 1, D)).astype(np.float32), dtype)
+    vn = _round(RNG.standard_normal((B, H, 1, D)).astype(np.float32), dtype)
+    got2 = gpu.decode_attention(_dev(gpu, q, dtype), _dev(gpu, kbad, dtype), _dev(gpu, vbad, dtype),
+                                gpu.from_numpy(lens + 1), k_new=_dev(gpu, kn, dtype), v_new=_dev(gpu, vn, dtype))
+    kref, vref = kc.copy(), vc.copy()
+    for b in range(B):
+        kref[b, :, lens[b]] = kn[b, :, 0]
+        vref[b, :, lens[b]] = vn[b, :, 0]
+    got2_h = _host(got2)
+    assert np.isfinite(got2_h).all()
+    assert rel_err(got2_h, _decode_ref(q, kref, vref, lens + 1)) < (1e-3 if dtype == "float32" else 2e-2)
+
+
 def test_decode_attention_matches_attention_on_full_cache(gpu):
     """With every row valid and Tq = 1 it is the reference's decode attention
     (non-causal over the whole cache) — the fused attention kernel's answer."""

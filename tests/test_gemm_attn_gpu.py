@@ -85,6 +85,21 @@ def test_fused_epilogues_through_graph(gpu):
     assert rel_err(z_np, r + ref) < 1e-3
 
 
+@pytest.mark.parametrize("xshape,rshape", [((1, 96), (70, 130)), ((70, 96), (3, 70, 130))])
+def test_broadcasting_residual_stays_unfused(gpu, xshape, rshape):
+    """An add that broadcasts the GEMM output ([1,N] + [M,N], or a 2-D
+    product + a 3-D residual) is evaluated as its own node, with the same
+    numbers as op by op."""
+    x, w, b, r = f32(*xshape), f32(96, 130), f32(130), f32(*rshape)
+    z = gpu.from_numpy(r) + gpu.add_bias(gpu.from_numpy(x) @ gpu.from_numpy(w), gpu.from_numpy(b))
+    got = z.to_numpy()
+    assert got.shape == np.broadcast_shapes(rshape, (xshape[0], 130))
+    assert rel_err(got, r + O.add_bias(O.matmul(x, w), b)) < 1e-3
+    # the residual on the other side of the add
+    z2 = gpu.add_bias(gpu.from_numpy(x) @ gpu.from_numpy(w), gpu.from_numpy(b)) + gpu.from_numpy(r)
+    assert rel_err(z2.to_numpy(), r + O.add_bias(O.matmul(x, w), b)) < 1e-3
+
+
 def test_linear_relu(gpu):
     x, w, b = f32(33, 64), f32(48, 64), f32(48)
     got = gpu.linear(gpu.from_numpy(x), gpu.from_numpy(w), gpu.from_numpy(b), "relu").to_numpy()
