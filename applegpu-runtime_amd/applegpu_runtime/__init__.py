@@ -341,9 +341,14 @@ def set_pool_watermark(mb: int):
 
 
 def graph_stats() -> dict:
-    out = (c_uint64 * 4)()
-    lib.applegpu_ffi_graph_stats(out)
-    return {"evals": out[0], "nodes": out[1], "fused_gemm_epilogues": out[2], "launches_saved": out[3]}
+    """Lazy-executor counters since the library loaded: evals, nodes,
+    GEMM epilogue fusions, launches saved by fusion, fused elementwise
+    chains and the nodes inside them, and kernel launcher calls."""
+    names = ("evals", "nodes", "fused_gemm_epilogues", "launches_saved", "fused_chains", "chain_nodes",
+             "launcher_calls")
+    out = (c_uint64 * len(names))()
+    lib.applegpu_ffi_graph_stats_ex(out, len(names))
+    return dict(zip(names, (int(v) for v in out)))
 
 
 # Streaming batches (reference lib.rs:1244-1257): one HIP stream is always

@@ -100,6 +100,7 @@ _SIGS = {
     "applegpu_ffi_set_limits": (None, [c_uint64, c_uint64, c_uint64]),
     "applegpu_ffi_device_name": (c_int32, [c_char_p, c_uint32]),
     "applegpu_ffi_graph_stats": (c_int32, [u64p]),
+    "applegpu_ffi_graph_stats_ex": (c_uint32, [u64p, c_uint32]),
     "applegpu_ffi_inject_alloc_failures": (None, [c_int32]),
     "applegpu_kv_write": (c_int32, [c_uint64, c_uint64, c_uint64]),
     "applegpu_kv_write_pair": (c_int32, [c_uint64, c_uint64, c_uint64, c_uint64, c_uint64]),

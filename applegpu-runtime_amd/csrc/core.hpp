@@ -54,6 +54,9 @@ struct Error : std::runtime_error {
 
 // Checks the launch that was just enqueued.
 void check_launch(const char* what);
+// Number of check_launch calls since the library loaded: one per kernel
+// launcher call on this path (the lazy executor's fusion tests count them).
+uint64_t launcher_calls();
 
 // ── device buffers ────────────────────────────────────────────────────────
 struct Arena;

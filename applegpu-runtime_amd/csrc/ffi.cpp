@@ -421,6 +421,16 @@ int32_t applegpu_ffi_graph_stats(uint64_t* out4) {
   return 0;
 }
 
+uint32_t applegpu_ffi_graph_stats_ex(uint64_t* out, uint32_t cap) {
+  std::lock_guard<std::recursive_mutex> g(big_lock());
+  GraphStats s = graph_stats();
+  const uint64_t v[] = {s.evals, s.nodes, s.fused_gemm_epilogues, s.launches_saved,
+                        s.fused_chains, s.chain_nodes, s.launcher_calls};
+  const uint32_t n = (uint32_t)(sizeof v / sizeof v[0]);
+  for (uint32_t i = 0; i < n && i < cap; ++i) out[i] = v[i];
+  return n;
+}
+
 // ── graph capture ──────────────────────────────────────────────────────────
 namespace {
 struct Captured {

@@ -301,7 +301,11 @@ std::vector<TensorP> record_op(int code, const std::vector<TensorP>& in, const s
 
 // ── eval ───────────────────────────────────────────────────────────────────
 static GraphStats g_stats;
-GraphStats graph_stats() { return g_stats; }
+GraphStats graph_stats() {
+  GraphStats s = g_stats;
+  s.launcher_calls = launcher_calls();
+  return s;
+}
 
 namespace {
 
@@ -316,6 +320,58 @@ struct Group {
   float ln_eps = 1e-5f;
   int64_t packed_n = 0;       // b is packed decode weights of this many columns
 };
+
+// An elementwise chain planned for one fused_chain launch.
+struct ChainPlan {
+  k::ChainProgram prog;
+  std::vector<const TensorP*> leaves;  // entries of the chain nodes' input lists
+  int len = 0;
+};
+
+// The kernel op code of a node a chain may hold (float unary or arithmetic
+// binary ops, crates/core/src/graph.rs is_elementwise), or -1.
+int chain_op(int code) {
+  switch (code) {
+    case OP_ADD: case OP_SUB: case OP_MUL: case OP_DIV: case OP_MIN: case OP_MAX: return code - OP_ADD;
+    case OP_NEG: return k::kNeg;
+    case OP_RELU: return k::kRelu;
+    case OP_EXP: return k::kExp;
+    case OP_LOG: return k::kLog;
+    case OP_SQRT: return k::kSqrt;
+    case OP_ABS: return k::kAbs;
+    case OP_SIGN: return k::kSign;
+    case OP_TANH: return k::kTanh;
+    case OP_SIN: return k::kSin;
+    case OP_COS: return k::kCos;
+    case OP_SIGMOID: return k::kSigmoid;
+    case OP_GELU: return k::kGelu;
+    case OP_GELU_EXACT: return k::kGeluExact;
+    case OP_SCALAR_MUL: return k::kScale;
+    case OP_POW: return k::kPow;
+    case OP_CLAMP: return k::kClamp;
+  }
+  return -1;
+}
+
+bool chain_binary(int code) { return code >= OP_ADD && code <= OP_MAX; }
+
+// Appends node n as the program's next step; `cur` is the chain node n
+// consumes (nullptr for the chain's first node, whose left input is the
+// starting accumulator).
+template <typename LeafOf>
+void add_chain_step(k::ChainProgram& prog, const Node* n, const Tensor* cur, LeafOf&& leaf_of) {
+  k::ChainStep& st = prog.step[prog.n_steps++];
+  st.op = chain_op(n->code);
+  if (chain_binary(n->code)) {
+    const bool acc_left = cur == nullptr || n->in[0].get() == cur;
+    st.acc_rhs = acc_left ? 0 : 1;
+    st.leaf = leaf_of(acc_left ? n->in[1] : n->in[0]);
+  } else {
+    st.leaf = -1;
+    st.p0 = n->f.size() > 0 ? (float)n->f[0] : 0.f;
+    st.p1 = n->f.size() > 1 ? (float)n->f[1] : 0.f;
+  }
+}
 
 bool is_single_internal_use(const TensorP& t, const std::unordered_map<Tensor*, int>& uses, int planner_refs = 0) {
   if (!t->pending() || t->ext_refs != 0) return false;
@@ -485,6 +541,74 @@ void eval_all(const std::vector<TensorP>& roots) {
     }
   }
 
+  // Elementwise chains (crates/core/src/fusion.rs:60-141, run on every eval
+  // at lazy.rs:237): starting at an elementwise node, follow its single
+  // consumer while that consumer is elementwise too and the current node
+  // has no other user, inside or outside the graph.  A chain of two or more
+  // runs as one fused_chain launch at its last node; the nodes before it are
+  // absorbed.  Nodes the GEMM planning above claimed stay with their GEMM.
+  std::unordered_map<Tensor*, ChainPlan> chains;  // keyed by the chain's last node
+  {
+    std::unordered_map<Tensor*, size_t> pos;
+    for (size_t i = 0; i < order.size(); ++i) pos[order[i].get()] = i;
+    std::unordered_map<Tensor*, Tensor*> consumer;  // valid for tensors with one internal use
+    for (auto& t : order)
+      for (auto& c : t->node->in)
+        if (c->pending()) consumer[c.get()] = t.get();
+    auto fusable = [&](Tensor* t) {
+      return chain_op(t->node->code) >= 0 && (t->dtype == DType::F32 || t->dtype == DType::F16 ||
+                                              t->dtype == DType::BF16) &&
+             !absorbed.count(t) && !groups.count(t) && !emb_adds.count(t) && !post_ln.count(t);
+    };
+    std::unordered_set<Tensor*> taken;
+    for (size_t i = 0; i < order.size(); ++i) {
+      Tensor* s = order[i].get();
+      if (taken.count(s) || !fusable(s)) continue;
+      std::vector<Tensor*> nodes{s};
+      std::vector<const TensorP*> leaves;
+      k::ChainProgram prog;
+      auto leaf_of = [&](const TensorP& x) {
+        for (size_t j = 0; j < leaves.size(); ++j)
+          if (leaves[j]->get() == x.get()) return (int)j;
+        leaves.push_back(&x);
+        return (int)leaves.size() - 1;
+      };
+      // first node: acc = its (left) input, then the node as a step
+      const Node* n0 = s->node.get();
+      prog.first = leaf_of(n0->in[0]);
+      add_chain_step(prog, n0, nullptr, leaf_of);
+      Tensor* cur = s;
+      for (;;) {
+        auto ci = consumer.find(cur);
+        if (ci == consumer.end() || !is_single_internal_use(order[pos[cur]], uses)) break;
+        Tensor* nx = ci->second;
+        if (taken.count(nx) || !fusable(nx) || nx->dtype != s->dtype) break;
+        const Node* nn = nx->node.get();
+        // the other operand (if any) must fit in the leaf table
+        int extra = 0;
+        if (nn->in.size() == 2) {
+          const TensorP& other = nn->in[0].get() == cur ? nn->in[1] : nn->in[0];
+          bool known = false;
+          for (auto* l : leaves) known |= l->get() == other.get();
+          extra = known ? 0 : 1;
+        }
+        if (prog.n_steps >= k::kChainMaxSteps || (int)leaves.size() + extra > k::kChainMaxLeaves) break;
+        add_chain_step(prog, nn, cur, leaf_of);
+        nodes.push_back(nx);
+        cur = nx;
+      }
+      if (nodes.size() < 2) continue;
+      prog.n_leaves = (int)leaves.size();
+      for (Tensor* t : nodes) taken.insert(t);
+      for (size_t j = 0; j + 1 < nodes.size(); ++j) absorbed.insert(nodes[j]);
+      ChainPlan cp;
+      cp.prog = prog;
+      cp.leaves = leaves;
+      cp.len = (int)nodes.size();
+      chains[cur] = cp;
+    }
+  }
+
   for (size_t i = 0; i < order.size(); ++i) {
     TensorP t = order[i];
     // Absorbed into a fused GEMM, or already filled by its multi-output
@@ -495,8 +619,17 @@ void eval_all(const std::vector<TensorP>& roots) {
     }
     Node* n = t->node.get();
     auto git = groups.find(t.get());
+    auto cit = chains.find(t.get());
     std::vector<TensorP> res;
-    if (git != groups.end()) {
+    if (cit != chains.end()) {
+      const ChainPlan& cp = cit->second;
+      std::vector<TensorP> leaves;
+      for (const TensorP* l : cp.leaves) leaves.push_back(*l);
+      res = {ops::fused_chain(leaves, cp.prog, t->dtype, t->dims())};
+      g_stats.fused_chains++;
+      g_stats.chain_nodes += cp.len;
+      g_stats.launches_saved += cp.len - 1;
+    } else if (git != groups.end()) {
       const Group& g = git->second;
       ops::Epilogue e;
       e.bias = g.bias;

@@ -62,6 +62,8 @@ void execute_compiled(const uint8_t* ops, size_t len, const uint64_t* inputs, ui
 
 struct GraphStats {
   uint64_t evals = 0, nodes = 0, fused_gemm_epilogues = 0, launches_saved = 0;
+  uint64_t fused_chains = 0, chain_nodes = 0;  // elementwise chains run as one launch, and their nodes
+  uint64_t launcher_calls = 0;                  // kernel launcher calls (one per launched kernel family)
 };
 GraphStats graph_stats();
 

@@ -56,6 +56,35 @@ void axpy(DType dt, void* y, const ND& sy, const void* x, const ND& sx, float al
 void add_bias(DType dt, const void* in, const void* bias, void* out, int64_t numel,
               int64_t channels, int64_t channel_stride, hipStream_t s);
 
+// ── fused elementwise chains ──────────────────────────────────────────────
+// One launch for a chain of float elementwise ops, the lazy executor's
+// fusion of single-consumer chains (crates/core/src/fusion.rs:60-282).  The
+// program is interpreted per element from the kernel arguments (no runtime
+// compilation): acc = leaf[first]; then each step is acc = un(acc),
+// acc = acc op leaf[j] or acc = leaf[j] op acc.  After every step acc is
+// rounded to the chain's dtype, as the unfused node would have stored it, so
+// results equal the op-by-op launches bit for bit.
+constexpr int kChainMaxLeaves = 8;
+constexpr int kChainMaxSteps = 16;
+struct ChainStep {
+  int32_t op = 0;       // Un code (unary step) or Bin code (binary step)
+  int32_t leaf = -1;    // binary: the other operand's leaf index; unary: -1
+  int32_t acc_rhs = 0;  // binary: the accumulator is the right operand
+  float p0 = 0.f, p1 = 0.f;
+};
+struct ChainProgram {
+  int32_t n_steps = 0, first = 0, n_leaves = 0;
+  ChainStep step[kChainMaxSteps];
+};
+struct ChainLeaves {
+  const void* ptr[kChainMaxLeaves] = {};
+  ND nd[kChainMaxLeaves];             // strides over the output shape (0 = broadcast)
+  int64_t period[kChainMaxLeaves] = {};  // filled by the launcher
+};
+// out (contiguous, shape `so`) = the program over the leaves; dt is F32, F16
+// or BF16 for every leaf and the output.
+void fused_chain(DType dt, const ChainProgram& prog, ChainLeaves leaves, void* out, const ND& so, hipStream_t s);
+
 // ── row kernels (last dim, row stride `ld`, unit column stride) ───────────
 enum RowOp : int { kSoftmax, kLogSoftmax, kSoftmaxCausal };
 void softmax_rows(int op, DType dt, const void* x, int64_t ldx, void* y, int64_t ldy,

@@ -298,6 +298,93 @@ __global__ void __launch_bounds__(256) add_bias_kernel(const T* __restrict__ in,
   }
 }
 
+// ── fused elementwise chains ────────────────────────────────────────────────
+// Every step computes in fp32 through bin_apply/un_apply, the functions the
+// unfused kernels use, and rounds to T as the unfused node's store would.
+template <typename T>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (std::is_same<T, float>::value) return v;
+  else return (float)(T)v;
+}
+
+template <typename T>
+__device__ __forceinline__ float chain_step(const ChainStep& st, float acc, float v) {
+  float r;
+  if (st.leaf < 0) r = un_apply<float>(st.op, acc, st.p0, st.p1);
+  else r = st.acc_rhs ? bin_apply<float>(st.op, v, acc, 0.f) : bin_apply<float>(st.op, acc, v, 0.f);
+  return round_to<T>(r);
+}
+
+// Four consecutive elements [base, base + 4) of leaf j in the flat layout:
+// element i reads leaf[i % period] (period == n: the whole output; 1: a
+// scalar; otherwise a multiple of 4 that divides n, so the four are
+// contiguous in the leaf).
+template <typename T>
+__device__ __forceinline__ void chain_load4(const ChainLeaves& L, int j, int64_t base, int64_t n, float (&v)[4]) {
+  const T* p = (const T*)L.ptr[j];
+  const int64_t period = L.period[j];
+  if (period == 1) {
+    const float s = (float)p[0];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = s;
+    return;
+  }
+  const int64_t off = period == n ? base : base % period;
+  T raw[4];
+  if constexpr (sizeof(T) == 4) *(float4*)raw = *(const float4*)(p + off);
+  else *(float2*)raw = *(const float2*)(p + off);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (float)raw[e];
+}
+
+// Contiguous, scalar and suffix-broadcast leaves: 4 elements per thread,
+// 16-byte (fp32) or 8-byte (16-bit) loads and stores.
+template <typename T>
+__global__ void __launch_bounds__(256) chain_flat(ChainProgram p, ChainLeaves L, T* __restrict__ o, int64_t n) {
+  const int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (base >= n) return;
+  if (base + 4 <= n) {
+    float acc[4];
+    chain_load4<T>(L, p.first, base, n, acc);
+    for (int s = 0; s < p.n_steps; ++s) {
+      const ChainStep st = p.step[s];
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (st.leaf >= 0) chain_load4<T>(L, st.leaf, base, n, v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = chain_step<T>(st, acc[e], v[e]);
+    }
+    T out[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = (T)acc[e];
+    if constexpr (sizeof(T) == 4) *(float4*)(o + base) = *(float4*)out;
+    else *(float2*)(o + base) = *(float2*)out;
+  } else {
+    for (int64_t i = base; i < n; ++i) {
+      auto at = [&](int j) { return (float)((const T*)L.ptr[j])[L.period[j] == 1 ? 0 : i % L.period[j]]; };
+      float acc = at(p.first);
+      for (int s = 0; s < p.n_steps; ++s) {
+        const ChainStep st = p.step[s];
+        acc = chain_step<T>(st, acc, st.leaf >= 0 ? at(st.leaf) : 0.f);
+      }
+      o[i] = (T)acc;
+    }
+  }
+}
+
+// Any leaf layout: each leaf read through its own strides over the output.
+template <typename I, typename T>
+__global__ void __launch_bounds__(256) chain_nd(ChainProgram p, ChainLeaves L, T* __restrict__ o, ND so, I n) {
+  for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (I)gridDim.x * blockDim.x) {
+    auto at = [&](int j) { return (float)((const T*)L.ptr[j])[nd_offset<I>(i, so, L.nd[j])]; };
+    float acc = at(p.first);
+    for (int s = 0; s < p.n_steps; ++s) {
+      const ChainStep st = p.step[s];
+      acc = chain_step<T>(st, acc, st.leaf >= 0 ? at(st.leaf) : 0.f);
+    }
+    o[i] = (T)acc;
+  }
+}
+
 bool fits32(int64_t n, const ND& a, const ND& b) {
   if (n >= (int64_t(1) << 31)) return false;
   int64_t ea = 0, eb = 0;
@@ -524,6 +611,58 @@ void axpy(DType dt, void* y, const ND& sy, const void* x, const ND& sx, float al
                                              (T*)y, (const T*)x, sx, sy, (uint64_t)n, alpha));
   }
   check_launch("axpy");
+}
+
+// The flat-path period of a leaf over the contiguous output `so`: n when it
+// is laid out like the output, 1 for a single broadcast value, the element
+// count of the output's trailing dims when it is contiguous over those and
+// broadcast over the leading ones; 0 when none applies.
+static int64_t chain_period(const ND& l, const ND& so, int64_t n) {
+  if (is_flat(l, so)) return n;
+  int d = so.ndim;
+  int64_t expect = 1;
+  while (d > 0 && (so.shape[d - 1] == 1 || l.stride[d - 1] == expect)) {
+    expect *= so.shape[d - 1];
+    --d;
+  }
+  for (int i = 0; i < d; ++i)
+    if (l.stride[i] != 0 && so.shape[i] != 1) return 0;
+  return expect;
+}
+
+void fused_chain(DType dt, const ChainProgram& prog, ChainLeaves L, void* out, const ND& so, hipStream_t s) {
+  const int64_t n = numel_of(so);
+  if (n == 0) return;
+  if (prog.n_leaves < 1 || prog.n_leaves > kChainMaxLeaves || prog.n_steps < 1 || prog.n_steps > kChainMaxSteps ||
+      prog.first < 0 || prog.first >= prog.n_leaves)
+    fail("fused_chain: malformed program");
+  for (int i = 0; i < prog.n_steps; ++i)
+    if (prog.step[i].leaf >= prog.n_leaves) fail("fused_chain: step %d names leaf %d", i, prog.step[i].leaf);
+  const size_t es = dt == DType::F32 ? 4 : 2;
+  bool flat = aligned16(out) || (es == 2 && ((uintptr_t)out & 7) == 0);
+  for (int j = 0; j < prog.n_leaves && flat; ++j) {
+    const int64_t per = chain_period(L.nd[j], so, n);
+    const bool vec_ok = ((uintptr_t)L.ptr[j] & (4 * es - 1)) == 0;
+    if (per == 1) L.period[j] = 1;
+    else if (per == n && vec_ok) L.period[j] = n;
+    else if (per > 1 && per % 4 == 0 && n % per == 0 && vec_ok) L.period[j] = per;
+    else flat = false;
+  }
+  if (flat) {
+    const unsigned g = (unsigned)((n + 1023) / 1024);
+    AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((chain_flat<T>), dim3(g), dim3(256), 0, s, prog, L, (T*)out, n));
+  } else {
+    bool small = n < (int64_t(1) << 31);
+    for (int j = 0; j < prog.n_leaves && small; ++j) small = fits32(n, L.nd[j], L.nd[j]);
+    if (small) {
+      AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((chain_nd<uint32_t, T>), dim3(grid_for(n)), dim3(256), 0, s, prog, L,
+                                               (T*)out, so, (uint32_t)n));
+    } else {
+      AGPU_FLOAT_SWITCH(dt, hipLaunchKernelGGL((chain_nd<uint64_t, T>), dim3(grid_for(n)), dim3(256), 0, s, prog, L,
+                                               (T*)out, so, (uint64_t)n));
+    }
+  }
+  check_launch("fused_chain");
 }
 
 void add_bias(DType dt, const void* in, const void* bias, void* out, int64_t numel, int64_t channels,

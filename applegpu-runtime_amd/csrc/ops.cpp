@@ -306,6 +306,27 @@ static Cls un_class(int op) {
   return kFloatOnly;
 }
 
+TensorP fused_chain(const std::vector<TensorP>& leaves, const k::ChainProgram& prog, DType dt,
+                    const std::vector<int64_t>& dims) {
+  if (dt != DType::F32 && dt != DType::F16 && dt != DType::BF16) fail("fused_chain: %s is not a float dtype", dtype_name(dt));
+  if (leaves.empty() || leaves.size() > (size_t)k::kChainMaxLeaves || (int)leaves.size() != prog.n_leaves)
+    fail("fused_chain: %zu leaves for a program of %d", leaves.size(), prog.n_leaves);
+  k::ChainLeaves L;
+  for (size_t j = 0; j < leaves.size(); ++j) {
+    if (leaves[j]->dtype != dt) fail("fused_chain: leaf %zu is %s, not %s", j, dtype_name(leaves[j]->dtype), dtype_name(dt));
+    if (broadcast_shapes(leaves[j]->dims(), dims) != dims) fail("fused_chain: leaf %zu does not broadcast to the output", j);
+  }
+  TensorP out = alloc_out(dt, dims);
+  LAUNCH {
+    for (size_t j = 0; j < leaves.size(); ++j) {
+      L.ptr[j] = leaves[j]->data();
+      L.nd[j] = nd_for(*leaves[j], dims);
+    }
+    k::fused_chain(dt, prog, L, out->data(), nd_shape(dims), rt().stream());
+  }
+  return out;
+}
+
 TensorP unary(int op, const TensorP& x, float p0, float p1) {
   check_dtype(un_name(op), un_class(op), x->dtype);
   DType odt = op == k::kLogicalNot ? DType::Bool : x->dtype;

@@ -36,6 +36,10 @@ TensorP masked_fill(const TensorP& x, const TensorP& mask, float value);
 TensorP tri(const TensorP& x, bool upper, int64_t diag);
 TensorP threshold_backward(const TensorP& grad, const TensorP& input, float thr);
 TensorP add_bias(const TensorP& x, const TensorP& bias);
+// One launch for a chain of float elementwise ops (k::fused_chain): leaves
+// broadcast onto `dims`, all of dtype `dt`.
+TensorP fused_chain(const std::vector<TensorP>& leaves, const k::ChainProgram& prog, DType dt,
+                    const std::vector<int64_t>& dims);
 TensorP full(DType dt, const std::vector<int64_t>& dims, float value);
 void axpy_inplace(const TensorP& self, const TensorP& other, float alpha);  // self += alpha*other
 void copy_into(const TensorP& dst, const TensorP& src);                      // dst (any strides) = src

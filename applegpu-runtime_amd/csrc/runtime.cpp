@@ -1,4 +1,5 @@
 // Runtime: device init, the single stream, the buffer pool and the id registry.
+#include <atomic>
 #include "core.hpp"
 
 #include <cstdarg>
@@ -78,7 +79,11 @@ void fail(const char* fmt, ...) {
   throw Error(buf);
 }
 
+static std::atomic<uint64_t> g_launcher_calls{0};
+uint64_t launcher_calls() { return g_launcher_calls.load(std::memory_order_relaxed); }
+
 void check_launch(const char* what) {
+  g_launcher_calls.fetch_add(1, std::memory_order_relaxed);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) fail("kernel launch %s failed: %s", what, hipGetErrorString(e));
 }

@@ -182,6 +182,13 @@ void applegpu_ffi_set_limits(uint64_t max_tensor_bytes, uint64_t max_memory_byte
 int32_t applegpu_ffi_device_name(char* out, uint32_t cap);
 /* out[0..4] = evals, nodes, fused GEMM epilogues, launches saved by fusion */
 int32_t applegpu_ffi_graph_stats(uint64_t* out4);
+/* The same counters and more, for the lazy executor's fusion pass
+ * (crates/core/src/fusion.rs:243-282 replaces chains of elementwise nodes
+ * by one fused node; the reference exposes no counters for it): writes up
+ * to `cap` of evals, nodes, fused GEMM epilogues, launches saved, fused
+ * elementwise chains, nodes inside those chains, kernel launcher calls;
+ * returns the number of counters available (7). */
+uint32_t applegpu_ffi_graph_stats_ex(uint64_t* out, uint32_t cap);
 /* Test hook (no reference counterpart): the next n device allocations fail,
  * so the out-of-memory path can be exercised from the host. */
 void applegpu_ffi_inject_alloc_failures(int32_t n);

@@ -49,7 +49,8 @@ def test_captured_c2_forward_full_size_vs_oracle(gpu):
             assert err < 1e-4, (r, err)
             outs.append(got)
             # eager work on the same stream between replays
-            (gpu.from_numpy(np.ones(1000, np.float32)) * 2.0).to_numpy()
+            t = gpu.from_numpy(np.ones(1000, np.float32))
+            (t + t).to_numpy()
         np.testing.assert_array_equal(outs[0], outs[1])
         np.testing.assert_array_equal(outs[0], outs[2])
         # greedy picks: equal wherever the oracle's top two are apart by more
