@@ -125,6 +125,7 @@ _SIGS = {
     "applegpu_eager_view_typed": (c_void_p, [c_uint64, u64p, u64p, c_uint32, c_uint64, c_int8, u64p]),
     "applegpu_eager_fill": (c_int32, [c_uint64, c_double]),
     "applegpu_eager_linear": (c_void_p, [c_uint64, c_uint64, c_uint64, c_int32, u64p]),
+    "applegpu_eager_linear_noalloc": (c_int32, [c_uint64, c_uint64, c_uint64, c_int32, c_uint64]),
     "applegpu_eager_matmul_masked": (c_void_p, [c_uint64, c_uint64, c_bool, c_bool, c_uint64, u64p]),
     "applegpu_eager_mse_loss": (c_void_p, [c_uint64, c_uint64, u64p]),
     "applegpu_eager_mse_loss_backward": (c_void_p, [c_uint64, c_uint64, c_uint64, u64p]),

@@ -58,6 +58,13 @@ void check_launch(const char* what);
 // launcher call on this path (the lazy executor's fusion tests count them).
 uint64_t launcher_calls();
 
+// Device scratch of the allocation-free entry point (csrc/noalloc.hip):
+// noalloc_setup looks up the scratch array's address on the current device
+// (the runtime's init calls it once the device is current); noalloc_scratch
+// returns that address and the array's size in bytes.
+bool noalloc_setup(std::string* err);
+void* noalloc_scratch(size_t* cap);
+
 // ── device buffers ────────────────────────────────────────────────────────
 struct Arena;
 

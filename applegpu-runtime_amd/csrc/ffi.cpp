@@ -829,6 +829,33 @@ uint8_t* applegpu_eager_linear(uint64_t x_id, uint64_t w_id, uint64_t bias_id, i
   });
 }
 
+int32_t applegpu_eager_linear_noalloc(uint64_t x_id, uint64_t w_id, uint64_t bias_id, int32_t act,
+                                      uint64_t out_id) {
+  return guarded<int32_t>(kEager, -1, [&]() -> int32_t {
+    // Inputs must hold values already: evaluating pending ops could allocate.
+    auto ready = [&](uint64_t id, const char* what) {
+      TensorP t = rt().lookup(id);
+      if (t->pending()) fail("linear_noalloc: %s has pending ops; evaluate it before this call", what);
+      if (!t->buf) fail("linear_noalloc: %s has no storage", what);
+      return t;
+    };
+    TensorP x = ready(x_id, "x"), w = ready(w_id, "weight"), out = ready(out_id, "out");
+    if (x->ndim != 2 || w->ndim != 2) fail("linear_noalloc: x [M, K] and weight [N, K] must be 2-D");
+    if (act < 0 || act > 3) fail("linear_noalloc: activation %d is not 0 (none), 1 (relu), 2 (gelu) or 3 (gelu_erf)", act);
+    if (out->buf == x->buf || out->buf == w->buf) fail("linear_noalloc: out must not share storage with x or weight");
+    ops::Epilogue e;
+    if (bias_id) {
+      e.bias = ready(bias_id, "bias");
+      if (out->buf == e.bias->buf) fail("linear_noalloc: out must not share storage with the bias");
+    }
+    e.act = act;
+    ops::NoAlloc na;
+    na.ws = noalloc_scratch(&na.cap);
+    ops::matmul(x, w, false, true, &e, out, nullptr, &na);
+    return 0;
+  });
+}
+
 uint8_t* applegpu_eager_matmul_masked(uint64_t a_id, uint64_t b_id, bool ta, bool tb, uint64_t mask_id,
                                       uint64_t* out_id) {
   return eager_out(out_id, [&] {

@@ -916,7 +916,17 @@ static void set_epilogue(k::Gemm& g, const Epilogue* epi, const std::vector<int6
 }
 
 TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const Epilogue* epi, const TensorP& into,
-               PostLn* post_ln) {
+               PostLn* post_ln, const NoAlloc* no_alloc) {
+  if (no_alloc) {
+    // Everything below must then run without a device allocation.
+    if (meta_mode()) fail("matmul: the allocation-free form runs eagerly only");
+    if (!into) fail("matmul: the allocation-free form writes into a caller-provided output");
+    if (post_ln) fail("matmul: the allocation-free form takes no layer_norm");
+    if (epi && (epi->ln_gamma || epi->residual || epi->mask))
+      fail("matmul: the allocation-free form takes a bias and an activation only");
+    if (epi && epi->bias && !epi->bias->is_contiguous())
+      fail("matmul: the allocation-free form needs a contiguous bias (a copy would allocate)");
+  }
   TensorP a = ta ? transpose_dims(a_in, a_in->ndim - 2, a_in->ndim - 1) : a_in;
   TensorP b = tb ? transpose_dims(b_in, b_in->ndim - 2, b_in->ndim - 1) : b_in;
   if (a_in->ndim < 2 || b_in->ndim < 2) fail("matmul requires at least 2D tensors, got %s and %s",
@@ -939,6 +949,8 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
   for (auto d : bdims) batch *= d;
 
   int64_t a_sb, b_sb;
+  if (no_alloc && (!batch_stride(*a, bdims, &a_sb) || !batch_stride(*b, bdims, &b_sb)))
+    fail("matmul: an operand's batch layout needs a copy, which the allocation-free form cannot make");
   if (!batch_stride(*a, bdims, &a_sb)) {
     // expand to the broadcast batch shape, contiguous
     std::vector<int64_t> full = bdims;
@@ -1019,6 +1031,13 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
     }
   }
   size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
+  if (no_alloc) {
+    if (wsb > no_alloc->cap)
+      fail("matmul: this %lld x %lld x %lld product needs %zu bytes of split-K workspace, more than the %zu "
+           "bytes the allocation-free form holds", (long long)M, (long long)N, (long long)K, wsb, no_alloc->cap);
+    LAUNCH k::gemm(g, wsb ? no_alloc->ws : nullptr, rt().stream());
+    return out;
+  }
   BufferP ws;
   if (wsb) ws = scratch(wsb);
   LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());

@@ -90,8 +90,16 @@ struct PostLn {
   float eps = 1e-5f;
   TensorP y;  // result
 };
+// No-allocation mode: the caller's output (`into`) and a caller-held split-K
+// workspace of `cap` bytes; any operand that would need a device copy, and
+// any plan whose workspace exceeds `cap`, is rejected instead.
+struct NoAlloc {
+  void* ws = nullptr;
+  size_t cap = 0;
+};
 TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = false,
-               const Epilogue* epi = nullptr, const TensorP& into = nullptr, PostLn* post_ln = nullptr);
+               const Epilogue* epi = nullptr, const TensorP& into = nullptr, PostLn* post_ln = nullptr,
+               const NoAlloc* no_alloc = nullptr);
 // w1[i1] + w2[i2] in one launch (token + position embedding), and with ln
 // also ln->y = layer_norm of the sum; embedding_add_fusable says whether the
 // operands fit the kernel.

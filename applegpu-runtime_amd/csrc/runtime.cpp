@@ -386,6 +386,10 @@ bool Runtime::init(std::string* err) {
       delete rt;
       return;
     }
+    if (!noalloc_setup(&g_init_err)) {
+      delete rt;
+      return;
+    }
     if (hipStreamCreateWithFlags(&rt->stream_, hipStreamNonBlocking) != hipSuccess) {
       g_init_err = "hipStreamCreate failed";
       delete rt;

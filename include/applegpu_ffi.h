@@ -302,6 +302,25 @@ uint8_t* applegpu_eager_view_typed(uint64_t base_id, const uint64_t* shape, cons
  * 2 gelu-tanh, 3 gelu-erf; bias_id 0 = none): replaces addmm's W^T copy +
  * matmul + bias add (backend_cpp/applegpu_backend.cpp:584-620). */
 uint8_t* applegpu_eager_linear(uint64_t x_id, uint64_t w_id, uint64_t bias_id, int32_t act, uint64_t* out_id);
+/* Allocation-free linear: no counterpart in the reference.  For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc): out = act(x W^T + b) as
+ * applegpu_eager_linear computes it (same kernels, same results), written
+ * into the caller's contiguous [M, N] tensor `out_id` of x's dtype.  x [M, K],
+ * weight [N, K] and the optional contiguous bias [N] (bias_id 0 = none) must
+ * already hold values, and out may not share storage with them.  The GEMM's
+ * split-K partial sums go to a static 64 MiB device array that each GPU the
+ * library runs on holds until the process ends; a product whose partials
+ * would exceed it (only reachable through a forced applegpu_ffi_gemm_tune
+ * split count: the planner's own choices stay below it) is rejected with an
+ * error.  Every call on one GPU shares
+ * that array and it keeps the last call's partials; calls are ordered on
+ * the library's one stream, but work that overlaps them on one GPU from
+ * another stream would race on it.  Nothing in it needs to start at zero:
+ * each split writes its whole partial tile before the reduction reads it.
+ * Returns 0, or -1 with the error set. */
+int32_t applegpu_eager_linear_noalloc(uint64_t x_id, uint64_t w_id, uint64_t bias_id, int32_t act,
+                                      uint64_t out_id);
 /* C = op(A) op(B) with a fused "mask" epilogue: out = (mask > 0) ? A@B : 0,
  * i.e. matmul followed by threshold_backward(., mask, 0) in one kernel
  * (eager.rs:485-560 + eager.rs:775-818). */
