@@ -90,6 +90,12 @@ def main():
     ap.add_argument("--only", default="",
                     help="with --suite: run only the sections whose name contains this text "
                          "(rows, c5, c4, decode)")
+    ap.add_argument("--c1", action="store_true",
+                    help="instead of the headline line, run config C1 (MLP 64-128-10 train step, batch 32) and "
+                         "print its JSON line: ms/step and kernels/step, with the CPU baseline")
+    ap.add_argument("--c5", action="store_true",
+                    help="instead of the headline line, run config C5 (int8 per-row quantize, dequantize and the "
+                         "[64,8192] x [8192,8192]^T GEMM) and print its JSON line, with the CPU baseline")
     ap.add_argument("--c4", action="store_true",
                     help="instead of the headline line, run config C4 (GPT-2 large fp16 prefill + greedy "
                          "decode over a KV cache) and print its JSON line")
@@ -103,6 +109,12 @@ def main():
         return
     if args.c4:
         c4_generate(args)
+        return
+    if args.c1:
+        c1_train(args)
+        return
+    if args.c5:
+        c5_pipeline(args)
         return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -619,10 +631,326 @@ def c4_cpu_baseline(wnp, cfg, ids, budget_s):
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "host": host_info(),
         "sample": f"torch {torch.__version__} CPU eager fp32 on fp16-rounded weights: prefill {B}x{T} "
                   f"{1e3 * pre_s:.0f} ms + {k} decode steps at {1e3 * step_s:.1f} ms/step, projected to "
                   f"{C4_STEPS} steps; host cpus {os.cpu_count()}",
     }
+
+
+C1_SIZES, C1_BATCH = [64, 128, 10], 32
+
+
+def _launcher_calls():
+    import applegpu_runtime as gpu
+    return gpu.graph_stats()["launcher_calls"]
+
+
+def c1_train(args):
+    """Config C1: Linear(64,128)-ReLU-Linear(128,10), batch 32, MSE, SGD lr
+    0.01 (torch.manual_seed(42), then the default Linear init, then x and y
+    from torch.randn, as python/tests/bench_comparison.py:23-28 seeds it).
+
+    value: one training step replayed as a captured HIP graph (the fused
+    C-ABI step: forward GEMMs with bias/ReLU epilogues, one MSE + gradient
+    launch, dX GEMM with the ReLU mask, dW GEMMs with the SGD update in the
+    epilogue, bias column sums with the update).  Also reported: the same
+    step op by op, and the reference's own route, the torch model on the
+    PrivateUse1 device with autograd and torch.optim.SGD
+    (bench_comparison.py:23-38: 5 warm-up steps, then the mean of 50).
+    kernels/step counts the kernel launchers one step calls."""
+    import torch
+    import applegpu_runtime as gpu
+    from applegpu_runtime import eager as E
+    from applegpu_runtime._native import lib
+    from applegpu_runtime.models.mlp import EagerMLP
+    from applegpu_runtime.cpp_backend import fallback_count, load_cpp_backend
+
+    gpu.init_backend()
+    load_cpp_backend()
+
+    def make():
+        torch.manual_seed(42)
+        m = torch.nn.Sequential(torch.nn.Linear(C1_SIZES[0], C1_SIZES[1]), torch.nn.ReLU(),
+                                torch.nn.Linear(C1_SIZES[1], C1_SIZES[2]))
+        x = torch.randn(C1_BATCH, C1_SIZES[0])
+        y = torch.randn(C1_BATCH, C1_SIZES[2])
+        return m, x, y
+
+    m, xt, yt = make()
+    params = [(m[0].weight.detach().numpy().copy(), m[0].bias.detach().numpy().copy()),
+              (m[2].weight.detach().numpy().copy(), m[2].bias.detach().numpy().copy())]
+    xnp, ynp = xt.numpy().copy(), yt.numpy().copy()
+    warm, iters = max(args.warmup, 5), max(args.steps, 50)
+
+    # C-ABI fused step: op by op, then one captured graph
+    mlp = EagerMLP(params)
+    x, y = E.from_numpy(xnp), E.from_numpy(ynp)
+    for _ in range(warm):
+        mlp.train_step(x, y, lr=0.01)
+    lib.applegpu_ffi_synchronize()
+    k0 = _launcher_calls()
+    mlp.train_step(x, y, lr=0.01)
+    kernels_fused = _launcher_calls() - k0
+    lib.applegpu_ffi_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        mlp.train_step(x, y, lr=0.01)
+    lib.applegpu_ffi_synchronize()
+    eager_ms = 1e3 * (time.perf_counter() - t0) / iters
+    mlp_g = EagerMLP(params)
+    g = gpu.capture(lambda: mlp_g.train_step(x, y, lr=0.01))
+    for _ in range(warm):
+        g.replay()
+    lib.applegpu_ffi_synchronize()
+    t0 = time.perf_counter()
+    lib.applegpu_ffi_event_record(0)
+    for _ in range(iters):
+        g.replay()
+    lib.applegpu_ffi_event_record(1)
+    lib.applegpu_ffi_synchronize()
+    graph_wall_ms = 1e3 * (time.perf_counter() - t0) / iters
+    graph_ms = lib.applegpu_ffi_event_elapsed_ms(0, 1) / iters
+    g.destroy()
+
+    # the reference's route: torch autograd on the PrivateUse1 device
+    md, xd, yd = make()
+    md = md.to("applegpu")
+    xd, yd = xd.to("applegpu"), yd.to("applegpu")
+    opt = torch.optim.SGD(md.parameters(), lr=0.01)
+
+    def torch_step():
+        loss = torch.nn.functional.mse_loss(md(xd), yd)
+        loss.backward()
+        opt.step()
+        opt.zero_grad()
+
+    for _ in range(warm):
+        torch_step()
+    torch.applegpu.synchronize()
+    f0, k0 = fallback_count(), _launcher_calls()
+    torch_step()
+    torch.applegpu.synchronize()
+    kernels_torch = _launcher_calls() - k0
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        torch_step()
+    torch.applegpu.synchronize()
+    torch_ms = 1e3 * (time.perf_counter() - t0) / iters
+    fallbacks = fallback_count() - f0
+
+    flop = mlp_flops(C1_SIZES, C1_BATCH)  # forward, dW of both layers, dX of the second
+    result = {
+        "metric": "C1 MLP 64-128-10 train ms/step (batch 32, MSE, SGD), 1 MI355X",
+        "value": round(graph_ms, 5),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": iters,
+        "warmup": warm,
+        "ms_per_step": round(graph_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C1 Linear(64,128)-ReLU-Linear(128,10) fp32, batch 32, MSE, SGD lr 0.01; one training "
+                        "step replayed as a captured HIP graph",
+            "kernels_per_step": kernels_fused,
+            "graph_replay_wall_ms": round(graph_wall_ms, 5),
+            "capi_op_by_op_ms": round(eager_ms, 5),
+            "torch_privateuse1_ms": round(torch_ms, 5),
+            "torch_privateuse1_kernels_per_step": kernels_torch,
+            "torch_privateuse1_cpu_fallbacks": fallbacks,
+            "flop_per_step": flop,
+        },
+        "roofline": {
+            "kernel": "whole training step (launch-bound: 38 KB of parameters, 1.29 MFLOP)",
+            "bound": "launch",
+            "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+            "ms_per_kernel": round(graph_ms / max(kernels_fused, 1), 5),
+        },
+    }
+    if not args.no_cpu_baseline:
+        mc, xc, yc = make()
+        oc = torch.optim.SGD(mc.parameters(), lr=0.01)
+
+        def cpu_step():
+            loss = torch.nn.functional.mse_loss(mc(xc), yc)
+            loss.backward()
+            oc.step()
+            oc.zero_grad()
+
+        for _ in range(5):
+            cpu_step()
+        times = []
+        for _ in range(50):
+            t0 = time.perf_counter()
+            cpu_step()
+            times.append(time.perf_counter() - t0)
+        result["cpu_baseline"] = {
+            "value": round(1e3 * float(np.mean(times)), 5),
+            "unit": "ms",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "host": host_info(),
+            "sample": f"torch {torch.__version__} CPU eager, 5 warm-up + 50 timed steps (python/tests/"
+                      f"bench_comparison.py:23-38); median {1e3 * float(np.median(times)):.4f} ms",
+        }
+    print(json.dumps(result), flush=True)
+
+
+def c5_pipeline(args):
+    """Config C5: W [8192, 8192] fp32 ~ N(0, 0.02) and X [64, 8192] ~ N(0, 1)
+    (seeded); per-row int8 quantize (scale = absmax(row)/127, round half to
+    even), dequantize, and Y = X @ deq^T, each stage timed on its own with
+    HIP events over back-to-back launches; W rotates over three copies
+    (805 MB) so the HBM-bound stages read past the 256 MB Infinity Cache.
+    value = the three stages' sum.  The int8 codes and scales are checked
+    bit for bit against a numpy restatement outside the timed region, Y
+    against the float64 product at the fp32 matmul bar."""
+    import applegpu_runtime as gpu
+    from applegpu_runtime import eager as E
+    from applegpu_runtime._native import lib
+    gpu.init_backend()
+    N, Mx = 8192, 64
+    rng = np.random.default_rng(42)
+    wnp = (rng.standard_normal((N, N), dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    xnp = rng.standard_normal((Mx, N), dtype=np.float32)
+    ws = [E.from_numpy(wnp)] + [E.from_numpy(rng.standard_normal((N, N), dtype=np.float32) * np.float32(0.02))
+                                for _ in range(2)]
+    X = E.from_numpy(xnp)
+    reps = max(args.steps, 12)
+
+    def timed(fn, inputs):
+        for i in range(2):
+            fn(inputs[i % len(inputs)])
+        lib.applegpu_ffi_synchronize()
+        lib.applegpu_ffi_event_record(0)
+        out = None
+        for i in range(reps):
+            out = None
+            out = fn(inputs[i % len(inputs)])
+        lib.applegpu_ffi_event_record(1)
+        return lib.applegpu_ffi_event_elapsed_ms(0, 1) / reps, out
+
+    q_ms, _ = timed(lambda w: E.op("quantize_per_row", [w], nout=2), ws)
+    q, sc = E.op("quantize_per_row", [ws[0]], nout=2)
+    qs = [q] + [E.op("quantize_per_row", [w], nout=2)[0] for w in ws[1:]]
+    scs = [sc] + [E.op("quantize_per_row", [w], nout=2)[1] for w in ws[1:]]
+    d_ms, _ = timed(lambda i: E.op("dequantize_per_row", [qs[i], scs[i]]), [0, 1, 2])
+    deq = E.op("dequantize_per_row", [q, sc])
+    gemm_ms, y = timed(lambda w: E.matmul_ex(X, w, False, True), [deq])
+    fused_ms, yf = timed(lambda i: E.op("linear_int8", [X, qs[i], scs[i]]), [0])
+    lib.applegpu_ffi_synchronize()
+
+    # parity outside the timed region
+    amax = np.abs(wnp).max(axis=1)
+    scale_ref = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q_ref = np.clip(np.rint(wnp / scale_ref[:, None]), -128, 127)
+    q_ref = np.where(scale_ref[:, None] == 0, 0, q_ref).astype(np.int8)
+    codes_exact = bool(np.array_equal(q.numpy(), q_ref)) and bool(np.array_equal(sc.numpy(), scale_ref))
+    deq_ref = q_ref.astype(np.float32) * scale_ref[:, None]
+    y_ref = xnp.astype(np.float64) @ deq_ref.T.astype(np.float64)
+    y_err = float(np.abs(y.numpy() - y_ref).max() / np.abs(y_ref).max())
+    yf_err = float(np.abs(yf.numpy() - y_ref).max() / np.abs(y_ref).max())
+    if not codes_exact or y_err > 1e-3 or yf_err > 1e-3:
+        raise RuntimeError(f"C5 parity failed: codes exact {codes_exact}, gemm err {y_err}, fused err {yf_err}")
+
+    qbytes = 4 * N * N + N * N + 4 * N
+    gemm_flop = 2.0 * Mx * N * N
+    total_ms = q_ms + d_ms + gemm_ms
+    q_gbs = qbytes / (q_ms * 1e-3) / 1e9
+    result = {
+        "metric": "C5 int8 per-row quantize + dequantize + [64,8192]x[8192,8192]^T GEMM, ms, 1 MI355X",
+        "value": round(total_ms, 5),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": reps,
+        "warmup": 2,
+        "ms_per_step": round(total_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32->i8->f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C5 W [8192,8192] fp32 N(0,0.02), X [64,8192] N(0,1); per-row absmax/127 int8 "
+                        "quantize (RNE), dequantize, X @ deq^T; three rotating W copies",
+            "quantize_us": round(q_ms * 1e3, 2),
+            "quantize_hbm_frac": round(q_gbs / HBM_PEAK_GBS, 4),
+            "dequantize_us": round(d_ms * 1e3, 2),
+            "dequantize_hbm_frac": round(qbytes / (d_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "gemm_us": round(gemm_ms * 1e3, 2),
+            "gemm_tflops": round(gemm_flop / (gemm_ms * 1e-3) / 1e12, 2),
+            "gemm_fp32_mfma_frac": round(gemm_flop / (gemm_ms * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "linear_int8_fused_us": round(fused_ms * 1e3, 2),
+            "codes_bit_exact": codes_exact,
+            "gemm_rel_err": y_err,
+            "linear_int8_rel_err": yf_err,
+        },
+        "roofline": {
+            "kernel": "quantize_per_row (row absmax, RNE int8 codes), [8192, 8192] fp32",
+            "bound": "hbm",
+            "achieved": round(q_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(q_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": qbytes,
+        },
+    }
+    if not args.no_cpu_baseline:
+        import torch
+        Wt, Xt = torch.from_numpy(wnp), torch.from_numpy(xnp)
+
+        def stage(fn, n=3):
+            fn()
+            t0 = time.perf_counter()
+            for _ in range(n):
+                out = fn()
+            return 1e3 * (time.perf_counter() - t0) / n, out
+
+        sc_ms, sct = stage(lambda: Wt.abs().amax(1) / 127.0)
+        qc_ms, qt = stage(lambda: torch.round(Wt / sct[:, None]).clamp(-128, 127).to(torch.int8))
+        dc_ms, dt = stage(lambda: qt.float() * sct[:, None])
+        gc_ms, _ = stage(lambda: Xt @ dt.T)
+        result["cpu_baseline"] = {
+            "value": round(sc_ms + qc_ms + dc_ms + gc_ms, 3),
+            "unit": "ms",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "host": host_info(),
+            "sample": f"torch {torch.__version__} CPU eager, the same expressions, 3 timed runs per "
+                      f"stage after one warm-up: scale {sc_ms:.1f} ms, quantize {qc_ms:.1f} ms, dequantize "
+                      f"{dc_ms:.1f} ms, GEMM {gc_ms:.1f} ms",
+        }
+    print(json.dumps(result), flush=True)
+
+
+def host_info():
+    """The CPU-baseline host: lscpu model name and core counts, the CPUs this
+    process may run on, and the threads torch uses."""
+    import subprocess
+    import torch
+    info = {"cpu_model": None, "sockets": None, "physical_cores": None, "logical_cpus": os.cpu_count(),
+            "cpus_allowed": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+            "torch_threads": torch.get_num_threads(), "torch": torch.__version__}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = {}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            kv[k.strip()] = v.strip()
+        info["cpu_model"] = kv.get("Model name")
+        sockets = int(kv.get("Socket(s)", "0") or 0)
+        per = int(kv.get("Core(s) per socket", "0") or 0)
+        info["sockets"] = sockets or None
+        info["physical_cores"] = sockets * per or None
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    return info
 
 
 def cpu_baseline(wnp, params, ids, xnp, ynp, budget_s):
@@ -652,6 +980,7 @@ def cpu_baseline(wnp, params, ids, xnp, ynp, budget_s):
         "unit": "ms",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "host": host_info(),
         "sample": f"{n} x (GPT-2 small fwd seq128 + MLP 4096 train step), torch {torch.__version__} CPU eager; "
                   f"gpt2 {1e3 * tg / n:.1f} ms, mlp {1e3 * tm / n:.1f} ms; host cpus {os.cpu_count()}",
     }
