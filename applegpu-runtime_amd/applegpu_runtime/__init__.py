@@ -468,10 +468,10 @@ def attention(q, k, v, scale=None):
 
 def qkv_attention(x, w, b, n_head, causal=True, batch=1, read_partials=False):
     """Attention of a fused QKV projection: heads of (x @ w + b) split into Q,
-    K, V (w [K, 3d] row-major, as GPT-2's c_attn), (causal) attention, heads
-    merged back: [batch*T, d].  read_partials (fp32): the attention kernel
-    reads the projection's split-K partial sums plus the bias itself, with no
-    reduction launch (same values; slower at GPT-2 small's shape)."""
+    K, V (w [K, 3d] row-major, as GPT-2's c_attn, or those weights packed by
+    pack_weight_x3), (causal) attention, heads merged back: [batch*T, d].
+    read_partials (fp32): the attention kernel reads the projection's split-K
+    partial sums plus the bias itself, with no reduction launch."""
     return _op(b"qkv_attention", [_t(x), _t(w), _t(b)],
                i=(int(n_head), int(bool(causal)), int(batch), int(bool(read_partials))))
 def attention_causal(q, k, v, scale=None):
@@ -562,8 +562,17 @@ def pack_weight(wt):
     return _op(b"pack_weight", [_t(wt)])
 
 
+def pack_weight_x3(b):
+    """fp32 weights for activations of few rows: b is the B operand [in, out]
+    of x @ b (any strides; in a multiple of 16), split once into bf16 hi/lo
+    MFMA fragments.  Use with matmul_packed(x, packed, out)."""
+    return _op(b"pack_weight_x3", [_t(b)])
+
+
 def matmul_packed(x, packed, out_features):
-    """x [rows <= 16, in] @ wt^T for packed = pack_weight(wt), wt [out, in]."""
+    """x @ W for packed weights: packed = pack_weight(wt) (fp16/bf16 wt [out,
+    in], x [rows <= 16, in]; the product is x @ wt^T), or packed =
+    pack_weight_x3(b) (fp32 b [in, out], x [any rows, in]; x @ b)."""
     return _op(b"matmul_packed", [_t(x), _t(packed)], i=(int(out_features),))
 
 

@@ -67,7 +67,7 @@ def random_weights(cfg: dict, seed: int = 42, std: float = 0.02) -> dict:
 CONV1D = (".attn.c_attn.weight", ".attn.c_proj.weight", ".mlp.c_fc.weight", ".mlp.c_proj.weight")
 
 
-def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None, packed=None) -> dict:
+def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None, packed=None, x3=None) -> dict:
     """Upload numpy weights; returns the model dict the forward pass takes.
 
     kmajor (default: on for fp16/bf16) stores the Conv1D projection weights
@@ -78,7 +78,10 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
     keeps every projection and the tied LM head in the skinny GEMM's packed
     layout (gpu.pack_weight) for calls with at most 16 token rows: one more
     copy of the weights (HBM is plentiful), read with contiguous 1 KB wave
-    loads during decode."""
+    loads during decode.  x3 (fp32 with n_embd a multiple of 16; off by
+    default) keeps every fp32 projection weight split once into bf16 hi/lo
+    MFMA fragments (gpu.pack_weight_x3), which the fp32 GEMMs of the forward
+    read instead of splitting the weights on every call."""
     gpu.init_backend()
     if kmajor is None:
         kmajor = dtype != "float32"
@@ -86,6 +89,10 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
         packed = kmajor
     if packed and (dtype == "float32" or not kmajor):
         raise ValueError("packed decode weights need fp16/bf16 k-major weights")
+    if x3 is None:
+        x3 = False
+    if x3 and (dtype != "float32" or kmajor or cfg["n_embd"] % 16 != 0):
+        raise ValueError("fp32-packed weights need fp32 [in, out] weights with n_embd a multiple of 16")
     w = {}
     for k, v in np_weights.items():
         a = np.asarray(v, dtype=np.float32)
@@ -102,15 +109,23 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
             if k.endswith(CONV1D) or k == "transformer.wte.weight":
                 p = gpu.pack_weight(t)
                 p.eval()
-                pk[k] = (p, t.shape[0])
-    return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor), "packed": pk}
+                pk[k] = (p, t.shape[0], "rows16")
+    if x3:
+        for k, t in w.items():
+            if k.endswith(CONV1D):
+                p = gpu.pack_weight_x3(t)
+                p.eval()
+                pk[k] = (p, t.shape[1], "x3")
+    return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor), "packed": pk,
+            "x3": bool(x3)}
 
 
 def _mm(model: dict, x, name: str, rows: int = None):
     """x @ W for a Conv1D weight (HF layout [in, out]) or x @ wte^T, whichever
-    way the weight is stored; calls with at most 16 rows use the packed copy."""
+    way the weight is stored; fp32 weights use their hi/lo packed copy, and
+    16-bit ones their decode-packed copy for calls with at most 16 rows."""
     pk = model.get("packed", {}).get(name)
-    if pk is not None and rows is not None and rows <= 16:
+    if pk is not None and (pk[2] == "x3" or (rows is not None and rows <= 16)):
         return gpu.matmul_packed(x, pk[0], pk[1])
     w = model["weights"][name]
     if name == "transformer.wte.weight":
@@ -153,9 +168,8 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
     for i in range(L):
         p = f"transformer.h.{i}"
         h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
-        if not cached and not need_cache and not model.get("kmajor"):
-            # projection + head split + causal attention in one op: the
-            # attention kernel reads the projection's partial sums directly
+        if not cached and not need_cache and not model.get("kmajor") and not model.get("x3"):
+            # projection + head split + causal attention in one op
             a = gpu.qkv_attention(h, w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"], H, causal=True)
         else:
             qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])

@@ -33,7 +33,7 @@ enum Op : int {
   OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
   OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD, OP_QKV_ATTENTION,
   OP_LAYER_NORM_BACKWARD, OP_LAYER_NORM_GRADS, OP_GELU_BACKWARD, OP_GELU_TANH_BACKWARD, OP_GELU_EXACT_BACKWARD,
-  OP_EMBEDDING_BACKWARD,
+  OP_EMBEDDING_BACKWARD, OP_PACK_WEIGHT_X3,
   OP_COUNT
 };
 
@@ -53,7 +53,7 @@ static const char* kNames[OP_COUNT] = {
     "decode_attention", "pack_weight", "matmul_packed",
     "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad", "qkv_attention",
     "layer_norm_backward", "layer_norm_grads", "gelu_backward", "gelu_tanh_backward", "gelu_exact_backward",
-    "embedding_backward",
+    "embedding_backward", "pack_weight_x3",
 };
 
 int op_code(const char* name) {
@@ -220,6 +220,7 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       need(in, 4, code);
       return {decode_attention(in[0], in[1], in[2], in[3])};
     case OP_PACK_WEIGHT: need(in, 1, code); return {pack_weight(in[0])};
+    case OP_PACK_WEIGHT_X3: need(in, 1, code); return {pack_weight_x3(in[0])};
     case OP_MATMUL_PACKED: need(in, 2, code); return {matmul_packed(in[0], in[1], ip(iv, 0, code))};
     case OP_SGD_MATMUL:
       need(in, 3, code);
@@ -468,8 +469,13 @@ void eval_all(const std::vector<TensorP>& roots) {
         // reader of an earlier group, holds one more reference to it)
         int paired = 0;
         for (auto& kv : post_ln) paired += kv.second.get() == la.get();
-        if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 && la->dtype != DType::F32 &&
-            la->shape[0] <= 16 && is_single_internal_use(la, uses, paired)) {
+        // (and fp32 GEMMs with hi/lo-packed weights whose plan reads whole
+        // rows: the row-panel kernel normalises its A rows in its prologue)
+        const bool x3_fold = x->node->code == OP_MATMUL_PACKED && ops::is_x3_packed(x->node->in[1]) &&
+                             la->dtype == DType::F32 &&
+                             k::gemm_x3_ln_ok(la->shape[0], x->node->iv[0], la->shape[1]);
+        if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 &&
+            ((la->dtype != DType::F32 && la->shape[0] <= 16) || x3_fold) && is_single_internal_use(la, uses, paired)) {
           for (auto pit = post_ln.begin(); pit != post_ln.end(); ++pit)
             if (pit->second.get() == la.get()) {  // normalised in this GEMM's prologue instead
               post_ln.erase(pit);
@@ -640,12 +646,13 @@ void eval_all(const std::vector<TensorP>& roots) {
       e.ln_eps = g.ln_eps;
       auto pit = post_ln.find(t.get());
       TensorP lnt = pit != post_ln.end() && pit->second->pending() ? pit->second : nullptr;
-      if (lnt && g.packed_n == 0) {
+      if (lnt && (g.packed_n == 0 || ops::is_x3_packed(g.b))) {
         ops::PostLn pl;
         pl.gamma = lnt->node->in[1];
         pl.beta = lnt->node->in[2];
         pl.eps = lnt->node->f.empty() ? 1e-5f : (float)lnt->node->f[0];
-        res = {ops::matmul(g.a, g.b, false, false, &e, nullptr, &pl)};
+        res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e, &pl)
+                              : ops::matmul(g.a, g.b, false, false, &e, nullptr, &pl)};
         assign(lnt, pl.y);
         g_stats.launches_saved++;
       } else {

@@ -178,6 +178,9 @@ struct Gemm {
   float ln_eps = 1e-5f;
   // B in the skinny kernel's packed layout (pack_weights), 16-bit, M <= 16
   bool b_packed = false;
+  // fp32 B split ahead of time into bf16 hi/lo MFMA fragments
+  // (pack_weights_x3); A fp32 with unit k stride, K % 16 == 0, one batch
+  bool b_x3 = false;
   // split-K launches leave the partial sums in the workspace (the caller
   // consumes them) instead of reducing them into C
   bool no_reduce = false;
@@ -188,6 +191,30 @@ struct Gemm {
   void* pln_y = nullptr;
   float pln_eps = 1e-5f;
 };
+// fp32 weights packed for the bf16x3 MFMA GEMM of few-row activations
+// (gemm_x3p.hip): B(k, n) read through strides (b_sk, b_sn) is split into
+// bf16 hi/lo and stored in the B-operand order of v_mfma_f32_32x32x16_bf16,
+// zero-padded to whole 32-column strips and 16-deep k steps
+// (packed_x3_elems bf16 elements).
+int64_t packed_x3_elems(int64_t K, int64_t N);
+void pack_weights_x3(const void* b, int64_t b_sk, int64_t b_sn, int64_t K, int64_t N, void* out, hipStream_t s);
+// Launch plan of the packed-weight GEMM: 128-row tiles, 64 (wide) or 32
+// columns, kt 16-deep k steps per block and K split `splits` ways.
+// rows: one 32 x 32 block per output tile over the whole K (K = 64 kpw, kpw
+// 4, 8, 12 or 16), no split and an optional layer_norm of A in the prologue.
+struct X3Plan {
+  bool rows = false;
+  int kpw = 0;
+  bool wide = true;
+  int64_t tiles_m = 0, tiles_n = 0;
+  int kt = 1, splits = 1;
+};
+X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus);
+// Whether the packed-weight GEMM of this shape normalises its A rows in its
+// prologue (the row-panel plan).
+bool gemm_x3_ln_ok(int64_t M, int64_t N, int64_t K);
+// Whether a packed-weight GEMM can take this A operand and problem.
+bool gemm_x3_ok(const Gemm& g);
 // Whether the launch ends in a split-K reduction that can also produce
 // layer_norm(C) (one batch, N <= 2048); otherwise the caller runs layer_norm.
 bool gemm_post_ln_fused(const Gemm& g);

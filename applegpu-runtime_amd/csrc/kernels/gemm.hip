@@ -345,8 +345,126 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
   }
 }
 
+// splitk_reduce_ln for more than 8 splits: one 4-wavefront block per row.
+// Wave w sums splits [w q, (w + 1) q) in order (q = ceil(splits / 4), all
+// its loads issued first), the four sums meet in LDS and wave 0 adds them in
+// wave order, then finishes as splitk_reduce_ln does (epilogue, store,
+// layer_norm of the stored row).  The order is fixed, so repeated launches
+// give identical bits.
+template <typename T, int NV, int MQ>  // MQ: splits per wave loaded up front
+__global__ void __launch_bounds__(256) splitk_reduce_ln_mw(GArgs p) {
+  __shared__ float sum_w[3][NV * 256];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int64_t N = p.N, total = p.M * p.N;
+  const int ns = p.splits;
+  const int q = (ns + 3) / 4;
+  const int s0 = w * q, s1 = s0 + q < ns ? s0 + q : ns;
+  float part[NV][MQ][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    const int64_t cc = c < N ? c : 0;
+#pragma unroll
+    for (int j = 0; j < MQ; ++j) {
+      const int sp = s0 + j < s1 ? s0 + j : 0;
+      const float4 v = *(const float4*)(p.ws + (int64_t)sp * total + row * N + cc);
+      part[i][j][0] = v.x; part[i][j][1] = v.y; part[i][j][2] = v.z; part[i][j][3] = v.w;
+    }
+  }
+  float bias[NV][4] = {}, res[NV][4] = {}, msk[NV][4] = {}, gam[NV][4], bet[NV][4];
+  if (w == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 4;
+      const int64_t cc = c < N ? c : 0;
+      if (p.bias) ld4f<T>((const T*)p.bias + cc, bias[i]);
+      if (p.res) ld4f<T>((const T*)p.res + row * p.r_sm + cc, res[i]);
+      if (p.mask) ld4f<T>((const T*)p.mask + row * p.k_sm + cc, msk[i]);
+      ld4f<T>((const T*)p.pln_g + cc, gam[i]);
+      ld4f<T>((const T*)p.pln_b + cc, bet[i]);
+    }
+  }
+  float acc[NV][4];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[i][e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < MQ; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][e] += s0 + j < s1 ? part[i][j][e] : 0.f;
+    for (int sp = s0 + MQ; sp < s1; ++sp)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[i][e] += c < N ? p.ws[(int64_t)sp * total + row * N + c + e] : 0.f;
+    if (w > 0) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum_w[w - 1][(i * 64 + lane) * 4 + e] = acc[i][e];
+    }
+  }
+  __syncthreads();
+  if (w > 0) return;
+  float v[NV][4];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float a = acc[i][e];
+#pragma unroll
+      for (int x = 0; x < 3; ++x) a += sum_w[x][(i * 64 + lane) * 4 + e];
+      float y = p.alpha * a;
+      if (p.bias) y += bias[i][e];
+      if (p.act == kActRelu) y = fmaxf(y, 0.f);
+      else if (p.act == kActGelu) y = gelu_tanh(y);
+      else if (p.act == kActGeluExact) y = 0.5f * y * (1.f + erff(y * 0.70710678118654752f));
+      if (p.res) y += res[i][e];
+      if (p.mask) y = msk[i][e] > 0.f ? y : 0.f;
+      o[e] = to_f(from_f<T>(y));  // the value as stored
+    }
+    if (c < N) st4<T>((T*)p.C + row * p.c_sm + c, o);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[i][e] = c < N ? o[e] : 0.f;
+      s += v[i][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)N;
+  float qq = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = c < N ? v[i][e] - mean : 0.f;
+      qq += d * d;
+    }
+  }
+  const float var = wave_sum(qq) / (float)N;
+  const float inv = 1.f / sqrtf(var + p.pln_eps);
+  T* y = (T*)p.pln_y + row * N;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = gam[i][e] * (v[i][e] - mean) * inv + bet[i][e];
+    if (c < N) st4<T>(y + c, o);
+  }
+}
+
 template <typename T, int NV>
 void launch_reduce_ln_nv(const GArgs& p, dim3 grid, dim3 block, hipStream_t s) {
+  if (p.splits > 8) {
+    // one 4-wave block per row
+    const dim3 g2((unsigned)p.M), b2(256);
+    if (p.splits <= 16) hipLaunchKernelGGL((splitk_reduce_ln_mw<T, NV, 4>), g2, b2, 0, s, p);
+    else hipLaunchKernelGGL((splitk_reduce_ln_mw<T, NV, 8>), g2, b2, 0, s, p);
+    return;
+  }
   if (p.splits <= 2) hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 2>), grid, block, 0, s, p);
   else if (p.splits <= 4) hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 4>), grid, block, 0, s, p);
   else hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 8>), grid, block, 0, s, p);
@@ -377,7 +495,7 @@ void launch_reduce_ln(const GArgs& p, hipStream_t s) {
 // residual and mask as vectors, all branch-free) and stores one vector.
 // Same sums in the same split order and the same epilogue arithmetic as
 // splitk_reduce.
-template <typename T, int MS>  // MS: partials loaded up front (the split count rounded up to 2, 4 or 8)
+template <typename T, int MS>  // MS: partials loaded up front (the split count rounded up to 2, 4, 8, 16 or 32)
 __global__ void __launch_bounds__(256) splitk_reduce_vec(GArgs p) {
   const int64_t total = p.M * p.N;
   const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
@@ -611,14 +729,21 @@ static bool reduce_vec_ok(const Gemm& g) {
          (!g.mask || g.k_sm % 4 == 0);
 }
 
+bool gemm_x3_ok(const Gemm& g) {
+  if (g.ln_gamma && (!g.ln_beta || !gemm_x3_ln_ok(g.M, g.N, g.K))) return false;
+  return g.b_x3 && g.dt == DType::F32 && g.batch == 1 && g.a_sk == 1 && g.K % 16 == 0 && g.K > 0 && al16(g.A) &&
+         (g.M == 1 || g.a_sm % 4 == 0) && al16(g.B) && !g.b_scale && g.c_sm == g.N;
+}
+
 int gemm_splits(const Gemm& g) {
+  if (g.b_x3) return x3_plan(g.M, g.N, g.K, cu_count()).splits;
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return 1;
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf ? pl.splits : 1;
 }
 
 bool gemm_post_ln_fused(const Gemm& g) {
-  if (skinny_plan(g, cu_count()).use || thin_kind(g)) return false;
+  if (!g.b_x3 && (skinny_plan(g, cu_count()).use || thin_kind(g))) return false;
   if (g.batch != 1 || g.N > 2048 || g.N % 4 != 0 || g.c_sm != g.N) return false;
   // four-element vector accesses of C, Y and the epilogue operands
   const uintptr_t al = 4 * dtype_size(g.dt) - 1;
@@ -626,6 +751,7 @@ bool gemm_post_ln_fused(const Gemm& g) {
   if (!ok(g.C) || !ok(g.bias) || !ok(g.residual) || !ok(g.mask) || !ok(g.pln_gamma) || !ok(g.pln_beta) ||
       !ok(g.pln_y) || (g.residual && g.r_sm % 4 != 0) || (g.mask && g.k_sm % 4 != 0))
     return false;
+  if (g.b_x3) return x3_plan(g.M, g.N, g.K, cu_count()).splits > 1;
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf && pl.splits > 1;
 }
@@ -661,6 +787,10 @@ const char* gemm_plan_name(const Gemm& g) {
 }
 
 size_t gemm_workspace_bytes(const Gemm& g) {
+  if (g.b_x3) {
+    const X3Plan xp = x3_plan(g.M, g.N, g.K, cu_count());
+    return xp.splits > 1 ? (size_t)xp.splits * g.M * g.N * sizeof(float) : 0;
+  }
   const SkinnyPlan sp = skinny_plan(g, cu_count());
   if (sp.use || thin_kind(g)) return 0;
   Plan pl = make_plan(g, cu_count());
@@ -668,8 +798,29 @@ size_t gemm_workspace_bytes(const Gemm& g) {
   return (size_t)pl.splits * g.batch * g.M * g.N * sizeof(float);
 }
 
+static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s);
+
 void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
+  if (g.b_x3) {
+    if (!gemm_x3_ok(g))
+      fail("gemm: packed fp32 weights need fp32 A with unit k stride and 16-byte aligned rows, K %% 16 == 0, "
+           "one batch and a contiguous output");
+    if (g.pln_y && !gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
+    const X3Plan xp = x3_plan(g.M, g.N, g.K, cu_count());
+    if (g.no_reduce && xp.splits < 2) fail("gemm: partial sums requested from a launch without a K split");
+    Plan one{};
+    one.bm = xp.rows ? 32 : 128;
+    one.bn = xp.rows || !xp.wide ? 32 : 64;
+    one.splits = xp.splits;
+    one.kps = xp.rows ? g.K : 16LL * xp.kt;
+    GArgs p = make_args(g, one);
+    p.ws = (float*)workspace;
+    if (xp.splits > 1 && !workspace) fail("gemm: split-K workspace missing");
+    gemm_x3p_launch(xp, p, s);
+    reduce_splits(g, p, s);
+    return;
+  }
   if (g.pln_y && !gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
   if (g.no_reduce && gemm_splits(g) < 2) fail("gemm: partial sums requested from a launch without a K split");
   const SkinnyPlan sp = skinny_plan(g, cu_count());
@@ -732,7 +883,13 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     else launch_mf_bf16(p, pl.cfg, ak, bk, fast, grid, s);
   }
   check_launch("gemm_mfma");
-  if (pl.splits > 1) {
+  reduce_splits(g, p, s);
+}
+
+// The split-K tail of a launch: partial sums in p.ws are reduced (in split
+// order) into C with the epilogue, and layer_norm(C) into Y when asked.
+static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s) {
+  if (p.splits > 1) {
     if (g.no_reduce) return;
     if (g.pln_y) {
       if (!gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
@@ -746,7 +903,9 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
       AGPU_FLOAT_SWITCH(g.dt, {
         if (p.splits <= 2) hipLaunchKernelGGL((splitk_reduce_vec<T, 2>), rgrid, dim3(256), 0, s, p);
         else if (p.splits <= 4) hipLaunchKernelGGL((splitk_reduce_vec<T, 4>), rgrid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((splitk_reduce_vec<T, 8>), rgrid, dim3(256), 0, s, p);
+        else if (p.splits <= 8) hipLaunchKernelGGL((splitk_reduce_vec<T, 8>), rgrid, dim3(256), 0, s, p);
+        else if (p.splits <= 16) hipLaunchKernelGGL((splitk_reduce_vec<T, 16>), rgrid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((splitk_reduce_vec<T, 32>), rgrid, dim3(256), 0, s, p);
       });
       check_launch("splitk_reduce");
       return;

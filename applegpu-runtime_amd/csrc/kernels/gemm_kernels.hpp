@@ -822,6 +822,10 @@ enum { kThinNone = 0, kThinN1, kThinM1, kThinK1 };
 int thin_kind(const Gemm& g);
 void gemm_thin(int kind, DType dt, const GArgs& p, hipStream_t s);
 
+// The packed-weight bf16x3 GEMM (gemm_x3p.hip): partial sums into p.ws when
+// the plan splits K, else the epilogue into C.
+void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s);
+
 // Defined in gemm_mf_{f32,f16,bf16}_{fast,edge}.hip.
 void launch_mf_f32(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);
 void launch_mf_f16(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);

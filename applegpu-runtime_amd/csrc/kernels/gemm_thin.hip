@@ -72,7 +72,7 @@ __global__ void __launch_bounds__(256) outer_k1(GArgs p) {
 
 int thin_kind(const Gemm& g) {
   const bool fl = g.dt == DType::F32 || g.dt == DType::F16 || g.dt == DType::BF16;
-  if (!fl || g.b_dt != g.dt || g.b_scale || g.ln_gamma || g.b_packed || g.batch > 65535) return kThinNone;
+  if (!fl || g.b_dt != g.dt || g.b_scale || g.ln_gamma || g.b_packed || g.b_x3 || g.batch > 65535) return kThinNone;
   if (g.K == 1) return kThinK1;
   if (g.N == 1) return kThinN1;
   if (g.M == 1 && g.dt == DType::F32 && g.b_sn == 1) return kThinM1;

@@ -1054,7 +1054,85 @@ TensorP pack_weight(const TensorP& wt) {
   return out;
 }
 
-TensorP matmul_packed(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi) {
+TensorP pack_weight_x3(const TensorP& b) {
+  if (b->ndim != 2) fail("pack_weight_x3: weights must be 2-D [in, out] (the B operand of x @ B)");
+  if (b->dtype != DType::F32) fail("pack_weight_x3: fp32 weights only, got %s", dtype_name(b->dtype));
+  const int64_t K = b->shape[0], N = b->shape[1];
+  if (K % 16 != 0 || K == 0 || N == 0) fail("pack_weight_x3: the reduction dim %lld must be a positive multiple of 16", (long long)K);
+  TensorP out = alloc_out(DType::BF16, {(N + 31) / 32, K / 16, 2, 64, 8});
+  LAUNCH k::pack_weights_x3(b->data(), b->strides[0], b->strides[1], K, N, out->data(), rt().stream());
+  return out;
+}
+
+bool is_x3_packed(const TensorP& t) {
+  return t->ndim == 5 && t->dtype == DType::BF16 && t->shape[2] == 2 && t->shape[3] == 64 && t->shape[4] == 8;
+}
+
+static TensorP matmul_x3(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln) {
+  const char* name = "matmul_packed";
+  if (a_in->ndim != 2) fail("%s: activations must be 2-D [rows, in]", name);
+  if (a_in->dtype != DType::F32) fail("%s: fp32-packed weights take fp32 activations, got %s", name, dtype_name(a_in->dtype));
+  const int64_t M = a_in->shape[0], K = a_in->shape[1];
+  if (N < 1 || pw->shape[0] != (N + 31) / 32 || pw->shape[1] * 16 != K)
+    fail("%s: packed weights hold [%lld/32, %lld/16] fragments, not [in %lld, out %lld]", name,
+         (long long)pw->shape[0] * 32, (long long)pw->shape[1] * 16, (long long)K, (long long)N);
+  // a layer_norm of A runs in the row-panel kernel's prologue when the plan
+  // has one (fp32 gamma/beta [K]); otherwise as its own launch first
+  if (epi && epi->ln_gamma &&
+      !(k::gemm_x3_ln_ok(M, N, K) && epi->ln_beta && epi->ln_gamma->dtype == DType::F32 &&
+        epi->ln_beta->dtype == DType::F32 && epi->ln_gamma->numel() == K && epi->ln_beta->numel() == K)) {
+    Epilogue plain = *epi;
+    plain.ln_gamma = plain.ln_beta = nullptr;
+    return matmul_x3(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), pw, N, &plain, post_ln);
+  }
+  TensorP a = a_in;
+  if (!meta_mode() && (a->strides[1] != 1 || (M > 1 && a->strides[0] % 4 != 0) || ((uintptr_t)a->data() & 15)))
+    a = materialize(a);
+  TensorP pc = contiguous(pw);
+  const std::vector<int64_t> od{M, N};
+  TensorP out = alloc_out(DType::F32, od);
+  k::Gemm g;
+  g.dt = g.b_dt = DType::F32;
+  g.M = M; g.N = N; g.K = K; g.batch = 1;
+  g.A = a->data(); g.a_sm = M == 1 ? K : a->strides[0]; g.a_sk = 1;
+  g.B = pc->data(); g.b_x3 = true;
+  g.C = out->data(); g.c_sm = N; g.c_sb = M * N;
+  EpiKeep keep;
+  set_epilogue(g, epi, od, {}, &keep);
+  TensorP pl_g, pl_b;
+  bool pln_fused = false;
+  if (post_ln) {
+    if (!post_ln->gamma || !post_ln->beta || post_ln->gamma->dtype != g.dt || post_ln->beta->dtype != g.dt ||
+        post_ln->gamma->numel() != N || post_ln->beta->numel() != N)
+      fail("%s: layer_norm gamma and beta must be [%lld] of the output dtype", name, (long long)N);
+    pl_g = contiguous(post_ln->gamma);
+    pl_b = contiguous(post_ln->beta);
+    if (!meta_mode()) {
+      TensorP y = alloc_out(g.dt, od);
+      k::Gemm probe = g;
+      probe.pln_gamma = pl_g->data();
+      probe.pln_beta = pl_b->data();
+      probe.pln_y = y->data();
+      probe.pln_eps = post_ln->eps;
+      pln_fused = k::gemm_post_ln_fused(probe);
+      if (pln_fused) {
+        g = probe;
+        post_ln->y = y;
+      }
+    }
+  }
+  if (!meta_mode() && !k::gemm_x3_ok(g)) fail("%s: this product cannot use the packed fp32 weights", name);
+  const size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
+  BufferP ws;
+  if (wsb) ws = scratch(wsb);
+  LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
+  if (post_ln && !pln_fused) post_ln->y = layer_norm(out, pl_g, pl_b, post_ln->eps);
+  return out;
+}
+
+TensorP matmul_packed(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln) {
+  if (is_x3_packed(pw)) return matmul_x3(a_in, pw, N, epi, post_ln);
+  if (post_ln) fail("matmul_packed: layer_norm of the output needs the fp32 packed layout");
   const char* name = "matmul_packed";
   if (a_in->ndim != 2) fail("%s: activations must be 2-D [rows, in]", name);
   if (pw->ndim != 4 || pw->shape[2] != 64 || pw->shape[3] != 8) fail("%s: weights are not packed (pack_weight)", name);
@@ -1190,11 +1268,17 @@ TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool ca
 TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int64_t n_head, bool causal,
                       int64_t batch, bool read_partials) {
   const char* name = "qkv_attention";
-  if (x->ndim != 2 || w->ndim != 2 || b->ndim != 1) fail("%s: x [B*T, K], w [K, 3d] and b [3d] expected", name);
+  // w is [K, 3d], or the same weights packed by pack_weight_x3 (fp32)
+  const bool x3 = is_x3_packed(w);
+  if (x->ndim != 2 || (w->ndim != 2 && !x3) || b->ndim != 1)
+    fail("%s: x [B*T, K], w [K, 3d] (or its pack_weight_x3 packing) and b [3d] expected", name);
   check_dtype(name, kFloatOnly, x->dtype);
-  if (w->dtype != x->dtype || b->dtype != x->dtype) fail("%s: dtypes differ", name);
-  const int64_t R = x->shape[0], K = x->shape[1], N = w->shape[1];
-  if (w->shape[0] != K || b->numel() != N || N % 3 != 0) fail("%s: w must be [%lld, 3d] and b [3d]", name, (long long)K);
+  if ((!x3 && w->dtype != x->dtype) || b->dtype != x->dtype || (x3 && x->dtype != DType::F32))
+    fail("%s: dtypes differ", name);
+  const int64_t R = x->shape[0], K = x->shape[1], N = x3 ? b->numel() : w->shape[1];
+  if ((x3 ? (w->shape[0] != (N + 31) / 32 || w->shape[1] * 16 != K) : w->shape[0] != K) || b->numel() != N ||
+      N % 3 != 0)
+    fail("%s: w must be [%lld, 3d] and b [3d]", name, (long long)K);
   const int64_t d = N / 3;
   if (n_head <= 0 || d % n_head != 0) fail("%s: %lld columns do not split into %lld heads", name, (long long)d,
                                            (long long)n_head);
@@ -1206,7 +1290,7 @@ TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int6
   auto composed = [&]() {
     Epilogue e;
     e.bias = b;
-    TensorP qkv = matmul(x, w, false, false, &e);
+    TensorP qkv = x3 ? matmul_packed(x, w, N, &e) : matmul(x, w, false, false, &e);
     auto heads = [&](int64_t lo) {
       TensorP part = slice(qkv, 1, lo, lo + d);
       return transpose_dims(reshape(part, {batch, T, n_head, hd}), 1, 2);
@@ -1216,16 +1300,24 @@ TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int6
   };
   if (meta_mode() || !read_partials || x->dtype != DType::F32) return composed();
 
-  TensorP xc = x->strides[1] == 1 ? x : contiguous(x);
-  TensorP wc = w->strides[1] == 1 ? w : contiguous(w);
+  TensorP xc = x;
+  if (x->strides[1] != 1 || (x3 && ((R > 1 && x->strides[0] % 4 != 0) || ((uintptr_t)x->data() & 15))))
+    xc = materialize(x);
+  TensorP wc = x3 || w->strides[1] == 1 ? w : contiguous(w);
   TensorP bc = contiguous(b);
   k::Gemm g;
   g.dt = g.b_dt = DType::F32;
   g.M = R; g.N = N; g.K = K; g.batch = 1;
-  g.A = xc->data(); g.a_sm = xc->strides[0]; g.a_sk = 1; g.a_sb = R * K;
-  g.B = wc->data(); g.b_sk = wc->strides[0]; g.b_sn = 1; g.b_sb = K * N;
+  g.A = xc->data(); g.a_sm = R == 1 ? K : xc->strides[0]; g.a_sk = 1; g.a_sb = R * K;
+  g.B = wc->data();
+  if (x3) {
+    g.b_x3 = true;
+  } else {
+    g.b_sk = wc->strides[0]; g.b_sn = 1; g.b_sb = K * N;
+  }
   g.C = nullptr; g.c_sm = N; g.c_sb = R * N;
   g.no_reduce = true;
+  if (x3 && !k::gemm_x3_ok(g)) return composed();
   const int splits = k::gemm_splits(g);
   k::Attn a;
   a.dt = DType::F32;

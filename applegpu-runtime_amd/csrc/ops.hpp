@@ -116,7 +116,17 @@ std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b);
 // GEMM (the operands of one wave instruction contiguous), and x [M <= 16, K]
 // times it: out [M, N] = epilogue(x @ wt^T).
 TensorP pack_weight(const TensorP& wt);
-TensorP matmul_packed(const TensorP& x, const TensorP& packed, int64_t N, const Epilogue* epi = nullptr);
+// fp32 weights for few-row activations: b is the B operand [K, N] of x @ b
+// (any strides), split into bf16 hi/lo and rearranged as MFMA fragments
+// (k::pack_weights_x3): a BF16 tensor [N/32, K/16, 2, 64, 8].
+TensorP pack_weight_x3(const TensorP& b);
+bool is_x3_packed(const TensorP& t);
+// x times packed weights: the 16-bit decode layout (pack_weight, at most 16
+// rows) or the fp32 hi/lo layout (pack_weight_x3, any rows), with the
+// epilogue and, for the fp32 layout, layer_norm of the output computed in the
+// split-K reduction.
+TensorP matmul_packed(const TensorP& x, const TensorP& packed, int64_t N, const Epilogue* epi = nullptr,
+                      PostLn* post_ln = nullptr);
 // int8 weights with per-row scales (out = x @ (q * scale[:,None])^T)
 TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
 

@@ -35,6 +35,22 @@ def test_captured_c2_forward_full_size_vs_oracle(gpu):
     wnp = G.random_weights(GPT2_SMALL, seed=42)
     model = G.load_model(wnp, GPT2_SMALL)
     ids = np.random.default_rng(42).integers(0, GPT2_SMALL["vocab_size"], 128).astype(np.int32)
+    _check_c2_graph(gpu, G, model, wnp, ids)
+
+
+def test_captured_c2_forward_packed_weights_vs_oracle(gpu):
+    """The same graph with the fp32 projection weights packed as bf16 hi/lo
+    fragments (load_model(x3=True)): the row-panel GEMMs with layer_norm in
+    their prologue and the packed split-K GEMM."""
+    from applegpu_runtime.models import gpt2 as G
+    print("C2 captured forward, packed fp32 weights", flush=True)
+    wnp = G.random_weights(GPT2_SMALL, seed=42)
+    model = G.load_model(wnp, GPT2_SMALL, x3=True)
+    ids = np.random.default_rng(42).integers(0, GPT2_SMALL["vocab_size"], 128).astype(np.int32)
+    _check_c2_graph(gpu, G, model, wnp, ids)
+
+
+def _check_c2_graph(gpu, G, model, wnp, ids):
     idx = gpu.from_numpy(ids)
     pos = gpu.from_numpy(np.arange(128, dtype=np.int32))
     graph = gpu.capture(lambda: G.gpt2_forward(model, idx, positions=pos, need_cache=False)[0])

@@ -1,0 +1,170 @@
+"""fp32 GEMM against weights packed once into bf16 hi/lo MFMA fragments
+(pack_weight_x3 + matmul_packed): the packed bits against a numpy
+restatement of the layout, products against the float64 oracle at the fp32
+matmul bar (1e-3, checked at 1e-4), and the graph's epilogue and layer_norm
+fusions on the packed path.  The reference computes these products with
+MPSMatrixMultiplication (swift/Sources/AppleGPUBridge/compute.swift:1544-1630)
+and its GPT-2 recipe multiplies x @ W for HF Conv1D weights
+(python/applegpu_runtime/models/gpt2.py:106-107)."""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from oracle import ops as O
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(31337)
+
+
+def f32(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def _bf16_rne_bits(x):
+    """bf16 bits of x rounded to nearest even (finite inputs)."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF).astype(np.uint16)
+
+
+def _bits_to_f32(b):
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def _bits_of(t):
+    """bf16 bits of a BF16 device tensor (read back as float32, exactly)."""
+    return (np.asarray(t.to_numpy(), np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def _packed_ref(b):
+    """Element ((s T + t) 2 + h) 512 + 8 l + j = part h of B(16 t + 8 (l // 32) + j, 32 s + l % 32)."""
+    K, N = b.shape
+    S, T = (N + 31) // 32, K // 16
+    hi = _bf16_rne_bits(b)
+    lo = _bf16_rne_bits(b - _bits_to_f32(hi))
+    out = np.zeros((S, T, 2, 64, 8), np.uint16)
+    for s in range(S):
+        for t in range(T):
+            for lane in range(64):
+                n = 32 * s + lane % 32
+                if n >= N:
+                    continue
+                k0 = 16 * t + 8 * (lane // 32)
+                out[s, t, 0, lane] = hi[k0:k0 + 8, n]
+                out[s, t, 1, lane] = lo[k0:k0 + 8, n]
+    return out
+
+
+def test_packed_layout_bit_exact(gpu):
+    b = f32(48, 70)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(b))
+    assert pk.shape == [3, 3, 2, 64, 8]
+    np.testing.assert_array_equal(_bits_of(pk), _packed_ref(b))
+    # hi + lo reconstructs b to within the dropped lo rounding (2^-16 relative)
+    hl = _bits_to_f32(_packed_ref(b)[:, :, 0]) + _bits_to_f32(_packed_ref(b)[:, :, 1])
+    assert np.isfinite(hl).all()
+
+
+def test_packed_layout_of_a_transposed_view(gpu):
+    """torch Linear weights [out, in]: B = W^T read through strides."""
+    w = f32(40, 32)
+    pk = gpu.pack_weight_x3(gpu.transpose(gpu.from_numpy(w)))
+    np.testing.assert_array_equal(_bits_of(pk), _packed_ref(np.ascontiguousarray(w.T)))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 16, 32), (5, 64, 70), (33, 48, 1536), (128, 768, 2304), (128, 768, 768),
+                                   (128, 3072, 768), (128, 768, 3072), (200, 256, 100), (256, 768, 2304)])
+def test_matmul_matches_oracle(gpu, M, K, N):
+    a, b = f32(M, K), f32(K, N, scale=0.05)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(b))
+    got = gpu.matmul_packed(gpu.from_numpy(a), pk, N).to_numpy()
+    assert got.shape == (M, N)
+    assert rel_err(got, O.matmul(a, b)) < 1e-4
+
+
+def test_exact_small_integers(gpu):
+    """Integers of a few bits are exact in bf16 hi alone: any fragment
+    mapping error shows as a wrong integer."""
+    a = RNG.integers(-3, 4, (130, 64)).astype(np.float32)
+    b = RNG.integers(-3, 4, (64, 96)).astype(np.float32)
+    got = gpu.matmul_packed(gpu.from_numpy(a), gpu.pack_weight_x3(gpu.from_numpy(b)), 96).to_numpy()
+    np.testing.assert_array_equal(got, a @ b)
+
+
+def test_strided_activations(gpu):
+    """A view with a row pitch that is not 16-byte aligned is copied first."""
+    base = f32(64, 70)
+    a = gpu.slice(gpu.from_numpy(base), 1, 3, 67)   # [64, 64], row pitch 70
+    b = f32(64, 96, scale=0.1)
+    got = gpu.matmul_packed(a, gpu.pack_weight_x3(gpu.from_numpy(b)), 96).to_numpy()
+    assert rel_err(got, O.matmul(base[:, 3:67], b)) < 1e-4
+
+
+def test_epilogues_and_layer_norm_through_the_graph(gpu):
+    """bias + gelu and bias + residual fuse into the packed GEMM's launch (or
+    its split-K reduction), and a layer_norm reading the residual sum is
+    computed by the reduction; results at the fp32 bars."""
+    M, K, N = 128, 768, 768
+    x, b, bias, r = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1), f32(M, N)
+    g, be = f32(N, scale=0.5) + 1.0, f32(N, scale=0.1)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(b))
+    before = gpu.graph_stats()
+    y = gpu.gelu(gpu.add_bias(gpu.matmul_packed(gpu.from_numpy(x), pk, N), gpu.from_numpy(bias)))
+    z = gpu.from_numpy(r) + gpu.add_bias(gpu.matmul_packed(gpu.from_numpy(x), pk, N), gpu.from_numpy(bias))
+    ln = gpu.layer_norm(z, gpu.from_numpy(g), gpu.from_numpy(be))
+    y_np, z_np, ln_np = y.to_numpy(), z.to_numpy(), ln.to_numpy()
+    after = gpu.graph_stats()
+    assert after["fused_gemm_epilogues"] - before["fused_gemm_epilogues"] == 2
+    ref = O.add_bias(O.matmul(x, b), bias)
+    assert rel_err(y_np, O.gelu_tanh(ref)) < 1e-4
+    assert rel_err(z_np, r + ref) < 1e-4
+    # the reduction's layer_norm equals layer_norm of the stored sum
+    np.testing.assert_allclose(ln_np, O.layer_norm(z_np, g, be), rtol=1e-5, atol=1e-5)
+
+
+def test_rejects_unsupported_operands(gpu):
+    with pytest.raises(ValueError, match="pack_weight_x3"):
+        gpu.pack_weight_x3(gpu.from_numpy(f32(40, 8))).eval()        # K not a multiple of 16
+    with pytest.raises(ValueError, match="pack_weight_x3"):
+        gpu.pack_weight_x3(gpu.cast(gpu.from_numpy(f32(32, 8)), "float16")).eval()
+    pk = gpu.pack_weight_x3(gpu.from_numpy(f32(32, 40)))
+    with pytest.raises(ValueError, match="matmul_packed"):
+        gpu.matmul_packed(gpu.from_numpy(f32(4, 48)), pk, 40).eval()  # K mismatch
+    with pytest.raises(ValueError, match="matmul_packed"):
+        gpu.matmul_packed(gpu.cast(gpu.from_numpy(f32(4, 32)), "float16"), pk, 40).eval()
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 768, 2304), (128, 768, 3072), (100, 256, 96), (33, 512, 64),
+                                   (128, 1024, 160), (1, 768, 768)])
+def test_layer_norm_folds_into_the_row_panel_prologue(gpu, M, K, N):
+    """layer_norm(x) @ W + b (+ gelu) for K of 256..1024: the row-panel
+    kernel normalises its rows itself, so the layer_norm costs no launch; the
+    result matches the oracle's layer_norm then product at the fp32 bar."""
+    x, b, bias = f32(M, K, scale=2.0) + 0.5, f32(K, N, scale=0.05), f32(N, scale=0.1)
+    g, be = f32(K, scale=0.5) + 1.0, f32(K, scale=0.1)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(b))
+    pk.eval()
+    xd, gd, bd, biasd = (gpu.from_numpy(a) for a in (x, g, be, bias))
+    for t in (xd, gd, bd, biasd):
+        t.eval()
+    y = gpu.gelu(gpu.add_bias(gpu.matmul_packed(gpu.layer_norm(xd, gd, bd), pk, N), biasd))
+    before = gpu.graph_stats()
+    got = y.to_numpy()
+    after = gpu.graph_stats()
+    assert after["launcher_calls"] - before["launcher_calls"] == 1
+    ref = O.gelu_tanh(O.add_bias(O.matmul(O.layer_norm(x, g, be), b), bias))
+    assert rel_err(got, ref) < 1e-4
+
+
+def test_row_panel_residual_epilogue_bitwise_stable(gpu):
+    """x + (a @ W + b) on the row-panel plan: at the fp32 bar, and identical
+    bits on a second evaluation (fixed summation order)."""
+    M, K, N = 128, 768, 768
+    a, b, bias, r = f32(M, K), f32(K, N, scale=0.05), f32(N), f32(M, N)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(b))
+    outs = []
+    for _ in range(2):
+        z = gpu.from_numpy(r) + gpu.add_bias(gpu.matmul_packed(gpu.from_numpy(a), pk, N), gpu.from_numpy(bias))
+        outs.append(z.to_numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    assert rel_err(outs[0], r + O.add_bias(O.matmul(a, b), bias)) < 1e-4
