@@ -576,6 +576,23 @@ def matmul_packed(x, packed, out_features):
     return _op(b"matmul_packed", [_t(x), _t(packed)], i=(int(out_features),))
 
 
+def pack_rows_x3(x):
+    """fp32 activations x [rows, cols] (cols a multiple of 16) split into
+    bf16 hi/lo MFMA A-operand fragments: [ceil(rows/32), cols/16, 2, 64, 8]
+    bfloat16.  Use with matmul_pp(packed_rows, rows, packed_weights, out).
+    Inside a lazy graph the producer of x (a packed-weight GEMM's epilogue,
+    a split-K reduction computing layer_norm, the fused embedding) writes the
+    packed rows directly."""
+    return _op(b"pack_rows_x3", [_t(x)])
+
+
+def matmul_pp(packed_rows, rows, packed, out_features):
+    """x @ b with both operands packed: packed_rows = pack_rows_x3(x) for x
+    [rows, in], packed = pack_weight_x3(b) for b [in, out]; fp32 result
+    [rows, out]."""
+    return _op(b"matmul_pp", [_t(packed_rows), _t(packed)], i=(int(rows), int(out_features)))
+
+
 def linear_int8(x, q, scale):
     """x @ (q * scale[:, None])^T with the dequantisation fused into the GEMM."""
     return _op(b"linear_int8", [_t(x), _t(q), _t(scale)])

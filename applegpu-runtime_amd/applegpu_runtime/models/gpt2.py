@@ -78,10 +78,12 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
     keeps every projection and the tied LM head in the skinny GEMM's packed
     layout (gpu.pack_weight) for calls with at most 16 token rows: one more
     copy of the weights (HBM is plentiful), read with contiguous 1 KB wave
-    loads during decode.  x3 (fp32 with n_embd a multiple of 16; off by
-    default) keeps every fp32 projection weight split once into bf16 hi/lo
-    MFMA fragments (gpu.pack_weight_x3), which the fp32 GEMMs of the forward
-    read instead of splitting the weights on every call."""
+    loads during decode.  x3 (default: on for fp32 [in, out] weights with
+    n_embd a multiple of 16) keeps every fp32 projection weight split once
+    into bf16 hi/lo MFMA fragments (gpu.pack_weight_x3), which the fp32 GEMMs
+    of the forward read instead of splitting the weights on every call; the
+    forward then also passes the activations after each layer_norm and gelu
+    as packed rows (gpu.pack_rows_x3), written by their producers."""
     gpu.init_backend()
     if kmajor is None:
         kmajor = dtype != "float32"
@@ -90,7 +92,7 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
     if packed and (dtype == "float32" or not kmajor):
         raise ValueError("packed decode weights need fp16/bf16 k-major weights")
     if x3 is None:
-        x3 = False
+        x3 = dtype == "float32" and not kmajor and cfg["n_embd"] % 16 == 0
     if x3 and (dtype != "float32" or kmajor or cfg["n_embd"] % 16 != 0):
         raise ValueError("fp32-packed weights need fp32 [in, out] weights with n_embd a multiple of 16")
     w = {}
@@ -133,6 +135,16 @@ def _mm(model: dict, x, name: str, rows: int = None):
     return x @ (gpu.transpose(w) if model.get("kmajor") else w)
 
 
+def _mm_rows(model: dict, x, name: str, rows: int):
+    """x @ W for an fp32 packed-weight model with x split into MFMA row
+    fragments first (gpu.pack_rows_x3): inside the lazy graph, x's producer
+    (the fused embedding or a split-K reduction computing layer_norm, or the
+    GEMM epilogue computing gelu) writes the fragments itself, so the product
+    reads both operands without conversion."""
+    pk = model["packed"][name]
+    return gpu.matmul_pp(gpu.pack_rows_x3(x), rows, pk[0], pk[1])
+
+
 def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cache=True):
     """Returns (logits [seq, vocab], new_kv_cache) for one sequence.
 
@@ -164,6 +176,10 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
         pos = gpu.from_numpy(np.arange(start, start + T, dtype=np.int32))
     x = gpu.embedding(w["transformer.wte.weight"], idx) + gpu.embedding(w["transformer.wpe.weight"], pos)
 
+    # fp32 packed-weight models: the projections that follow a layer_norm or
+    # gelu take their activations as packed rows
+    rows = model.get("x3", False)
+    mm_in = (lambda t, name: _mm_rows(model, t, name, T)) if rows else (lambda t, name: _mm(model, t, name))
     new_cache = []
     for i in range(L):
         p = f"transformer.h.{i}"
@@ -172,7 +188,7 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
             # projection + head split + causal attention in one op
             a = gpu.qkv_attention(h, w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"], H, causal=True)
         else:
-            qkv = gpu.add_bias(_mm(model, h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
+            qkv = gpu.add_bias(mm_in(h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
 
             def heads(lo):
                 part = gpu.slice(qkv, 1, lo, lo + d)
@@ -189,8 +205,8 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
         x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
 
         h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
-        f = gpu.gelu(gpu.add_bias(_mm(model, h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
-        x = x + gpu.add_bias(_mm(model, f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
+        f = gpu.gelu(gpu.add_bias(mm_in(h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
+        x = x + gpu.add_bias(mm_in(f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
 
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
     logits = x @ gpu.transpose(w["transformer.wte.weight"])

@@ -33,7 +33,7 @@ enum Op : int {
   OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
   OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD, OP_QKV_ATTENTION,
   OP_LAYER_NORM_BACKWARD, OP_LAYER_NORM_GRADS, OP_GELU_BACKWARD, OP_GELU_TANH_BACKWARD, OP_GELU_EXACT_BACKWARD,
-  OP_EMBEDDING_BACKWARD, OP_PACK_WEIGHT_X3,
+  OP_EMBEDDING_BACKWARD, OP_PACK_WEIGHT_X3, OP_PACK_ROWS_X3, OP_MATMUL_PP,
   OP_COUNT
 };
 
@@ -53,7 +53,7 @@ static const char* kNames[OP_COUNT] = {
     "decode_attention", "pack_weight", "matmul_packed",
     "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad", "qkv_attention",
     "layer_norm_backward", "layer_norm_grads", "gelu_backward", "gelu_tanh_backward", "gelu_exact_backward",
-    "embedding_backward", "pack_weight_x3",
+    "embedding_backward", "pack_weight_x3", "pack_rows_x3", "matmul_pp",
 };
 
 int op_code(const char* name) {
@@ -222,6 +222,8 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
     case OP_PACK_WEIGHT: need(in, 1, code); return {pack_weight(in[0])};
     case OP_PACK_WEIGHT_X3: need(in, 1, code); return {pack_weight_x3(in[0])};
     case OP_MATMUL_PACKED: need(in, 2, code); return {matmul_packed(in[0], in[1], ip(iv, 0, code))};
+    case OP_PACK_ROWS_X3: need(in, 1, code); return {pack_rows_x3(in[0])};
+    case OP_MATMUL_PP: need(in, 2, code); return {matmul_pp(in[0], ip(iv, 0, code), in[1], ip(iv, 1, code))};
     case OP_SGD_MATMUL:
       need(in, 3, code);
       return {sgd_matmul_(in[0], in[1], in[2], iv.size() > 0 && iv[0], iv.size() > 1 && iv[1], (float)fp(f, 0, code))};
@@ -320,6 +322,7 @@ struct Group {
   TensorP ln_gamma, ln_beta;  // a = layer_norm(a) folded into the GEMM
   float ln_eps = 1e-5f;
   int64_t packed_n = 0;       // b is packed decode weights of this many columns
+  int64_t a_rows = -1;        // a is packed x3 rows of this many rows (matmul_pp)
 };
 
 // An elementwise chain planned for one fused_chain launch.
@@ -450,15 +453,21 @@ void eval_all(const std::vector<TensorP>& roots) {
   std::unordered_set<Tensor*> absorbed;
   std::unordered_map<Tensor*, TensorP> post_ln;  // group final node (or embedding sum) -> layer_norm reading it
   std::unordered_set<Tensor*> emb_adds;            // embedding + embedding nodes run as one kernel
+  std::unordered_map<Tensor*, TensorP> pack_of;    // group final node or paired layer_norm -> pack_rows_x3 of it
   for (auto& t : order) {
     Node* n = t->node.get();
     if (n->code == OP_ADD_BIAS && t->ndim == 2) {
       const TensorP& x = n->in[0];
-      if (x->pending() && (x->node->code == OP_MATMUL || x->node->code == OP_MATMUL_PACKED) && x->ndim == 2 &&
-          is_single_internal_use(x, uses) && n->in[1]->ndim == 1) {
+      if (x->pending() &&
+          (x->node->code == OP_MATMUL || x->node->code == OP_MATMUL_PACKED || x->node->code == OP_MATMUL_PP) &&
+          x->ndim == 2 && is_single_internal_use(x, uses) && n->in[1]->ndim == 1) {
         Group g;
         g.mm = x.get();
         if (x->node->code == OP_MATMUL_PACKED) g.packed_n = x->node->iv[0];
+        if (x->node->code == OP_MATMUL_PP) {
+          g.a_rows = x->node->iv[0];
+          g.packed_n = x->node->iv[1];
+        }
         // layer_norm -> matmul: the GEMM normalises its A rows itself when
         // its kernel can (ops::matmul falls back to an explicit layer_norm)
         const TensorP& la = x->node->in[0];
@@ -474,7 +483,7 @@ void eval_all(const std::vector<TensorP>& roots) {
         const bool x3_fold = x->node->code == OP_MATMUL_PACKED && ops::is_x3_packed(x->node->in[1]) &&
                              la->dtype == DType::F32 &&
                              k::gemm_x3_ln_ok(la->shape[0], x->node->iv[0], la->shape[1]);
-        if (la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 &&
+        if (g.a_rows < 0 && la->pending() && la->node->code == OP_LAYER_NORM && la->ndim == 2 &&
             ((la->dtype != DType::F32 && la->shape[0] <= 16) || x3_fold) && is_single_internal_use(la, uses, paired)) {
           for (auto pit = post_ln.begin(); pit != post_ln.end(); ++pit)
             if (pit->second.get() == la.get()) {  // normalised in this GEMM's prologue instead
@@ -505,6 +514,25 @@ void eval_all(const std::vector<TensorP>& roots) {
         groups.erase(it);
         absorbed.insert(x.get());
         groups[t.get()] = g;
+      }
+    } else if (n->code == OP_PACK_ROWS_X3) {
+      // Packed rows written by their producer: a packed-weight GEMM group's
+      // row-panel epilogue, or the split-K reduction (or fused embedding)
+      // that computes the layer_norm being packed.  The fp32 matrix is then
+      // never stored.
+      const TensorP& x = n->in[0];
+      if (!x->pending() || x->dtype != DType::F32 || x->ndim != 2 || x->shape[1] % 16 != 0) continue;
+      auto git = groups.find(x.get());
+      if (git != groups.end() && git->second.packed_n > 0 && ops::is_x3_packed(git->second.b) &&
+          !post_ln.count(x.get()) && is_single_internal_use(x, uses)) {
+        pack_of[x.get()] = t;
+        continue;
+      }
+      int paired = 0;
+      for (auto& kv : post_ln) paired += kv.second.get() == x.get();
+      if (paired == 1 && x->node->code == OP_LAYER_NORM && is_single_internal_use(x, uses, 1)) {
+        pack_of[x.get()] = t;
+        absorbed.insert(x.get());
       }
     } else if (n->code == OP_LAYER_NORM && t->ndim == 2) {
       const TensorP& x = n->in[0];
@@ -646,17 +674,44 @@ void eval_all(const std::vector<TensorP>& roots) {
       e.ln_eps = g.ln_eps;
       auto pit = post_ln.find(t.get());
       TensorP lnt = pit != post_ln.end() && pit->second->pending() ? pit->second : nullptr;
-      if (lnt && (g.packed_n == 0 || ops::is_x3_packed(g.b))) {
+      const bool x3 = g.packed_n > 0 && ops::is_x3_packed(g.b);
+      auto packed_product = [&](ops::PostLn* pl, ops::PackOut* po) {
+        return g.a_rows >= 0 ? ops::matmul_pp(g.a, g.a_rows, g.b, g.packed_n, &e, pl, po)
+                             : ops::matmul_packed(g.a, g.b, g.packed_n, &e, pl, po);
+      };
+      auto pk = pack_of.find(t.get());
+      if (pk != pack_of.end() && x3) {
+        // only the packed rows are wanted
+        ops::PackOut po;
+        po.want_c = false;
+        packed_product(nullptr, &po);
+        assign(pk->second, po.pk);
+        g_stats.fused_gemm_epilogues++;
+        g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0) + 1;
+        order[i].reset();
+        continue;
+      }
+      if (lnt && (g.packed_n == 0 || x3)) {
         ops::PostLn pl;
         pl.gamma = lnt->node->in[1];
         pl.beta = lnt->node->in[2];
         pl.eps = lnt->node->f.empty() ? 1e-5f : (float)lnt->node->f[0];
-        res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e, &pl)
+        auto lp = pack_of.find(lnt.get());
+        if (lp != pack_of.end() && x3) {
+          pl.want_y = false;
+          pl.want_pk = true;
+        }
+        res = {g.packed_n > 0 ? packed_product(&pl, nullptr)
                               : ops::matmul(g.a, g.b, false, false, &e, nullptr, &pl)};
-        assign(lnt, pl.y);
+        if (pl.want_pk) {
+          assign(lp->second, pl.ypk);
+          g_stats.launches_saved++;
+        } else {
+          assign(lnt, pl.y);
+        }
         g_stats.launches_saved++;
       } else {
-        res = {g.packed_n > 0 ? ops::matmul_packed(g.a, g.b, g.packed_n, &e) : ops::matmul(g.a, g.b, false, false, &e)};
+        res = {g.packed_n > 0 ? packed_product(nullptr, nullptr) : ops::matmul(g.a, g.b, false, false, &e)};
       }
       g_stats.fused_gemm_epilogues++;
       g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0) + (g.ln_gamma ? 1 : 0);
@@ -687,8 +742,18 @@ void eval_all(const std::vector<TensorP>& roots) {
         pl.gamma = lnt->node->in[1];
         pl.beta = lnt->node->in[2];
         pl.eps = lnt->node->f.empty() ? 1e-5f : (float)lnt->node->f[0];
+        auto lp = pack_of.find(lnt.get());
+        if (lp != pack_of.end()) {
+          pl.want_y = false;
+          pl.want_pk = true;
+        }
         res = {ops::embedding_add(e1->in[0], e1->in[1], e2->in[0], e2->in[1], &pl)};
-        assign(lnt, pl.y);
+        if (pl.want_pk) {
+          assign(lp->second, pl.ypk);
+          g_stats.launches_saved++;
+        } else {
+          assign(lnt, pl.y);
+        }
         g_stats.launches_saved += 3;
       } else {
         res = {ops::embedding_add(e1->in[0], e1->in[1], e2->in[0], e2->in[1], nullptr)};

@@ -107,11 +107,12 @@ size_t layer_norm_param_ws_bytes(int64_t rows, int64_t cols);
 void layer_norm_param_grads(DType dt, const void* dy, const void* x, const float* stats, void* dgamma, void* dbeta,
                             float* ws, int64_t rows, int64_t cols, hipStream_t s);
 // x[r] = w1[i1[r]] + w2[i2[r]] over [rows, cols] (cols <= 2048; contiguous
-// [vocab, cols] tables), and when gamma is given also y = layer_norm(x).
+// [vocab, cols] tables), and when gamma is given also y = layer_norm(x),
+// into y and/or (fp32, cols % 16 == 0) ypk as packed x3 rows.
 bool embedding_add_ok(int64_t cols);
 void embedding_add(DType dt, const void* w1, DType i1_dt, const void* i1, int64_t v1, const void* w2, DType i2_dt,
-                   const void* i2, int64_t v2, void* x, const void* gamma, const void* beta, void* y, int64_t rows,
-                   int64_t cols, float eps, hipStream_t s);
+                   const void* i2, int64_t v2, void* x, const void* gamma, const void* beta, void* y, void* ypk,
+                   int64_t rows, int64_t cols, float eps, hipStream_t s);
 // Softmax backward: dx = y * (dy - sum(dy * y)) per row.
 void softmax_backward(DType dt, const void* dy, const void* y, void* dx, int64_t rows,
                       int64_t cols, hipStream_t s);
@@ -181,6 +182,12 @@ struct Gemm {
   // fp32 B split ahead of time into bf16 hi/lo MFMA fragments
   // (pack_weights_x3); A fp32 with unit k stride, K % 16 == 0, one batch
   bool b_x3 = false;
+  // with b_x3: A given as packed x3 rows ([ceil(M/32), K/16, 2, 64, 8] bf16,
+  // x3_row_offset in the kernels) instead of fp32; a_sm/a_sk unused
+  bool a_x3 = false;
+  // with b_x3: C also (or, with C null, only) written as packed x3 rows, for
+  // a following packed-A GEMM (row-panel plans, N % 16 == 0)
+  void* c_pk = nullptr;
   // split-K launches leave the partial sums in the workspace (the caller
   // consumes them) instead of reducing them into C
   bool no_reduce = false;
@@ -190,6 +197,8 @@ struct Gemm {
   const void* pln_beta = nullptr;
   void* pln_y = nullptr;
   float pln_eps = 1e-5f;
+  // Y also (or, with pln_y null, only) written as packed x3 rows (N % 16 == 0)
+  void* pln_ypk = nullptr;
 };
 // fp32 weights packed for the bf16x3 MFMA GEMM of few-row activations
 // (gemm_x3p.hip): B(k, n) read through strides (b_sk, b_sn) is split into
@@ -200,21 +209,32 @@ int64_t packed_x3_elems(int64_t K, int64_t N);
 void pack_weights_x3(const void* b, int64_t b_sk, int64_t b_sn, int64_t K, int64_t N, void* out, hipStream_t s);
 // Launch plan of the packed-weight GEMM: 128-row tiles, 64 (wide) or 32
 // columns, kt 16-deep k steps per block and K split `splits` ways.
-// rows: one 32 x 32 block per output tile over the whole K (K = 64 kpw, kpw
-// 4, 8, 12 or 16), no split and an optional layer_norm of A in the prologue.
+// rows: one 32 x 32 block per output tile over the whole K, no split: with
+// fp32 A, K = 64 kpw (kpw 4, 8, 12 or 16) and an optional layer_norm of A in
+// the prologue; with packed A (apk), K = 128 kpw (kpw 2..12, even).
+// split: a plan that ends in a split-K reduction is required (the reduction
+// computes a layer_norm of the output).
 struct X3Plan {
   bool rows = false;
+  bool apk = false;
   int kpw = 0;
   bool wide = true;
   int64_t tiles_m = 0, tiles_n = 0;
   int kt = 1, splits = 1;
 };
-X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus);
+X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus, bool apk = false, bool split = false);
+// Packed x3 rows of an fp32 matrix X [M, K] read through strides (x_sm,
+// x_sk), K % 16 == 0: the A-operand counterpart of pack_weights_x3
+// (packed_x3_elems(K, M) bf16 elements).
+void pack_rows_x3(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, int64_t K, void* out, hipStream_t s);
 // Whether the packed-weight GEMM of this shape normalises its A rows in its
 // prologue (the row-panel plan).
 bool gemm_x3_ln_ok(int64_t M, int64_t N, int64_t K);
 // Whether a packed-weight GEMM can take this A operand and problem.
 bool gemm_x3_ok(const Gemm& g);
+// Whether a packed-A, packed-weight GEMM of this shape can write its output
+// as packed x3 rows (the packed-A row-panel plan).
+bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K);
 // Whether the launch ends in a split-K reduction that can also produce
 // layer_norm(C) (one batch, N <= 2048); otherwise the caller runs layer_norm.
 bool gemm_post_ln_fused(const Gemm& g);

@@ -341,7 +341,9 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
     float o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[j] = gam[i][j] * (v[i][j] - mean) * inv + bet[i][j];
-    if (c < N) st4<T>(y + c, o);
+    if (c < N && p.pln_y) st4<T>(y + c, o);
+    if constexpr (sizeof(T) == 4)
+      if (c < N && p.pln_ypk) x3_store4(p.pln_ypk, N / 16, row, c, o);
   }
 }
 
@@ -452,7 +454,9 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln_mw(GArgs p) {
     float o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = gam[i][e] * (v[i][e] - mean) * inv + bet[i][e];
-    if (c < N) st4<T>(y + c, o);
+    if (c < N && p.pln_y) st4<T>(y + c, o);
+    if constexpr (sizeof(T) == 4)
+      if (c < N && p.pln_ypk) x3_store4(p.pln_ypk, N / 16, row, c, o);
   }
 }
 
@@ -687,6 +691,9 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   p.pln_b = g.pln_beta;
   p.pln_y = g.pln_y;
   p.pln_eps = g.pln_eps;
+  p.a_x3 = g.a_x3;
+  p.c_pk = (bf16_t*)g.c_pk;
+  p.pln_ypk = (bf16_t*)g.pln_ypk;
   const size_t esz = dtype_size(g.dt);
   const int vw = (int)(16 / esz);  // elements per 16-byte vector
   // Vector loads need 16-byte aligned runs along the contiguous axis.
@@ -729,14 +736,38 @@ static bool reduce_vec_ok(const Gemm& g) {
          (!g.mask || g.k_sm % 4 == 0);
 }
 
+// The packed-weight plan of g: split-K when the reduction must produce a
+// layer_norm of the output.
+static X3Plan x3_plan_of(const Gemm& g) {
+  return x3_plan(g.M, g.N, g.K, cu_count(), g.a_x3, g.pln_y != nullptr || g.pln_ypk != nullptr);
+}
+
 bool gemm_x3_ok(const Gemm& g) {
-  if (g.ln_gamma && (!g.ln_beta || !gemm_x3_ln_ok(g.M, g.N, g.K))) return false;
-  return g.b_x3 && g.dt == DType::F32 && g.batch == 1 && g.a_sk == 1 && g.K % 16 == 0 && g.K > 0 && al16(g.A) &&
-         (g.M == 1 || g.a_sm % 4 == 0) && al16(g.B) && !g.b_scale && g.c_sm == g.N;
+  if (!g.b_x3 || g.dt != DType::F32 || g.batch != 1 || g.K % 16 != 0 || g.K <= 0 || !al16(g.A) || !al16(g.B) ||
+      g.b_scale)
+    return false;
+  if (g.a_x3) {
+    if (g.ln_gamma) return false;
+  } else {
+    if (g.ln_gamma && (!g.ln_beta || !gemm_x3_ln_ok(g.M, g.N, g.K))) return false;
+    if (g.a_sk != 1 || (g.M > 1 && g.a_sm % 4 != 0)) return false;
+  }
+  if (g.c_pk) {
+    const X3Plan pl = x3_plan_of(g);
+    if (!(pl.rows && pl.apk && pl.splits == 1 && g.N % 16 == 0 && al16(g.c_pk))) return false;
+  } else if (!g.C && !g.no_reduce) {
+    return false;
+  }
+  return g.c_sm == g.N;
+}
+
+bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K) {
+  const X3Plan pl = x3_plan(M, N, K, cu_count(), true, false);
+  return pl.rows && pl.splits == 1 && N % 16 == 0;
 }
 
 int gemm_splits(const Gemm& g) {
-  if (g.b_x3) return x3_plan(g.M, g.N, g.K, cu_count()).splits;
+  if (g.b_x3) return x3_plan_of(g).splits;
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return 1;
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf ? pl.splits : 1;
@@ -751,7 +782,11 @@ bool gemm_post_ln_fused(const Gemm& g) {
   if (!ok(g.C) || !ok(g.bias) || !ok(g.residual) || !ok(g.mask) || !ok(g.pln_gamma) || !ok(g.pln_beta) ||
       !ok(g.pln_y) || (g.residual && g.r_sm % 4 != 0) || (g.mask && g.k_sm % 4 != 0))
     return false;
-  if (g.b_x3) return x3_plan(g.M, g.N, g.K, cu_count()).splits > 1;
+  // the packed layer_norm output: fp32, whole 16-column k steps, 16-byte aligned
+  if (g.pln_ypk && (g.dt != DType::F32 || g.N % 16 != 0 || !al16(g.pln_ypk))) return false;
+  if (!g.pln_y && !g.pln_ypk) return false;
+  if (!g.C || g.c_pk) return false;
+  if (g.b_x3) return x3_plan_of(g).splits > 1;
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf && pl.splits > 1;
 }
@@ -788,7 +823,7 @@ const char* gemm_plan_name(const Gemm& g) {
 
 size_t gemm_workspace_bytes(const Gemm& g) {
   if (g.b_x3) {
-    const X3Plan xp = x3_plan(g.M, g.N, g.K, cu_count());
+    const X3Plan xp = x3_plan_of(g);
     return xp.splits > 1 ? (size_t)xp.splits * g.M * g.N * sizeof(float) : 0;
   }
   const SkinnyPlan sp = skinny_plan(g, cu_count());
@@ -806,14 +841,15 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     if (!gemm_x3_ok(g))
       fail("gemm: packed fp32 weights need fp32 A with unit k stride and 16-byte aligned rows, K %% 16 == 0, "
            "one batch and a contiguous output");
-    if (g.pln_y && !gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
-    const X3Plan xp = x3_plan(g.M, g.N, g.K, cu_count());
+    if ((g.pln_y || g.pln_ypk) && !gemm_post_ln_fused(g))
+      fail("gemm: this launch cannot fuse layer_norm into its reduction");
+    const X3Plan xp = x3_plan_of(g);
     if (g.no_reduce && xp.splits < 2) fail("gemm: partial sums requested from a launch without a K split");
     Plan one{};
     one.bm = xp.rows ? 32 : 128;
     one.bn = xp.rows || !xp.wide ? 32 : 64;
     one.splits = xp.splits;
-    one.kps = xp.rows ? g.K : 16LL * xp.kt;
+    one.kps = xp.rows ? (xp.apk ? 128LL * xp.kpw : g.K) : 16LL * xp.kt;
     GArgs p = make_args(g, one);
     p.ws = (float*)workspace;
     if (xp.splits > 1 && !workspace) fail("gemm: split-K workspace missing");
@@ -821,6 +857,7 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     reduce_splits(g, p, s);
     return;
   }
+  if (g.a_x3 || g.c_pk || g.pln_ypk) fail("gemm: packed x3 rows need packed fp32 weights");
   if (g.pln_y && !gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
   if (g.no_reduce && gemm_splits(g) < 2) fail("gemm: partial sums requested from a launch without a K split");
   const SkinnyPlan sp = skinny_plan(g, cu_count());
@@ -891,7 +928,7 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
 static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s) {
   if (p.splits > 1) {
     if (g.no_reduce) return;
-    if (g.pln_y) {
+    if (g.pln_y || g.pln_ypk) {
       if (!gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
       AGPU_FLOAT_SWITCH(g.dt, launch_reduce_ln<T>(p, s));
       check_launch("splitk_reduce_ln");
@@ -914,7 +951,7 @@ static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s) {
     if (blocks > 65536) blocks = 65536;
     AGPU_FLOAT_SWITCH(g.dt, hipLaunchKernelGGL((splitk_reduce<T>), dim3((unsigned)blocks), dim3(256), 0, s, p));
     check_launch("splitk_reduce");
-  } else if (g.pln_y) {
+  } else if (g.pln_y || g.pln_ypk) {
     fail("gemm: layer_norm fusion needs a split-K launch");
   }
 }

@@ -36,6 +36,11 @@ struct GArgs {
   const float* b_scale;
   const void* ln_g; const void* ln_b; float ln_eps;
   const void* pln_g; const void* pln_b; void* pln_y; float pln_eps;
+  // packed-x3 row operands (bf16 hi/lo MFMA fragments, see x3_row_offset):
+  // A read packed, C and the layer_norm output also (or only) written packed
+  bool a_x3;
+  bf16_t* c_pk;
+  bf16_t* pln_ypk;
 };
 
 // Epilogue operands of one output, loadable ahead of the product (they do
@@ -170,6 +175,29 @@ __device__ __forceinline__ void split_bf16x2(float x0, float x1, bf16x2_t& hi, b
   r.x = __builtin_isfinite(x0) ? r.x : 0.f;
   r.y = __builtin_isfinite(x1) ? r.y : 0.f;
   lo = __builtin_convertvector(r, bf16x2_t);
+}
+
+// Packed x3 rows: a matrix X [M, K] (K % 16 == 0) stored as the A operand
+// of v_mfma_f32_32x32x16_bf16, hi = bf16(x), lo = bf16(x - hi).  Element
+// (r, k) of part h sits at ((s T + t) 2 + h) 512 + 8 l + j with s = r / 32,
+// t = k / 16, l = r % 32 + 32 ((k / 8) % 2), j = k % 8 and T = K / 16: one
+// lane's operand (8 consecutive k of one row) is 16 contiguous bytes and one
+// wavefront's fragment 1 KB.  Rows past M (up to the next multiple of 32) are
+// never written; the products they feed are never stored.  It is the layout
+// of the packed weights with rows in place of columns.
+__device__ __forceinline__ int64_t x3_row_offset(int64_t r, int64_t k, int64_t T) {
+  const int64_t l = (r & 31) + 32 * ((k >> 3) & 1);
+  return (((r >> 5) * T + (k >> 4)) * 2) * 512 + l * 8 + (k & 7);
+}
+// Stores x[0..3] = X(r, k..k+3), k % 4 == 0, as hi and lo (8 bytes each).
+__device__ __forceinline__ void x3_store4(bf16_t* pk, int64_t T, int64_t r, int64_t k, const float (&x)[4]) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x2_t h0, l0, h1, l1;
+  split_bf16x2(x[0], x[1], h0, l0);
+  split_bf16x2(x[2], x[3], h1, l1);
+  bf16_t* d = pk + x3_row_offset(r, k, T);
+  *(bf16x4_t*)d = bf16x4_t{h0.x, h0.y, h1.x, h1.y};
+  *(bf16x4_t*)(d + 512) = bf16x4_t{l0.x, l0.y, l1.x, l1.y};
 }
 
 // Per-thread share of a ROWS x BK operand slice.  KCONT: the operand is

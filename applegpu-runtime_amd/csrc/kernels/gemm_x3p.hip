@@ -52,7 +52,7 @@ __global__ void __launch_bounds__(256) pack_x3_kernel(const float* __restrict__ 
   *(bf16x8_t*)(dst + 512) = lo;
 }
 
-template <int FR, int FC, int WR, int WC, int KT>
+template <int FR, int FC, int WR, int WC, int KT, bool APK>
 __global__ void __launch_bounds__(256) gemm_x3p(GArgs p, int64_t T) {
   static_assert(WR * WC == 4, "four wavefronts per block");
   constexpr int BM = 32 * FR * WR, BN = 32 * FC * WC, KB = 16 * KT;
@@ -60,7 +60,7 @@ __global__ void __launch_bounds__(256) gemm_x3p(GArgs p, int64_t T) {
   constexpr int F4R = KB / 4;             // float4 per A row
   constexpr int NQ = BM * F4R / 256;      // float4 per thread
   static_assert(BM * F4R % 256 == 0, "A tile split over 256 threads");
-  __shared__ __attribute__((aligned(16))) bf16_t sA[2][BM * LDA];
+  __shared__ __attribute__((aligned(16))) bf16_t sA[2][APK ? 8 : BM * LDA];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wr = wave / WC, wc = wave % WC;
@@ -85,32 +85,51 @@ __global__ void __launch_bounds__(256) gemm_x3p(GArgs p, int64_t T) {
       bl[j][t] = *(const bf16x8_t*)(src + t * 1024 + 512);
     }
   }
-  // 2. The block's A tile, BM rows x KB k (rows past M read row M - 1).
-  const float* A = (const float*)p.A;
-  const int64_t kbeg = t0 * 16;
-  float4 av[NQ];
+  // 2. A.  Packed (APK): this wave's fragments of its FR row strips, like
+  //    B's (strips past M read the last strip; never stored).  fp32: the
+  //    block's BM x KB tile (rows past M read row M - 1), split into hi/lo
+  //    in LDS, [row][k] with k contiguous.
+  [[maybe_unused]] bf16x8_t ah_r[APK ? FR : 1][APK ? KT : 1], al_r[APK ? FR : 1][APK ? KT : 1];
+  if constexpr (APK) {
+    const int64_t Sm = (p.M + 31) / 32;
+    const bf16_t* Ap = (const bf16_t*)p.A;
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    const int q = threadIdx.x + 256 * i;
-    const int r = q / F4R, c4 = q % F4R;
-    const int64_t row = m0 + r < p.M ? m0 + r : p.M - 1;
-    av[i] = *(const float4*)(A + row * p.a_sm + kbeg + 4 * c4);
-  }
-  // 3. hi/lo into LDS, [row][k] with k contiguous.
+    for (int i = 0; i < FR; ++i) {
+      int64_t s = (m0 >> 5) + wr * FR + i;
+      s = s < Sm ? s : Sm - 1;
+      const bf16_t* src = Ap + ((s * T + t0) * 2) * 512 + lane * 8;
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) {
-    const int q = threadIdx.x + 256 * i;
-    const int r = q / F4R, c4 = q % F4R;
-    bf16x2_t h0, l0, h1, l1;
-    split_bf16x2(av[i].x, av[i].y, h0, l0);
-    split_bf16x2(av[i].z, av[i].w, h1, l1);
-    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-    const bf16x4_t hv = {h0.x, h0.y, h1.x, h1.y};
-    const bf16x4_t lv = {l0.x, l0.y, l1.x, l1.y};
-    *(bf16x4_t*)&sA[0][r * LDA + 4 * c4] = hv;
-    *(bf16x4_t*)&sA[1][r * LDA + 4 * c4] = lv;
+      for (int t = 0; t < KT; ++t) {
+        ah_r[i][t] = *(const bf16x8_t*)(src + t * 1024);
+        al_r[i][t] = *(const bf16x8_t*)(src + t * 1024 + 512);
+      }
+    }
+  } else {
+    const float* A = (const float*)p.A;
+    const int64_t kbeg = t0 * 16;
+    float4 av[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int r = q / F4R, c4 = q % F4R;
+      const int64_t row = m0 + r < p.M ? m0 + r : p.M - 1;
+      av[i] = *(const float4*)(A + row * p.a_sm + kbeg + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int q = threadIdx.x + 256 * i;
+      const int r = q / F4R, c4 = q % F4R;
+      bf16x2_t h0, l0, h1, l1;
+      split_bf16x2(av[i].x, av[i].y, h0, l0);
+      split_bf16x2(av[i].z, av[i].w, h1, l1);
+      typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+      const bf16x4_t hv = {h0.x, h0.y, h1.x, h1.y};
+      const bf16x4_t lv = {l0.x, l0.y, l1.x, l1.y};
+      *(bf16x4_t*)&sA[0][r * LDA + 4 * c4] = hv;
+      *(bf16x4_t*)&sA[1][r * LDA + 4 * c4] = lv;
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   // 4. The products.
   f32x16 acc[FR][FC];
@@ -126,8 +145,14 @@ __global__ void __launch_bounds__(256) gemm_x3p(GArgs p, int64_t T) {
 #pragma unroll
     for (int i = 0; i < FR; ++i) {
       const int r = (wr * FR + i) * 32 + (lane & 31);
-      const bf16x8_t ah = *(const bf16x8_t*)&sA[0][r * LDA + ko];
-      const bf16x8_t al = *(const bf16x8_t*)&sA[1][r * LDA + ko];
+      bf16x8_t ah, al;
+      if constexpr (APK) {
+        ah = ah_r[i][t];
+        al = al_r[i][t];
+      } else {
+        ah = *(const bf16x8_t*)&sA[0][r * LDA + ko];
+        al = *(const bf16x8_t*)&sA[1][r * LDA + ko];
+      }
 #pragma unroll
       for (int j = 0; j < FC; ++j) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[j][t], acc[i][j], 0, 0, 0);
@@ -333,15 +358,133 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
   }
 }
 
-template <int FR, int FC, int WR, int WC>
+// Row panel over packed A: the block (8 wavefronts) owns 32 rows x 32
+// columns over a K range of 8 KPW k steps (split blockIdx.y; the whole K when
+// splits == 1); wave w multiplies k steps [w KPW, (w + 1) KPW) of the range
+// with its A and B fragments loaded straight from global memory into
+// registers (both operands are stored in MFMA order), so the product needs
+// no LDS, no barrier and no conversion.  The eight partial 32 x 32 blocks
+// meet in LDS; threads 0..255 then finish row t / 8, columns 4 (t % 8) .. + 3,
+// adding the partials in wave order (fixed: repeated launches give identical
+// bits).  Without a split they apply the epilogue, whose operands they load
+// while the products run, and write C (fp32) and/or, as packed x3 rows,
+// c_pk (N % 16 == 0) for the next packed-A GEMM; with one, the split's sums
+// go to the workspace for the split-K reduction.  Blocks of one column strip
+// share an XCD, as in gemm_x3_rows.
+template <int KPW>
+__global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
+  constexpr int W = 8;
+  const int64_t T = p.K >> 4;
+  __shared__ __attribute__((aligned(16))) float red[W * 16 * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int tm, tn;
+  {
+    const int id = blockIdx.x;
+    if ((p.tiles_n & 7) == 0) {
+      const int g = id / (8 * p.tiles_m), r = id % (8 * p.tiles_m);
+      tm = r / 8;
+      tn = g * 8 + (r & 7);
+    } else {
+      tm = id / p.tiles_n;
+      tn = id % p.tiles_n;
+    }
+  }
+  const int64_t m0 = (int64_t)tm * 32, n0 = (int64_t)tn * 32;
+  const int64_t t0 = (int64_t)blockIdx.y * (W * KPW) + (int64_t)wave * KPW;
+
+  // 1. Fragments: tiles_m and tiles_n equal the strip counts, so tm and tn
+  //    name existing strips.
+  bf16x8_t ah[KPW], al[KPW], bh[KPW], bl[KPW];
+  {
+    const bf16_t* as = (const bf16_t*)p.A + (((int64_t)tm * T + t0) * 2) * 512 + lane * 8;
+    const bf16_t* bs = (const bf16_t*)p.B + (((int64_t)tn * T + t0) * 2) * 512 + lane * 8;
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      bh[i] = *(const bf16x8_t*)(bs + i * 1024);
+      bl[i] = *(const bf16x8_t*)(bs + i * 1024 + 512);
+      ah[i] = *(const bf16x8_t*)(as + i * 1024);
+      al[i] = *(const bf16x8_t*)(as + i * 1024 + 512);
+    }
+  }
+  // 2. Epilogue operands of this thread's four outputs (waves 0..3).
+  const int r = (threadIdx.x >> 3) & 31, q = threadIdx.x & 7;
+  const int64_t row = m0 + r, rc = row < p.M ? row : p.M - 1;
+  float bias[4] = {0.f, 0.f, 0.f, 0.f}, res[4] = {0.f, 0.f, 0.f, 0.f}, msk[4] = {1.f, 1.f, 1.f, 1.f};
+  if (wave < 4 && p.splits == 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + 4 * q + j, cc = col < p.N ? col : p.N - 1;
+      if (p.bias) bias[j] = ((const float*)p.bias)[cc];
+      if (p.res) res[j] = ((const float*)p.res)[rc * p.r_sm + cc];
+      if (p.mask) msk[j] = ((const float*)p.mask)[rc * p.k_sm + cc];
+    }
+  }
+  // 3. This wave's k steps.
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[i], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[i], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[i], acc, 0, 0, 0);
+  }
+  // 4. Partials to LDS: register e of lane l is row 8 (e / 4) + 4 (l / 32) +
+  //    e % 4, column l % 32.
+#pragma unroll
+  for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
+  __syncthreads();
+  if (wave >= 4 || row >= p.M) return;
+  // 5. Row r, columns 4q..4q+3: register 4 (r / 8) + r % 4 of lanes
+  //    32 ((r / 4) % 2) + 4q + 0..3 in every wave.
+  const int e = 4 * (r >> 3) + (r & 3);
+  const int lb = 32 * ((r >> 2) & 1) + 4 * q;
+  float v[4];
+  {
+    const float4 w0 = *(const float4*)&red[e * 64 + lb];
+    v[0] = w0.x; v[1] = w0.y; v[2] = w0.z; v[3] = w0.w;
+  }
+#pragma unroll
+  for (int x = 1; x < W; ++x) {
+    const float4 w = *(const float4*)&red[(x * 16 + e) * 64 + lb];
+    v[0] += w.x; v[1] += w.y; v[2] += w.z; v[3] += w.w;
+  }
+  const int64_t col = n0 + 4 * q;
+  if (p.splits > 1) {
+    float* ws = p.ws + (int64_t)blockIdx.y * p.M * p.N + row * p.N;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (col + j < p.N) ws[col + j] = v[j];
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float y = p.alpha * v[j] + bias[j];
+    if (p.act == kActRelu) y = fmaxf(y, 0.f);
+    else if (p.act == kActGelu) y = gelu_tanh(y);
+    else if (p.act == kActGeluExact) y = 0.5f * y * (1.f + erff(y * 0.70710678118654752f));
+    y += res[j];
+    if (p.mask) y = msk[j] > 0.f ? y : 0.f;
+    v[j] = y;
+  }
+  if (p.C) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (col + j < p.N) ((float*)p.C)[row * p.c_sm + col + j] = v[j];
+  }
+  if (p.c_pk && col < p.N) x3_store4(p.c_pk, p.N / 16, row, col, v);
+}
+
+template <int FR, int FC, int WR, int WC, bool APK>
 void launch_x3p_kt(const GArgs& p, int kt, int64_t T, dim3 grid, hipStream_t s) {
   switch (kt) {
-    case 1: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 1>), grid, dim3(256), 0, s, p, T); break;
-    case 2: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 2>), grid, dim3(256), 0, s, p, T); break;
-    case 3: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 3>), grid, dim3(256), 0, s, p, T); break;
-    case 4: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 4>), grid, dim3(256), 0, s, p, T); break;
-    case 6: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 6>), grid, dim3(256), 0, s, p, T); break;
-    case 8: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 8>), grid, dim3(256), 0, s, p, T); break;
+    case 1: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 1, APK>), grid, dim3(256), 0, s, p, T); break;
+    case 2: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 2, APK>), grid, dim3(256), 0, s, p, T); break;
+    case 3: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 3, APK>), grid, dim3(256), 0, s, p, T); break;
+    case 4: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 4, APK>), grid, dim3(256), 0, s, p, T); break;
+    case 6: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 6, APK>), grid, dim3(256), 0, s, p, T); break;
+    case 8: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 8, APK>), grid, dim3(256), 0, s, p, T); break;
+    case 12: hipLaunchKernelGGL((gemm_x3p<FR, FC, WR, WC, 12, APK>), grid, dim3(256), 0, s, p, T); break;
     default: fail("gemm_x3p: %d k steps per block not built", kt);
   }
 }
@@ -359,11 +502,49 @@ void pack_weights_x3(const void* b, int64_t b_sk, int64_t b_sn, int64_t K, int64
   check_launch("pack_weights_x3");
 }
 
-X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus) {
+void pack_rows_x3(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, int64_t K, void* out, hipStream_t s) {
+  // X(m, k) = B(k, n = m): the weights' kernel with rows as columns
+  pack_weights_x3(x, x_sk, x_sm, K, M, out, s);
+}
+
+X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus, bool apk, bool split) {
   X3Plan pl;
+  pl.apk = apk;
   const int64_t T = (K + 15) / 16;
-  // Whole rows per block when K allows it: no split-K reduction launch.
-  if (gemm_tune().splits == 0 && K % 64 == 0 && (K / 64 == 4 || K / 64 == 8 || K / 64 == 12 || K / 64 == 16)) {
+  const int forced = gemm_tune().splits;
+  // A forced tile family (applegpu_ffi_gemm_tune's cfg for packed weights):
+  // 0 wide split tiles, 1 narrow split tiles, 2 the packed-A row panel.
+  const int fcfg = gemm_tune().cfg;
+  // Packed A: the 8-wave row-panel kernel over K ranges of 8 kpw k steps,
+  // whole K per block when that fits (no split-K reduction launch), else the
+  // deepest range whose grid still gives every CU a block.
+  if (apk && T % 8 == 0 && (fcfg == -1 || fcfg == 2)) {
+    static const int kKpw[] = {12, 10, 8, 6, 4, 3, 2, 1};
+    const int64_t tiles = ((M + 31) / 32) * ((N + 31) / 32);
+    int kpw = 0;
+    for (int c : kKpw) {
+      if (T % (8 * c)) continue;
+      const int64_t sp = T / (8 * c);
+      if (forced > 0) {
+        if (sp == forced) kpw = c;
+        continue;
+      }
+      if (sp > 64 || (split && sp < 2)) continue;
+      kpw = c;
+      if (sp == 1 || tiles * sp >= (int64_t)cus * 3 / 4) break;
+    }
+    if (kpw) {
+      pl.rows = true;
+      pl.kpw = kpw;
+      pl.tiles_m = (M + 31) / 32;
+      pl.tiles_n = (N + 31) / 32;
+      pl.splits = (int)(T / (8 * kpw));
+      return pl;
+    }
+  }
+  // fp32 A: whole rows per block when K allows it: no split-K reduction launch.
+  const bool rows_k = !apk && K % 64 == 0 && (K / 64 == 4 || K / 64 == 8 || K / 64 == 12 || K / 64 == 16);
+  if (forced == 0 && !split && rows_k && (fcfg == -1 || fcfg == 2)) {
     pl.rows = true;
     pl.kpw = (int)(K / 64);
     pl.tiles_m = (M + 31) / 32;
@@ -371,21 +552,21 @@ X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus) {
     pl.splits = 1;
     return pl;
   }
-  // Wide tiles (128 x 64: each wave 64 rows x 32 columns) when N gives a
-  // dozen of them; narrow ones (128 x 32: each wave 32 rows, the four waves
-  // share their B fragments) below that.
-  pl.wide = N >= 768;
+  // Wide tiles (128 x 64: each wave 64 rows x 32 columns) for wide outputs;
+  // narrow ones (128 x 32: each wave 32 rows, the four waves share their B
+  // fragments, and each weight column is read by one block per K range)
+  // up to 1024 columns.
+  pl.wide = fcfg == 0 || fcfg == 1 ? fcfg == 0 : N > 1024;
   const int64_t bn = pl.wide ? 64 : 32;
   pl.tiles_m = (M + 127) / 128;
   pl.tiles_n = (N + bn - 1) / bn;
   const int64_t tiles = pl.tiles_m * pl.tiles_n;
   // The deepest per-block K range (fewest splits) whose grid still gives
   // nearly every CU a block; failing that, the most splits on offer.
-  static const int kKt[] = {8, 6, 4, 3, 2, 1};
+  static const int kKt[] = {12, 8, 6, 4, 3, 2, 1};
   pl.kt = 0;
   // A forced split count (applegpu_ffi_gemm_tune) applies when it leaves a
   // k-step count the kernel is built for.
-  const int forced = gemm_tune().splits;
   if (forced > 0 && T % forced == 0) {
     const int64_t kt = T / forced;
     for (int c : kKt)
@@ -408,6 +589,22 @@ X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus) {
 
 bool gemm_x3_ln_ok(int64_t M, int64_t N, int64_t K) { return x3_plan(M, N, K, 256).rows; }
 
+static void launch_rows_pk(const X3Plan& pl, const GArgs& p, hipStream_t s) {
+  if (p.K != 128LL * pl.kpw * pl.splits) fail("internal: gemm_x3_rows_pk plan does not cover K");
+  const dim3 grid((unsigned)(pl.tiles_m * pl.tiles_n), (unsigned)pl.splits);
+  switch (pl.kpw) {
+    case 1: hipLaunchKernelGGL((gemm_x3_rows_pk<1>), grid, dim3(512), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gemm_x3_rows_pk<2>), grid, dim3(512), 0, s, p); break;
+    case 3: hipLaunchKernelGGL((gemm_x3_rows_pk<3>), grid, dim3(512), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gemm_x3_rows_pk<4>), grid, dim3(512), 0, s, p); break;
+    case 6: hipLaunchKernelGGL((gemm_x3_rows_pk<6>), grid, dim3(512), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((gemm_x3_rows_pk<8>), grid, dim3(512), 0, s, p); break;
+    case 10: hipLaunchKernelGGL((gemm_x3_rows_pk<10>), grid, dim3(512), 0, s, p); break;
+    case 12: hipLaunchKernelGGL((gemm_x3_rows_pk<12>), grid, dim3(512), 0, s, p); break;
+    default: fail("gemm_x3_rows_pk: %d k steps per wave not built", pl.kpw);
+  }
+}
+
 template <bool LN>
 static void launch_rows(const X3Plan& pl, const GArgs& p, hipStream_t s) {
   const dim3 grid((unsigned)(pl.tiles_m * pl.tiles_n));
@@ -421,6 +618,15 @@ static void launch_rows(const X3Plan& pl, const GArgs& p, hipStream_t s) {
 }
 
 void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s) {
+  if (pl.apk != p.a_x3) fail("internal: gemm_x3p plan and A operand disagree");
+  if (p.c_pk && !(pl.rows && pl.apk && pl.splits == 1 && p.N % 16 == 0))
+    fail("gemm_x3p: packed output needs the unsplit packed-A row-panel plan and N %% 16 == 0");
+  if (pl.rows && pl.apk) {
+    if (p.ln_g) fail("gemm_x3p: a layer_norm prologue needs fp32 A");
+    launch_rows_pk(pl, p, s);
+    check_launch("gemm_x3_rows_pk");
+    return;
+  }
   if (pl.rows) {
     if (p.ln_g) launch_rows<true>(pl, p, s);
     else launch_rows<false>(pl, p, s);
@@ -430,8 +636,13 @@ void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s) {
   if (p.ln_g) fail("gemm_x3p: a layer_norm prologue needs the row-panel plan");
   const int64_t T = (p.K + 15) / 16;
   const dim3 grid((unsigned)(pl.tiles_m * pl.tiles_n), (unsigned)pl.splits);
-  if (pl.wide) launch_x3p_kt<2, 1, 2, 2>(p, pl.kt, T, grid, s);
-  else launch_x3p_kt<1, 1, 4, 1>(p, pl.kt, T, grid, s);
+  if (pl.apk) {
+    if (pl.wide) launch_x3p_kt<2, 1, 2, 2, true>(p, pl.kt, T, grid, s);
+    else launch_x3p_kt<1, 1, 4, 1, true>(p, pl.kt, T, grid, s);
+  } else {
+    if (pl.wide) launch_x3p_kt<2, 1, 2, 2, false>(p, pl.kt, T, grid, s);
+    else launch_x3p_kt<1, 1, 4, 1, false>(p, pl.kt, T, grid, s);
+  }
   check_launch("gemm_x3p");
 }
 

@@ -13,6 +13,7 @@
 // row (rows up to 2048 columns stay in registers: a single HBM read and a
 // single write), and a 256-thread workgroup owns longer rows.
 #include "device.hpp"
+#include "gemm_kernels.hpp"  // x3_store4: packed x3 rows of the layer_norm output
 
 namespace agpu {
 namespace k {
@@ -432,8 +433,9 @@ template <typename T, typename I, int NV, bool LN>
 __global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, const I* __restrict__ i1, int64_t v1,
                                                       const T* __restrict__ w2, const I* __restrict__ i2, int64_t v2,
                                                       T* __restrict__ x, const T* __restrict__ g,
-                                                      const T* __restrict__ b, T* __restrict__ y, int64_t rows,
-                                                      int64_t cols, float eps, bool vec) {
+                                                      const T* __restrict__ b, T* __restrict__ y,
+                                                      bf16_t* __restrict__ ypk, int64_t rows, int64_t cols, float eps,
+                                                      bool vec) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // one wavefront per row
   if (row >= rows) return;
@@ -478,7 +480,9 @@ __global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, 
       load4<T>(b, col, cols, vec, 0.f, bv);
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[i][j] = gv[j] * (v[i][j] - mean) * inv + bv[j];
-      store4<T>(y + row * cols, col, cols, vec, v[i]);
+      if (y) store4<T>(y + row * cols, col, cols, vec, v[i]);
+      if constexpr (sizeof(T) == 4)
+        if (ypk && col < cols) x3_store4(ypk, cols / 16, row, col, v[i]);
     }
   }
 }
@@ -999,7 +1003,7 @@ bool embedding_add_ok(int64_t cols) { return cols > 0 && cols <= 2048; }
 namespace {
 struct EaArgs {
   const void *w1, *i1, *w2, *i2, *g, *b;
-  void *x, *y;
+  void *x, *y, *ypk;
   int64_t v1, v2, rows, cols;
   float eps;
   bool vec;
@@ -1013,11 +1017,11 @@ void ea_nv(const EaArgs& a, hipStream_t s) {
   if (a.g)
     hipLaunchKernelGGL((embed_add_wave<T, I, NV, true>), grid, block, 0, s, (const T*)a.w1,
                        (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)a.g,
-                       (const T*)a.b, (T*)a.y, a.rows, a.cols, a.eps, a.vec);
+                       (const T*)a.b, (T*)a.y, (bf16_t*)a.ypk, a.rows, a.cols, a.eps, a.vec);
   else
     hipLaunchKernelGGL((embed_add_wave<T, I, NV, false>), grid, block, 0, s, (const T*)a.w1,
                        (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)nullptr,
-                       (const T*)nullptr, (T*)nullptr, a.rows, a.cols, a.eps, a.vec);
+                       (const T*)nullptr, (T*)nullptr, (bf16_t*)nullptr, a.rows, a.cols, a.eps, a.vec);
 }
 
 template <typename T, typename I>
@@ -1035,17 +1039,19 @@ void ea_launch(const EaArgs& a, hipStream_t s) {
 }  // namespace
 
 void embedding_add(DType dt, const void* w1, DType i1_dt, const void* i1, int64_t v1, const void* w2, DType i2_dt,
-                   const void* i2, int64_t v2, void* x, const void* gamma, const void* beta, void* y, int64_t rows,
-                   int64_t cols, float eps, hipStream_t s) {
+                   const void* i2, int64_t v2, void* x, const void* gamma, const void* beta, void* y, void* ypk,
+                   int64_t rows, int64_t cols, float eps, hipStream_t s) {
   if (rows == 0) return;
   if (!embedding_add_ok(cols)) fail("embedding_add: %lld columns (at most 2048)", (long long)cols);
   if (i1_dt != i2_dt) fail("embedding_add: index dtypes differ");
   if (rows > 0x7fffffffLL) fail("embedding_add: too many rows");
+  if (ypk && (dt != DType::F32 || cols % 16 != 0 || ((uintptr_t)ypk & 15)))
+    fail("embedding_add: packed layer_norm rows need fp32, 16-aligned columns");
   const size_t es = dtype_size(dt);
   const bool ln = gamma != nullptr;
-  EaArgs a{w1, i1, w2, i2, gamma, beta, x, y, v1, v2, rows, cols, eps, false};
+  EaArgs a{w1, i1, w2, i2, gamma, beta, x, y, ypk, v1, v2, rows, cols, eps, false};
   a.vec = vec_ok(w1, cols, es) && vec_ok(w2, cols, es) && vec_ok(x, cols, es) &&
-          (!ln || (vec_ok(y, cols, es) && vec_ok(gamma, 0, es) && vec_ok(beta, 0, es)));
+          (!ln || ((y == nullptr || vec_ok(y, cols, es)) && vec_ok(gamma, 0, es) && vec_ok(beta, 0, es)));
   AGPU_FLOAT_SWITCH(dt, {
     typedef T TV;
     AGPU_INT_SWITCH(i1_dt, ea_launch<TV, I>(a, s));

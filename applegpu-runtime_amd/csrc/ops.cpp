@@ -764,11 +764,15 @@ TensorP embedding_add(const TensorP& w1, const TensorP& i1, const TensorP& w2, c
       fail("embedding_add: layer_norm gamma/beta must be [%lld] of the table dtype", (long long)cols);
     gc = contiguous(ln->gamma);
     bc = contiguous(ln->beta);
-    ln->y = alloc_out(w1->dtype, od);
+    if (ln->want_pk && (w1->dtype != DType::F32 || cols % 16 != 0 || od.size() != 2))
+      fail("embedding_add: packed layer_norm rows need fp32 [rows, cols] with cols %% 16 == 0");
+    ln->y = ln->want_y ? alloc_out(w1->dtype, od) : nullptr;
+    ln->ypk = ln->want_pk ? alloc_out(DType::BF16, {(rows + 31) / 32, cols / 16, 2, 64, 8}) : nullptr;
   }
   LAUNCH k::embedding_add(w1->dtype, w1->data(), a->dtype, a->data(), w1->shape[0], w2->data(), c->dtype, c->data(),
                           w2->shape[0], x->data(), ln ? gc->data() : nullptr, ln ? bc->data() : nullptr,
-                          ln ? ln->y->data() : nullptr, rows, cols, ln ? ln->eps : 1e-5f, rt().stream());
+                          ln && ln->y ? ln->y->data() : nullptr, ln && ln->ypk ? ln->ypk->data() : nullptr, rows,
+                          cols, ln ? ln->eps : 1e-5f, rt().stream());
   return x;
 }
 
@@ -1068,35 +1072,77 @@ bool is_x3_packed(const TensorP& t) {
   return t->ndim == 5 && t->dtype == DType::BF16 && t->shape[2] == 2 && t->shape[3] == 64 && t->shape[4] == 8;
 }
 
-static TensorP matmul_x3(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln) {
-  const char* name = "matmul_packed";
-  if (a_in->ndim != 2) fail("%s: activations must be 2-D [rows, in]", name);
-  if (a_in->dtype != DType::F32) fail("%s: fp32-packed weights take fp32 activations, got %s", name, dtype_name(a_in->dtype));
-  const int64_t M = a_in->shape[0], K = a_in->shape[1];
+TensorP pack_rows_x3(const TensorP& x) {
+  if (x->ndim != 2) fail("pack_rows_x3: rows must be 2-D [rows, cols]");
+  if (x->dtype != DType::F32) fail("pack_rows_x3: fp32 rows only, got %s", dtype_name(x->dtype));
+  const int64_t M = x->shape[0], K = x->shape[1];
+  if (K % 16 != 0 || K == 0 || M == 0)
+    fail("pack_rows_x3: the column count %lld must be a positive multiple of 16", (long long)K);
+  TensorP out = alloc_out(DType::BF16, {(M + 31) / 32, K / 16, 2, 64, 8});
+  LAUNCH k::pack_rows_x3(x->data(), x->strides[0], x->strides[1], M, K, out->data(), rt().stream());
+  return out;
+}
+
+// The packed-weight product.  a_rows < 0: a_in is fp32 [M, K]; otherwise a_in
+// holds packed x3 rows of an [a_rows, K] matrix.
+static TensorP matmul_x3(const TensorP& a_in, int64_t a_rows, const TensorP& pw, int64_t N, const Epilogue* epi,
+                         PostLn* post_ln, PackOut* po) {
+  const bool apk = a_rows >= 0;
+  const char* name = apk ? "matmul_pp" : "matmul_packed";
+  int64_t M, K;
+  if (apk) {
+    if (!is_x3_packed(a_in) || a_rows < 1 || a_in->shape[0] != (a_rows + 31) / 32)
+      fail("%s: A must be pack_rows_x3 of [%lld, K] rows", name, (long long)a_rows);
+    M = a_rows;
+    K = a_in->shape[1] * 16;
+  } else {
+    if (a_in->ndim != 2) fail("%s: activations must be 2-D [rows, in]", name);
+    if (a_in->dtype != DType::F32)
+      fail("%s: fp32-packed weights take fp32 activations, got %s", name, dtype_name(a_in->dtype));
+    M = a_in->shape[0];
+    K = a_in->shape[1];
+  }
   if (N < 1 || pw->shape[0] != (N + 31) / 32 || pw->shape[1] * 16 != K)
     fail("%s: packed weights hold [%lld/32, %lld/16] fragments, not [in %lld, out %lld]", name,
          (long long)pw->shape[0] * 32, (long long)pw->shape[1] * 16, (long long)K, (long long)N);
   // a layer_norm of A runs in the row-panel kernel's prologue when the plan
   // has one (fp32 gamma/beta [K]); otherwise as its own launch first
-  if (epi && epi->ln_gamma &&
-      !(k::gemm_x3_ln_ok(M, N, K) && epi->ln_beta && epi->ln_gamma->dtype == DType::F32 &&
-        epi->ln_beta->dtype == DType::F32 && epi->ln_gamma->numel() == K && epi->ln_beta->numel() == K)) {
-    Epilogue plain = *epi;
-    plain.ln_gamma = plain.ln_beta = nullptr;
-    return matmul_x3(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), pw, N, &plain, post_ln);
+  if (epi && epi->ln_gamma) {
+    if (apk) fail("%s: a layer_norm of packed rows is not available", name);
+    if (!(k::gemm_x3_ln_ok(M, N, K) && epi->ln_beta && epi->ln_gamma->dtype == DType::F32 &&
+          epi->ln_beta->dtype == DType::F32 && epi->ln_gamma->numel() == K && epi->ln_beta->numel() == K)) {
+      Epilogue plain = *epi;
+      plain.ln_gamma = plain.ln_beta = nullptr;
+      return matmul_x3(layer_norm(a_in, epi->ln_gamma, epi->ln_beta, epi->ln_eps), -1, pw, N, &plain, post_ln, po);
+    }
   }
   TensorP a = a_in;
-  if (!meta_mode() && (a->strides[1] != 1 || (M > 1 && a->strides[0] % 4 != 0) || ((uintptr_t)a->data() & 15)))
+  if (apk) a = contiguous(a_in);
+  else if (!meta_mode() && (a->strides[1] != 1 || (M > 1 && a->strides[0] % 4 != 0) || ((uintptr_t)a->data() & 15)))
     a = materialize(a);
   TensorP pc = contiguous(pw);
   const std::vector<int64_t> od{M, N};
-  TensorP out = alloc_out(DType::F32, od);
+  const std::vector<int64_t> pkd{(M + 31) / 32, N / 16, 2, 64, 8};
+  // the packed output straight from the row-panel epilogue when it can
+  const bool pk_direct = po && apk && !post_ln && k::gemm_x3_pk_out_ok(M, N, K);
+  const bool want_c = !po || po->want_c || !pk_direct;
+  TensorP out = want_c ? alloc_out(DType::F32, od) : nullptr;
   k::Gemm g;
   g.dt = g.b_dt = DType::F32;
   g.M = M; g.N = N; g.K = K; g.batch = 1;
-  g.A = a->data(); g.a_sm = M == 1 ? K : a->strides[0]; g.a_sk = 1;
+  g.A = a->data();
+  if (apk) {
+    g.a_x3 = true;
+  } else {
+    g.a_sm = M == 1 ? K : a->strides[0];
+    g.a_sk = 1;
+  }
   g.B = pc->data(); g.b_x3 = true;
-  g.C = out->data(); g.c_sm = N; g.c_sb = M * N;
+  g.C = out ? out->data() : nullptr; g.c_sm = N; g.c_sb = M * N;
+  if (pk_direct) {
+    po->pk = alloc_out(DType::BF16, pkd);
+    g.c_pk = po->pk->data();
+  }
   EpiKeep keep;
   set_epilogue(g, epi, od, {}, &keep);
   TensorP pl_g, pl_b;
@@ -1105,19 +1151,23 @@ static TensorP matmul_x3(const TensorP& a_in, const TensorP& pw, int64_t N, cons
     if (!post_ln->gamma || !post_ln->beta || post_ln->gamma->dtype != g.dt || post_ln->beta->dtype != g.dt ||
         post_ln->gamma->numel() != N || post_ln->beta->numel() != N)
       fail("%s: layer_norm gamma and beta must be [%lld] of the output dtype", name, (long long)N);
+    if (post_ln->want_pk && N % 16 != 0) fail("%s: packed layer_norm rows need N %% 16 == 0", name);
     pl_g = contiguous(post_ln->gamma);
     pl_b = contiguous(post_ln->beta);
     if (!meta_mode()) {
-      TensorP y = alloc_out(g.dt, od);
+      TensorP y = post_ln->want_y ? alloc_out(g.dt, od) : nullptr;
+      TensorP ypk = post_ln->want_pk ? alloc_out(DType::BF16, pkd) : nullptr;
       k::Gemm probe = g;
       probe.pln_gamma = pl_g->data();
       probe.pln_beta = pl_b->data();
-      probe.pln_y = y->data();
+      probe.pln_y = y ? y->data() : nullptr;
+      probe.pln_ypk = ypk ? ypk->data() : nullptr;
       probe.pln_eps = post_ln->eps;
       pln_fused = k::gemm_post_ln_fused(probe);
       if (pln_fused) {
         g = probe;
         post_ln->y = y;
+        post_ln->ypk = ypk;
       }
     }
   }
@@ -1126,13 +1176,26 @@ static TensorP matmul_x3(const TensorP& a_in, const TensorP& pw, int64_t N, cons
   BufferP ws;
   if (wsb) ws = scratch(wsb);
   LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
-  if (post_ln && !pln_fused) post_ln->y = layer_norm(out, pl_g, pl_b, post_ln->eps);
-  return out;
+  if (post_ln && !pln_fused) {
+    TensorP y = layer_norm(out, pl_g, pl_b, post_ln->eps);
+    if (post_ln->want_y) post_ln->y = y;
+    if (post_ln->want_pk) post_ln->ypk = pack_rows_x3(y);
+  }
+  if (po && !pk_direct) po->pk = pack_rows_x3(out);
+  return po && !po->want_c ? nullptr : out;
 }
 
-TensorP matmul_packed(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln) {
-  if (is_x3_packed(pw)) return matmul_x3(a_in, pw, N, epi, post_ln);
-  if (post_ln) fail("matmul_packed: layer_norm of the output needs the fp32 packed layout");
+TensorP matmul_pp(const TensorP& apk, int64_t M, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln,
+                  PackOut* po) {
+  if (!is_x3_packed(pw)) fail("matmul_pp: weights must be packed by pack_weight_x3");
+  if (M < 0) fail("matmul_pp: negative row count");
+  return matmul_x3(apk, M, pw, N, epi, post_ln, po);
+}
+
+TensorP matmul_packed(const TensorP& a_in, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln,
+                      PackOut* po) {
+  if (is_x3_packed(pw)) return matmul_x3(a_in, -1, pw, N, epi, post_ln, po);
+  if (post_ln || po) fail("matmul_packed: layer_norm or packed rows of the output need the fp32 packed layout");
   const char* name = "matmul_packed";
   if (a_in->ndim != 2) fail("%s: activations must be 2-D [rows, in]", name);
   if (pw->ndim != 4 || pw->shape[2] != 64 || pw->shape[3] != 8) fail("%s: weights are not packed (pack_weight)", name);

@@ -89,6 +89,15 @@ struct PostLn {
   TensorP gamma, beta;
   float eps = 1e-5f;
   TensorP y;  // result
+  // y as packed x3 rows too (fp32 output, N % 16 == 0), or instead of y
+  bool want_y = true, want_pk = false;
+  TensorP ypk;
+};
+// Output form of a packed-weight product: fp32 C (want_c) and/or the same
+// values as packed x3 rows (pk) for a following packed-A product.
+struct PackOut {
+  bool want_c = true;
+  TensorP pk;
 };
 // No-allocation mode: the caller's output (`into`) and a caller-held split-K
 // workspace of `cap` bytes; any operand that would need a device copy, and
@@ -126,7 +135,17 @@ bool is_x3_packed(const TensorP& t);
 // epilogue and, for the fp32 layout, layer_norm of the output computed in the
 // split-K reduction.
 TensorP matmul_packed(const TensorP& x, const TensorP& packed, int64_t N, const Epilogue* epi = nullptr,
-                      PostLn* post_ln = nullptr);
+                      PostLn* post_ln = nullptr, PackOut* po = nullptr);
+// Packed x3 rows of an fp32 matrix x [M, K] (K % 16 == 0): hi/lo bf16 in the
+// MFMA A-operand order (k::pack_rows_x3), a BF16 tensor [ceil(M/32), K/16, 2,
+// 64, 8].  The row count is not recoverable from the shape; matmul_pp takes it.
+TensorP pack_rows_x3(const TensorP& x);
+// apk (pack_rows_x3 of an [M, K] matrix) times fp32 weights packed by
+// pack_weight_x3 ([K, N]): out [M, N] fp32 with the epilogue, and optionally
+// layer_norm of the output (split-K reduction) and packed outputs.  Returns
+// null when po asks for the packed output only.
+TensorP matmul_pp(const TensorP& apk, int64_t M, const TensorP& packed, int64_t N, const Epilogue* epi = nullptr,
+                  PostLn* post_ln = nullptr, PackOut* po = nullptr);
 // int8 weights with per-row scales (out = x @ (q * scale[:,None])^T)
 TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
 

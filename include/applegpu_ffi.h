@@ -250,7 +250,9 @@ uint64_t applegpu_graph_bytes(int64_t handle);
  * 1 = native fp32 MFMA (v_mfma_f32_32x32x2_f32; also APPLEGPU_GEMM_F32=native).
  * cfg: -1 = heuristic, 0..10 = tile configuration (BM x BN x BK: 128x128x32,
  * 64x128x32, 64x64x64, 32x64x64, 32x32x64, 128x128x64, 64x64x64, 64x128x64,
- * 32x32x256, 32x64x256, 64x64x128).  splits: 0 = heuristic, n = split K across n blocks.
+ * 32x32x256, 32x64x256, 64x64x128); for fp32 weights packed by pack_weight_x3:
+ * 0 = 128x64 split tiles, 1 = 128x32 split tiles, 2 = 32x32 row panels.
+ * splits: 0 = heuristic, n = split K across n blocks.
  * Returns 0, or -1 for an out-of-range value. */
 int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits);
 /* GEMMs with at most 16 rows of A (decode steps) run a weight-streaming

@@ -27,25 +27,28 @@ GPT2_LARGE = dict(n_layer=36, n_head=20, n_embd=1280, vocab_size=50257, n_positi
 
 
 def test_captured_c2_forward_full_size_vs_oracle(gpu):
-    """bench.py's C2 graph: every replay at the fp32 matmul/attention bar
-    (1e-3 normwise, checked at 1e-4), replays bitwise identical to each other
-    with eager work between them, greedy picks equal to the oracle's."""
+    """The C2 graph with unpacked fp32 weights (the tiled split-K GEMMs and
+    qkv_attention): every replay at the fp32 matmul/attention bar (1e-3
+    normwise, checked at 1e-4), replays bitwise identical to each other with
+    eager work between them, greedy picks equal to the oracle's."""
     from applegpu_runtime.models import gpt2 as G
-    print("C2 captured forward: 12x768, seq 128", flush=True)
+    print("C2 captured forward: 12x768, seq 128, unpacked weights", flush=True)
     wnp = G.random_weights(GPT2_SMALL, seed=42)
-    model = G.load_model(wnp, GPT2_SMALL)
+    model = G.load_model(wnp, GPT2_SMALL, x3=False)
     ids = np.random.default_rng(42).integers(0, GPT2_SMALL["vocab_size"], 128).astype(np.int32)
     _check_c2_graph(gpu, G, model, wnp, ids)
 
 
 def test_captured_c2_forward_packed_weights_vs_oracle(gpu):
-    """The same graph with the fp32 projection weights packed as bf16 hi/lo
-    fragments (load_model(x3=True)): the row-panel GEMMs with layer_norm in
-    their prologue and the packed split-K GEMM."""
+    """bench.py's C2 graph: the fp32 projection weights packed as bf16 hi/lo
+    fragments (load_model's default), activations passed as packed rows
+    written by the embedding, the layer_norm reductions and the fc epilogue,
+    the packed-A row panels and split GEMMs."""
     from applegpu_runtime.models import gpt2 as G
-    print("C2 captured forward, packed fp32 weights", flush=True)
+    print("C2 captured forward, packed fp32 weights and rows", flush=True)
     wnp = G.random_weights(GPT2_SMALL, seed=42)
-    model = G.load_model(wnp, GPT2_SMALL, x3=True)
+    model = G.load_model(wnp, GPT2_SMALL)
+    assert model["x3"]
     ids = np.random.default_rng(42).integers(0, GPT2_SMALL["vocab_size"], 128).astype(np.int32)
     _check_c2_graph(gpu, G, model, wnp, ids)
 

@@ -168,3 +168,153 @@ def test_row_panel_residual_epilogue_bitwise_stable(gpu):
         outs.append(z.to_numpy())
     np.testing.assert_array_equal(outs[0], outs[1])
     assert rel_err(outs[0], r + O.add_bias(O.matmul(a, b), bias)) < 1e-4
+
+
+# ── packed activation rows (pack_rows_x3 + matmul_pp) ─────────────────────
+def test_pack_rows_layout_bit_exact(gpu):
+    """Rows are packed in the weights' layout with rows in place of columns:
+    pack_rows_x3(x) == pack_weight_x3(x^T), zero past the last row."""
+    x = f32(45, 64)
+    pk = gpu.pack_rows_x3(gpu.from_numpy(x))
+    assert pk.shape == [2, 4, 2, 64, 8]
+    np.testing.assert_array_equal(_bits_of(pk), _packed_ref(np.ascontiguousarray(x.T)))
+    # a strided view packs the values it shows
+    base = f32(40, 80)
+    v = gpu.slice(gpu.from_numpy(base), 1, 8, 40)
+    np.testing.assert_array_equal(_bits_of(gpu.pack_rows_x3(v)), _packed_ref(np.ascontiguousarray(base[:, 8:40].T)))
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 768, 2304), (128, 768, 3072), (128, 3072, 768), (33, 256, 96),
+                                   (1, 768, 768), (100, 1280, 160), (64, 1536, 64), (40, 2048, 48), (7, 16, 40)])
+def test_matmul_pp_matches_oracle(gpu, M, K, N):
+    """Both operands packed: row-panel plans for K = 256..1536 (K % 256 ==
+    0), split-K plans otherwise; at the fp32 bar."""
+    a, b = f32(M, K), f32(K, N, scale=0.05)
+    apk = gpu.pack_rows_x3(gpu.from_numpy(a))
+    got = gpu.matmul_pp(apk, M, gpu.pack_weight_x3(gpu.from_numpy(b)), N).to_numpy()
+    assert got.shape == (M, N)
+    assert rel_err(got, O.matmul(a, b)) < 1e-4
+
+
+def test_matmul_pp_exact_small_integers(gpu):
+    a = RNG.integers(-3, 4, (70, 256)).astype(np.float32)
+    b = RNG.integers(-3, 4, (256, 96)).astype(np.float32)
+    got = gpu.matmul_pp(gpu.pack_rows_x3(gpu.from_numpy(a)), 70, gpu.pack_weight_x3(gpu.from_numpy(b)), 96)
+    np.testing.assert_array_equal(got.to_numpy(), a @ b)
+
+
+def test_matmul_pp_rejects_mismatches(gpu):
+    apk = gpu.pack_rows_x3(gpu.from_numpy(f32(40, 64)))
+    pk = gpu.pack_weight_x3(gpu.from_numpy(f32(64, 32)))
+    with pytest.raises(ValueError, match="matmul_pp"):
+        gpu.matmul_pp(apk, 70, pk, 32).eval()           # 70 rows need 3 strips, not 2
+    with pytest.raises(ValueError, match="matmul_pp"):
+        gpu.matmul_pp(apk, 40, gpu.pack_weight_x3(gpu.from_numpy(f32(48, 32))), 32).eval()  # K 64 vs 48
+    with pytest.raises(ValueError, match="pack_rows_x3"):
+        gpu.pack_rows_x3(gpu.from_numpy(f32(8, 40))).eval()
+
+
+@pytest.mark.parametrize("M,K,N,N2", [(128, 768, 768, 3072), (128, 3072, 768, 2304), (50, 512, 256, 96)])
+def test_reduction_writes_packed_layer_norm_rows(gpu, M, K, N, N2):
+    """The split-K reduction that computes layer_norm(r + x W + b) writes it
+    straight as packed rows for the next product: the same bits as the
+    layer_norm stored in fp32 and packed by its own launch (forced by holding
+    the layer_norm tensor), one launch fewer, and at the fp32 bar against the
+    oracle."""
+    x, w, bias, r = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1), f32(M, N)
+    g, be = f32(N, scale=0.5) + 1.0, f32(N, scale=0.1)
+    w2, b2 = f32(N, N2, scale=0.05), f32(N2, scale=0.1)
+    dev = [gpu.from_numpy(a) for a in (x, bias, r, g, be, b2)]
+    pk_w, pk_w2 = gpu.pack_weight_x3(gpu.from_numpy(w)), gpu.pack_weight_x3(gpu.from_numpy(w2))
+    for t in dev + [pk_w, pk_w2]:
+        t.eval()
+    xd, bd, rd, gd, bed, bd2 = dev
+    outs, ln_np = [], None
+    for keep in (False, True):
+        z = rd + gpu.add_bias(gpu.matmul_packed(xd, pk_w, N), bd)
+        ln = gpu.layer_norm(z, gd, bed)
+        y = gpu.add_bias(gpu.matmul_pp(gpu.pack_rows_x3(ln), M, pk_w2, N2), bd2)
+        if not keep:
+            del ln
+        before = gpu.graph_stats()
+        y.eval()
+        after = gpu.graph_stats()
+        outs.append((z.to_numpy(), y.to_numpy(), after["launcher_calls"] - before["launcher_calls"]))
+        if keep:
+            ln_np = ln.to_numpy()
+            del ln
+    (z0, y0, n0), (z1, y1, n1) = outs
+    np.testing.assert_array_equal(z0, z1)
+    np.testing.assert_array_equal(y0, y1)
+    assert n0 == n1 - 1, (n0, n1)
+    np.testing.assert_allclose(ln_np, O.layer_norm(z1, g, be), rtol=1e-5, atol=1e-5)
+    ref = O.add_bias(O.matmul(O.layer_norm(r + O.add_bias(O.matmul(x, w), bias), g, be), w2), b2)
+    assert rel_err(y0, ref) < 1e-4
+
+
+@pytest.mark.parametrize("M,K,N,N2", [(128, 768, 3072, 768), (70, 256, 512, 64)])
+def test_gemm_epilogue_writes_packed_gelu_rows(gpu, M, K, N, N2):
+    """gelu(pack_rows(x) W + b) feeding another packed product: the row-panel
+    epilogue writes the packed rows itself (no fp32 store, no pack launch);
+    bitwise equal to the stored-then-packed path and at the fp32 bar."""
+    x, w, bias = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1)
+    w2, b2 = f32(N, N2, scale=0.05), f32(N2, scale=0.1)
+    pk_w, pk_w2 = gpu.pack_weight_x3(gpu.from_numpy(w)), gpu.pack_weight_x3(gpu.from_numpy(w2))
+    bd, bd2 = gpu.from_numpy(bias), gpu.from_numpy(b2)
+    apk = gpu.pack_rows_x3(gpu.from_numpy(x))
+    for t in (pk_w, pk_w2, bd, bd2, apk):
+        t.eval()
+    res, f_np = [], None
+    for keep in (False, True):
+        f = gpu.gelu(gpu.add_bias(gpu.matmul_pp(apk, M, pk_w, N), bd))
+        y = gpu.add_bias(gpu.matmul_pp(gpu.pack_rows_x3(f), M, pk_w2, N2), bd2)
+        if not keep:
+            del f
+        before = gpu.graph_stats()
+        y.eval()
+        after = gpu.graph_stats()
+        res.append((y.to_numpy(), after["launcher_calls"] - before["launcher_calls"]))
+        if keep:
+            f_np = f.to_numpy()
+            del f
+    (y0, n0), (y1, n1) = res
+    np.testing.assert_array_equal(y0, y1)
+    assert n0 == n1 - 1, (n0, n1)
+    f_ref = O.gelu_tanh(O.add_bias(O.matmul(x, w), bias))
+    assert rel_err(f_np, f_ref) < 1e-4
+    assert rel_err(y0, O.add_bias(O.matmul(f_ref, w2), b2)) < 1e-4
+
+
+def test_embedding_writes_packed_layer_norm_rows(gpu):
+    """token + position embedding -> layer_norm -> packed rows: one fused
+    embedding launch writes the packed rows; same bits as packing the stored
+    layer_norm, and the product at the fp32 bar."""
+    V, P, T, D, N = 97, 64, 50, 128, 96
+    wte, wpe = f32(V, D), f32(P, D, scale=0.3)
+    g, be = f32(D, scale=0.5) + 1.0, f32(D, scale=0.1)
+    w = f32(D, N, scale=0.05)
+    ids = RNG.integers(0, V, T).astype(np.int32)
+    pos = np.arange(T, dtype=np.int32)
+    dev = [gpu.from_numpy(a) for a in (wte, wpe, g, be, ids, pos)]
+    pk_w = gpu.pack_weight_x3(gpu.from_numpy(w))
+    for t in dev + [pk_w]:
+        t.eval()
+    wte_d, wpe_d, g_d, be_d, ids_d, pos_d = dev
+    res = []
+    for keep in (False, True):
+        e = gpu.embedding(wte_d, ids_d) + gpu.embedding(wpe_d, pos_d)
+        ln = gpu.layer_norm(e, g_d, be_d)
+        y = gpu.matmul_pp(gpu.pack_rows_x3(ln), T, pk_w, N)
+        if not keep:
+            del ln
+        before = gpu.graph_stats()
+        y.eval()
+        after = gpu.graph_stats()
+        res.append((y.to_numpy(), after["launcher_calls"] - before["launcher_calls"]))
+        if keep:
+            del ln
+    (y0, n0), (y1, n1) = res
+    np.testing.assert_array_equal(y0, y1)
+    assert n0 == n1 - 1, (n0, n1)
+    ref = O.matmul(O.layer_norm(wte[ids] + wpe[pos], g, be), w)
+    assert rel_err(y0, ref) < 1e-4

@@ -91,7 +91,7 @@ def test_gpt2_forward_without_cache_is_identical(gpu):
     from oracle import models as M
     cfg = {"vocab_size": 500, "n_positions": 128, "n_embd": 128, "n_layer": 2, "n_head": 2}
     w = G.random_weights(cfg, seed=5)
-    model = G.load_model(w, cfg)
+    model = G.load_model(w, cfg, x3=False)   # qkv_attention serves unpacked fp32 weights
     ids = RNG.integers(0, cfg["vocab_size"], 40).astype(np.int32)
     a, cache_a = G.gpt2_forward(model, ids)
     b, cache_b = G.gpt2_forward(model, ids, need_cache=False)
