@@ -253,8 +253,17 @@ void Pool::release(Buffer* b) {
       if (b->arena->capturing) b->arena->free[b->bytes].push_back(b);
       return;
     }
-    // Nothing is freed while a capture records the stream.
-    keep = active_ != nullptr || pooled_ + b->bytes <= watermark_;
+    if (active_) {
+      // Allocated before the capture and let go during it: a recorded kernel
+      // may read it (an input of the graph), so it stays with the graph until
+      // the graph is destroyed: neither reused by the graph's later nodes
+      // (a replay would read what they wrote) nor by work after the capture.
+      b->arena = active_;
+      active_->owned.push_back(b);
+      active_->bytes += b->bytes;
+      return;
+    }
+    keep = pooled_ + b->bytes <= watermark_;
     if (keep) {
       buckets_[b->bytes].push_back(b);
       pooled_ += b->bytes;

@@ -78,3 +78,30 @@ def test_capture_errors(gpu):
     assert lib.applegpu_graph_replay(10 ** 9) == -1
     g.destroy()
     assert lib.applegpu_graph_replay(g.handle if g.handle else 10 ** 9 + 1) == -1
+
+
+def test_input_released_during_capture_stays_with_the_graph(gpu):
+    """A tensor made before the capture whose last reference goes away inside
+    it (here: the captured op's input, dropped by the graph walk once read)
+    is an input of every replay: its storage must not be handed to tensors
+    made after the capture, nor to the graph's own later nodes."""
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((256, 256)).astype(np.float32)
+    held = [gpu.relu(gpu.from_numpy(a))]
+    held[0].eval()
+
+    def fn():
+        y = held.pop()                 # the only reference, dropped during the capture
+        return gpu.exp(y) + gpu.neg(y)
+
+    g = gpu.capture(fn)
+    want = np.exp(np.maximum(a, 0)) - np.maximum(a, 0)
+    for rep in range(3):
+        # same-size tensors made and written after the capture
+        others = [gpu.from_numpy(np.full((256, 256), 7.0 + i, np.float32)) for i in range(6)]
+        for t in others:
+            t.eval()
+        g.replay()
+        np.testing.assert_allclose(g.outputs.to_numpy(), want, rtol=1e-6, atol=1e-6, err_msg=f"replay {rep}")
+        del others
+    g.destroy()

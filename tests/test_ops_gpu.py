@@ -65,8 +65,15 @@ def test_rows_vs_golden(gpu, fixtures, name):
     np.testing.assert_allclose(gpu.log_softmax(tx).to_numpy(), fixtures[f"log_softmax_{name}_y"], rtol=1e-5,
                                atol=1e-5)
     g, b = gpu.from_numpy(fixtures[f"layer_norm_{name}_g"]), gpu.from_numpy(fixtures[f"layer_norm_{name}_b"])
-    np.testing.assert_allclose(gpu.layer_norm(tx, g, b).to_numpy(), fixtures[f"layer_norm_{name}_y"],
-                               rtol=1e-5, atol=2e-5)
+    _check_norm(gpu.layer_norm(tx, g, b).to_numpy(), fixtures[f"layer_norm_{name}_y"])
+
+
+def _check_norm(got, ref):
+    """The 1e-5 relative bar for norms: normwise, and per element with an
+    absolute floor of 1e-6 of the output scale for values that cancel to
+    near zero (gamma * x_hat + beta)."""
+    assert rel_err(got, ref) < 1e-5
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-6 * max(1.0, float(np.abs(ref).max())))
 
 
 @pytest.mark.parametrize("shape", [(1, 1), (3, 5), (17, 255), (4, 256), (5, 1024), (2, 2047), (2, 2049),
@@ -85,7 +92,7 @@ def test_layer_norm_shapes(gpu, shape):
     x = f32(*shape, scale=2.0) + 1.5
     g, b = f32(shape[-1]), f32(shape[-1])
     got = gpu.layer_norm(gpu.from_numpy(x), gpu.from_numpy(g), gpu.from_numpy(b)).to_numpy()
-    np.testing.assert_allclose(got, O.layer_norm(x, g, b), rtol=1e-5, atol=2e-5)
+    _check_norm(got, O.layer_norm(x, g, b))
 
 
 @pytest.mark.parametrize("dt,tol", [("float16", 1e-2), ("bfloat16", 2e-2)])
