@@ -1,6 +1,7 @@
 """Benchmark of the MI355X backend on BASELINE.json's headline metric:
 GPT-2-small forward ms at seq 128 (config 2) + MLP h=4096 train ms/step
-(config 3), on one MI355X, with the roofline fraction of the dominant kernel.
+(config 3), on one MI355X, with the roofline fraction of the kernel that
+takes the most time per step.
 
 A step = one GPT-2-small fp32 forward over 128 token ids (the lazy graph of
 the reference's gpt2_forward recipe) + one training step of
@@ -13,13 +14,23 @@ MLP) and inputs synthetic, seeded; everything is resident in HBM before the
 timed region.  value = gpt2_fwd_ms + mlp_train_ms, each the mean over
 --steps replays bracketed by stream synchronisations.
 
-Roofline: the dominant single kernel of the step, the MLP weight-gradient
-GEMM dW = g^T h (M = N = 4096, K = 256; fp32 operands split into bf16 hi/lo,
-three bf16 MFMAs per product), timed with HIP events on the library stream
-over back-to-back launches; algorithmic work 2*M*N*K flop per launch.  Its
-HBM traffic comes from the rocprofv3 --pmc summaries committed under
-profiles/ (FETCH_SIZE, WRITE_SIZE of that kernel, scaled by the same counters
-read for the 256 MiB calibration copy this script runs), when present.
+Roofline (`roofline`): the kernel with the largest time per step, the
+packed-A row-panel GEMM gemm_x3_rows_pk<6> of GPT-2's qkv (128 x 768 x 2304,
+bias) and fc (128 x 768 x 3072, bias + gelu, output written as packed rows)
+projections, 24 launches per forward.  Both operands are pre-split bf16 hi/lo
+MFMA fragments (three bf16 MFMAs per product) and the weights are read once
+per launch, so the kernel is bound by HBM: algorithmic bytes per launch =
+packed A + packed weights + bias + output.  Its launch duration is timed with
+HIP events on the library stream over a captured graph of back-to-back
+launches that rotate through 40 weight sets per shape (more than the 256 MB
+Infinity Cache holds, so the weights stream from HBM as in the forward).
+The same launches in MFMA terms are reported beside it (against the fp32
+MFMA peak and against the bf16x3 ceiling, one third of the bf16 MFMA peak).
+`roofline_mlp_dw` is the MLP weight-gradient GEMM with its SGD step
+(W += -lr g^T h, M = N = 4096, K = 256), MFMA-bound.  HBM traffic comes from
+the rocprofv3 --pmc summaries committed under profiles/ (FETCH_SIZE,
+WRITE_SIZE of each kernel, scaled by the same counters read for the 256 MiB
+calibration copy this script runs), when present.
 
 Prints ONE JSON line.  `python bench.py --gpus N` with N > 1 exits: this
 build runs on one GPU.
@@ -48,6 +59,8 @@ MLP_BATCH = 256
 SEQ = 128
 CALIB_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mlp_dw_gemm_traffic.json")
+PROJ_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gpt2_proj_gemm_traffic.json")
+BF16X3_CEILING_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 
 
 def gpt2_flops(cfg, T):
@@ -67,14 +80,65 @@ def mlp_flops(sizes, B):
     return f
 
 
-def load_traffic():
-    """HBM bytes per launch of the roofline kernel from the committed PMC summary."""
+def load_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch of a roofline kernel from a committed PMC summary."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             t = json.load(f)
         return float(t["bytes_per_launch"]), t
     except (OSError, KeyError, ValueError):
         return None, None
+
+
+PROJ_SHAPES = (("qkv", 2304, False), ("fc", 3072, True))
+
+
+def proj_gemm_roofline(gpu, lib, rng, reps=4, nw=40):
+    """The dominant kernel, as the forward runs it: packed rows [128, 768]
+    times packed weights of each shape, bias (qkv) or bias + gelu with the
+    output written as packed rows (fc).  Each shape: one captured graph of
+    `nw` launches over `nw` weight sets, replayed `reps` times between HIP
+    events on the library stream."""
+    M, K = SEQ, GPT2_CFG["n_embd"]
+    a = gpu.from_numpy(rng.standard_normal((M, K), dtype=np.float32))
+    apk = gpu.pack_rows_x3(a)
+    apk.eval()
+    out = {}
+    for name, N, gelu in PROJ_SHAPES:
+        ws = [gpu.pack_weight_x3(gpu.from_numpy(rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)))
+              for _ in range(nw)]
+        bias = gpu.from_numpy(np.zeros(N, np.float32))
+        for t in ws + [bias]:
+            t.eval()
+
+        def launches():
+            outs = []
+            for w in ws:
+                y = gpu.add_bias(gpu.matmul_pp(apk, M, w, N), bias)
+                y = gpu.pack_rows_x3(gpu.gelu(y)) if gelu else y
+                y.eval()
+                outs.append(y)
+            return outs[-1]
+
+        before = gpu.graph_stats()["launcher_calls"]
+        g = gpu.capture(launches)
+        calls = gpu.graph_stats()["launcher_calls"] - before
+        if calls != nw:
+            raise RuntimeError(f"{name}: {calls} launches for {nw} products (epilogue not fused)")
+        g.replay()
+        lib.applegpu_ffi_synchronize()
+        lib.applegpu_ffi_event_record(0)
+        for _ in range(reps):
+            g.replay()
+        lib.applegpu_ffi_event_record(1)
+        ms = lib.applegpu_ffi_event_elapsed_ms(0, 1) / (reps * nw)
+        g.destroy()
+        # packed A, packed weights (hi + lo), bias, output (fp32 or packed hi + lo)
+        nbytes = 4 * M * K + 4 * K * N + 4 * N + 4 * M * N
+        out[name] = {"M": M, "N": N, "K": K, "avg_launch_ms": round(ms, 5), "algorithmic_bytes": nbytes,
+                     "flop": 2 * M * N * K, "epilogue": "bias + gelu, packed-row output" if gelu else "bias"}
+        del ws
+    return out
 
 
 def main():
@@ -224,6 +288,15 @@ def main():
     lib.applegpu_ffi_gemm_plan(M_, N_, K_, 1, 0, False, False, plan, 96)
     traffic, tinfo = load_traffic()
 
+    # ── roofline: the dominant kernel (GPT-2's packed qkv / fc projections) ──
+    shapes = proj_gemm_roofline(gpu, lib, rng)
+    p_ms = sum(v["avg_launch_ms"] for v in shapes.values())
+    p_bytes = sum(v["algorithmic_bytes"] for v in shapes.values())
+    p_flop = sum(v["flop"] for v in shapes.values())
+    p_gbs = p_bytes / (p_ms * 1e-3) / 1e9
+    p_tflops = p_flop / (p_ms * 1e-3) / 1e12
+    p_traffic, p_tinfo = load_traffic(PROJ_TRAFFIC_FILE)
+
     result = {
         "metric": METRIC,
         "value": round(ms_per_step, 4),
@@ -251,6 +324,28 @@ def main():
             "device": dev,
         },
         "roofline": {
+            "kernel": "gemm_x3_rows_pk<6>: packed-A row-panel GEMM of GPT-2's qkv and fc projections "
+                      "(bf16 hi/lo fragments of both operands, 8 wavefronts x 6 k-steps, whole K per block); "
+                      "one qkv + one fc launch",
+            "bound": "hbm",
+            "achieved": round(p_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(p_gbs / HBM_PEAK_GBS, 4),
+            "traffic": p_traffic,
+            "avg_launch_ms": round(p_ms / len(shapes), 5),
+            "shapes": shapes,
+            "mfma_view": {
+                "achieved_tflops_fp32_equiv": round(p_tflops, 2),
+                "frac_fp32_peak": round(p_tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+                "bf16x3_ceiling_tflops": round(BF16X3_CEILING_TFLOPS, 1),
+                "frac_bf16x3_ceiling": round(p_tflops / BF16X3_CEILING_TFLOPS, 4),
+            },
+            "timing": "captured graph of 40 back-to-back launches per shape over 40 weight sets (cold, as in "
+                      "the forward), HIP events on the library stream",
+            "traffic_source": os.path.relpath(PROJ_TRAFFIC_FILE, ROOT) if p_tinfo else None,
+        },
+        "roofline_mlp_dw": {
             "kernel": "gemm_mf W += -lr * g^T h (MLP weight gradient with its SGD step in the epilogue; "
                       "M=4096 N=4096 K=256, fp32 via bf16x3), plan " + plan.value.decode(),
             "bound": "mfma",
@@ -262,6 +357,7 @@ def main():
             "avg_launch_ms": round(gemm_ms, 5),
             "flop_per_launch": gemm_flop,
             "bf16_mfma_utilisation": round(3 * achieved / BF16_MFMA_PEAK_TFLOPS, 4),
+            "frac_bf16x3_ceiling": round(achieved / BF16X3_CEILING_TFLOPS, 4),
             "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if tinfo else None,
         },
     }
