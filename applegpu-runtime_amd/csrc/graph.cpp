@@ -643,6 +643,42 @@ void eval_all(const std::vector<TensorP>& roots) {
     }
   }
 
+  // Read-ahead of packed weights: a launch that leaves most CUs idle (a
+  // split-K layer_norm reduction, the fused embedding) gets
+  // extra blocks that read the packed weights of the GEMMs after it, up to
+  // and including the next such launch, so that those GEMMs find their
+  // weights in the Infinity Cache instead of HBM (GPT-2 small forward
+  // 0.695 -> 0.681 ms; spreading the reads more evenly over the launches
+  // measured slower).  Results are unchanged.
+  std::vector<k::Prefetch> pf_for(order.size());
+  {
+    auto x3_weights = [&](size_t j) -> const Tensor* {
+      auto it = groups.find(order[j].get());
+      if (it == groups.end() || absorbed.count(order[j].get())) return nullptr;
+      const Group& g = it->second;
+      if (g.packed_n <= 0 || !ops::is_x3_packed(g.b) || g.b->pending() || !g.b->buf) return nullptr;
+      return g.b.get();
+    };
+    auto reads_ahead = [&](size_t j) {
+      Tensor* t = order[j].get();
+      if (absorbed.count(t)) return false;
+      if (groups.count(t)) return post_ln.count(t) > 0;
+      return emb_adds.count(t) > 0;
+    };
+    for (size_t i = 0; i < order.size(); ++i) {
+      if (!reads_ahead(i)) continue;
+      k::Prefetch& pf = pf_for[i];
+      for (size_t j = i + 1; j < order.size() && pf.n < 3; ++j) {
+        if (const Tensor* w = x3_weights(j)) {
+          pf.ptr[pf.n] = w->data();
+          pf.bytes[pf.n] = (int64_t)w->nbytes();
+          ++pf.n;
+        }
+        if (reads_ahead(j)) break;
+      }
+    }
+  }
+
   for (size_t i = 0; i < order.size(); ++i) {
     TensorP t = order[i];
     // Absorbed into a fused GEMM, or already filled by its multi-output
@@ -651,6 +687,7 @@ void eval_all(const std::vector<TensorP>& roots) {
       order[i].reset();
       continue;
     }
+    k::set_prefetch(pf_for[i]);
     Node* n = t->node.get();
     auto git = groups.find(t.get());
     auto cit = chains.find(t.get());
@@ -769,6 +806,7 @@ void eval_all(const std::vector<TensorP>& roots) {
     assign(t, res[0]);
     order[i].reset();
   }
+  k::set_prefetch(k::Prefetch{});
 }
 
 }  // namespace agpu

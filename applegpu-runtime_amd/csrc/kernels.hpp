@@ -223,6 +223,17 @@ struct X3Plan {
   int kt = 1, splits = 1;
 };
 X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus, bool apk = false, bool split = false);
+// Read-ahead of the next GEMMs' weights: the ranges set here are read by
+// extra blocks of the next launch that supports it (the split-K layer_norm
+// reductions, fp32 fused attention, the fused embedding), which then clears
+// them; any other launch leaves them set.  Up to three ranges.
+struct Prefetch {
+  const void* ptr[3] = {nullptr, nullptr, nullptr};
+  int64_t bytes[3] = {0, 0, 0};
+  int n = 0;
+};
+void set_prefetch(const Prefetch& pf);
+Prefetch take_prefetch();
 // Packed x3 rows of an fp32 matrix X [M, K] read through strides (x_sm,
 // x_sk), K % 16 == 0: the A-operand counterpart of pack_weights_x3
 // (packed_x3_elems(K, M) bf16 elements).

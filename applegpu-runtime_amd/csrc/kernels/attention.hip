@@ -46,6 +46,7 @@ struct AArgs {
   // NSP > 0 partials `plane` elements apart) plus a bias, b_sh per head
   const float* qb; const float* kb; const float* vb;
   int64_t b_sh, plane;
+  PfArgs pf;  // read-ahead blocks (fp32 kernel)
 };
 
 // Four consecutive fp32 values: a plain load, or (NSP > 0) the sum of NSP
@@ -533,6 +534,7 @@ struct FaTile32 {
 template <int D, bool KSPLIT, int NSP>
 __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
   static_assert(D % 64 == 0, "d must be a multiple of 64");
+  if (prefetch_block(p.pf)) return;
   constexpr int QB_ROWS = KSPLIT ? 16 : kFaWaves * 16;  // query rows per block
   constexpr int NT = KSPLIT ? 1 : 4;  // 16-key sub-tiles per wavefront and tile (KSPLIT: sub-tile w)
   constexpr int KP = D + 4;          // K and V tile row pitch (floats)
@@ -795,7 +797,10 @@ static void launch_fa32_d(const AArgs& p, int nsp, unsigned blocks, hipStream_t 
 }
 
 template <bool KS>
-static void launch_fa32(const AArgs& p, const Attn& a, unsigned blocks, hipStream_t s) {
+static void launch_fa32(const AArgs& p0, const Attn& a, unsigned blocks, hipStream_t s) {
+  AArgs p = p0;
+  p.pf = make_prefetch((int)blocks, 64 * kFaWaves);
+  blocks += (unsigned)p.pf.blocks;
   if (a.D == 64) launch_fa32_d<KS, 64>(p, a.nsplit, blocks, s);
   else launch_fa32_d<KS, 128>(p, a.nsplit, blocks, s);
 }

@@ -42,6 +42,41 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x / (1.f + expf(-2.f * u));
 }
 
+// Read-ahead blocks: a launch may carry extra blocks that read one dword of
+// every 64-byte line of up to three ranges (the weights of the next GEMMs),
+// so that those lines are in the memory-side Infinity Cache and the L2 when
+// the GEMMs run; blocks from `first` on do this and return before anything
+// else (no barrier is reached).  The loaded values feed an empty asm
+// statement, so the loads are kept, and nothing is stored.
+struct PfArgs {
+  const char* p[3];
+  int64_t lines[3];
+  int n;
+  int first;   // first read-ahead block (gridDim.x when there are none)
+  int blocks;  // read-ahead blocks
+};
+__device__ __forceinline__ bool prefetch_block(const PfArgs& pf) {
+  if ((int)blockIdx.x < pf.first) return false;
+  const int64_t stride = (int64_t)pf.blocks * blockDim.x;
+  const int64_t t0 = (int64_t)(blockIdx.x - pf.first) * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  for (int r = 0; r < pf.n; ++r) {
+#pragma unroll 4
+    for (int64_t l = t0; l < pf.lines[r]; l += stride) acc ^= *(const uint32_t*)(pf.p[r] + (l << 6));
+  }
+  asm volatile("" ::"v"(acc));
+  return true;
+}
+
+}  // namespace dev
+namespace k {
+// Read-ahead blocks for a launch of `main` blocks of `threads` threads: the
+// pending ranges (take_prefetch, which clears them), one block per 32 KB of
+// lines, at most 256; none when no range is pending.
+dev::PfArgs make_prefetch(int main, int threads);
+}  // namespace k
+namespace dev {
+
 // Launch geometry helpers
 inline unsigned blocks_for(int64_t n, int per_block) {
   int64_t b = (n + per_block - 1) / per_block;

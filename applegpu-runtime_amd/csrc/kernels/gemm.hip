@@ -256,6 +256,7 @@ __device__ __forceinline__ void st4(T* dst, const float (&v)[4]) {
 
 template <typename T, int NV, int MS>  // MS: partials loaded up front; more are added afterwards
 __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
+  if (prefetch_block(p.pf)) return;
   const int lane = threadIdx.x & 63;
   // one wavefront per row; a block holds blockDim.x / 64 rows
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -356,6 +357,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln(GArgs p) {
 template <typename T, int NV, int MQ>  // MQ: splits per wave loaded up front
 __global__ void __launch_bounds__(256) splitk_reduce_ln_mw(GArgs p) {
   __shared__ float sum_w[3][NV * 256];
+  if (prefetch_block(p.pf)) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = blockIdx.x;
   const int64_t N = p.N, total = p.M * p.N;
@@ -461,14 +463,18 @@ __global__ void __launch_bounds__(256) splitk_reduce_ln_mw(GArgs p) {
 }
 
 template <typename T, int NV>
-void launch_reduce_ln_nv(const GArgs& p, dim3 grid, dim3 block, hipStream_t s) {
+void launch_reduce_ln_nv(const GArgs& p0, dim3 grid, dim3 block, hipStream_t s) {
+  GArgs p = p0;
   if (p.splits > 8) {
     // one 4-wave block per row
-    const dim3 g2((unsigned)p.M), b2(256);
+    p.pf = make_prefetch((int)p.M, 256);
+    const dim3 g2((unsigned)(p.M + p.pf.blocks)), b2(256);
     if (p.splits <= 16) hipLaunchKernelGGL((splitk_reduce_ln_mw<T, NV, 4>), g2, b2, 0, s, p);
     else hipLaunchKernelGGL((splitk_reduce_ln_mw<T, NV, 8>), g2, b2, 0, s, p);
     return;
   }
+  p.pf = make_prefetch((int)grid.x, (int)block.x);
+  grid.x += p.pf.blocks;
   if (p.splits <= 2) hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 2>), grid, block, 0, s, p);
   else if (p.splits <= 4) hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 4>), grid, block, 0, s, p);
   else hipLaunchKernelGGL((splitk_reduce_ln<T, NV, 8>), grid, block, 0, s, p);
@@ -668,6 +674,7 @@ Plan make_plan(const Gemm& g, int cus) {
 
 GArgs make_args(const Gemm& g, const Plan& pl) {
   GArgs p{};
+  p.pf.first = 0x7fffffff;  // no read-ahead blocks unless a launcher adds them
   p.A = g.A; p.B = g.B; p.C = g.C;
   p.M = g.M; p.N = g.N; p.K = g.K;
   p.a_sm = g.a_sm; p.a_sk = g.a_sk; p.a_sb = g.a_sb;
@@ -921,6 +928,43 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   }
   check_launch("gemm_mfma");
   reduce_splits(g, p, s);
+}
+
+namespace {
+Prefetch& pending_prefetch() {
+  static Prefetch pf;
+  return pf;
+}
+}  // namespace
+
+void set_prefetch(const Prefetch& pf) { pending_prefetch() = pf; }
+
+Prefetch take_prefetch() {
+  Prefetch pf = pending_prefetch();
+  pending_prefetch() = Prefetch{};
+  return pf;
+}
+
+PfArgs make_prefetch(int main, int threads) {
+  PfArgs a{};
+  a.first = main;
+  const Prefetch pf = take_prefetch();
+  int64_t lines = 0;
+  for (int i = 0; i < pf.n && i < 3; ++i) {
+    if (!pf.ptr[i] || pf.bytes[i] < 64) continue;
+    a.p[a.n] = (const char*)pf.ptr[i];
+    a.lines[a.n] = pf.bytes[i] >> 6;
+    lines += a.lines[a.n];
+    ++a.n;
+  }
+  if (!a.n) return a;
+  // one thread per line per pass; 32 KB (512 lines) per block, at most 256
+  // blocks (more blocks measured slower: their dispatch lengthens the launch)
+  int64_t blocks = (lines + 511) / 512;
+  blocks = blocks < 1 ? 1 : blocks > 256 ? 256 : blocks;
+  (void)threads;
+  a.blocks = (int)blocks;
+  return a;
 }
 
 // The split-K tail of a launch: partial sums in p.ws are reduced (in split

@@ -41,6 +41,7 @@ struct GArgs {
   bool a_x3;
   bf16_t* c_pk;
   bf16_t* pln_ypk;
+  PfArgs pf;  // read-ahead blocks (split-K layer_norm reductions)
 };
 
 // Epilogue operands of one output, loadable ahead of the product (they do

@@ -369,26 +369,18 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
 // bits).  Without a split they apply the epilogue, whose operands they load
 // while the products run, and write C (fp32) and/or, as packed x3 rows,
 // c_pk (N % 16 == 0) for the next packed-A GEMM; with one, the split's sums
-// go to the workspace for the split-K reduction.  Blocks of one column strip
-// share an XCD, as in gemm_x3_rows.
+// go to the workspace for the split-K reduction.  Block ids run along the
+// columns (tm = id / tiles_n): with cold weights this measured faster than
+// dealing the row tiles of one column strip to one XCD back to back (qkv's
+// weight loads 8.7 vs 10.5 us), whose simultaneous misses on the same lines
+// are not merged.
 template <int KPW>
 __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
   constexpr int W = 8;
   const int64_t T = p.K >> 4;
   __shared__ __attribute__((aligned(16))) float red[W * 16 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int tm, tn;
-  {
-    const int id = blockIdx.x;
-    if ((p.tiles_n & 7) == 0) {
-      const int g = id / (8 * p.tiles_m), r = id % (8 * p.tiles_m);
-      tm = r / 8;
-      tn = g * 8 + (r & 7);
-    } else {
-      tm = id / p.tiles_n;
-      tn = id % p.tiles_n;
-    }
-  }
+  const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x % p.tiles_n;
   const int64_t m0 = (int64_t)tm * 32, n0 = (int64_t)tn * 32;
   const int64_t t0 = (int64_t)blockIdx.y * (W * KPW) + (int64_t)wave * KPW;
 

@@ -435,7 +435,8 @@ __global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, 
                                                       T* __restrict__ x, const T* __restrict__ g,
                                                       const T* __restrict__ b, T* __restrict__ y,
                                                       bf16_t* __restrict__ ypk, int64_t rows, int64_t cols, float eps,
-                                                      bool vec) {
+                                                      bool vec, PfArgs pf) {
+  if (prefetch_block(pf)) return;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // one wavefront per row
   if (row >= rows) return;
@@ -1013,15 +1014,17 @@ template <typename T, typename I, int NV>
 void ea_nv(const EaArgs& a, hipStream_t s) {
   // up to 1024 rows, one row per block: the rows reach as many CUs
   const int rpb = a.rows <= 1024 ? 1 : kRowsPerBlock;
-  const dim3 grid((unsigned)((a.rows + rpb - 1) / rpb)), block(64 * rpb);
+  const unsigned main = (unsigned)((a.rows + rpb - 1) / rpb);
+  const PfArgs pf = make_prefetch((int)main, 64 * rpb);
+  const dim3 grid(main + (unsigned)pf.blocks), block(64 * rpb);
   if (a.g)
     hipLaunchKernelGGL((embed_add_wave<T, I, NV, true>), grid, block, 0, s, (const T*)a.w1,
                        (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)a.g,
-                       (const T*)a.b, (T*)a.y, (bf16_t*)a.ypk, a.rows, a.cols, a.eps, a.vec);
+                       (const T*)a.b, (T*)a.y, (bf16_t*)a.ypk, a.rows, a.cols, a.eps, a.vec, pf);
   else
     hipLaunchKernelGGL((embed_add_wave<T, I, NV, false>), grid, block, 0, s, (const T*)a.w1,
                        (const I*)a.i1, a.v1, (const T*)a.w2, (const I*)a.i2, a.v2, (T*)a.x, (const T*)nullptr,
-                       (const T*)nullptr, (T*)nullptr, (bf16_t*)nullptr, a.rows, a.cols, a.eps, a.vec);
+                       (const T*)nullptr, (T*)nullptr, (bf16_t*)nullptr, a.rows, a.cols, a.eps, a.vec, pf);
 }
 
 template <typename T, typename I>
