@@ -593,6 +593,25 @@ def matmul_pp(packed_rows, rows, packed, out_features):
     return _op(b"matmul_pp", [_t(packed_rows), _t(packed)], i=(int(rows), int(out_features)))
 
 
+def row_stats_x3(x):
+    """Row statistics of fp32 x [rows, cols] (cols a multiple of 32) per
+    32-column tile: [rows, cols/32, 2] = (sum, sum of squared deviations
+    from the tile mean), the input of matmul_pp_norm.  Inside a lazy graph
+    the packed-weight GEMM producing x writes them from its epilogue."""
+    return _op(b"row_stats_x3", [_t(x)])
+
+
+def matmul_pp_norm(packed_rows, stats, rows, packed, cs, out_features, eps=1e-5):
+    """layer_norm(x) @ W without normalising x first: packed_rows =
+    pack_rows_x3(x), stats = row_stats_x3(x), packed = pack_weight_x3(gamma[:,
+    None] * W), cs = column sums of gamma[:, None] * W.  Returns
+    inv * (x @ (gamma W) - mean * cs) per row (mean and inv =
+    1 / sqrt(var + eps) from the statistics); adding beta @ W (+ the layer's
+    bias) gives layer_norm(x, gamma, beta) @ W (+ bias)."""
+    return _op(b"matmul_pp_norm", [_t(packed_rows), _t(stats), _t(packed), _t(cs)],
+               f=(float(eps),), i=(int(rows), int(out_features)))
+
+
 def linear_int8(x, q, scale):
     """x @ (q * scale[:, None])^T with the dequantisation fused into the GEMM."""
     return _op(b"linear_int8", [_t(x), _t(q), _t(scale)])

@@ -112,14 +112,44 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
                 p = gpu.pack_weight(t)
                 p.eval()
                 pk[k] = (p, t.shape[0], "rows16")
+    fold = {}
     if x3:
         for k, t in w.items():
             if k.endswith(CONV1D):
                 p = gpu.pack_weight_x3(t)
                 p.eval()
                 pk[k] = (p, t.shape[1], "x3")
+        if cfg["n_embd"] in _FOLD_WIDTHS:
+            for i in range(cfg["n_layer"]):
+                fold[i] = _fold_ln2(np_weights, f"transformer.h.{i}")
     return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor), "packed": pk,
-            "x3": bool(x3)}
+            "x3": bool(x3), "fold_ln2": fold}
+
+
+# Widths whose projections both run unsplit row-panel GEMMs (fp32 rows into
+# c_proj, packed rows into c_fc), the condition for folding ln_2 into c_fc.
+_FOLD_WIDTHS = (256, 512, 768, 1024)
+
+
+def _fold_ln2(np_weights: dict, p: str):
+    """ln_2 folded into c_fc: layer_norm(x, g, b) @ W + c = inv * (x @ (g W)
+    - mean * colsum(g W)) + (b @ W + c) per row, so that c_fc can read the
+    residual stream x itself (as packed rows with the row statistics the
+    producing GEMM writes) instead of a normalised copy.  g W is rounded to
+    fp32 once, and colsum is taken over those fp32 values so that the mean
+    term cancels against the product of the same weights."""
+    g = np.asarray(np_weights[f"{p}.ln_2.weight"], np.float64)
+    b = np.asarray(np_weights[f"{p}.ln_2.bias"], np.float64)
+    W = np.asarray(np_weights[f"{p}.mlp.c_fc.weight"], np.float64)
+    c = np.asarray(np_weights[f"{p}.mlp.c_fc.bias"], np.float64)
+    gw = (g[:, None] * W).astype(np.float32)
+    cs = gw.astype(np.float64).sum(0).astype(np.float32)
+    bb = (b @ W + c).astype(np.float32)
+    packed = gpu.pack_weight_x3(gpu.from_numpy(gw))
+    cs_t, bb_t = gpu.from_numpy(cs), gpu.from_numpy(bb)
+    for t in (packed, cs_t, bb_t):
+        t.eval()
+    return packed, cs_t, bb_t, W.shape[1]
 
 
 def _mm(model: dict, x, name: str, rows: int = None):
@@ -204,8 +234,16 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
             a = gpu.reshape(gpu.transpose_dims(a, 0, 1), [T, d])
         x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
 
-        h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
-        f = gpu.gelu(gpu.add_bias(mm_in(h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
+        fold = model.get("fold_ln2", {}).get(i)
+        if fold is not None:
+            # ln_2 folded into c_fc: the proj GEMM writes x as packed rows and
+            # row statistics besides fp32, c_fc normalises in its epilogue
+            packed, cs, bb, n_fc = fold
+            h = gpu.matmul_pp_norm(gpu.pack_rows_x3(x), gpu.row_stats_x3(x), T, packed, cs, n_fc)
+            f = gpu.gelu(gpu.add_bias(h, bb))
+        else:
+            h = gpu.layer_norm(x, w[f"{p}.ln_2.weight"], w[f"{p}.ln_2.bias"])
+            f = gpu.gelu(gpu.add_bias(mm_in(h, f"{p}.mlp.c_fc.weight"), w[f"{p}.mlp.c_fc.bias"]))
         x = x + gpu.add_bias(mm_in(f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
 
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])

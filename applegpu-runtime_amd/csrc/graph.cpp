@@ -33,7 +33,7 @@ enum Op : int {
   OP_DECODE_ATTENTION, OP_PACK_WEIGHT, OP_MATMUL_PACKED,
   OP_SGD_MATMUL, OP_SGD_SUM_ROWS, OP_MSE_LOSS_GRAD, OP_QKV_ATTENTION,
   OP_LAYER_NORM_BACKWARD, OP_LAYER_NORM_GRADS, OP_GELU_BACKWARD, OP_GELU_TANH_BACKWARD, OP_GELU_EXACT_BACKWARD,
-  OP_EMBEDDING_BACKWARD, OP_PACK_WEIGHT_X3, OP_PACK_ROWS_X3, OP_MATMUL_PP,
+  OP_EMBEDDING_BACKWARD, OP_PACK_WEIGHT_X3, OP_PACK_ROWS_X3, OP_MATMUL_PP, OP_ROW_STATS_X3, OP_MATMUL_PP_NORM,
   OP_COUNT
 };
 
@@ -53,7 +53,7 @@ static const char* kNames[OP_COUNT] = {
     "decode_attention", "pack_weight", "matmul_packed",
     "sgd_matmul_", "sgd_sum_rows_", "mse_loss_grad", "qkv_attention",
     "layer_norm_backward", "layer_norm_grads", "gelu_backward", "gelu_tanh_backward", "gelu_exact_backward",
-    "embedding_backward", "pack_weight_x3", "pack_rows_x3", "matmul_pp",
+    "embedding_backward", "pack_weight_x3", "pack_rows_x3", "matmul_pp", "row_stats_x3", "matmul_pp_norm",
 };
 
 int op_code(const char* name) {
@@ -224,6 +224,11 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
     case OP_MATMUL_PACKED: need(in, 2, code); return {matmul_packed(in[0], in[1], ip(iv, 0, code))};
     case OP_PACK_ROWS_X3: need(in, 1, code); return {pack_rows_x3(in[0])};
     case OP_MATMUL_PP: need(in, 2, code); return {matmul_pp(in[0], ip(iv, 0, code), in[1], ip(iv, 1, code))};
+    case OP_ROW_STATS_X3: need(in, 1, code); return {row_stats_x3(in[0])};
+    case OP_MATMUL_PP_NORM:
+      need(in, 4, code);
+      return {matmul_pp_norm(in[0], in[1], ip(iv, 0, code), in[2], in[3], ip(iv, 1, code),
+                             f.empty() ? 1e-5f : (float)f[0])};
     case OP_SGD_MATMUL:
       need(in, 3, code);
       return {sgd_matmul_(in[0], in[1], in[2], iv.size() > 0 && iv[0], iv.size() > 1 && iv[1], (float)fp(f, 0, code))};
@@ -323,6 +328,8 @@ struct Group {
   float ln_eps = 1e-5f;
   int64_t packed_n = 0;       // b is packed decode weights of this many columns
   int64_t a_rows = -1;        // a is packed x3 rows of this many rows (matmul_pp)
+  TensorP norm_stats, norm_cs;  // folded layer_norm of a (matmul_pp_norm)
+  float norm_eps = 1e-5f;
 };
 
 // An elementwise chain planned for one fused_chain launch.
@@ -454,19 +461,33 @@ void eval_all(const std::vector<TensorP>& roots) {
   std::unordered_map<Tensor*, TensorP> post_ln;  // group final node (or embedding sum) -> layer_norm reading it
   std::unordered_set<Tensor*> emb_adds;            // embedding + embedding nodes run as one kernel
   std::unordered_map<Tensor*, TensorP> pack_of;    // group final node or paired layer_norm -> pack_rows_x3 of it
+  std::unordered_map<Tensor*, TensorP> stats_of;   // group final node -> row_stats_x3 of it
   for (auto& t : order) {
     Node* n = t->node.get();
     if (n->code == OP_ADD_BIAS && t->ndim == 2) {
       const TensorP& x = n->in[0];
       if (x->pending() &&
-          (x->node->code == OP_MATMUL || x->node->code == OP_MATMUL_PACKED || x->node->code == OP_MATMUL_PP) &&
+          (x->node->code == OP_MATMUL || x->node->code == OP_MATMUL_PACKED || x->node->code == OP_MATMUL_PP ||
+           x->node->code == OP_MATMUL_PP_NORM) &&
           x->ndim == 2 && is_single_internal_use(x, uses) && n->in[1]->ndim == 1) {
         Group g;
         g.mm = x.get();
         if (x->node->code == OP_MATMUL_PACKED) g.packed_n = x->node->iv[0];
-        if (x->node->code == OP_MATMUL_PP) {
+        if (x->node->code == OP_MATMUL_PP || x->node->code == OP_MATMUL_PP_NORM) {
           g.a_rows = x->node->iv[0];
           g.packed_n = x->node->iv[1];
+        }
+        if (x->node->code == OP_MATMUL_PP_NORM) {
+          g.a = x->node->in[0];
+          g.norm_stats = x->node->in[1];
+          g.b = x->node->in[2];
+          g.norm_cs = x->node->in[3];
+          g.norm_eps = x->node->f.empty() ? 1e-5f : (float)x->node->f[0];
+          g.bias = n->in[1];
+          g.has_bias = true;
+          absorbed.insert(x.get());
+          groups[t.get()] = g;
+          continue;
         }
         // layer_norm -> matmul: the GEMM normalises its A rows itself when
         // its kernel can (ops::matmul falls back to an explicit layer_norm)
@@ -524,7 +545,7 @@ void eval_all(const std::vector<TensorP>& roots) {
       if (!x->pending() || x->dtype != DType::F32 || x->ndim != 2 || x->shape[1] % 16 != 0) continue;
       auto git = groups.find(x.get());
       if (git != groups.end() && git->second.packed_n > 0 && ops::is_x3_packed(git->second.b) &&
-          !post_ln.count(x.get()) && is_single_internal_use(x, uses)) {
+          !post_ln.count(x.get()) && !pack_of.count(x.get())) {
         pack_of[x.get()] = t;
         continue;
       }
@@ -534,6 +555,13 @@ void eval_all(const std::vector<TensorP>& roots) {
         pack_of[x.get()] = t;
         absorbed.insert(x.get());
       }
+    } else if (n->code == OP_ROW_STATS_X3) {
+      // row statistics from the producing packed-weight GEMM's epilogue
+      const TensorP& x = n->in[0];
+      auto git = groups.find(x.get());
+      if (x->pending() && git != groups.end() && git->second.packed_n > 0 && ops::is_x3_packed(git->second.b) &&
+          !post_ln.count(x.get()) && !stats_of.count(x.get()) && x->ndim == 2 && x->dtype == DType::F32)
+        stats_of[x.get()] = t;
     } else if (n->code == OP_LAYER_NORM && t->ndim == 2) {
       const TensorP& x = n->in[0];
       // (computed where x is, which comes before gamma and beta in the walk:
@@ -573,6 +601,20 @@ void eval_all(const std::vector<TensorP>& roots) {
         break;
       }
     }
+  }
+
+  // Group outputs whose packed rows or statistics come from their GEMM's
+  // epilogue: stored in fp32 as well only when something else reads them
+  // (another node, or a tensor held outside the graph).
+  std::unordered_set<Tensor*> c_needed;
+  for (auto& t : order) {
+    Tensor* p = t.get();
+    if (!groups.count(p)) continue;
+    const int special = (pack_of.count(p) ? 1 : 0) + (stats_of.count(p) ? 1 : 0);
+    if (!special) continue;
+    auto u = uses.find(p);
+    const int internal = u == uses.end() ? 0 : u->second;
+    if (internal != special || t.use_count() != 1 + special) c_needed.insert(p);
   }
 
   // Elementwise chains (crates/core/src/fusion.rs:60-141, run on every eval
@@ -668,10 +710,14 @@ void eval_all(const std::vector<TensorP>& roots) {
     for (size_t i = 0; i < order.size(); ++i) {
       if (!reads_ahead(i)) continue;
       k::Prefetch& pf = pf_for[i];
+      int64_t total = 0;
       for (size_t j = i + 1; j < order.size() && pf.n < 3; ++j) {
         if (const Tensor* w = x3_weights(j)) {
+          const int64_t nb = (int64_t)w->nbytes();
+          if (pf.n > 0 && total + nb > (12LL << 20)) break;  // keep the reads inside the launch's latency
           pf.ptr[pf.n] = w->data();
-          pf.bytes[pf.n] = (int64_t)w->nbytes();
+          pf.bytes[pf.n] = nb;
+          total += nb;
           ++pf.n;
         }
         if (reads_ahead(j)) break;
@@ -716,15 +762,29 @@ void eval_all(const std::vector<TensorP>& roots) {
         return g.a_rows >= 0 ? ops::matmul_pp(g.a, g.a_rows, g.b, g.packed_n, &e, pl, po)
                              : ops::matmul_packed(g.a, g.b, g.packed_n, &e, pl, po);
       };
+      e.norm_stats = g.norm_stats;
+      e.norm_cs = g.norm_cs;
+      e.norm_eps = g.norm_eps;
       auto pk = pack_of.find(t.get());
-      if (pk != pack_of.end() && x3) {
-        // only the packed rows are wanted
+      auto st = stats_of.find(t.get());
+      if ((pk != pack_of.end() || st != stats_of.end()) && x3 && !lnt) {
+        // packed rows and/or row statistics of the output from the same
+        // launch; the fp32 output too when anything else reads it
         ops::PackOut po;
-        po.want_c = false;
-        packed_product(nullptr, &po);
-        assign(pk->second, po.pk);
+        po.want_pk = pk != pack_of.end();
+        po.want_stats = st != stats_of.end();
+        po.want_c = c_needed.count(t.get()) > 0;
+        TensorP out = packed_product(nullptr, &po);
+        if (po.want_pk) assign(pk->second, po.pk);
+        if (po.want_stats) assign(st->second, po.stats);
         g_stats.fused_gemm_epilogues++;
-        g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0) + 1;
+        g_stats.launches_saved += (g.has_bias ? 1 : 0) + (g.act ? 1 : 0) + (g.residual ? 1 : 0) +
+                                  (po.want_pk ? 1 : 0) + (po.want_stats ? 1 : 0);
+        if (!po.want_c) {
+          order[i].reset();
+          continue;
+        }
+        assign(t, out);
         order[i].reset();
         continue;
       }

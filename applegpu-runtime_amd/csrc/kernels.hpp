@@ -199,6 +199,19 @@ struct Gemm {
   float pln_eps = 1e-5f;
   // Y also (or, with pln_y null, only) written as packed x3 rows (N % 16 == 0)
   void* pln_ypk = nullptr;
+  // with b_x3, unsplit row-panel plans: rs_out receives the output's row
+  // statistics per 32-column tile ([M, N/32, 2]: sum, squared deviations
+  // from the tile mean; N % 32 == 0); with rs_in (A's statistics [M,
+  // rs_tiles, 2] over rs_n columns, packed A) the epilogue computes
+  // inv * (acc - mean * rs_cs[n]) before the bias: a layer_norm of A whose
+  // gamma is folded into the weights (rs_cs = column sums of the folded
+  // weights) and whose beta is folded into the bias
+  float* rs_out = nullptr;
+  const float* rs_in = nullptr;
+  const float* rs_cs = nullptr;
+  int rs_tiles = 0;
+  int64_t rs_n = 0;
+  float rs_eps = 1e-5f;
 };
 // fp32 weights packed for the bf16x3 MFMA GEMM of few-row activations
 // (gemm_x3p.hip): B(k, n) read through strides (b_sk, b_sn) is split into
@@ -234,6 +247,13 @@ struct Prefetch {
 };
 void set_prefetch(const Prefetch& pf);
 Prefetch take_prefetch();
+// Row statistics per 32-column tile of an fp32 matrix [M, N] (N % 32 == 0,
+// 16-byte aligned rows): out [M, N/32, 2] = (sum, sum of squared deviations
+// from the tile mean), identical to what a row-panel GEMM writes (rs_out).
+void row_tile_stats(const float* x, int64_t x_sm, int64_t M, int64_t N, float* out, hipStream_t s);
+// Whether the packed-weight GEMM of this shape runs an unsplit row-panel
+// plan (packed outputs and row statistics come from its epilogue).
+bool gemm_x3_panel_ok(int64_t M, int64_t N, int64_t K, bool apk);
 // Packed x3 rows of an fp32 matrix X [M, K] read through strides (x_sm,
 // x_sk), K % 16 == 0: the A-operand counterpart of pack_weights_x3
 // (packed_x3_elems(K, M) bf16 elements).

@@ -701,6 +701,12 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   p.a_x3 = g.a_x3;
   p.c_pk = (bf16_t*)g.c_pk;
   p.pln_ypk = (bf16_t*)g.pln_ypk;
+  p.rs_out = g.rs_out;
+  p.rs_in = g.rs_in;
+  p.rs_cs = g.rs_cs;
+  p.rs_tiles = g.rs_tiles;
+  p.rs_n = g.rs_n;
+  p.rs_eps = g.rs_eps;
   const size_t esz = dtype_size(g.dt);
   const int vw = (int)(16 / esz);  // elements per 16-byte vector
   // Vector loads need 16-byte aligned runs along the contiguous axis.
@@ -759,18 +765,23 @@ bool gemm_x3_ok(const Gemm& g) {
     if (g.ln_gamma && (!g.ln_beta || !gemm_x3_ln_ok(g.M, g.N, g.K))) return false;
     if (g.a_sk != 1 || (g.M > 1 && g.a_sm % 4 != 0)) return false;
   }
-  if (g.c_pk) {
+  if (g.c_pk || g.rs_out || g.rs_in) {
     const X3Plan pl = x3_plan_of(g);
-    if (!(pl.rows && pl.apk && pl.splits == 1 && g.N % 16 == 0 && al16(g.c_pk))) return false;
-  } else if (!g.C && !g.no_reduce) {
-    return false;
+    if (!(pl.rows && pl.splits == 1)) return false;
+    if (g.c_pk && (g.N % 16 != 0 || !al16(g.c_pk))) return false;
+    if (g.rs_out && (g.N % 32 != 0 || ((uintptr_t)g.rs_out & 7))) return false;
+    if (g.rs_in && (!g.a_x3 || !g.rs_cs || g.rs_tiles < 1 || g.rs_tiles > 48 || g.rs_n < 1 || ((uintptr_t)g.rs_in & 7)))
+      return false;
   }
+  if (!g.C && !g.c_pk && !g.no_reduce) return false;
   return g.c_sm == g.N;
 }
 
-bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K) {
-  const X3Plan pl = x3_plan(M, N, K, cu_count(), true, false);
-  return pl.rows && pl.splits == 1 && N % 16 == 0;
+bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K) { return gemm_x3_panel_ok(M, N, K, true) && N % 16 == 0; }
+
+bool gemm_x3_panel_ok(int64_t M, int64_t N, int64_t K, bool apk) {
+  const X3Plan pl = x3_plan(M, N, K, cu_count(), apk, false);
+  return pl.rows && pl.splits == 1;
 }
 
 int gemm_splits(const Gemm& g) {

@@ -42,6 +42,17 @@ struct GArgs {
   bf16_t* c_pk;
   bf16_t* pln_ypk;
   PfArgs pf;  // read-ahead blocks (split-K layer_norm reductions)
+  // row statistics for a layer_norm folded into the next GEMM (row-panel
+  // plans): rs_out receives, per output row and 32-column tile, the tile's
+  // sum and sum of squared deviations from the tile mean ([M, N / 32, 2]);
+  // with rs_in (the A rows' statistics, [M, rs_tiles, 2] over rs_n columns)
+  // the epilogue forms inv * (acc - mean * rs_cs[n]) before the bias
+  float* rs_out;
+  const float* rs_in;
+  const float* rs_cs;
+  int rs_tiles;
+  int64_t rs_n;
+  float rs_eps;
 };
 
 // Epilogue operands of one output, loadable ahead of the product (they do

@@ -210,6 +210,116 @@ __global__ void __launch_bounds__(256) gemm_x3p(GArgs p, int64_t T) {
     }
 }
 
+// ── the row-major finish of a 32 x 32 row-panel block ────────────────────
+// Thread t < 256 owns row t / 8 of the block and columns 4 (t % 8) .. + 3;
+// the eight threads of a row are consecutive lanes of one wavefront.
+
+// A row's tile statistics (rs_in) as lane q of the row's eight holds them:
+// tiles q, q + 8, ..., at most kRsPerLane (48 tiles: K <= 1536), loaded
+// together.
+constexpr int kRsPerLane = 6;
+struct RowStats {
+  float2 v[kRsPerLane];
+};
+// Tiles past the end read the row's last tile (not merged): a load under a
+// per-lane condition would be waited for on its own.  Call with rs_in set.
+__device__ __forceinline__ void row_norm_load(const GArgs& p, int64_t row, int q, RowStats& rs) {
+  const float* st = p.rs_in + row * (int64_t)p.rs_tiles * 2;
+#pragma unroll
+  for (int i = 0; i < kRsPerLane; ++i) {
+    const int j = q + 8 * i < p.rs_tiles ? q + 8 * i : p.rs_tiles - 1;
+    rs.v[i] = *(const float2*)(st + 2 * j);
+  }
+}
+
+// mean and 1 / sqrt(var + eps) of the row from its tile statistics (each
+// tile 32 values: sum s_t, squared deviations D_t from its mean): mean =
+// sum of s_t / n, then var = sum over tiles of (D_t + 32 (s_t / 32 - mean)^2)
+// / n (Chan, Golub and LeVeque's combination of partial variances, through
+// the overall mean).  Each lane adds its tiles in order and the eight lanes
+// combine by an xor butterfly, which gives all eight the same bits.
+// Population variance, as layer_norm's.
+__device__ __forceinline__ void row_norm_stats(const GArgs& p, int q, const RowStats& rs, float& mean, float& inv) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRsPerLane; ++i)
+    if (q + 8 * i < p.rs_tiles) s += rs.v[i].x;
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  s += __shfl_xor(s, 4, 64);
+  const float rn = 1.f / (float)p.rs_n;
+  mean = s * rn;
+  float m2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRsPerLane; ++i) {
+    const float d = rs.v[i].x * (1.f / 32.f) - mean;
+    if (q + 8 * i < p.rs_tiles) m2 += rs.v[i].y + 32.f * d * d;
+  }
+  m2 += __shfl_xor(m2, 1, 64);
+  m2 += __shfl_xor(m2, 2, 64);
+  m2 += __shfl_xor(m2, 4, 64);
+  inv = 1.f / sqrtf(m2 * rn + p.rs_eps);
+}
+
+struct RowEpi {
+  float bias[4], res[4], msk[4], cs[4];
+};
+
+// Epilogue operands of the thread's four outputs (row clamped to M - 1 and
+// columns to N - 1: legal addresses; such outputs are not stored).  Absent
+// operands (uniform tests) are not loaded.
+__device__ __forceinline__ void row_epi_load(const GArgs& p, int64_t row, int64_t col, RowEpi& e) {
+  const int64_t rc = row < p.M ? row : p.M - 1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t cc = col + j < p.N ? col + j : p.N - 1;
+    e.bias[j] = p.bias ? ((const float*)p.bias)[cc] : 0.f;
+    e.res[j] = p.res ? ((const float*)p.res)[rc * p.r_sm + cc] : 0.f;
+    e.msk[j] = p.mask ? ((const float*)p.mask)[rc * p.k_sm + cc] : 1.f;
+    e.cs[j] = p.rs_in ? p.rs_cs[cc] : 0.f;
+  }
+}
+
+// v (the summed products) -> epilogue -> C, packed rows (c_pk) and this
+// block's tile statistics (rs_out: sum and squared deviations from the tile
+// mean over the 32 stored values of the row).  The eight threads of the row
+// all call it (row < M).
+__device__ __forceinline__ void row_epi_store(const GArgs& p, int64_t row, int64_t col, int q, int tn, float (&v)[4],
+                                              const RowEpi& e, float mean, float inv) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float y = v[j];
+    if (p.rs_in) y = inv * (y - mean * e.cs[j]);
+    y = p.alpha * y + e.bias[j];
+    if (p.act == kActRelu) y = fmaxf(y, 0.f);
+    else if (p.act == kActGelu) y = gelu_tanh(y);
+    else if (p.act == kActGeluExact) y = 0.5f * y * (1.f + erff(y * 0.70710678118654752f));
+    y += e.res[j];
+    if (p.mask) y = e.msk[j] > 0.f ? y : 0.f;
+    v[j] = y;
+  }
+  if (p.C) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (col + j < p.N) ((float*)p.C)[row * p.c_sm + col + j] = v[j];
+  }
+  if (p.c_pk && col < p.N) x3_store4(p.c_pk, p.N / 16, row, col, v);
+  if (p.rs_out) {
+    float sm = (v[0] + v[1]) + (v[2] + v[3]);
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    sm += __shfl_xor(sm, 4, 64);
+    const float mt = sm * (1.f / 32.f);
+    float d2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d2 += (v[j] - mt) * (v[j] - mt);
+    d2 += __shfl_xor(d2, 1, 64);
+    d2 += __shfl_xor(d2, 2, 64);
+    d2 += __shfl_xor(d2, 4, 64);
+    if (q == 0) *(float2*)(p.rs_out + (row * (int64_t)p.tiles_n + tn) * 2) = make_float2(sm, d2);
+  }
+}
+
 // Row panel: one block owns 32 rows x 32 columns over the whole K (K = 64
 // KPW), so no split-K reduction launch follows it, and a layer_norm of the A
 // rows can run in its prologue (the block holds whole rows).  The four
@@ -229,18 +339,7 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
   __shared__ __attribute__((aligned(16))) bf16_t sA[2][32 * LDA];
   __shared__ __attribute__((aligned(16))) float sGB[LN ? 2 * K : 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int tm, tn;
-  {
-    const int id = blockIdx.x;
-    if ((p.tiles_n & 7) == 0) {
-      const int g = id / (8 * p.tiles_m), r = id % (8 * p.tiles_m);
-      tm = r / 8;
-      tn = g * 8 + (r & 7);
-    } else {
-      tm = id / p.tiles_n;
-      tn = id % p.tiles_n;
-    }
-  }
+  const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x % p.tiles_n;
   const int64_t m0 = (int64_t)tm * 32, n0 = (int64_t)tn * 32;
   const int64_t S = (p.N + 31) / 32;
   constexpr int64_t T = K / 16;
@@ -263,6 +362,9 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
   float4 av[NQ];
 #pragma unroll
   for (int i = 0; i < NQ; ++i) av[i] = *(const float4*)(arow + 4 * (j + 8 * i));
+  // the epilogue's operands (thread t finishes row t / 8, columns 4 (t % 8) .. + 3)
+  RowEpi ep;
+  row_epi_load(p, m0 + r, n0 + 4 * j, ep);
   if constexpr (LN) {
     for (int e = threadIdx.x; e < K; e += 256) {
       sGB[e] = ((const float*)p.ln_g)[e];
@@ -328,34 +430,28 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[i], acc, 0, 0, 0);
   }
 
-  // 5. The four partials meet in LDS (the A tiles are no longer read); wave
-  //    w finishes registers 4w..4w+3 of every lane: rows 8w..8w+7.
+  // 5. The four partials meet in LDS (the A tiles are no longer read): row
+  //    r, columns 4q..4q+3 are register 4 (r / 8) + r % 4 of lanes
+  //    32 ((r / 4) % 2) + 4q + 0..3 in every wave, summed in wave order.
   __syncthreads();
   float* red = (float*)&sA[0][0];
 #pragma unroll
   for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
   __syncthreads();
-  const int64_t col = n0 + (lane & 31);
-  const int64_t cc = col < p.N ? col : p.N - 1;
-  const float bias = p.bias ? ((const float*)p.bias)[cc] : 0.f;
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int e = 4 * wave + rr;
-    const int64_t orow = m0 + 8 * wave + 4 * (lane >> 5) + rr;
-    const int64_t rc = orow < p.M ? orow : p.M - 1;
-    const float res = p.res ? ((const float*)p.res)[rc * p.r_sm + cc] : 0.f;
-    const float msk = p.mask ? ((const float*)p.mask)[rc * p.k_sm + cc] : 1.f;
-    float v = red[(0 * 16 + e) * 64 + lane];
-#pragma unroll
-    for (int x = 1; x < 4; ++x) v += red[(x * 16 + e) * 64 + lane];
-    v = p.alpha * v + bias;
-    if (p.act == kActRelu) v = fmaxf(v, 0.f);
-    else if (p.act == kActGelu) v = gelu_tanh(v);
-    else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
-    v += res;
-    if (p.mask) v = msk > 0.f ? v : 0.f;
-    if (orow < p.M && col < p.N) ((float*)p.C)[orow * p.c_sm + col] = v;
+  if (m0 + r >= p.M) return;
+  const int e = 4 * (r >> 3) + (r & 3);
+  const int lb = 32 * ((r >> 2) & 1) + 4 * j;
+  float v[4];
+  {
+    const float4 w0 = *(const float4*)&red[e * 64 + lb];
+    v[0] = w0.x; v[1] = w0.y; v[2] = w0.z; v[3] = w0.w;
   }
+#pragma unroll
+  for (int x = 1; x < 4; ++x) {
+    const float4 w = *(const float4*)&red[(x * 16 + e) * 64 + lb];
+    v[0] += w.x; v[1] += w.y; v[2] += w.z; v[3] += w.w;
+  }
+  row_epi_store(p, m0 + r, n0 + 4 * j, j, tn, v, ep, 0.f, 1.f);
 }
 
 // Row panel over packed A: the block (8 wavefronts) owns 32 rows x 32
@@ -398,18 +494,15 @@ __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
       al[i] = *(const bf16x8_t*)(as + i * 1024 + 512);
     }
   }
-  // 2. Epilogue operands of this thread's four outputs (waves 0..3).
+  // 2. Epilogue operands of this thread's four outputs (waves 0..3), and
+  //    with a folded layer_norm the statistics of its row of A.
   const int r = (threadIdx.x >> 3) & 31, q = threadIdx.x & 7;
   const int64_t row = m0 + r, rc = row < p.M ? row : p.M - 1;
-  float bias[4] = {0.f, 0.f, 0.f, 0.f}, res[4] = {0.f, 0.f, 0.f, 0.f}, msk[4] = {1.f, 1.f, 1.f, 1.f};
+  RowEpi ep;
+  RowStats rs;
   if (wave < 4 && p.splits == 1) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + 4 * q + j, cc = col < p.N ? col : p.N - 1;
-      if (p.bias) bias[j] = ((const float*)p.bias)[cc];
-      if (p.res) res[j] = ((const float*)p.res)[rc * p.r_sm + cc];
-      if (p.mask) msk[j] = ((const float*)p.mask)[rc * p.k_sm + cc];
-    }
+    row_epi_load(p, row, n0 + 4 * q, ep);
+    if (p.rs_in) row_norm_load(p, rc, q, rs);
   }
   // 3. This wave's k steps.
   f32x16 acc;
@@ -449,22 +542,42 @@ __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
       if (col + j < p.N) ws[col + j] = v[j];
     return;
   }
+  float mean = 0.f, inv = 1.f;
+  if (p.rs_in) row_norm_stats(p, q, rs, mean, inv);
+  row_epi_store(p, row, col, q, tn, v, ep, mean, inv);
+}
+
+// Tile statistics of an fp32 matrix [M, N] (N % 32 == 0): per row and
+// 32-column tile, the sum and the sum of squared deviations from the tile
+// mean, formed in row_epi_store's order (four-column groups, then the
+// pairwise tree over the eight groups), so that they equal the statistics a
+// row-panel GEMM writes for the same values.  One thread per (row, tile).
+__global__ void __launch_bounds__(256) row_tile_stats_kernel(const float* __restrict__ x, int64_t sm, int64_t M,
+                                                             int64_t tiles, float* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= M * tiles) return;
+  const int64_t row = gid / tiles, t = gid % tiles;
+  const float* src = x + row * sm + t * 32;
+  float v[32];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float y = p.alpha * v[j] + bias[j];
-    if (p.act == kActRelu) y = fmaxf(y, 0.f);
-    else if (p.act == kActGelu) y = gelu_tanh(y);
-    else if (p.act == kActGeluExact) y = 0.5f * y * (1.f + erff(y * 0.70710678118654752f));
-    y += res[j];
-    if (p.mask) y = msk[j] > 0.f ? y : 0.f;
-    v[j] = y;
+  for (int i = 0; i < 8; ++i) {
+    const float4 a = *(const float4*)(src + 4 * i);
+    v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
   }
-  if (p.C) {
+  float g[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (col + j < p.N) ((float*)p.C)[row * p.c_sm + col + j] = v[j];
+  for (int i = 0; i < 8; ++i) g[i] = (v[4 * i] + v[4 * i + 1]) + (v[4 * i + 2] + v[4 * i + 3]);
+  const float sm_ = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+  const float mt = sm_ * (1.f / 32.f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float d = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) d += (v[4 * i + j] - mt) * (v[4 * i + j] - mt);
+    g[i] = d;
   }
-  if (p.c_pk && col < p.N) x3_store4(p.c_pk, p.N / 16, row, col, v);
+  const float d2 = ((g[0] + g[1]) + (g[2] + g[3])) + ((g[4] + g[5]) + (g[6] + g[7]));
+  *(float2*)(out + gid * 2) = make_float2(sm_, d2);
 }
 
 template <int FR, int FC, int WR, int WC, bool APK>
@@ -492,6 +605,15 @@ void pack_weights_x3(const void* b, int64_t b_sk, int64_t b_sn, int64_t K, int64
   hipLaunchKernelGGL(pack_x3_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, (const float*)b, b_sk,
                      b_sn, K, N, T, (bf16_t*)out);
   check_launch("pack_weights_x3");
+}
+
+void row_tile_stats(const float* x, int64_t x_sm, int64_t M, int64_t N, float* out, hipStream_t s) {
+  if (N % 32 != 0 || ((uintptr_t)x & 15) || x_sm % 4 != 0) fail("row_tile_stats: N %% 32 == 0 and 16-byte rows needed");
+  const int64_t n = M * (N / 32);
+  if (n == 0) return;
+  hipLaunchKernelGGL(row_tile_stats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, x_sm, M, N / 32,
+                     out);
+  check_launch("row_tile_stats");
 }
 
 void pack_rows_x3(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, int64_t K, void* out, hipStream_t s) {
@@ -611,8 +733,12 @@ static void launch_rows(const X3Plan& pl, const GArgs& p, hipStream_t s) {
 
 void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s) {
   if (pl.apk != p.a_x3) fail("internal: gemm_x3p plan and A operand disagree");
-  if (p.c_pk && !(pl.rows && pl.apk && pl.splits == 1 && p.N % 16 == 0))
-    fail("gemm_x3p: packed output needs the unsplit packed-A row-panel plan and N %% 16 == 0");
+  const bool panel = pl.rows && pl.splits == 1;
+  if (p.c_pk && !(panel && p.N % 16 == 0))
+    fail("gemm_x3p: packed output needs an unsplit row-panel plan and N %% 16 == 0");
+  if (p.rs_out && !(panel && p.N % 32 == 0))
+    fail("gemm_x3p: row statistics need an unsplit row-panel plan and N %% 32 == 0");
+  if (p.rs_in && !(panel && pl.apk)) fail("gemm_x3p: a folded layer_norm needs the unsplit packed-A row-panel plan");
   if (pl.rows && pl.apk) {
     if (p.ln_g) fail("gemm_x3p: a layer_norm prologue needs fp32 A");
     launch_rows_pk(pl, p, s);

@@ -1123,9 +1123,15 @@ static TensorP matmul_x3(const TensorP& a_in, int64_t a_rows, const TensorP& pw,
   TensorP pc = contiguous(pw);
   const std::vector<int64_t> od{M, N};
   const std::vector<int64_t> pkd{(M + 31) / 32, N / 16, 2, 64, 8};
-  // the packed output straight from the row-panel epilogue when it can
-  const bool pk_direct = po && apk && !post_ln && k::gemm_x3_pk_out_ok(M, N, K);
-  const bool want_c = !po || po->want_c || !pk_direct;
+  // packed rows and row statistics straight from an unsplit row-panel
+  // epilogue when the plan has one
+  const bool panel = !post_ln && k::gemm_x3_panel_ok(M, N, K, apk);
+  const bool pk_direct = po && po->want_pk && panel && N % 16 == 0;
+  const bool st_direct = po && po->want_stats && panel && N % 32 == 0;
+  const bool norm = epi && epi->norm_stats;
+  if (norm && !(apk && k::gemm_x3_panel_ok(M, N, K, true)))
+    fail("%s: a folded layer_norm needs packed rows and a row-panel plan (K = 256..1536 in steps of 256)", name);
+  const bool want_c = !po || po->want_c || (po->want_pk && !pk_direct) || (po->want_stats && !st_direct);
   TensorP out = want_c ? alloc_out(DType::F32, od) : nullptr;
   k::Gemm g;
   g.dt = g.b_dt = DType::F32;
@@ -1142,6 +1148,25 @@ static TensorP matmul_x3(const TensorP& a_in, int64_t a_rows, const TensorP& pw,
   if (pk_direct) {
     po->pk = alloc_out(DType::BF16, pkd);
     g.c_pk = po->pk->data();
+  }
+  if (st_direct) {
+    po->stats = alloc_out(DType::F32, {M, N / 32, 2});
+    g.rs_out = (float*)po->stats->data();
+  }
+  TensorP nst, ncs;
+  if (norm) {
+    if (!epi->norm_cs || epi->norm_stats->dtype != DType::F32 || epi->norm_cs->dtype != DType::F32 ||
+        epi->norm_stats->ndim != 3 || epi->norm_stats->shape[0] != M || epi->norm_stats->shape[1] * 32 != K ||
+        epi->norm_stats->shape[2] != 2 || epi->norm_cs->numel() != N)
+      fail("%s: layer_norm statistics must be row_stats_x3 of the [%lld, %lld] rows and cs [%lld] fp32", name,
+           (long long)M, (long long)K, (long long)N);
+    nst = contiguous(epi->norm_stats);
+    ncs = contiguous(epi->norm_cs);
+    g.rs_in = (const float*)nst->data();
+    g.rs_cs = (const float*)ncs->data();
+    g.rs_tiles = (int)(K / 32);
+    g.rs_n = K;
+    g.rs_eps = epi->norm_eps;
   }
   EpiKeep keep;
   set_epilogue(g, epi, od, {}, &keep);
@@ -1181,8 +1206,30 @@ static TensorP matmul_x3(const TensorP& a_in, int64_t a_rows, const TensorP& pw,
     if (post_ln->want_y) post_ln->y = y;
     if (post_ln->want_pk) post_ln->ypk = pack_rows_x3(y);
   }
-  if (po && !pk_direct) po->pk = pack_rows_x3(out);
+  if (po && po->want_pk && !pk_direct) po->pk = pack_rows_x3(out);
+  if (po && po->want_stats && !st_direct) po->stats = row_stats_x3(out);
   return po && !po->want_c ? nullptr : out;
+}
+
+TensorP row_stats_x3(const TensorP& x) {
+  if (x->ndim != 2 || x->dtype != DType::F32) fail("row_stats_x3: fp32 [rows, cols] expected");
+  const int64_t M = x->shape[0], N = x->shape[1];
+  if (N % 32 != 0 || N == 0) fail("row_stats_x3: the column count %lld must be a positive multiple of 32", (long long)N);
+  TensorP a = x;
+  if (!meta_mode() && (a->strides[1] != 1 || a->strides[0] % 4 != 0 || ((uintptr_t)a->data() & 15))) a = materialize(a);
+  TensorP out = alloc_out(DType::F32, {M, N / 32, 2});
+  LAUNCH k::row_tile_stats((const float*)a->data(), M == 1 ? N : a->strides[0], M, N, (float*)out->data(),
+                           rt().stream());
+  return out;
+}
+
+TensorP matmul_pp_norm(const TensorP& apk, const TensorP& stats, int64_t M, const TensorP& folded,
+                       const TensorP& cs, int64_t N, float eps, const Epilogue* epi, PackOut* po) {
+  Epilogue e = epi ? *epi : Epilogue{};
+  e.norm_stats = stats;
+  e.norm_cs = cs;
+  e.norm_eps = eps;
+  return matmul_pp(apk, M, folded, N, &e, nullptr, po);
 }
 
 TensorP matmul_pp(const TensorP& apk, int64_t M, const TensorP& pw, int64_t N, const Epilogue* epi, PostLn* post_ln,

@@ -82,6 +82,11 @@ struct Epilogue {
   // explicit layer_norm first)
   TensorP ln_gamma, ln_beta;
   float ln_eps = 1e-5f;
+  // packed-A products only: A = layer_norm(X) with gamma folded into the
+  // weights and beta into the bias; norm_stats = row_stats_x3(X), norm_cs =
+  // the folded weights' column sums (matmul_pp_norm)
+  TensorP norm_stats, norm_cs;
+  float norm_eps = 1e-5f;
 };
 // Also y = layer_norm(out, gamma, beta, eps) over the last dim; computed by
 // the GEMM's split-K reduction when its plan has one, else by layer_norm.
@@ -93,11 +98,16 @@ struct PostLn {
   bool want_y = true, want_pk = false;
   TensorP ypk;
 };
-// Output form of a packed-weight product: fp32 C (want_c) and/or the same
-// values as packed x3 rows (pk) for a following packed-A product.
+// Outputs of a packed-weight product beyond fp32 C (want_c): the same
+// values as packed x3 rows (pk) for a following packed-A product, and their
+// row statistics per 32-column tile (stats, as row_stats_x3) for a
+// layer_norm folded into that product.  Written by the product's epilogue
+// when its plan allows, else by their own launches.
 struct PackOut {
   bool want_c = true;
-  TensorP pk;
+  bool want_pk = true;
+  bool want_stats = false;
+  TensorP pk, stats;
 };
 // No-allocation mode: the caller's output (`into`) and a caller-held split-K
 // workspace of `cap` bytes; any operand that would need a device copy, and
@@ -146,6 +156,17 @@ TensorP pack_rows_x3(const TensorP& x);
 // null when po asks for the packed output only.
 TensorP matmul_pp(const TensorP& apk, int64_t M, const TensorP& packed, int64_t N, const Epilogue* epi = nullptr,
                   PostLn* post_ln = nullptr, PackOut* po = nullptr);
+// Row statistics of an fp32 matrix x [M, N] (N % 32 == 0) per 32-column
+// tile: [M, N/32, 2] = (sum, sum of squared deviations from the tile mean).
+TensorP row_stats_x3(const TensorP& x);
+// layer_norm(X) @ W + b as one packed product, for X given as packed rows
+// (apk = pack_rows_x3(X)) with its statistics (stats = row_stats_x3(X)):
+// folded = gamma[:, None] * W packed by pack_weight_x3, cs = column sums of
+// gamma[:, None] * W, and the caller adds beta @ W + b as the bias.  The
+// result is inv * (X @ folded - mean * cs) per row, with mean and
+// inv = 1 / sqrt(var + eps) merged from the tile statistics.
+TensorP matmul_pp_norm(const TensorP& apk, const TensorP& stats, int64_t M, const TensorP& folded,
+                       const TensorP& cs, int64_t N, float eps, const Epilogue* epi = nullptr, PackOut* po = nullptr);
 // int8 weights with per-row scales (out = x @ (q * scale[:,None])^T)
 TensorP linear_int8(const TensorP& x, const TensorP& q, const TensorP& scale);
 

@@ -43,6 +43,15 @@ def _bits_of(t):
     return (np.asarray(t.to_numpy(), np.float32).view(np.uint32) >> 16).astype(np.uint16)
 
 
+def _valid_rows(bits, M):
+    """The elements of packed rows [S, T, 2, 64, 8] that belong to rows < M
+    (rows past M up to the next multiple of 32 are never written by a fused
+    producer)."""
+    S = bits.shape[0]
+    row = 32 * np.arange(S)[:, None, None, None, None] + (np.arange(64) % 32)[None, None, None, :, None]
+    return bits[np.broadcast_to(row < M, bits.shape)]
+
+
 def _packed_ref(b):
     """Element ((s T + t) 2 + h) 512 + 8 l + j = part h of B(16 t + 8 (l // 32) + j, 32 s + l % 32)."""
     K, N = b.shape
@@ -262,8 +271,10 @@ def test_reduction_writes_packed_layer_norm_rows(gpu, M, K, N, N2):
 @pytest.mark.parametrize("M,K,N,N2", [(128, 768, 3072, 768), (70, 256, 512, 64)])
 def test_gemm_epilogue_writes_packed_gelu_rows(gpu, M, K, N, N2):
     """gelu(pack_rows(x) W + b) feeding another packed product: the row-panel
-    epilogue writes the packed rows itself (no fp32 store, no pack launch);
-    bitwise equal to the stored-then-packed path and at the fp32 bar."""
+    epilogue writes the packed rows itself, with no pack launch, whether or
+    not the fp32 output is also kept (held outside the graph: then the same
+    launch stores it too); both results are bitwise equal and at the fp32
+    bar."""
     x, w, bias = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1)
     w2, b2 = f32(N, N2, scale=0.05), f32(N2, scale=0.1)
     pk_w, pk_w2 = gpu.pack_weight_x3(gpu.from_numpy(w)), gpu.pack_weight_x3(gpu.from_numpy(w2))
@@ -271,10 +282,11 @@ def test_gemm_epilogue_writes_packed_gelu_rows(gpu, M, K, N, N2):
     apk = gpu.pack_rows_x3(gpu.from_numpy(x))
     for t in (pk_w, pk_w2, bd, bd2, apk):
         t.eval()
-    res, f_np = [], None
+    res, f_np, apk_f = [], None, None
     for keep in (False, True):
         f = gpu.gelu(gpu.add_bias(gpu.matmul_pp(apk, M, pk_w, N), bd))
-        y = gpu.add_bias(gpu.matmul_pp(gpu.pack_rows_x3(f), M, pk_w2, N2), bd2)
+        fp = gpu.pack_rows_x3(f)
+        y = gpu.add_bias(gpu.matmul_pp(fp, M, pk_w2, N2), bd2)
         if not keep:
             del f
         before = gpu.graph_stats()
@@ -283,10 +295,13 @@ def test_gemm_epilogue_writes_packed_gelu_rows(gpu, M, K, N, N2):
         res.append((y.to_numpy(), after["launcher_calls"] - before["launcher_calls"]))
         if keep:
             f_np = f.to_numpy()
+            apk_f = fp
             del f
     (y0, n0), (y1, n1) = res
     np.testing.assert_array_equal(y0, y1)
-    assert n0 == n1 - 1, (n0, n1)
+    assert n0 == n1, (n0, n1)
+    np.testing.assert_array_equal(_valid_rows(_bits_of(gpu.pack_rows_x3(gpu.from_numpy(f_np))), M),
+                                  _valid_rows(_bits_of(apk_f), M))
     f_ref = O.gelu_tanh(O.add_bias(O.matmul(x, w), bias))
     assert rel_err(f_np, f_ref) < 1e-4
     assert rel_err(y0, O.add_bias(O.matmul(f_ref, w2), b2)) < 1e-4
@@ -325,3 +340,84 @@ def test_embedding_writes_packed_layer_norm_rows(gpu):
     assert n0 == n1 - 1, (n0, n1)
     ref = O.matmul(O.layer_norm(wte[ids] + wpe[pos], g, be), w)
     assert rel_err(y0, ref) < 1e-4
+
+
+# ── layer_norm folded into the next packed product (row_stats_x3 + matmul_pp_norm)
+def _tile_stats_ref(x):
+    """(sum, sum of squared deviations from the tile mean) per 32-column tile, float64."""
+    M, N = x.shape
+    t = x.astype(np.float64).reshape(M, N // 32, 32)
+    s = t.sum(-1)
+    return np.stack([s, ((t - (s / 32)[..., None]) ** 2).sum(-1)], -1)
+
+
+def test_row_stats_vs_float64(gpu):
+    x = f32(37, 160, scale=3.0) + 2.0
+    got = gpu.row_stats_x3(gpu.from_numpy(x)).to_numpy()
+    assert got.shape == (37, 5, 2)
+    np.testing.assert_allclose(got, _tile_stats_ref(x), rtol=1e-5, atol=1e-4)
+    with pytest.raises(ValueError, match="row_stats_x3"):
+        gpu.row_stats_x3(gpu.from_numpy(f32(4, 48))).eval()
+
+
+def _fold(g, be, W, c):
+    gw = (g.astype(np.float64)[:, None] * W).astype(np.float32)
+    return gw, gw.astype(np.float64).sum(0).astype(np.float32), (be.astype(np.float64) @ W + c).astype(np.float32)
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 768, 3072), (50, 256, 96), (1, 512, 64), (33, 1024, 160)])
+def test_matmul_pp_norm_vs_oracle(gpu, M, K, N):
+    """layer_norm(x) @ W + c as inv * (x @ (g W) - mean * colsum(g W)) +
+    (b @ W + c), with x's statistics from row_stats_x3: at the fp32 bar
+    against the oracle's layer_norm then product, for rows whose mean is
+    far from zero."""
+    x = f32(M, K, scale=1.5) + 3.0
+    g, be = f32(K, scale=0.5) + 1.0, f32(K, scale=0.1)
+    W, c = f32(K, N, scale=0.05), f32(N, scale=0.1)
+    gw, cs, bb = _fold(g, be, W, c)
+    xd = gpu.from_numpy(x)
+    y = gpu.gelu(gpu.add_bias(gpu.matmul_pp_norm(gpu.pack_rows_x3(xd), gpu.row_stats_x3(xd), M,
+                                                 gpu.pack_weight_x3(gpu.from_numpy(gw)), gpu.from_numpy(cs), N),
+                              gpu.from_numpy(bb)))
+    ref = O.gelu_tanh(O.add_bias(O.matmul(O.layer_norm(x, g, be), W), c))
+    assert rel_err(y.to_numpy(), ref) < 1e-4
+
+
+def test_matmul_pp_norm_rejects_split_plans(gpu):
+    x = f32(16, 2048)
+    xd = gpu.from_numpy(x)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(f32(2048, 64)))
+    with pytest.raises(ValueError, match="matmul_pp"):
+        gpu.matmul_pp_norm(gpu.pack_rows_x3(xd), gpu.row_stats_x3(xd), 16, pk, gpu.from_numpy(f32(64)), 64).eval()
+
+
+@pytest.mark.parametrize("M,K,N,N2", [(128, 768, 768, 3072), (70, 512, 256, 512)])
+def test_producer_writes_rows_and_statistics(gpu, M, K, N, N2):
+    """x1 = r + (a @ W + b) on the fp32-A row panel writes x1, its packed rows
+    and its row statistics in one launch (the same bits as row_stats_x3 and
+    pack_rows_x3 of the stored x1), and the folded layer_norm product reading
+    them is one more launch, at the fp32 bar against the oracle."""
+    a, W, b, r = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1), f32(M, N)
+    g, be = f32(N, scale=0.5) + 1.0, f32(N, scale=0.1)
+    W2, c2 = f32(N, N2, scale=0.05), f32(N2, scale=0.1)
+    gw, cs, bb = _fold(g, be, W2, c2)
+    dev = [gpu.from_numpy(v) for v in (a, b, r, cs, bb)]
+    pk_w, pk_g = gpu.pack_weight_x3(gpu.from_numpy(W)), gpu.pack_weight_x3(gpu.from_numpy(gw))
+    for t in dev + [pk_w, pk_g]:
+        t.eval()
+    ad, bd, rd, csd, bbd = dev
+    x1 = rd + gpu.add_bias(gpu.matmul_packed(ad, pk_w, N), bd)
+    st, xp = gpu.row_stats_x3(x1), gpu.pack_rows_x3(x1)
+    y = gpu.gelu(gpu.add_bias(gpu.matmul_pp_norm(xp, st, M, pk_g, csd, N2), bbd))
+    before = gpu.graph_stats()
+    y.eval()
+    after = gpu.graph_stats()
+    assert after["launcher_calls"] - before["launcher_calls"] == 2
+    x1_np, st_np = x1.to_numpy(), st.to_numpy()
+    np.testing.assert_array_equal(st_np, gpu.row_stats_x3(gpu.from_numpy(x1_np)).to_numpy())
+    np.testing.assert_array_equal(_valid_rows(_bits_of(xp), M),
+                                  _valid_rows(_bits_of(gpu.pack_rows_x3(gpu.from_numpy(x1_np))), M))
+    x1_ref = r + O.add_bias(O.matmul(a, W), b)
+    assert rel_err(x1_np, x1_ref) < 1e-4
+    ref = O.gelu_tanh(O.add_bias(O.matmul(O.layer_norm(x1_ref, g, be), W2), c2))
+    assert rel_err(y.to_numpy(), ref) < 1e-4
