@@ -126,9 +126,9 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
             "x3": bool(x3), "fold_ln2": fold}
 
 
-# Widths whose projections both run unsplit row-panel GEMMs (fp32 rows into
-# c_proj, packed rows into c_fc), the condition for folding ln_2 into c_fc.
-_FOLD_WIDTHS = (256, 512, 768, 1024)
+# Widths whose c_proj and c_fc run unsplit packed-row panel GEMMs (K a
+# multiple of 256 up to 1536), the condition for folding ln_2 into c_fc.
+_FOLD_WIDTHS = (256, 512, 768, 1024, 1280, 1536)
 
 
 def _fold_ln2(np_weights: dict, p: str):
@@ -206,8 +206,9 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
         pos = gpu.from_numpy(np.arange(start, start + T, dtype=np.int32))
     x = gpu.embedding(w["transformer.wte.weight"], idx) + gpu.embedding(w["transformer.wpe.weight"], pos)
 
-    # fp32 packed-weight models: the projections that follow a layer_norm or
-    # gelu take their activations as packed rows
+    # fp32 packed-weight models: every projection takes its activations as
+    # packed rows, written by their producer (the embedding or a split-K
+    # reduction computing layer_norm, the attention kernel, a GEMM epilogue)
     rows = model.get("x3", False)
     mm_in = (lambda t, name: _mm_rows(model, t, name, T)) if rows else (lambda t, name: _mm(model, t, name))
     new_cache = []
@@ -232,7 +233,7 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
             new_cache.append((k, v))
             a = gpu.attention(q, k, v) if cached else gpu.attention_causal(q, k, v)
             a = gpu.reshape(gpu.transpose_dims(a, 0, 1), [T, d])
-        x = x + gpu.add_bias(_mm(model, a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
+        x = x + gpu.add_bias(mm_in(a, f"{p}.attn.c_proj.weight"), w[f"{p}.attn.c_proj.bias"])
 
         fold = model.get("fold_ln2", {}).get(i)
         if fold is not None:

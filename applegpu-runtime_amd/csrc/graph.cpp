@@ -462,6 +462,7 @@ void eval_all(const std::vector<TensorP>& roots) {
   std::unordered_set<Tensor*> emb_adds;            // embedding + embedding nodes run as one kernel
   std::unordered_map<Tensor*, TensorP> pack_of;    // group final node or paired layer_norm -> pack_rows_x3 of it
   std::unordered_map<Tensor*, TensorP> stats_of;   // group final node -> row_stats_x3 of it
+  std::unordered_map<Tensor*, TensorP> attn_pack;  // attention node -> pack_rows_x3 of its head-merged output
   for (auto& t : order) {
     Node* n = t->node.get();
     if (n->code == OP_ADD_BIAS && t->ndim == 2) {
@@ -543,6 +544,24 @@ void eval_all(const std::vector<TensorP>& roots) {
       // never stored.
       const TensorP& x = n->in[0];
       if (!x->pending() || x->dtype != DType::F32 || x->ndim != 2 || x->shape[1] % 16 != 0) continue;
+      // attention [H, T, D] -> transpose(0, 1) -> reshape [T, H*D] -> packed
+      // rows: the attention kernel writes the packed rows itself
+      if (x->node->code == OP_RESHAPE && is_single_internal_use(x, uses)) {
+        const TensorP& y = x->node->in[0];
+        if (y->pending() && y->node->code == OP_TRANSPOSE_DIMS && y->ndim == 3 && y->node->iv.size() == 2 &&
+            std::min(y->node->iv[0], y->node->iv[1]) == 0 && std::max(y->node->iv[0], y->node->iv[1]) == 1 &&
+            is_single_internal_use(y, uses)) {
+          const TensorP& a = y->node->in[0];
+          if (a->pending() && (a->node->code == OP_ATTENTION || a->node->code == OP_ATTENTION_CAUSAL) &&
+              a->ndim == 3 && a->dtype == DType::F32 && x->shape[0] == a->shape[1] &&
+              x->shape[1] == a->shape[0] * a->shape[2] && is_single_internal_use(a, uses)) {
+            attn_pack[a.get()] = t;
+            absorbed.insert(x.get());
+            absorbed.insert(y.get());
+            continue;
+          }
+        }
+      }
       auto git = groups.find(x.get());
       if (git != groups.end() && git->second.packed_n > 0 && ops::is_x3_packed(git->second.b) &&
           !post_ln.count(x.get()) && !pack_of.count(x.get())) {
@@ -857,9 +876,27 @@ void eval_all(const std::vector<TensorP>& roots) {
         g_stats.launches_saved += 2;
       }
     } else if (n->code == OP_ATTENTION || n->code == OP_ATTENTION_CAUSAL) {
+      const float scale = n->f.empty() ? 0.f : (float)n->f[0];
+      auto ap = attn_pack.find(t.get());
+      if (ap != attn_pack.end()) {
+        TensorP pk = ops::attention_rows_x3(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, scale);
+        if (pk) {
+          assign(ap->second, pk);
+          g_stats.launches_saved += 1;
+          order[i].reset();
+          continue;
+        }
+        // the kernel cannot write packed rows: the absorbed head merge and
+        // the pack run as ops after the attention
+        TensorP o = ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true, scale);
+        const Node* pn = ap->second->node.get();
+        const TensorP& xr = pn->in[0];
+        assign(ap->second, ops::pack_rows_x3(ops::reshape(ops::transpose_dims(o, 0, 1), xr->dims())));
+        order[i].reset();
+        continue;
+      }
       // Head-interleaved output: a following transpose(0,1)+reshape is free.
-      res = {ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true,
-                            n->f.empty() ? 0.f : (float)n->f[0])};
+      res = {ops::attention(n->in[0], n->in[1], n->in[2], n->code == OP_ATTENTION_CAUSAL, true, scale)};
     } else {
       res = run_op(n->code, n->in, n->f, n->iv);
     }

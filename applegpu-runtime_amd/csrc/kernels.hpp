@@ -309,6 +309,10 @@ struct Attn {
   const void* k = nullptr; int64_t k_sb = 0, k_sh = 0, k_st = 0;
   const void* v = nullptr; int64_t v_sb = 0, v_sh = 0, v_st = 0;
   void* o = nullptr; int64_t o_sb = 0, o_sh = 0, o_st = 0;
+  // fp32 MFMA kernel only: the output written instead as packed x3 rows of
+  // the [B*Tq, H*D] matrix whose row is one query of one batch entry (heads
+  // side by side), for a following packed-A GEMM (H*D % 16 == 0)
+  void* o_pk = nullptr;
   bool causal = false;   // key j visible to query i iff j <= i (diagonal at (0,0))
   float scale = 1.f;
   // nsplit > 0 (2, 4 or 8; fp32): q, k, v point at split 0 of a split-K GEMM

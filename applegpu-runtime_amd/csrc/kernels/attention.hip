@@ -22,6 +22,7 @@
 // (flash_attn_mfma for 16-bit, flash_attn_f32 below); other cases take the
 // scalar kernel.
 #include "device.hpp"
+#include "gemm_kernels.hpp"  // x3_store4: packed x3 rows of the output
 
 #include <type_traits>
 
@@ -47,6 +48,7 @@ struct AArgs {
   const float* qb; const float* kb; const float* vb;
   int64_t b_sh, plane;
   PfArgs pf;  // read-ahead blocks (fp32 kernel)
+  bf16_t* o_pk;  // fp32 kernel: packed x3 rows of [B*Tq, H*D] instead of o
 };
 
 // Four consecutive fp32 values: a plain load, or (NSP > 0) the sum of NSP
@@ -753,8 +755,14 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
 #pragma unroll
     for (int u = 0; u < DT; ++u) o[u] = acc[u][r] * inv;
 #pragma unroll
-    for (int u = 0; u < DT; u += 4)
-      *(float4*)(O + DT * (4 * g + r) + u) = make_float4(o[u], o[u + 1], o[u + 2], o[u + 3]);
+    for (int u = 0; u < DT; u += 4) {
+      if (p.o_pk) {
+        const float o4[4] = {o[u], o[u + 1], o[u + 2], o[u + 3]};
+        x3_store4(p.o_pk, p.H * D / 16, b * p.Tq + qi, h * D + DT * (4 * g + r) + u, o4);
+      } else {
+        *(float4*)(O + DT * (4 * g + r) + u) = make_float4(o[u], o[u + 1], o[u + 2], o[u + 3]);
+      }
+    }
   }
 }
 }  // namespace
@@ -825,7 +833,10 @@ void attention(const Attn& a, hipStream_t s) {
   p.causal = a.causal ? 1 : 0;
   p.qb = (const float*)a.qb; p.kb = (const float*)a.kb; p.vb = (const float*)a.vb;
   p.b_sh = a.b_sh; p.plane = a.plane;
+  p.o_pk = (bf16_t*)a.o_pk;
   if (a.nsplit > 0 && !attention_partials_ok(a)) fail("fused attention: projection partials need the fp32 MFMA kernel");
+  if (a.o_pk && !(attention_mfma_ok(a) && a.dt == DType::F32 && (a.H * a.D) % 16 == 0 && ((uintptr_t)a.o_pk & 15) == 0))
+    fail("fused attention: packed-row output needs the fp32 MFMA kernel and H*D %% 16 == 0");
   if (attention_mfma_ok(a) && a.dt == DType::F32) {
     // 64 queries per block when that gives every CU a block; else 16 per
     // block with the key tiles split across the block's wavefronts

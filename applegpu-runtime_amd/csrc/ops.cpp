@@ -1375,6 +1375,38 @@ TensorP attention(const TensorP& q, const TensorP& kk, const TensorP& v, bool ca
   return out;
 }
 
+TensorP attention_rows_x3(const TensorP& q, const TensorP& kk, const TensorP& v, bool causal, float scale_arg) {
+  if (q->ndim < 3 || q->ndim > 4 || kk->ndim != q->ndim || v->ndim != q->ndim) return nullptr;
+  if (q->dtype != DType::F32 || kk->dtype != DType::F32 || v->dtype != DType::F32) return nullptr;
+  for (int i = 0; i < q->ndim - 2; ++i)
+    if (kk->shape[i] != q->shape[i] || v->shape[i] != q->shape[i]) return nullptr;
+  const int64_t D = q->shape[q->ndim - 1], Tq = q->shape[q->ndim - 2], Tk = kk->shape[kk->ndim - 2];
+  if (kk->shape[kk->ndim - 1] != D || v->shape[v->ndim - 1] != D || v->shape[v->ndim - 2] != Tk) return nullptr;
+  if (q->strides[q->ndim - 1] != 1 || kk->strides[kk->ndim - 1] != 1 || v->strides[v->ndim - 1] != 1) return nullptr;
+  if (scale_arg < 0.f || !std::isfinite(scale_arg)) return nullptr;
+  k::Attn a;
+  a.dt = DType::F32;
+  a.Tq = Tq; a.Tk = Tk; a.D = D;
+  a.causal = causal;
+  a.scale = scale_arg > 0.f ? scale_arg : 1.0f / std::sqrt((float)D);
+  if (!k::attention_supported(a)) return nullptr;
+  a.B = q->ndim == 4 ? q->shape[0] : 1;
+  a.H = q->ndim == 4 ? q->shape[1] : q->shape[0];
+  if ((a.H * D) % 16 != 0) return nullptr;
+  auto lead = [](const Tensor& t, int64_t* sb, int64_t* sh) {
+    if (t.ndim == 3) { *sb = 0; *sh = t.strides[0]; }
+    else { *sb = t.strides[0]; *sh = t.strides[1]; }
+  };
+  a.q = q->data(); lead(*q, &a.q_sb, &a.q_sh); a.q_st = q->strides[q->ndim - 2];
+  a.k = kk->data(); lead(*kk, &a.k_sb, &a.k_sh); a.k_st = kk->strides[kk->ndim - 2];
+  a.v = v->data(); lead(*v, &a.v_sb, &a.v_sh); a.v_st = v->strides[v->ndim - 2];
+  const int64_t rows = a.B * Tq;
+  TensorP out = alloc_out(DType::BF16, {(rows + 31) / 32, a.H * D / 16, 2, 64, 8});
+  a.o_pk = out->data();
+  LAUNCH k::attention(a, rt().stream());
+  return out;
+}
+
 TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int64_t n_head, bool causal,
                       int64_t batch, bool read_partials) {
   const char* name = "qkv_attention";

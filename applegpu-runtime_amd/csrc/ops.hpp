@@ -187,6 +187,11 @@ TensorP qkv_attention(const TensorP& x, const TensorP& w, const TensorP& b, int6
 // (crates/core/src/ops.rs:1531-1620).
 TensorP attention(const TensorP& q, const TensorP& k, const TensorP& v, bool causal,
                   bool out_layout_thd = false, float scale = 0.f);
+// The same attention (fp32, fused kernel) with its output written as packed
+// x3 rows (pack_rows_x3) of the [B*Tq, H*D] matrix of head-merged query rows:
+// the A operand of the following projection (matmul_pp), never stored in
+// fp32.  Null when the fused fp32 kernel cannot take the operands.
+TensorP attention_rows_x3(const TensorP& q, const TensorP& k, const TensorP& v, bool causal, float scale = 0.f);
 // q [B, H, Tq, D] against the first lens[b] rows of the [B, H, Tmax, D] caches
 // (lens int32 [B] on the device; the queries' own keys are the last Tq of
 // them); the output is logically [B, H, Tq, D], stored as [B, Tq, H, D].

@@ -421,3 +421,33 @@ def test_producer_writes_rows_and_statistics(gpu, M, K, N, N2):
     assert rel_err(x1_np, x1_ref) < 1e-4
     ref = O.gelu_tanh(O.add_bias(O.matmul(O.layer_norm(x1_ref, g, be), W2), c2))
     assert rel_err(y.to_numpy(), ref) < 1e-4
+
+
+@pytest.mark.parametrize("H,T,D,causal", [(12, 128, 64, True), (4, 50, 64, False), (2, 33, 128, True)])
+def test_attention_writes_packed_rows(gpu, H, T, D, causal):
+    """attention -> heads merged ([H, T, D] -> [T, H*D]) -> packed rows: the
+    attention kernel writes the packed rows itself (one launch for the three
+    ops); the same bits as packing the merged fp32 output, and the product
+    reading them at the fp32 bar."""
+    q, k, v = f32(H, T, D), f32(H, T, D), f32(H, T, D)
+    N = 96
+    w = f32(H * D, N, scale=0.05)
+    pk = gpu.pack_weight_x3(gpu.from_numpy(w))
+    dq, dk, dv = (gpu.from_numpy(a) for a in (q, k, v))
+    for t in (pk, dq, dk, dv):
+        t.eval()
+    att = gpu.attention_causal if causal else gpu.attention
+    merged = gpu.reshape(gpu.transpose_dims(att(dq, dk, dv), 0, 1), [T, H * D])
+    rows = gpu.pack_rows_x3(merged)
+    del merged
+    before = gpu.graph_stats()
+    rows.eval()
+    after = gpu.graph_stats()
+    assert after["launcher_calls"] - before["launcher_calls"] == 1
+    ref_merged = gpu.reshape(gpu.transpose_dims(att(dq, dk, dv), 0, 1), [T, H * D]).to_numpy()
+    np.testing.assert_array_equal(_valid_rows(_bits_of(rows), T),
+                                  _valid_rows(_bits_of(gpu.pack_rows_x3(gpu.from_numpy(ref_merged))), T))
+    o = O.attention(q, k, v, causal=causal)
+    assert rel_err(ref_merged, o.transpose(1, 0, 2).reshape(T, H * D)) < 1e-4
+    y = gpu.matmul_pp(rows, T, pk, N).to_numpy()
+    assert rel_err(y, O.matmul(o.transpose(1, 0, 2).reshape(T, H * D), w)) < 1e-4
