@@ -119,6 +119,11 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
                 p = gpu.pack_weight_x3(t)
                 p.eval()
                 pk[k] = (p, t.shape[1], "x3")
+        # the tied LM head as B = wte^T, for the weight-streaming GEMM
+        wte = w["transformer.wte.weight"]
+        p = gpu.pack_weight_x3(gpu.transpose(wte))
+        p.eval()
+        pk["transformer.wte.weight"] = (p, wte.shape[0], "x3")
         if cfg["n_embd"] in _FOLD_WIDTHS:
             for i in range(cfg["n_layer"]):
                 fold[i] = _fold_ln2(np_weights, f"transformer.h.{i}")
@@ -248,7 +253,10 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
         x = x + gpu.add_bias(mm_in(f, f"{p}.mlp.c_proj.weight"), w[f"{p}.mlp.c_proj.bias"])
 
     x = gpu.layer_norm(x, w["transformer.ln_f.weight"], w["transformer.ln_f.bias"])
-    logits = x @ gpu.transpose(w["transformer.wte.weight"])
+    if rows:
+        logits = mm_in(x, "transformer.wte.weight")
+    else:
+        logits = x @ gpu.transpose(w["transformer.wte.weight"])
     return logits, (new_cache if need_cache or cached else None)
 
 

@@ -227,8 +227,11 @@ void pack_weights_x3(const void* b, int64_t b_sk, int64_t b_sn, int64_t K, int64
 // the prologue; with packed A (apk), K = 128 kpw (kpw 2..12, even).
 // split: a plan that ends in a split-K reduction is required (the reduction
 // computes a layer_norm of the output).
+// stream: packed A, many columns (a vocabulary head): one block per 128 rows
+// x 128 columns over the whole K, so that every weight byte is read once.
 struct X3Plan {
   bool rows = false;
+  bool stream = false;
   bool apk = false;
   int kpw = 0;
   bool wide = true;

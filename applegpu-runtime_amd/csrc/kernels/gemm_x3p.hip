@@ -580,6 +580,111 @@ __global__ void __launch_bounds__(256) row_tile_stats_kernel(const float* __rest
   *(float2*)(out + gid * 2) = make_float2(sm_, d2);
 }
 
+// Weight-streaming panel for packed A and many columns (a vocabulary head:
+// 128 x 768 x 50257).  A row panel reads each weight strip once per 32-row
+// tile, so at four row tiles the weights would come from HBM four times; here
+// one block (four wavefronts) owns up to 128 rows (wave w: A strip w) and
+// NC column strips over the whole K, so each weight byte is read once.  K is
+// walked in chunks of KC k steps: chunk c's weight fragments are loaded into
+// registers S chunks ahead (256 threads share the loads), written to one of
+// two LDS buffers when chunk c comes up, and read from there by every wave;
+// each wave loads its own A fragments (small, L2-resident) S chunks ahead too.
+// One barrier per chunk.  Epilogue per element as gemm_x3p's unsplit path.
+// Launched as NC = 4 strips, KC = 1 step, S = 8 chunks ahead: for GPT-2's
+// head (cold weights) 50 us against 52-78 us for deeper chunks, fewer or more
+// strips, and 67 us for the fp32 tiled GEMM.
+template <int NC, int KC, int S>
+__global__ void __launch_bounds__(256, 2) gemm_x3_stream(GArgs p) {
+  constexpr int NV = NC * KC * 2 * 64;  // 16-byte fragment pieces per chunk
+  static_assert(NV % 256 == 0, "chunk split over 256 threads");
+  constexpr int PER = NV / 256;
+  __shared__ __attribute__((aligned(16))) bf16x8_t sB[2][NV];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t T = p.K >> 4;
+  const int nch = (int)(T / KC);
+  const int64_t Sm = (p.M + 31) / 32, Sn = (p.N + 31) / 32;
+  const int64_t tn = blockIdx.x, tm = blockIdx.y;
+  int64_t sa = tm * 4 + wave;
+  sa = sa < Sm ? sa : Sm - 1;
+  const bf16_t* Ap = (const bf16_t*)p.A + (sa * T * 2) * 512 + lane * 8;
+  const bf16_t* Bp = (const bf16_t*)p.B;
+  // this thread's pieces of a chunk: piece i -> (strip j, step kk, part h, lane l)
+  int64_t boff[PER];
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int i = threadIdx.x + 256 * r;
+    const int l = i & 63, h = (i >> 6) & 1, kk = (i >> 7) % KC, j = i / (128 * KC);
+    int64_t st = tn * NC + j;
+    st = st < Sn ? st : Sn - 1;
+    boff[r] = ((st * T + kk) * 2 + h) * 512 + l * 8;
+  }
+  bf16x8_t bst[S][PER], ah[S][KC], al[S][KC];
+  f32x16 acc[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+
+#define AGPU_STREAM_ISSUE(c, u)                                                                   \
+  {                                                                                               \
+    _Pragma("unroll") for (int r = 0; r < PER; ++r) bst[u][r] =                                    \
+        *(const bf16x8_t*)(Bp + boff[r] + (int64_t)(c) * KC * 1024);                               \
+    _Pragma("unroll") for (int kk = 0; kk < KC; ++kk) {                                            \
+      ah[u][kk] = *(const bf16x8_t*)(Ap + ((int64_t)(c) * KC + kk) * 1024);                         \
+      al[u][kk] = *(const bf16x8_t*)(Ap + ((int64_t)(c) * KC + kk) * 1024 + 512);                   \
+    }                                                                                             \
+  }
+#pragma unroll
+  for (int u = 0; u < S; ++u)
+    if (u < nch) AGPU_STREAM_ISSUE(u, u)
+  for (int cb = 0; cb < nch; cb += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int c = cb + u;
+      if (c >= nch) break;
+      const int buf = c & 1;
+      // chunk c's weight fragments into LDS (the other buffer may still be
+      // read by a wave finishing chunk c - 1), then one barrier
+#pragma unroll
+      for (int r = 0; r < PER; ++r) sB[buf][threadIdx.x + 256 * r] = bst[u][r];
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < KC; ++kk) {
+#pragma unroll
+        for (int j = 0; j < NC; ++j) {
+          const bf16x8_t bh = sB[buf][((j * KC + kk) * 2 + 0) * 64 + lane];
+          const bf16x8_t bl = sB[buf][((j * KC + kk) * 2 + 1) * 64 + lane];
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[u][kk], bh, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[u][kk], bl, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[u][kk], bh, acc[j], 0, 0, 0);
+        }
+      }
+      if (c + S < nch) AGPU_STREAM_ISSUE(c + S, u)
+    }
+  }
+#undef AGPU_STREAM_ISSUE
+  // output block (wave, j): lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
+  const int64_t r0 = (tm * 4 + wave) * 32 + 4 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int64_t col = (tn * NC + j) * 32 + (lane & 31);
+    const int64_t cc = col < p.N ? col : p.N - 1;
+    const float bias = p.bias ? ((const float*)p.bias)[cc] : 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = r0 + 8 * (r >> 2) + (r & 3);
+      if (row >= p.M || col >= p.N) continue;
+      float v = p.alpha * acc[j][r] + bias;
+      if (p.act == kActRelu) v = fmaxf(v, 0.f);
+      else if (p.act == kActGelu) v = gelu_tanh(v);
+      else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+      if (p.res) v += ((const float*)p.res)[row * p.r_sm + col];
+      if (p.mask) v = ((const float*)p.mask)[row * p.k_sm + col] > 0.f ? v : 0.f;
+      ((float*)p.C)[row * p.c_sm + col] = v;
+    }
+  }
+}
+
 template <int FR, int FC, int WR, int WC, bool APK>
 void launch_x3p_kt(const GArgs& p, int kt, int64_t T, dim3 grid, hipStream_t s) {
   switch (kt) {
@@ -629,6 +734,16 @@ X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus, bool apk, bool split) {
   // A forced tile family (applegpu_ffi_gemm_tune's cfg for packed weights):
   // 0 wide split tiles, 1 narrow split tiles, 2 the packed-A row panel.
   const int fcfg = gemm_tune().cfg;
+  // Packed A with many columns (each weight strip would be read by several
+  // row panels): the weight-streaming panel, 128 x 128 per block, whole K.
+  if (apk && !split && forced == 0 && (fcfg == -1 || fcfg == 3) && K % 32 == 0 &&
+      (fcfg == 3 || (N >= 8192 && ((M + 31) / 32) * ((N + 31) / 32) >= 2048))) {
+    pl.stream = true;
+    pl.tiles_m = (M + 127) / 128;
+    pl.tiles_n = (N + 127) / 128;
+    pl.splits = 1;
+    return pl;
+  }
   // Packed A: the 8-wave row-panel kernel over K ranges of 8 kpw k steps,
   // whole K per block when that fits (no split-K reduction launch), else the
   // deepest range whose grid still gives every CU a block.
@@ -739,6 +854,13 @@ void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s) {
   if (p.rs_out && !(panel && p.N % 32 == 0))
     fail("gemm_x3p: row statistics need an unsplit row-panel plan and N %% 32 == 0");
   if (p.rs_in && !(panel && pl.apk)) fail("gemm_x3p: a folded layer_norm needs the unsplit packed-A row-panel plan");
+  if (pl.stream) {
+    if (p.ln_g || !pl.apk) fail("internal: the weight-streaming panel takes packed A only");
+    if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535) fail("gemm_x3_stream: grid too large");
+    hipLaunchKernelGGL((gemm_x3_stream<4, 1, 8>), dim3((unsigned)pl.tiles_n, (unsigned)pl.tiles_m), dim3(256), 0, s, p);
+    check_launch("gemm_x3_stream");
+    return;
+  }
   if (pl.rows && pl.apk) {
     if (p.ln_g) fail("gemm_x3p: a layer_norm prologue needs fp32 A");
     launch_rows_pk(pl, p, s);

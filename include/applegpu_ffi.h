@@ -251,7 +251,8 @@ uint64_t applegpu_graph_bytes(int64_t handle);
  * cfg: -1 = heuristic, 0..10 = tile configuration (BM x BN x BK: 128x128x32,
  * 64x128x32, 64x64x64, 32x64x64, 32x32x64, 128x128x64, 64x64x64, 64x128x64,
  * 32x32x256, 32x64x256, 64x64x128); for fp32 weights packed by pack_weight_x3:
- * 0 = 128x64 split tiles, 1 = 128x32 split tiles, 2 = 32x32 row panels.
+ * 0 = 128x64 split tiles, 1 = 128x32 split tiles, 2 = 32x32 row panels,
+ * 3 = 128x128 weight-streaming panels (packed activation rows).
  * splits: 0 = heuristic, n = split K across n blocks.
  * Returns 0, or -1 for an out-of-range value. */
 int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits);

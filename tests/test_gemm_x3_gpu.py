@@ -451,3 +451,27 @@ def test_attention_writes_packed_rows(gpu, H, T, D, causal):
     assert rel_err(ref_merged, o.transpose(1, 0, 2).reshape(T, H * D)) < 1e-4
     y = gpu.matmul_pp(rows, T, pk, N).to_numpy()
     assert rel_err(y, O.matmul(o.transpose(1, 0, 2).reshape(T, H * D), w)) < 1e-4
+
+
+@pytest.mark.parametrize("M,K,N,forced", [(128, 768, 16448, False), (200, 256, 300, True), (1, 64, 130, True),
+                                          (33, 512, 1000, True), (130, 96, 260, True)])
+def test_weight_streaming_panel_matches_oracle(gpu, M, K, N, forced):
+    """Packed rows times many columns (a vocabulary head) runs the
+    weight-streaming panel (every weight byte read once, LDS-staged); forced
+    through gemm_tune's cfg 3 for small and ragged shapes and more than 128
+    rows; at the fp32 bar, and exact on small integers."""
+    from applegpu_runtime._native import lib
+    a, b = f32(M, K), f32(K, N, scale=0.05)
+    if forced:
+        assert lib.applegpu_ffi_gemm_tune(0, 3, 0) == 0
+    try:
+        got = gpu.matmul_pp(gpu.pack_rows_x3(gpu.from_numpy(a)), M, gpu.pack_weight_x3(gpu.from_numpy(b)), N)
+        got = got.to_numpy()
+        ai = RNG.integers(-3, 4, (M, K)).astype(np.float32)
+        bi = RNG.integers(-3, 4, (K, N)).astype(np.float32)
+        exact = gpu.matmul_pp(gpu.pack_rows_x3(gpu.from_numpy(ai)), M, gpu.pack_weight_x3(gpu.from_numpy(bi)), N)
+        exact = exact.to_numpy()
+    finally:
+        lib.applegpu_ffi_gemm_tune(0, -1, 0)
+    assert rel_err(got, O.matmul(a, b)) < 1e-4
+    np.testing.assert_array_equal(exact, ai @ bi)
