@@ -728,6 +728,95 @@ __global__ void __launch_bounds__(256) dequantize_rows_kernel(const int8_t* __re
   }
 }
 
+// ── 16-values-per-thread quantize (C5's [8192, 8192]) ─────────────────────
+// A thread owns groups of 16 consecutive values: 64 bytes of fp32 in (four
+// 16-byte loads), 16 bytes of codes out (one store).  C5: 60 us, 0.69 of HBM
+// peak, against 65 us with four values per thread and 4-byte code stores.
+// (The same layout for dequantize measured 96 us: its 64-byte-per-lane
+// stores are not coalesced within an instruction; dequantize_rows_4x4 keeps
+// every access coalesced instead.  Nontemporal loads and stores made both
+// far slower.)
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_v __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ void load16(const T* __restrict__ p, float (&v)[16]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4_v a = ((const f32x4_v*)p)[i];
+      v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const u32x4_v a = ((const u32x4_v*)p)[i];
+      const T* h = (const T*)&a;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[8 * i + j] = to_f(h[j]);
+    }
+  }
+}
+// Per-row int8 quantize, one 256-thread block per row of 4096 NG values
+// (cols % 4096 == 0, 16-byte aligned rows); the arithmetic of
+// quantize_rows_kernel.
+template <typename T, int NG>
+__global__ void __launch_bounds__(256) quantize_rows_v16(const T* __restrict__ x, int8_t* __restrict__ q,
+                                                         float* __restrict__ scale, int64_t cols) {
+  __shared__ float sh[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * cols;
+  int8_t* qr = q + row * cols;
+  float v[NG][16];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) load16<T>(xr + ((int64_t)g * 256 + threadIdx.x) * 16, v[g]);
+  float m = 0.f;
+#pragma unroll
+  for (int g = 0; g < NG; ++g)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[g][j]));
+  const float sc = block_max(m, sh) / 127.f;
+  if (threadIdx.x == 0) scale[row] = sc;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    u32x4_v out;
+    int8_t* b = (int8_t*)&out;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float r = sc == 0.f ? 0.f : rintf(v[g][j] / sc);
+      r = fminf(fmaxf(r, -128.f), 127.f);
+      b[j] = (int8_t)(int)r;
+    }
+    *(u32x4_v*)(qr + ((int64_t)g * 256 + threadIdx.x) * 16) = out;
+  }
+}
+
+// y = codes * scale[row] for a block of 4096 columns of one row: thread t
+// takes columns 4 (t + 256 i) .. + 3 for i = 0..3, so each of its four
+// 4-byte code loads and 16-byte (fp32) stores is one coalesced wavefront
+// access, and the four pairs are in flight together.  cols % 4096 == 0,
+// 16-byte aligned rows.  C5: 61 us, 0.69 of HBM peak (68 us with one group
+// per thread).
+template <typename T>
+__global__ void __launch_bounds__(256) dequantize_rows_4x4(const int8_t* __restrict__ q,
+                                                           const float* __restrict__ scale, T* __restrict__ y,
+                                                           int64_t cols) {
+  const int64_t row = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * 4096 + threadIdx.x * 4;
+  const float sc = scale[row];
+  int32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = *(const int32_t*)(q + row * cols + c0 + 1024 * i);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int8_t* b = (const int8_t*)&w[i];
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (float)b[j] * sc;
+    store4<T, true>(y + row * cols, c0 + 1024 * i, cols, true, v);
+  }
+}
+
 // Per-row int8 quantize with one wavefront per row for rows of up to 2048
 // columns: the row stays in registers, the absmax is a wave reduction (no
 // block barrier), then the codes are written 4 per lane.  Longer rows take
@@ -896,6 +985,15 @@ void q_launch(const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols
   }
   int64_t nv = (cols + 1023) / 1024;
   dim3 g((unsigned)rows);
+  if (vec && cols % 4096 == 0 && cols <= 4096 * 4 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 15) == 0 &&
+      (cols * (int64_t)sizeof(T)) % 16 == 0) {
+    switch (cols / 4096) {
+      case 1: hipLaunchKernelGGL((quantize_rows_v16<T, 1>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
+      case 2: hipLaunchKernelGGL((quantize_rows_v16<T, 2>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
+      case 3: hipLaunchKernelGGL((quantize_rows_v16<T, 3>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
+      default: hipLaunchKernelGGL((quantize_rows_v16<T, 4>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
+    }
+  }
 #define AGPU_Q(NV)                                                                                   \
   if (vec && cols == NV * 1024)                                                                      \
     hipLaunchKernelGGL((quantize_rows_kernel<T, NV, true>), g, dim3(256), 0, s, (const T*)x, q, scale, cols, vec); \
@@ -1073,6 +1171,12 @@ void dequantize_rows(DType out, const int8_t* q, const float* scale, void* y, in
                      hipStream_t s) {
   if (rows == 0 || cols == 0) return;
   AGPU_FLOAT_SWITCH(out, {
+    if (cols % 4096 == 0 && rows <= 65535 && ((uintptr_t)q % 16) == 0 && ((uintptr_t)y % 16) == 0) {
+      hipLaunchKernelGGL((dequantize_rows_4x4<T>), dim3((unsigned)(cols / 4096), (unsigned)rows), dim3(256), 0, s, q,
+                         scale, (T*)y, cols);
+      check_launch("dequantize_rows");
+      return;
+    }
     const bool vec = ((uintptr_t)q % 4) == 0 && ((uintptr_t)y % (4 * sizeof(T))) == 0 && cols % 4 == 0;
     dim3 grid((unsigned)((cols + 1023) / 1024), (unsigned)(rows < 65535 ? rows : 65535));
     if (vec) hipLaunchKernelGGL((dequantize_rows_kernel<T, true>), grid, dim3(256), 0, s, q, scale, (T*)y, rows, cols);

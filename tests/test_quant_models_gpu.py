@@ -205,3 +205,29 @@ def test_mlp_config3_step_vs_oracle(gpu):
         # the update itself (lr * grad, a product of GEMMs): fp32 GEMM bar 1e-3
         assert rel_err(w - w0, wr - w0) < 1e-3
         assert rel_err(b - b0, br - b0) < 1e-3
+
+
+@pytest.mark.parametrize("rows,cols", [(4, 4096), (3, 12288), (2, 16384), (5, 1040), (6, 8192)])
+@pytest.mark.parametrize("dt", ["float32", "float16", "bfloat16"])
+def test_quantize_dequantize_wide_rows_bit_exact(gpu, rows, cols, dt):
+    """The 16-values-per-thread paths (rows of 4096 k values for quantize,
+    16-aligned rows of >= 1024 for dequantize), from fp32 and 16-bit input and
+    into each float output: codes and scales bit-exact against the oracle on
+    the input as stored, dequantized values equal to the oracle's rounded to
+    the output dtype."""
+    w32 = (RNG.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    w = gpu.from_numpy(w32)
+    if dt != "float32":
+        w = gpu.cast(w, dt)
+    w_stored = w.to_numpy().astype(np.float32)
+    q, s = gpu.quantize_per_row(w)
+    qr, sr = O.quantize_per_row(w_stored)
+    np.testing.assert_array_equal(s.to_numpy(), sr)
+    np.testing.assert_array_equal(q.to_numpy(), qr)
+    d = gpu.dequantize_per_row(q, s, dt).to_numpy().astype(np.float32)
+    ref = O.dequantize_per_row(qr, sr)
+    if dt == "float32":
+        np.testing.assert_array_equal(d, ref)
+    else:
+        want = gpu.cast(gpu.from_numpy(ref), dt).to_numpy().astype(np.float32)
+        np.testing.assert_array_equal(d, want)
