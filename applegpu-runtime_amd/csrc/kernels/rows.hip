@@ -66,6 +66,71 @@ __device__ __forceinline__ void store4(T* __restrict__ row, int64_t c, int64_t l
   }
 }
 
+// Register-resident rows: group i of a lane holds 4 consecutive columns.
+// fp32: lane l's group i starts at column 4 (64 i + l) (one 16-byte load).
+// 16-bit: groups 2p and 2p + 1 are 8 consecutive columns starting at
+// 512 p + 8 l, so that one 16-byte load fills both; with an odd group count
+// the last group alone covers columns 256 (NV - 1) + 4 l.  Either way a
+// wavefront covers columns [0, 256 NV), each exactly once.
+template <typename T, int NV>
+__device__ __forceinline__ int64_t gcol(int i, int lane) {
+  if constexpr (sizeof(T) == 4) {
+    return ((int64_t)i * 64 + lane) * 4;
+  } else {
+    if (NV % 2 == 1 && i == NV - 1) return (int64_t)256 * (NV - 1) + 4 * lane;
+    return ((int64_t)(i >> 1) * 64 + lane) * 8 + (i & 1) * 4;
+  }
+}
+// The 16-bit wide loads need 16-byte aligned rows: the base 16-byte aligned
+// and the leading dimension a multiple of 16 bytes.
+inline bool vec16_ok(const void* p, int64_t ld, size_t esz) {
+  return ((uintptr_t)p % 16) == 0 && ((ld * (int64_t)esz) % 16) == 0;
+}
+template <typename T, int NV, bool FULL>
+__device__ __forceinline__ void load_groups(const T* __restrict__ row, int lane, int64_t limit, bool vec, float fill,
+                                            float (&v)[NV][4]) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = gcol<T, NV>(i, lane);
+    if constexpr (sizeof(T) == 2) {
+      if (i % 2 == 0 && i + 1 < NV && (FULL || (vec && c + 8 <= limit))) {
+        T tmp[8];
+        *(uint4*)tmp = *(const uint4*)(row + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[i][j] = to_f(tmp[j]);
+          v[i + 1][j] = to_f(tmp[4 + j]);
+        }
+        continue;
+      }
+      if (i % 2 == 1 && (FULL || (vec && c + 4 <= limit))) continue;  // filled with group i - 1
+    }
+    load4<T, FULL>(row, c, limit, vec, fill, v[i]);
+  }
+}
+template <typename T, int NV, bool FULL>
+__device__ __forceinline__ void store_groups(T* __restrict__ row, int lane, int64_t limit, bool vec,
+                                             const float (&v)[NV][4]) {
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = gcol<T, NV>(i, lane);
+    if constexpr (sizeof(T) == 2) {
+      if (i % 2 == 0 && i + 1 < NV && (FULL || (vec && c + 8 <= limit))) {
+        T tmp[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          tmp[j] = from_f<T>(v[i][j]);
+          tmp[4 + j] = from_f<T>(v[i + 1][j]);
+        }
+        *(uint4*)(row + c) = *(const uint4*)tmp;
+        continue;
+      }
+      if (i % 2 == 1 && (FULL || (vec && c + 4 <= limit))) continue;  // stored with group i - 1
+    }
+    store4<T, FULL>(row, c, limit, vec, v[i]);
+  }
+}
+
 // ── softmax family, register-resident (cols <= 256 * NV) ─────────────────
 template <typename T, int NV, bool FULL>
 __global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict__ x, int64_t ldx,
@@ -83,29 +148,36 @@ __global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict_
   }
   float v[NV][4];
   float mx = -INFINITY;
+  // Columns at or past `valid` hold -inf from here on (the guarded loads
+  // fill them, the full-row path masks them), so exp gives them 0.
+  load_groups<T, NV, FULL>(xr, lane, FULL ? cols : valid, vec, -INFINITY, v);
+  if (FULL && op == kSoftmaxCausal) {
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    int64_t c = ((int64_t)i * 64 + lane) * 4;
-    if constexpr (FULL) load4<T, true>(xr, c, cols, vec, -INFINITY, v[i]);
-    else load4(xr, c, valid, vec, -INFINITY, v[i]);
-  }
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = gcol<T, NV>(i, lane);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    int64_t c = ((int64_t)i * 64 + lane) * 4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (FULL && c + j >= valid) v[i][j] = -INFINITY;  // causal mask
-      mx = fmaxf(mx, v[i][j]);
+      for (int j = 0; j < 4; ++j)
+        if (c + j >= valid) v[i][j] = -INFINITY;
     }
   }
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, v[i][j]);
   mx = wave_max(mx);
+  // 16-bit outputs round to 2^-11 or coarser: exp(v - mx) as 2^(v log2 e -
+  // mx log2 e) on the hardware exp2 (about 1 ulp of fp32) is well inside
+  // that; fp32 rows keep the correctly range-reduced expf.
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float mxl = mx * kLog2e;
   float sum = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    int64_t c = ((int64_t)i * 64 + lane) * 4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      float e = (c + j < valid) ? expf(v[i][j] - mx) : 0.f;
+      float e;
+      if constexpr (sizeof(T) == 2) e = __builtin_amdgcn_exp2f(fmaf(v[i][j], kLog2e, -mxl));
+      else e = expf(v[i][j] - mx);
       sum += e;
       if (op != kLogSoftmax) v[i][j] = e;
     }
@@ -114,22 +186,17 @@ __global__ void __launch_bounds__(256) softmax_wave(int op, const T* __restrict_
   if (op == kLogSoftmax) {
     const float ls = logf(sum);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      int64_t c = ((int64_t)i * 64 + lane) * 4;
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[i][j] = v[i][j] - mx - ls;
-      store4<T, FULL>(yr, c, cols, vec, v[i]);
-    }
   } else {
     const float inv = 1.f / sum;  // one division per row, then products
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      int64_t c = ((int64_t)i * 64 + lane) * 4;
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[i][j] = (c + j < valid) ? v[i][j] * inv : 0.f;
-      store4<T, FULL>(yr, c, cols, vec, v[i]);
-    }
+      for (int j = 0; j < 4; ++j) v[i][j] *= inv;
   }
+  store_groups<T, NV, FULL>(yr, lane, cols, vec, v);
 }
 
 // Block-wide reductions for 256 threads.
@@ -196,18 +263,16 @@ __global__ void __launch_bounds__(256) layer_norm_wave(const T* __restrict__ x, 
   T* yr = y + row * cols;
   float v[NV][4];
   float s = 0.f;
+  load_groups<T, NV, FULL>(xr, lane, cols, vec, 0.f, v);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    int64_t c = ((int64_t)i * 64 + lane) * 4;
-    load4<T, FULL>(xr, c, cols, vec, 0.f, v[i]);
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s += v[i][j];
-  }
   const float mean = wave_sum(s) / (float)cols;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    int64_t c = ((int64_t)i * 64 + lane) * 4;
+    const int64_t c = gcol<T, NV>(i, lane);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float d = (c + j < cols) ? v[i][j] - mean : 0.f;
@@ -216,16 +281,14 @@ __global__ void __launch_bounds__(256) layer_norm_wave(const T* __restrict__ x, 
   }
   const float var = wave_sum(q) / (float)cols;
   const float inv = 1.f / sqrtf(var + eps);
+  float gv[NV][4], bv[NV][4];
+  load_groups<T, NV, FULL>(g, lane, cols, vec, 0.f, gv);
+  load_groups<T, NV, FULL>(b, lane, cols, vec, 0.f, bv);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    int64_t c = ((int64_t)i * 64 + lane) * 4;
-    float gv[4], bv[4];
-    load4<T, FULL>(g, c, cols, vec, 0.f, gv);
-    load4<T, FULL>(b, c, cols, vec, 0.f, bv);
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[i][j] = gv[j] * (v[i][j] - mean) * inv + bv[j];
-    store4<T, FULL>(yr, c, cols, vec, v[i]);
-  }
+    for (int j = 0; j < 4; ++j) v[i][j] = gv[i][j] * (v[i][j] - mean) * inv + bv[i][j];
+  store_groups<T, NV, FULL>(yr, lane, cols, vec, v);
 }
 
 template <typename T>
@@ -270,14 +333,12 @@ __global__ void __launch_bounds__(256) layer_norm_bwd_wave(const T* __restrict__
   const T* dr = dy + row * cols;
   float v[NV][4], d[NV][4];
   float s = 0.f;
+  load_groups<T, NV, FULL>(xr, lane, cols, vec, 0.f, v);
+  load_groups<T, NV, FULL>(dr, lane, cols, vec, 0.f, d);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c = ((int64_t)i * 64 + lane) * 4;
-    load4<T, FULL>(xr, c, cols, vec, 0.f, v[i]);
-    load4<T, FULL>(dr, c, cols, vec, 0.f, d[i]);
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) s += v[i][j];
-  }
   float mean, inv;
   if (mean_in) {
     mean = to_f(mean_in[row]);
@@ -287,7 +348,7 @@ __global__ void __launch_bounds__(256) layer_norm_bwd_wave(const T* __restrict__
     float q = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int64_t c = ((int64_t)i * 64 + lane) * 4;
+      const int64_t c = gcol<T, NV>(i, lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float e = (c + j < cols) ? v[i][j] - mean : 0.f;
@@ -297,30 +358,29 @@ __global__ void __launch_bounds__(256) layer_norm_bwd_wave(const T* __restrict__
     inv = 1.f / sqrtf(wave_sum(q) / (float)cols + eps);
   }
   float s1 = 0.f, s2 = 0.f;
+  {
+    float gv[NV][4];
+    load_groups<T, NV, FULL>(g, lane, cols, vec, 0.f, gv);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c = ((int64_t)i * 64 + lane) * 4;
-    float gv[4];
-    load4<T, FULL>(g, c, cols, vec, 0.f, gv);
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = gcol<T, NV>(i, lane);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float xh = (c + j < cols) ? (v[i][j] - mean) * inv : 0.f;
-      const float dg = d[i][j] * gv[j];  // 0 past the row (both loads fill 0)
-      v[i][j] = xh;
-      d[i][j] = dg;
-      s1 += dg;
-      s2 += dg * xh;
+      for (int j = 0; j < 4; ++j) {
+        const float xh = (c + j < cols) ? (v[i][j] - mean) * inv : 0.f;
+        const float dg = d[i][j] * gv[i][j];  // 0 past the row (both loads fill 0)
+        v[i][j] = xh;
+        d[i][j] = dg;
+        s1 += dg;
+        s2 += dg * xh;
+      }
     }
   }
   const float m1 = wave_sum(s1) / (float)cols, m2 = wave_sum(s2) / (float)cols;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t c = ((int64_t)i * 64 + lane) * 4;
-    float o[4];
+  for (int i = 0; i < NV; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = inv * (d[i][j] - m1 - v[i][j] * m2);
-    store4<T, FULL>(dx + row * cols, c, cols, vec, o);
-  }
+    for (int j = 0; j < 4; ++j) v[i][j] = inv * (d[i][j] - m1 - v[i][j] * m2);
+  store_groups<T, NV, FULL>(dx + row * cols, lane, cols, vec, v);
   if (stats && lane == 0) {
     stats[2 * row] = mean;
     stats[2 * row + 1] = inv;
@@ -446,26 +506,28 @@ __global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, 
   const T* rc = w2 + (okc ? c : 0) * cols;
   float v[NV][4];
   float s = 0.f;
+  {
+    float q[NV][4];
+    load_groups<T, NV, false>(ra, lane, cols, vec, 0.f, v);
+    load_groups<T, NV, false>(rc, lane, cols, vec, 0.f, q);
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int64_t col = ((int64_t)i * 64 + lane) * 4;
-    float p[4], q[4];
-    load4<T>(ra, col, cols, vec, 0.f, p);
-    load4<T>(rc, col, cols, vec, 0.f, q);
+    for (int i = 0; i < NV; ++i) {
+      const int64_t col = gcol<T, NV>(i, lane);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      // the sum as stored (rounded to T), which is what layer_norm reads
-      v[i][j] = to_f(from_f<T>((oka ? p[j] : 0.f) + (okc ? q[j] : 0.f)));
-      s += col + j < cols ? v[i][j] : 0.f;
+      for (int j = 0; j < 4; ++j) {
+        // the sum as stored (rounded to T), which is what layer_norm reads
+        v[i][j] = to_f(from_f<T>((oka ? v[i][j] : 0.f) + (okc ? q[i][j] : 0.f)));
+        s += col + j < cols ? v[i][j] : 0.f;
+      }
     }
-    store4<T>(x + row * cols, col, cols, vec, v[i]);
   }
+  store_groups<T, NV, false>(x + row * cols, lane, cols, vec, v);
   if constexpr (LN) {
     const float mean = wave_sum(s) / (float)cols;
     float qs = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int64_t col = ((int64_t)i * 64 + lane) * 4;
+      const int64_t col = gcol<T, NV>(i, lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float d = col + j < cols ? v[i][j] - mean : 0.f;
@@ -473,17 +535,22 @@ __global__ void __launch_bounds__(256) embed_add_wave(const T* __restrict__ w1, 
       }
     }
     const float inv = 1.f / sqrtf(wave_sum(qs) / (float)cols + eps);
+    float gv[NV][4], bv[NV][4];
+    load_groups<T, NV, false>(g, lane, cols, vec, 0.f, gv);
+    load_groups<T, NV, false>(b, lane, cols, vec, 0.f, bv);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t col = ((int64_t)i * 64 + lane) * 4;
-      float gv[4], bv[4];
-      load4<T>(g, col, cols, vec, 0.f, gv);
-      load4<T>(b, col, cols, vec, 0.f, bv);
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[i][j] = gv[j] * (v[i][j] - mean) * inv + bv[j];
-      if (y) store4<T>(y + row * cols, col, cols, vec, v[i]);
-      if constexpr (sizeof(T) == 4)
-        if (ypk && col < cols) x3_store4(ypk, cols / 16, row, col, v[i]);
+      for (int j = 0; j < 4; ++j) v[i][j] = gv[i][j] * (v[i][j] - mean) * inv + bv[i][j];
+    if (y) store_groups<T, NV, false>(y + row * cols, lane, cols, vec, v);
+    if constexpr (sizeof(T) == 4) {
+      if (ypk) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int64_t col = gcol<T, NV>(i, lane);
+          if (col < cols) x3_store4(ypk, cols / 16, row, col, v[i]);
+        }
+      }
     }
   }
 }
@@ -832,8 +899,7 @@ __global__ void __launch_bounds__(256) quantize_rows_wave(const T* __restrict__ 
   int8_t* qr = q + row * cols;
   float v[NV][4];
   float m = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i) load4<T, FULL>(xr, ((int64_t)i * 64 + lane) * 4, cols, vec, 0.f, v[i]);
+  load_groups<T, NV, FULL>(xr, lane, cols, vec, 0.f, v);
 #pragma unroll
   for (int i = 0; i < NV; ++i)
 #pragma unroll
@@ -842,7 +908,7 @@ __global__ void __launch_bounds__(256) quantize_rows_wave(const T* __restrict__ 
   if (lane == 0) scale[row] = sc;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int64_t c = ((int64_t)i * 64 + lane) * 4;
+    const int64_t c = gcol<T, NV>(i, lane);
     int8_t b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -880,7 +946,7 @@ void sm_nv(int op, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t row
 template <typename T>
 void sm_launch(int op, const void* x, int64_t ldx, void* y, int64_t ldy, int64_t rows, int64_t cols, int64_t crow,
                hipStream_t s) {
-  bool vec = vec_ok(x, ldx, sizeof(T)) && vec_ok(y, ldy, sizeof(T));
+  bool vec = vec16_ok(x, ldx, sizeof(T)) && vec16_ok(y, ldy, sizeof(T));
   switch ((cols + 255) / 256) {
     case 1: sm_nv<T, 1>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
     case 2: sm_nv<T, 2>(op, x, ldx, y, ldy, rows, cols, crow, vec, s); break;
@@ -910,8 +976,8 @@ void ln_nv(const void* x, int64_t ldx, const void* g, const void* b, void* y, in
 template <typename T>
 void ln_launch(const void* x, int64_t ldx, const void* g, const void* b, void* y, int64_t rows, int64_t cols,
                float eps, hipStream_t s) {
-  bool vec = vec_ok(x, ldx, sizeof(T)) && vec_ok(y, cols, sizeof(T)) && vec_ok(g, 0, sizeof(T)) &&
-             vec_ok(b, 0, sizeof(T));
+  bool vec = vec16_ok(x, ldx, sizeof(T)) && vec16_ok(y, cols, sizeof(T)) && vec16_ok(g, 0, sizeof(T)) &&
+             vec16_ok(b, 0, sizeof(T));
   switch ((cols + 255) / 256) {
     case 1: ln_nv<T, 1>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
     case 2: ln_nv<T, 2>(x, ldx, g, b, y, rows, cols, eps, vec, s); break;
@@ -949,8 +1015,8 @@ void lnb_nv(const LnbArgs& a, bool vec, hipStream_t s) {
 
 template <typename T>
 void lnb_launch(const LnbArgs& a, hipStream_t s) {
-  const bool vec = vec_ok(a.x, a.cols, sizeof(T)) && vec_ok(a.dy, a.cols, sizeof(T)) &&
-                   vec_ok(a.dx, a.cols, sizeof(T)) && vec_ok(a.g, 0, sizeof(T));
+  const bool vec = vec16_ok(a.x, a.cols, sizeof(T)) && vec16_ok(a.dy, a.cols, sizeof(T)) &&
+                   vec16_ok(a.dx, a.cols, sizeof(T)) && vec16_ok(a.g, 0, sizeof(T));
   switch ((a.cols + 255) / 256) {
     case 1: lnb_nv<T, 1>(a, vec, s); break;
     case 2: lnb_nv<T, 2>(a, vec, s); break;
@@ -969,7 +1035,7 @@ void lnb_launch(const LnbArgs& a, hipStream_t s) {
 
 template <typename T>
 void q_launch(const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols, hipStream_t s) {
-  bool vec = vec_ok(x, cols, sizeof(T)) && vec_ok(q, cols, 1);
+  bool vec = vec16_ok(x, cols, sizeof(T)) && vec_ok(q, cols, 1);
   if (cols <= 2048) {
     const int64_t nw = (cols + 255) / 256;  // float4 groups per lane
     dim3 gw(rows_grid(rows));
@@ -1151,8 +1217,8 @@ void embedding_add(DType dt, const void* w1, DType i1_dt, const void* i1, int64_
   const size_t es = dtype_size(dt);
   const bool ln = gamma != nullptr;
   EaArgs a{w1, i1, w2, i2, gamma, beta, x, y, ypk, v1, v2, rows, cols, eps, false};
-  a.vec = vec_ok(w1, cols, es) && vec_ok(w2, cols, es) && vec_ok(x, cols, es) &&
-          (!ln || ((y == nullptr || vec_ok(y, cols, es)) && vec_ok(gamma, 0, es) && vec_ok(beta, 0, es)));
+  a.vec = vec16_ok(w1, cols, es) && vec16_ok(w2, cols, es) && vec16_ok(x, cols, es) &&
+          (!ln || ((y == nullptr || vec16_ok(y, cols, es)) && vec16_ok(gamma, 0, es) && vec16_ok(beta, 0, es)));
   AGPU_FLOAT_SWITCH(dt, {
     typedef T TV;
     AGPU_INT_SWITCH(i1_dt, ea_launch<TV, I>(a, s));

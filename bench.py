@@ -441,6 +441,16 @@ def rows_section(timed, line, randn):
     ms, _ = timed(lambda x: E.add(x, xs[0]), xs[1:], 20)
     line("add", [R, C], 3 * R * C * 4, ms)
     del xs
+    # fp16 rows at GPT-2 large's width (C4's layer_norm and attention softmax dtype)
+    R, C = 262144, 1280
+    xs = [randn((R, C), np.float16) for _ in range(2)]
+    g, b = randn((C,), np.float16), randn((C,), np.float16)
+    row_bytes = 2 * R * C * 2
+    ms, _ = timed(lambda x: E.softmax(x), xs, 20)
+    line("softmax_fp16", [R, C], row_bytes, ms)
+    ms, _ = timed(lambda x: E.layer_norm(x, g, b), xs, 20)
+    line("layer_norm_fp16", [R, C], row_bytes + 2 * C * 2, ms)
+    del xs
 
 
 def c5_section(timed, line, randn):

@@ -106,6 +106,33 @@ def test_rows_half_precision(gpu, dt, tol):
     assert rel_err(ln.astype(np.float32), O.layer_norm(x, g, b)) < 4 * tol
 
 
+@pytest.mark.parametrize("dt", ["float16", "bfloat16"])
+@pytest.mark.parametrize("cols", [256, 300, 768, 772, 1024, 1280, 1800, 2048])
+def test_rows_16bit_each_column_once(gpu, dt, cols):
+    """The register-resident 16-bit row kernels (a lane reads 8 consecutive
+    values per 16-byte load; an odd group count ends in a 4-value group;
+    772 columns are not 16-byte aligned rows and take the guarded path):
+    softmax, log_softmax, causal softmax, layer_norm and its backward against
+    the oracle in float64 on the input as stored, within one rounding of the
+    output dtype (rtol 2^-10 fp16, 2^-7 bf16), so a column read, reduced or
+    written in the wrong place fails."""
+    rtol = 2.0 ** -10 if dt == "float16" else 2.0 ** -7
+    rows = 9
+    cast = lambda a: gpu.cast(gpu.from_numpy(a), dt)
+    back = lambda t: t.to_numpy().astype(np.float64)
+    x, g, b, dy = cast(f32(rows, cols, scale=2.0)), cast(f32(cols)), cast(f32(cols)), cast(f32(rows, cols))
+    xs, gs, bs, dys = back(x), back(g), back(b), back(dy)
+
+    def close(got, ref, what):
+        np.testing.assert_allclose(back(got), ref, rtol=rtol, atol=1e-5 * np.abs(ref).max(), err_msg=what)
+
+    close(gpu.softmax(x), O.softmax(xs), "softmax")
+    close(gpu.log_softmax(x), O.log_softmax(xs), "log_softmax")
+    close(gpu.softmax_causal(x), O.softmax_causal(xs), "softmax_causal")
+    close(gpu.layer_norm(x, g, b), O.layer_norm(xs, gs, bs), "layer_norm")
+    close(gpu.layer_norm_backward(dy, x, g), O.layer_norm_backward(dys, xs, gs), "layer_norm_backward")
+
+
 def test_gelu_vs_golden(gpu, fixtures):
     t = gpu.from_numpy(fixtures["gelu_x"])
     np.testing.assert_allclose(gpu.gelu(t).to_numpy(), fixtures["gelu_tanh_y"], rtol=1e-5, atol=1e-6)

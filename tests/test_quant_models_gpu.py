@@ -207,11 +207,14 @@ def test_mlp_config3_step_vs_oracle(gpu):
         assert rel_err(b - b0, br - b0) < 1e-3
 
 
-@pytest.mark.parametrize("rows,cols", [(4, 4096), (3, 12288), (2, 16384), (5, 1040), (6, 8192)])
+@pytest.mark.parametrize("rows,cols", [(4, 4096), (3, 12288), (2, 16384), (5, 1040), (6, 8192), (7, 768),
+                                       (4, 1024), (3, 2048), (2, 1284)])
 @pytest.mark.parametrize("dt", ["float32", "float16", "bfloat16"])
 def test_quantize_dequantize_wide_rows_bit_exact(gpu, rows, cols, dt):
     """The 16-values-per-thread paths (rows of 4096 k values for quantize,
-    16-aligned rows of >= 1024 for dequantize), from fp32 and 16-bit input and
+    16-aligned rows of >= 1024 for dequantize) and the one-wavefront-per-row
+    quantize (rows of <= 2048, 16-bit rows read 16 bytes per lane; 1284
+    columns are not 16-byte aligned rows), from fp32 and 16-bit input and
     into each float output: codes and scales bit-exact against the oracle on
     the input as stored, dequantized values equal to the oracle's rounded to
     the output dtype."""
