@@ -49,10 +49,11 @@ using namespace dev;
 
 namespace {
 
-constexpr int kSkWaves = 16;        // waves per block, splitting K
 constexpr int kSkMaxM = 16;
-constexpr int kSkXlds = 16384;      // A elements staged in LDS (32 KB)
-constexpr int kSkRowMaxK = 2048;    // row a wave holds in registers for the LN statistics
+constexpr int kSkXlds = 16384;      // A elements staged in LDS (32 KB): M K <= 16384, K <= 2048
+constexpr int kSkXldsWide = 49152;  // the wide staging (96 KB, one block per CU): M <= 8, K <= 6144
+constexpr int kSkRowMaxK = 2048;    // row a wave normalises in registers (the layer-norm prologue)
+constexpr int kSkMaxUn = 12;        // steps in flight per wave
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -70,14 +71,19 @@ template <> struct Mfma16<bf16_t> {
   }
 };
 
-// UN: steps in flight per wave; LN: layer-norm the A rows (needs XLDS);
-// PACKED: B in the packed layout; XS > 0: A rows staged in LDS (XS elements).
-template <typename T, int UN, bool LN, bool PACKED, int XS>
-__global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
+// W: waves per block (8 when M <= 8, else 16; wave w stages row w); UN:
+// steps in flight per wave (the launch picks ceil(steps / W), so no wave
+// loads a step it does not own); LN: layer-norm the A rows (needs XLDS);
+// PACKED: B in the packed layout; XS > 0: A rows staged in LDS (XS
+// elements), R = ceil(W UN / 16) 8-runs per lane covering a row of K.
+template <typename T, int W, int UN, bool LN, bool PACKED, int XS>
+__global__ void __launch_bounds__(64 * W) gemm_skinny_mfma(GArgs p) {
   constexpr bool XLDS = XS > 0;
+  constexpr int R = XLDS ? (W * UN + 15) / 16 : 1;
   static_assert(!LN || XLDS, "the layer-norm prologue stages A in LDS");
+  static_assert(!LN || R <= kSkRowMaxK / 512, "the layer-norm row is held in registers");
   typedef typename Mfma16<T>::vec V8;
-  __shared__ float red[kSkWaves][16 * 16];
+  __shared__ float red[W][16 * 16];
   __shared__ __attribute__((aligned(16))) T xs[XLDS ? XS : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
@@ -92,7 +98,7 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
   auto load_b = [&](V8 (&b)[UN], int64_t s0) {
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int64_t st = s0 + (int64_t)u * kSkWaves;
+      const int64_t st = s0 + (int64_t)u * W;
       if constexpr (PACKED) {
         b[u] = *(const V8*)(B0 + (st < steps ? st : 0) * 512);
         if (st >= steps) {
@@ -112,66 +118,69 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
     }
   };
 
-  // The staged A row (and gamma, beta) is loaded first, then this wave's
-  // first B steps, then the epilogue operands: a wave's loads complete in
-  // issue order, so the staging below waits for its row only, while the
-  // weight stream is still in flight.
-  constexpr int R = kSkRowMaxK / 512;  // 8-runs per lane of a staged row
+  // Wave w < M stages row w: it loads the row (and gamma, beta) first, then
+  // every wave issues its first B steps, so the staging waits for its own
+  // loads only (a wave's loads complete in issue order) while the weights
+  // stream in.  The lanes' runs past K load from clamped in-range addresses
+  // rather than under a per-lane branch, which would make the wave wait for
+  // each load as it issues.  Waves past M load nothing here: every load
+  // instruction of the block takes the CU's one vector-memory path, and the
+  // weights should not queue behind copies of rows that are not needed.
+  // The epilogue operands are loaded after the staging.
+  const bool stager = XLDS && w < p.M;
   V8 run[XLDS ? R : 1], lg[LN ? R : 1], lb[LN ? R : 1];
-  if constexpr (XLDS) {
-    if (w < p.M) {
-      const T* xr = (const T*)p.A + w * p.a_sm;
+  if (stager) {
+    const T* xr = (const T*)p.A + w * p.a_sm;
 #pragma unroll
-      for (int c = 0; c < R; ++c) {
-        const int64_t kk = (int64_t)(lane + 64 * c) * 8;
-        if (kk < p.K) {
-          run[c] = *(const V8*)(xr + kk);
-          if constexpr (LN) {
-            lg[c] = *(const V8*)((const T*)p.ln_g + kk);
-            lb[c] = *(const V8*)((const T*)p.ln_b + kk);
-          }
-        }
+    for (int c = 0; c < R; ++c) {
+      const int64_t kk = (int64_t)(lane + 64 * c) * 8;
+      const int64_t kc = kk < p.K ? kk : 0;
+      run[c] = *(const V8*)(xr + kc);
+      if constexpr (LN) {
+        lg[c] = *(const V8*)((const T*)p.ln_g + kc);
+        lb[c] = *(const V8*)((const T*)p.ln_b + kc);
       }
     }
   }
+  // Compiler and scheduling barriers keep the issue order: staging loads,
+  // then the weights, then the staging arithmetic.  Without them the
+  // compiler sinks gamma/beta into the store below and schedules the weight
+  // loads behind the statistics, and the staging then waits for the weights.
+  if constexpr (XLDS) __builtin_amdgcn_sched_barrier(0);
   V8 b[UN];
-  load_b(b, w);  // in flight during the staging below
-  // threads 0..255 each finish one output (m, n0 + c): its bias/residual now
-  // (every thread loads, from a clamped legal element: no divergent branch
-  // around the loads)
-  const int om = (tid >> 4) & 15, oc = tid & 15;
-  const bool owns = tid < 256 && om < p.M && n0 + oc < p.N;
-  const EpiIn<T> ein = epilogue_load<T>(p, 0, om < p.M ? om : p.M - 1, n0 + oc < p.N ? n0 + oc : p.N - 1);
+  load_b(b, w);
+  if constexpr (XLDS) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   if constexpr (XLDS) {
-    if (w < p.M) {
+    if (stager) {
       if constexpr (LN) {
         float sum = 0.f;
 #pragma unroll
-        for (int c = 0; c < R; ++c)
-          if ((int64_t)(lane + 64 * c) * 8 < p.K) {
+        for (int c = 0; c < R; ++c) {
+          const bool in = (int64_t)(lane + 64 * c) * 8 < p.K;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) sum += (float)run[c][e];
-          }
+          for (int e = 0; e < 8; ++e) sum += in ? (float)run[c][e] : 0.f;
+        }
         const float mean = wave_sum(sum) / (float)p.K;
         float sq = 0.f;
 #pragma unroll
-        for (int c = 0; c < R; ++c)
-          if ((int64_t)(lane + 64 * c) * 8 < p.K) {
+        for (int c = 0; c < R; ++c) {
+          const bool in = (int64_t)(lane + 64 * c) * 8 < p.K;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float d = (float)run[c][e] - mean;
-              sq += d * d;
-            }
+          for (int e = 0; e < 8; ++e) {
+            const float d = (float)run[c][e] - mean;
+            sq += in ? d * d : 0.f;
           }
+        }
         const float rs = 1.f / sqrtf(wave_sum(sq) / (float)p.K + p.ln_eps);
 #pragma unroll
         for (int c = 0; c < R; ++c) {
-          if ((int64_t)(lane + 64 * c) * 8 < p.K) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-              run[c][e] = T((float)lg[c][e] * ((float)run[c][e] - mean) * rs + (float)lb[c][e]);
-          }
+          for (int e = 0; e < 8; ++e)
+            run[c][e] = T((float)lg[c][e] * ((float)run[c][e] - mean) * rs + (float)lb[c][e]);
         }
       }
 #pragma unroll
@@ -182,13 +191,19 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
     }
     __syncthreads();
   }
+  // threads 0..255 each finish one output (m, n0 + c): its bias/residual now
+  // (every thread loads, from a clamped legal element: no divergent branch
+  // around the loads), behind the weights still in flight
+  const int om = (tid >> 4) & 15, oc = tid & 15;
+  const bool owns = tid < 256 && om < p.M && n0 + oc < p.N;
+  const EpiIn<T> ein = epilogue_load<T>(p, 0, om < p.M ? om : p.M - 1, n0 + oc < p.N ? n0 + oc : p.N - 1);
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t s0 = w; s0 < steps; s0 += (int64_t)kSkWaves * UN) {
+  for (int64_t s0 = w; s0 < steps; s0 += (int64_t)W * UN) {
     V8 a[UN];
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int64_t st = s0 + (int64_t)u * kSkWaves;
+      const int64_t st = s0 + (int64_t)u * W;
       const bool ok = st < steps && st * 32 + kq < p.K;
       const int64_t kc = ok ? st * 32 + kq : 0;
       if constexpr (XLDS) a[u] = *(const V8*)&xs[row * p.K + kc];
@@ -200,7 +215,7 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
     }
 #pragma unroll
     for (int u = 0; u < UN; ++u) acc = Mfma16<T>::run(a[u], b[u], acc);
-    if (s0 + (int64_t)kSkWaves * UN < steps) load_b(b, s0 + (int64_t)kSkWaves * UN);
+    if (s0 + (int64_t)W * UN < steps) load_b(b, s0 + (int64_t)W * UN);
   }
 
   // C layout of a 16x16 MFMA tile: lane l, register r -> row 4*(l/16) + r,
@@ -211,7 +226,7 @@ __global__ void __launch_bounds__(64 * kSkWaves) gemm_skinny_mfma(GArgs p) {
   if (!owns) return;
   float v = 0.f;
 #pragma unroll
-  for (int ww = 0; ww < kSkWaves; ++ww) v += red[ww][tid];
+  for (int ww = 0; ww < W; ++ww) v += red[ww][tid];
   epilogue_finish<T>(p, 0, om, n0 + oc, v, ein);
 }
 
@@ -260,9 +275,11 @@ static bool skinny_a_ok(const Gemm& g) {
          gemm_tune().cfg < 0 && gemm_tune().splits == 0;
 }
 
-// LDS staging of A: 0 = none, else the array size the launch uses.
+// LDS staging of A: 0 = none (A operands from global memory), else the
+// staging array the launch uses.
 static int skinny_xlds(const Gemm& g) {
   if (g.M * g.K <= kSkXlds && g.K <= kSkRowMaxK) return kSkXlds;
+  if (g.M <= 8 && g.M * g.K <= kSkXldsWide && (g.K + 511) / 512 <= kSkMaxUn) return kSkXldsWide;
   return 0;
 }
 
@@ -285,16 +302,56 @@ SkinnyPlan skinny_plan(const Gemm& g, int cus) {
   return pl;
 }
 
+// Launch shapes: 8 waves when M <= 8 (one staged row each; several blocks
+// share a CU), 16 otherwise, and for the wide staging (one block per CU
+// streaming a long K); UN = ceil(steps / W), so that each wave's first
+// loads are exactly its steps (capped at kSkMaxUn for unstaged long K,
+// which loops).
+template <int U, int LO, int HI>
+constexpr int clamp_un() { return U < LO ? LO : (U > HI ? HI : U); }
+
+// UN in [LO, HI]: only those variants are instantiated.
+template <typename T, bool PK, int W, bool LN, int XS, int LO, int HI>
+static void launch_un(const GArgs& p, dim3 grid, int un, hipStream_t s) {
+  const dim3 blk(64 * W);
+#define AGPU_SK(U) \
+  hipLaunchKernelGGL((gemm_skinny_mfma<T, W, clamp_un<U, LO, HI>(), LN, PK, XS>), grid, blk, 0, s, p)
+  switch (un < LO ? LO : (un > HI ? HI : un)) {
+    case 1: AGPU_SK(1); break;
+    case 2: AGPU_SK(2); break;
+    case 3: AGPU_SK(3); break;
+    case 4: AGPU_SK(4); break;
+    case 5: AGPU_SK(5); break;
+    case 6: AGPU_SK(6); break;
+    case 7: AGPU_SK(7); break;
+    case 8: AGPU_SK(8); break;
+    case 9: AGPU_SK(9); break;
+    case 10: AGPU_SK(10); break;
+    case 11: AGPU_SK(11); break;
+    default: AGPU_SK(12); break;
+  }
+#undef AGPU_SK
+}
+
 template <typename T, bool PK>
-static void launch_skinny(const GArgs& p, dim3 grid, bool deep, bool ln, int xs, hipStream_t s) {
-  const dim3 blk(64 * kSkWaves);
-  if (ln) hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, true, PK, kSkXlds>), grid, blk, 0, s, p);
-  else if (xs) {
-    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, kSkXlds>), grid, blk, 0, s, p);
-    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, kSkXlds>), grid, blk, 0, s, p);
+static void launch_skinny(const GArgs& p, dim3 grid, bool ln, int xs, hipStream_t s) {
+  const int64_t steps = (p.K + 31) / 32;
+  auto un_for = [&](int w) { return (int)std::min<int64_t>((steps + w - 1) / w, kSkMaxUn); };
+  if (xs == kSkXlds) {
+    if (p.M <= 8) {
+      // K <= 2048: at most 8 steps per wave
+      if (ln) launch_un<T, PK, 8, true, kSkXlds, 1, 8>(p, grid, un_for(8), s);
+      else launch_un<T, PK, 8, false, kSkXlds, 1, 8>(p, grid, un_for(8), s);
+    } else {
+      // M K <= 16384 with M > 8: K < 2048, at most 4 steps per wave
+      if (ln) launch_un<T, PK, 16, true, kSkXlds, 1, 4>(p, grid, un_for(16), s);
+      else launch_un<T, PK, 16, false, kSkXlds, 1, 4>(p, grid, un_for(16), s);
+    }
+  } else if (xs == kSkXldsWide) {
+    // 2048 < K <= 6144 (M <= 8): 5 to 12 steps per wave
+    launch_un<T, PK, 16, false, kSkXldsWide, 5, kSkMaxUn>(p, grid, un_for(16), s);
   } else {
-    if (deep) hipLaunchKernelGGL((gemm_skinny_mfma<T, 12, false, PK, 0>), grid, blk, 0, s, p);
-    else hipLaunchKernelGGL((gemm_skinny_mfma<T, 4, false, PK, 0>), grid, blk, 0, s, p);
+    launch_un<T, PK, 16, false, 0, 1, kSkMaxUn>(p, grid, un_for(16), s);
   }
 }
 
@@ -303,15 +360,13 @@ void gemm_skinny(const Gemm& g, const SkinnyPlan& pl, const GArgs& p, hipStream_
   const bool ln = g.ln_gamma != nullptr;
   if (ln && !gemm_skinny_ln_ok(g)) fail("gemm: layer-norm prologue not supported for this operand");
   if (g.b_packed && !al16(g.B)) fail("gemm: packed weights must be 16-byte aligned");
-  // 4 steps in flight when each wave has at most 4 (K <= 2048), else 12
-  const bool deep = (g.K + 32 * kSkWaves - 1) / (32 * kSkWaves) > 4;
   const int xlds = skinny_xlds(g);
   if (g.dt == DType::F16) {
-    if (g.b_packed) launch_skinny<half_t, true>(p, grid, deep, ln, xlds, s);
-    else launch_skinny<half_t, false>(p, grid, deep, ln, xlds, s);
+    if (g.b_packed) launch_skinny<half_t, true>(p, grid, ln, xlds, s);
+    else launch_skinny<half_t, false>(p, grid, ln, xlds, s);
   } else {
-    if (g.b_packed) launch_skinny<bf16_t, true>(p, grid, deep, ln, xlds, s);
-    else launch_skinny<bf16_t, false>(p, grid, deep, ln, xlds, s);
+    if (g.b_packed) launch_skinny<bf16_t, true>(p, grid, ln, xlds, s);
+    else launch_skinny<bf16_t, false>(p, grid, ln, xlds, s);
   }
   check_launch("gemm_skinny");
 }

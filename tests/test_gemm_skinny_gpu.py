@@ -51,10 +51,14 @@ TOL = {"float32": 1e-3, "float16": 1e-2, "bfloat16": 2e-2}
 
 @pytest.mark.parametrize("dt", ["float16", "bfloat16"])
 @pytest.mark.parametrize("M", [1, 3, 8, 16])
-@pytest.mark.parametrize("K,N", [(1280, 3840), (5120, 1280), (1280, 50257), (8, 5), (776, 1001), (96, 17)])
+@pytest.mark.parametrize("K,N", [(1280, 3840), (5120, 1280), (1280, 50257), (8, 5), (776, 1001), (96, 17),
+                                 (2056, 33), (6144, 48), (6152, 40)])
 def test_skinny_mfma_vs_oracle(gpu, dt, M, K, N):
     """x [M, K] @ W^T with W [N, K] (torch Linear layout, tied LM head, the
-    k-major GPT-2 weights): ragged N, K not a multiple of 32, K = 8."""
+    k-major GPT-2 weights): ragged N, K not a multiple of 32, K = 8; rows
+    staged in LDS (K <= 2048, or the wide staging up to K = 6144 for M <= 8)
+    or read from global memory (K = 6152: more steps than a wave keeps in
+    flight, so the k loop turns)."""
     assert _plan(M, N, K, dt, True).startswith("skinny")
     x = _round(RNG.standard_normal((M, K)).astype(np.float32), dt)
     w = _round((RNG.standard_normal((N, K)) * 0.05).astype(np.float32), dt)
@@ -167,7 +171,8 @@ def test_skinny_graph_replay(gpu):
 
 
 @pytest.mark.parametrize("dt", ["float16", "bfloat16"])
-@pytest.mark.parametrize("M,K,N", [(8, 1280, 3840), (1, 1280, 5120), (16, 4096, 64), (5, 8, 24)])
+@pytest.mark.parametrize("M,K,N", [(8, 1280, 3840), (1, 1280, 5120), (16, 4096, 64), (5, 8, 24), (12, 1360, 100),
+                                   (8, 2048, 50)])
 def test_layer_norm_folded_into_skinny_gemm(gpu, dt, M, K, N):
     """add_bias(layer_norm(x) @ W^T) with the layer_norm output used once:
     the graph folds the normalisation into the skinny kernel's A loads."""
