@@ -574,6 +574,7 @@ int32_t applegpu_ffi_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t batch, i
     g.M = M; g.N = N; g.K = K; g.batch = batch;
     g.a_sk = a_kcontig ? 1 : M; g.a_sm = a_kcontig ? K : 1;
     g.b_sk = b_kcontig ? 1 : N; g.b_sn = b_kcontig ? K : 1;
+    g.c_sm = N;
     snprintf(out, cap, "%s", k::gemm_plan_name(g));
     return 0;
   });

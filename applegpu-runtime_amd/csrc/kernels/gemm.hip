@@ -784,8 +784,16 @@ bool gemm_x3_panel_ok(int64_t M, int64_t N, int64_t K, bool apk) {
   return pl.rows && pl.splits == 1;
 }
 
+// The outer-product plan (gemm_x3p.hip) for fp32 products it fits, unless a
+// tile configuration, a split count or the native fp32 kernels are forced.
+static bool use_outer(const Gemm& g) {
+  const GemmTune& tu = gemm_tune();
+  return tu.cfg < 0 && tu.splits == 0 && tu.f32_mode != kF32Native && gemm_x3_outer_ok(g);
+}
+
 int gemm_splits(const Gemm& g) {
   if (g.b_x3) return x3_plan_of(g).splits;
+  if (use_outer(g)) return 1;
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return 1;
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf ? pl.splits : 1;
@@ -832,6 +840,10 @@ const char* gemm_plan_name(const Gemm& g) {
     snprintf(buf, sizeof buf, "thin %s", tk == kThinN1 ? "n1" : tk == kThinM1 ? "m1" : "k1");
     return buf;
   }
+  if (use_outer(g)) {
+    snprintf(buf, sizeof buf, "x3 outer 128x128 tiles=%lld", (long long)((g.M / 128) * (g.N / 128)));
+    return buf;
+  }
   Plan pl = make_plan(g, cu_count());
   const char* kind = pl.kind == kGeneric ? "generic" : pl.kind == kNative32 ? "f32-native" : "mf";
   snprintf(buf, sizeof buf, "%s cfg%d %dx%dx%d splits=%d", kind, pl.kind == kMf ? pl.cfg : -1, pl.bm, pl.bn, pl.bk,
@@ -840,6 +852,7 @@ const char* gemm_plan_name(const Gemm& g) {
 }
 
 size_t gemm_workspace_bytes(const Gemm& g) {
+  if (use_outer(g)) return gemm_x3_outer_workspace(g);
   if (g.b_x3) {
     const X3Plan xp = x3_plan_of(g);
     return xp.splits > 1 ? (size_t)xp.splits * g.M * g.N * sizeof(float) : 0;
@@ -897,6 +910,14 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   }
   if (g.ln_gamma) fail("gemm: a layer-norm prologue needs the skinny kernel");
   if (g.b_packed) fail("gemm: packed weights need the skinny kernel (at most 16 fp16/bf16 rows)");
+  if (use_outer(g)) {
+    Plan one{};
+    one.bm = one.bn = 64;
+    one.splits = 1;
+    one.kps = g.K;
+    gemm_x3_outer(g, make_args(g, one), workspace, s);
+    return;
+  }
   Plan pl = make_plan(g, cu_count());
   GArgs p = make_args(g, pl);
   p.ws = (float*)workspace;

@@ -866,6 +866,14 @@ void gemm_thin(int kind, DType dt, const GArgs& p, hipStream_t s);
 // the plan splits K, else the epilogue into C.
 void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s);
 
+// Outer-shaped fp32 products (M, N multiples of 128 with at least 256 tiles
+// of 128 x 128, K = 128, 256 or 512; one batch, no mask): both operands
+// packed into the workspace (gemm_x3_outer_workspace bytes), then one
+// four-wavefront block per 128 x 128 tile over the whole K (gemm_x3p.hip).
+bool gemm_x3_outer_ok(const Gemm& g);
+size_t gemm_x3_outer_workspace(const Gemm& g);
+void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s);
+
 // Defined in gemm_mf_{f32,f16,bf16}_{fast,edge}.hip.
 void launch_mf_f32(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);
 void launch_mf_f16(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);

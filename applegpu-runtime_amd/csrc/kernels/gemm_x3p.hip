@@ -27,29 +27,53 @@ namespace k {
 
 namespace {
 
-__global__ void __launch_bounds__(256) pack_x3_kernel(const float* __restrict__ B, int64_t b_sk, int64_t b_sn,
-                                                      int64_t K, int64_t N, int64_t T, bf16_t* __restrict__ out) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t S = (N + 31) / 32;
-  if (gid >= S * T * 64) return;
+// One lane-fragment of the packed layout: thread gid of S T 64 (S column
+// strips, T k steps).  Every load is issued unconditionally from a clamped
+// in-range address (the padding past K and N is zeroed after the load): a
+// per-lane branch around the loads would make each of them wait as it
+// issues.
+struct PackSrc {
+  const float* B;
+  int64_t b_sk, b_sn, K, N, T;
+  bf16_t* out;
+};
+__device__ __forceinline__ void pack_x3_one(const PackSrc& a, int64_t gid) {
+  const int64_t S = (a.N + 31) / 32;
+  if (gid >= S * a.T * 64) return;
   const int l = (int)(gid & 63);
   const int64_t st = gid >> 6;
-  const int64_t t = st % T, s = st / T;
+  const int64_t t = st % a.T, s = st / a.T;
   const int64_t n = 32 * s + (l & 31);
   const int64_t k0 = 16 * t + 8 * (l >> 5);
-  bf16x8_t h, lo;
+  const bool nin = n < a.N;
+  const int64_t nc = nin ? n : a.N - 1;
+  float x[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int64_t k = k0 + j;
-    const float x = (n < N && k < K) ? B[k * b_sk + n * b_sn] : 0.f;
+    x[j] = a.B[(k < a.K ? k : a.K - 1) * a.b_sk + nc * a.b_sn];
+  }
+  bf16x8_t h, lo;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
     bf16_t hj, lj;
-    split_bf16(x, hj, lj);
+    split_bf16(nin && k0 + j < a.K ? x[j] : 0.f, hj, lj);
     h[j] = hj;
     lo[j] = lj;
   }
-  bf16_t* dst = out + (st * 2) * 512 + l * 8;
+  bf16_t* dst = a.out + (st * 2) * 512 + l * 8;
   *(bf16x8_t*)dst = h;
   *(bf16x8_t*)(dst + 512) = lo;
+}
+
+__global__ void __launch_bounds__(256) pack_x3_kernel(PackSrc a) {
+  pack_x3_one(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// Two operands in one launch: blocks [0, nb0) pack a, the rest b.
+__global__ void __launch_bounds__(256) pack_x3_pair_kernel(PackSrc a, PackSrc b, int64_t nb0) {
+  if ((int64_t)blockIdx.x < nb0) pack_x3_one(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
+  else pack_x3_one(b, ((int64_t)blockIdx.x - nb0) * 256 + threadIdx.x);
 }
 
 template <int FR, int FC, int WR, int WC, int KT, bool APK>
@@ -707,9 +731,172 @@ void pack_weights_x3(const void* b, int64_t b_sk, int64_t b_sn, int64_t K, int64
   const int64_t T = (K + 15) / 16, S = (N + 31) / 32;
   const int64_t threads = S * T * 64;
   if (threads == 0) return;
-  hipLaunchKernelGGL(pack_x3_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, (const float*)b, b_sk,
-                     b_sn, K, N, T, (bf16_t*)out);
+  hipLaunchKernelGGL(pack_x3_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                     PackSrc{(const float*)b, b_sk, b_sn, K, N, T, (bf16_t*)out});
   check_launch("pack_weights_x3");
+}
+
+namespace {
+
+// Outer-shaped fp32 GEMMs: M and N large, K at most a few hundred (the MLP
+// weight gradient g^T h, M = N = 4096, K = 256, with its SGD step W += alpha
+// g^T h as the epilogue).  Both operands are split once into packed x3
+// fragments in the workspace (pack_x3_kernel: any strides, so g^T is read in
+// place).  A block of four wavefronts owns a 128 x 128 output tile over the
+// whole K; per k step it needs 16 fragments (4 row strips and 4 column
+// strips, hi and lo; 1 KB each, contiguous), which its wavefronts copy
+// global -> LDS with global_load_lds_dwordx4 (no registers, no conversion),
+// four each, two k steps per stage, two stages in flight; each wavefront then
+// reads the 8 fragments of its 64 x 64 quarter from LDS and runs 12 MFMAs per
+// k step.  Loading each strip once per block instead of once per wavefront
+// halves the L2 -> CU traffic, which bounds this kernel (measured on MI355X,
+// M = N = 4096, K = 256 with the SGD epilogue: 54 us per-wavefront, 41 us
+// shared; 256 x 128 and 256 x 256 tiles were not faster).  The residual and
+// bias are loaded after the products and each output is written once by the
+// lane whose accumulator holds it.
+template <int T>
+__global__ void __launch_bounds__(256) gemm_x3_outer_kernel(GArgs p, const bf16_t* __restrict__ apk,
+                                                           const bf16_t* __restrict__ bpk) {
+  constexpr int S = 2;                  // k steps per stage
+  constexpr int STAGE = S * 16 * 512;   // bf16 elements per stage
+  constexpr int NST = T / S;
+  static_assert(T % S == 0, "whole stages");
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * STAGE];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t tiles_m = p.M >> 7, tiles_n = p.N >> 7;
+  int64_t tm, tn;
+  if (tiles_m % 2 == 0 && tiles_n % 4 == 0) {
+    // Workgroups go to the 8 XCDs in turn (block b to XCD b % 8): XCD x
+    // takes the tiles of row half x / 4 and column quarter x % 4, so that
+    // its L2 holds the half of A and the quarter of B it reads.
+    const int64_t x = blockIdx.x & 7, local = blockIdx.x >> 3;
+    const int64_t qn = tiles_n / 4;
+    tm = (x >> 2) * (tiles_m / 2) + local / qn;
+    tn = (x & 3) * qn + local % qn;
+  } else {
+    tm = (int64_t)blockIdx.x / tiles_n;
+    tn = (int64_t)blockIdx.x % tiles_n;
+  }
+  // Fragment f of a k step (0..15): f < 8 row strip f / 2 of the tile, else
+  // column strip (f - 8) / 2; part f % 2 (hi, lo).  Packed strip s, step t,
+  // part h: ((s T + t) 2 + h) 512 + 8 l.  Wavefront w copies 4w .. 4w + 3.
+  const bf16_t* src[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int f = 4 * w + q, g = f & 7;
+    const bf16_t* base = f < 8 ? apk + (4 * tm + (g >> 1)) * T * 1024 : bpk + (4 * tn + (g >> 1)) * T * 1024;
+    src[q] = base + (g & 1) * 512 + lane * 8;
+  }
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    bf16_t* dst = lds + (st & 1) * STAGE;
+#pragma unroll
+    for (int d = 0; d < S; ++d)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        __builtin_amdgcn_global_load_lds(src[q] + (int64_t)(st * S + d) * 1024,
+                                         (lds_ptr)(dst + (d * 16 + 4 * w + q) * 512), 16, 0, 0);
+  };
+  const int wm = w >> 1, wn = w & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  issue(0);
+#pragma unroll
+  for (int st = 0; st < NST; ++st) {
+    // this wavefront's copies of stage st have landed; after the barrier
+    // every wavefront's have, and every wavefront is done with stage st - 1,
+    // whose buffer stage st + 1 then overwrites
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (st + 1 < NST) issue(st + 1);
+    const bf16_t* b = lds + (st & 1) * STAGE;
+#pragma unroll
+    for (int d = 0; d < S; ++d) {
+      bf16x8_t ah[2], al[2], bh[2], bl[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        ah[i] = *(const bf16x8_t*)(b + (d * 16 + (2 * wm + i) * 2) * 512 + lane * 8);
+        al[i] = *(const bf16x8_t*)(b + (d * 16 + (2 * wm + i) * 2 + 1) * 512 + lane * 8);
+        bh[i] = *(const bf16x8_t*)(b + (d * 16 + 8 + (2 * wn + i) * 2) * 512 + lane * 8);
+        bl[i] = *(const bf16x8_t*)(b + (d * 16 + 8 + (2 * wn + i) * 2 + 1) * 512 + lane * 8);
+      }
+      // small terms first, then hi * hi (the row panels' order)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+        }
+    }
+  }
+  // register e of subtile (i, j): row 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4,
+  // column 32 j + lane % 32 of the wavefront's 64 x 64 quarter
+  const int64_t rbase = tm * 128 + wm * 64 + 4 * (lane >> 5), cbase = tn * 128 + wn * 64 + (lane & 31);
+  float res[2][2][16];
+  if (p.res) {
+    const float* R = (const float*)p.res;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          res[i][j][e] = R[(rbase + 32 * i + 8 * (e >> 2) + (e & 3)) * p.r_sm + cbase + 32 * j];
+  }
+  float bias[2] = {0.f, 0.f};
+  if (p.bias) {
+    bias[0] = ((const float*)p.bias)[cbase];
+    bias[1] = ((const float*)p.bias)[cbase + 32];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        EpiIn<float> in;
+        in.bias = bias[j];
+        in.res = p.res ? res[i][j][e] : 0.f;
+        epilogue_finish<float>(p, 0, rbase + 32 * i + 8 * (e >> 2) + (e & 3), cbase + 32 * j, acc[i][j][e], in);
+      }
+}
+
+}  // namespace
+
+bool gemm_x3_outer_ok(const Gemm& g) {
+  return g.dt == DType::F32 && g.b_dt == DType::F32 && g.batch == 1 && !g.b_scale && !g.b_x3 && !g.a_x3 &&
+         !g.b_packed && !g.ln_gamma && !g.mask && !g.pln_y && !g.pln_ypk && !g.c_pk && !g.no_reduce &&
+         g.c_sm == g.N && g.M % 128 == 0 && g.N % 128 == 0 && (g.K == 128 || g.K == 256 || g.K == 512) &&
+         (g.M / 128) * (g.N / 128) >= 256;
+}
+
+size_t gemm_x3_outer_workspace(const Gemm& g) { return (size_t)(g.M + g.N) * g.K * 4; }
+
+void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s) {
+  if (!gemm_x3_outer_ok(g) || !ws) fail("gemm: the outer-product plan does not fit this product");
+  bf16_t* apk = (bf16_t*)ws;
+  bf16_t* bpk = apk + g.M * g.K * 2;
+  // A(m, k) = B'(k, n = m): A's rows packed as the weights' columns; both
+  // operands in one launch
+  const int64_t T = g.K / 16;
+  const PackSrc pa{(const float*)g.A, g.a_sk, g.a_sm, g.K, g.M, T, apk};
+  const PackSrc pb{(const float*)g.B, g.b_sk, g.b_sn, g.K, g.N, T, bpk};
+  const int64_t nba = ((g.M / 32) * T * 64 + 255) / 256, nbb = ((g.N / 32) * T * 64 + 255) / 256;
+  hipLaunchKernelGGL(pack_x3_pair_kernel, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, pa, pb, nba);
+  check_launch("pack_x3_pair");
+  const int64_t tiles = (g.M / 128) * (g.N / 128);
+  const dim3 grid((unsigned)tiles);
+  if (g.K == 128) hipLaunchKernelGGL(gemm_x3_outer_kernel<8>, grid, dim3(256), 0, s, p, apk, bpk);
+  else if (g.K == 256) hipLaunchKernelGGL(gemm_x3_outer_kernel<16>, grid, dim3(256), 0, s, p, apk, bpk);
+  else hipLaunchKernelGGL(gemm_x3_outer_kernel<32>, grid, dim3(256), 0, s, p, apk, bpk);
+  check_launch("gemm_x3_outer");
 }
 
 void row_tile_stats(const float* x, int64_t x_sm, int64_t M, int64_t N, float* out, hipStream_t s) {

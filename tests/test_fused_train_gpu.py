@@ -104,6 +104,46 @@ def test_sgd_matmul_matches_unfused(gpu, rows, cols, inner):
     np.testing.assert_allclose(fused, unfused, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("K", [128, 256, 512])
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (False, False)])
+@pytest.mark.parametrize("M,N", [(2048, 2048), (2304, 1920)])
+def test_outer_plan_products(gpu, K, ta, tb, M, N):
+    """fp32 products with many 128 x 128 output tiles and K of 128, 256 or
+    512 (the MLP weight gradient's shape) take the outer-product plan: both
+    operands packed as bf16 hi/lo fragments, one four-wavefront block per
+    tile over the whole K (tiles dealt to the XCDs by row half and column
+    quarter, or in plain order when the tile grid does not divide so); the
+    stored operand layouts (g^T read in place, W^T) and the fused epilogues
+    (alpha and the residual of sgd_matmul_, bias with ReLU) against the
+    float64 oracle at the fp32 GEMM bar."""
+    from applegpu_runtime import eager as E
+    assert _plan(M, N, K, a_kcontig=not ta, b_kcontig=tb).startswith("x3 outer")
+    a = f32(K, M) if ta else f32(M, K)
+    b = f32(N, K) if tb else f32(K, N)
+    a64 = (a.T if ta else a).astype(np.float64)
+    b64 = (b.T if tb else b).astype(np.float64)
+    ref = a64 @ b64
+    got = E.matmul_ex(E.from_numpy(a), E.from_numpy(b), ta, tb).numpy()
+    assert rel_err(got, ref) < 1e-5
+    # W += alpha op(a) op(b) in place
+    w0 = f32(M, N)
+    wd = E.from_numpy(w0)
+    E.sgd_matmul_(wd, E.from_numpy(a), E.from_numpy(b), ta, tb, -0.01)
+    assert rel_err(wd.numpy() - w0, -0.01 * ref) < 1e-5
+    # bias + ReLU through the lazy graph's fused epilogue
+    if not ta and not tb:
+        bias = f32(N)
+        out = gpu.relu(gpu.add_bias(gpu.from_numpy(a) @ gpu.from_numpy(b), gpu.from_numpy(bias))).to_numpy()
+        want = np.maximum(ref + bias, 0)
+        assert rel_err(out, want) < 1e-5
+
+
+def test_outer_plan_declines_other_shapes():
+    assert not _plan(2048, 2048, 192, a_kcontig=False).startswith("x3 outer")   # K not 128/256/512
+    assert not _plan(2048, 1984, 256, a_kcontig=False).startswith("x3 outer")   # N % 128 != 0
+    assert not _plan(512, 512, 256, a_kcontig=False).startswith("x3 outer")     # too few tiles
+
+
 def test_sgd_matmul_rejects_bad_parameter(gpu):
     from applegpu_runtime import eager as E
     w = E.from_numpy(f32(8, 8))
