@@ -791,9 +791,16 @@ static bool use_outer(const Gemm& g) {
   return tu.cfg < 0 && tu.splits == 0 && tu.f32_mode != kF32Native && gemm_x3_outer_ok(g);
 }
 
+// The 16-bit large-tile plan (gemm_h16.hip), unless a configuration or a
+// split count is forced.
+static bool use_h16(const Gemm& g) {
+  const GemmTune& tu = gemm_tune();
+  return tu.cfg < 0 && tu.splits == 0 && gemm_h16_ok(g, cu_count());
+}
+
 int gemm_splits(const Gemm& g) {
   if (g.b_x3) return x3_plan_of(g).splits;
-  if (use_outer(g)) return 1;
+  if (use_outer(g) || use_h16(g)) return 1;
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return 1;
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf ? pl.splits : 1;
@@ -813,6 +820,12 @@ bool gemm_post_ln_fused(const Gemm& g) {
   if (!g.pln_y && !g.pln_ypk) return false;
   if (!g.C || g.c_pk) return false;
   if (g.b_x3) return x3_plan_of(g).splits > 1;
+  {
+    Gemm q = g;  // the product itself takes the large-tile plan: no reduction
+    q.pln_gamma = q.pln_beta = nullptr;
+    q.pln_y = q.pln_ypk = nullptr;
+    if (use_h16(q)) return false;
+  }
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf && pl.splits > 1;
 }
@@ -844,6 +857,10 @@ const char* gemm_plan_name(const Gemm& g) {
     snprintf(buf, sizeof buf, "x3 outer 128x128 tiles=%lld", (long long)((g.M / 128) * (g.N / 128)));
     return buf;
   }
+  if (use_h16(g)) {
+    snprintf(buf, sizeof buf, "h16 256x256 w16");
+    return buf;
+  }
   Plan pl = make_plan(g, cu_count());
   const char* kind = pl.kind == kGeneric ? "generic" : pl.kind == kNative32 ? "f32-native" : "mf";
   snprintf(buf, sizeof buf, "%s cfg%d %dx%dx%d splits=%d", kind, pl.kind == kMf ? pl.cfg : -1, pl.bm, pl.bn, pl.bk,
@@ -853,6 +870,7 @@ const char* gemm_plan_name(const Gemm& g) {
 
 size_t gemm_workspace_bytes(const Gemm& g) {
   if (use_outer(g)) return gemm_x3_outer_workspace(g);
+  if (use_h16(g)) return 0;
   if (g.b_x3) {
     const X3Plan xp = x3_plan_of(g);
     return xp.splits > 1 ? (size_t)xp.splits * g.M * g.N * sizeof(float) : 0;
@@ -916,6 +934,14 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     one.splits = 1;
     one.kps = g.K;
     gemm_x3_outer(g, make_args(g, one), workspace, s);
+    return;
+  }
+  if (use_h16(g)) {
+    Plan one{};
+    one.bm = one.bn = 128;
+    one.splits = 1;
+    one.kps = g.K;
+    gemm_h16(g, make_args(g, one), cu_count(), s);
     return;
   }
   Plan pl = make_plan(g, cu_count());

@@ -871,6 +871,12 @@ void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s);
 // packed into the workspace (gemm_x3_outer_workspace bytes), then one
 // four-wavefront block per 128 x 128 tile over the whole K (gemm_x3p.hip).
 bool gemm_x3_outer_ok(const Gemm& g);
+// Large fp16 / bf16 products with both operands contiguous along k (A rows,
+// W [N][K]), M >= 256, K % 64 == 0, one batch, no mask: swizzled direct
+// global -> LDS tiles of 256 x 256 for grids that fill one round of the
+// CUs (gemm_h16.hip).
+bool gemm_h16_ok(const Gemm& g, int cus);
+void gemm_h16(const Gemm& g, const GArgs& p, int cus, hipStream_t s);
 size_t gemm_x3_outer_workspace(const Gemm& g);
 void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s);
 
