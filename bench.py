@@ -144,6 +144,31 @@ def proj_gemm_roofline(gpu, lib, rng, reps=4, nw=40):
     return out
 
 
+def c2_replays(n):
+    """The headline's C2 forward graph alone, replayed n times; prints the
+    mean replay time.  Under rocprofv3 --kernel-trace every dispatch of the
+    run is then one of the forward's kernels."""
+    import applegpu_runtime as gpu
+    from applegpu_runtime._native import lib
+    from applegpu_runtime.models import gpt2 as G
+    gpu.init_backend()
+    wnp = G.random_weights(GPT2_CFG, seed=42)
+    model = G.load_model(wnp, GPT2_CFG)
+    ids = np.random.default_rng(42).integers(0, GPT2_CFG["vocab_size"], SEQ).astype(np.int32)
+    idx = gpu.from_numpy(ids)
+    pos = gpu.from_numpy(np.arange(SEQ, dtype=np.int32))
+    g = gpu.capture(lambda: G.gpt2_forward(model, idx, positions=pos, need_cache=False)[0])
+    g.replay()
+    lib.applegpu_ffi_synchronize()
+    lib.applegpu_ffi_event_record(0)
+    for _ in range(n):
+        g.replay()
+    lib.applegpu_ffi_event_record(1)
+    lib.applegpu_ffi_synchronize()
+    print(json.dumps({"c2_replays": n, "ms_per_replay": round(lib.applegpu_ffi_event_elapsed_ms(0, 1) / n, 4)}))
+    g.destroy()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,7 +195,13 @@ def main():
     ap.add_argument("--c4-reps", type=int, default=3)
     ap.add_argument("--c4-eager", action="store_true",
                     help="C4 with op-by-op launches instead of graph replays (same kernels; for kernel traces)")
+    ap.add_argument("--c2-replays", type=int, default=0,
+                    help="instead of the headline line, capture the C2 forward and replay it this many times "
+                         "(nothing else runs: a per-forward kernel trace of exactly the timed graph)")
     args = ap.parse_args()
+    if args.c2_replays > 0:
+        c2_replays(args.c2_replays)
+        return
     if args.suite:
         kernel_suite(args.only)
         return
