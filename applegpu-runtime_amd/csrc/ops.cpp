@@ -1037,8 +1037,9 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
   size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
   if (no_alloc) {
     if (wsb > no_alloc->cap)
-      fail("matmul: this %lld x %lld x %lld product needs %zu bytes of split-K workspace, more than the %zu "
-           "bytes the allocation-free form holds", (long long)M, (long long)N, (long long)K, wsb, no_alloc->cap);
+      fail("matmul: this %lld x %lld x %lld product needs %zu bytes of workspace (split-K partial sums or "
+           "packed operands), more than the %zu bytes the allocation-free form holds",
+           (long long)M, (long long)N, (long long)K, wsb, no_alloc->cap);
     LAUNCH k::gemm(g, wsb ? no_alloc->ws : nullptr, rt().stream());
     return out;
   }
