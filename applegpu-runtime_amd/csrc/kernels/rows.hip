@@ -826,8 +826,10 @@ __device__ __forceinline__ void load16(const T* __restrict__ p, float (&v)[16]) 
 }
 // Per-row int8 quantize, one 256-thread block per row of 4096 NG values
 // (cols % 4096 == 0, 16-byte aligned rows); the arithmetic of
-// quantize_rows_kernel.
-template <typename T, int NG>
+// quantize_rows_kernel.  NT: the codes are written with nontemporal stores
+// (for outputs too large to stay cached for a consumer: C5's 64 MiB of codes
+// 59.9 -> 57.5 us, measured over three rotating 256 MiB inputs).
+template <typename T, int NG, bool NT>
 __global__ void __launch_bounds__(256) quantize_rows_v16(const T* __restrict__ x, int8_t* __restrict__ q,
                                                          float* __restrict__ scale, int64_t cols) {
   __shared__ float sh[4];
@@ -854,35 +856,59 @@ __global__ void __launch_bounds__(256) quantize_rows_v16(const T* __restrict__ x
       r = fminf(fmaxf(r, -128.f), 127.f);
       b[j] = (int8_t)(int)r;
     }
-    *(u32x4_v*)(qr + ((int64_t)g * 256 + threadIdx.x) * 16) = out;
+    u32x4_v* dst = (u32x4_v*)(qr + ((int64_t)g * 256 + threadIdx.x) * 16);
+    if constexpr (NT) __builtin_nontemporal_store(out, dst);
+    else *dst = out;
   }
 }
 
-// y = codes * scale[row] for a block of 4096 columns of one row: thread t
-// takes columns 4 (t + 256 i) .. + 3 for i = 0..3, so each of its four
-// 4-byte code loads and 16-byte (fp32) stores is one coalesced wavefront
-// access, and the four pairs are in flight together.  cols % 4096 == 0,
-// 16-byte aligned rows.  C5: 61 us, 0.69 of HBM peak (68 us with one group
-// per thread).
-template <typename T>
-__global__ void __launch_bounds__(256) dequantize_rows_4x4(const int8_t* __restrict__ q,
+// y = codes * scale[row] for a block of 4096 columns of one row.  The codes
+// come in with one 16-byte load per thread and are staged through LDS; then
+// thread t writes columns 4 (t + 256 i) .. + 3 for i = 0..3, so each of its
+// four stores (16 bytes of fp32) is one coalesced wavefront access.
+// cols % 4096 == 0, 16-byte aligned rows.  NT: nontemporal stores, for
+// outputs too large to stay cached for a consumer.  C5 ([8192, 8192] fp32,
+// codes rotating over 6 copies so that they come from HBM): 57.8 us with NT
+// stores against 60.1 us for 4-byte code loads and plain stores (and 68 us
+// with one group per thread).
+template <typename T, bool NT>
+__global__ void __launch_bounds__(256) dequantize_rows_lds(const int8_t* __restrict__ q,
                                                            const float* __restrict__ scale, T* __restrict__ y,
                                                            int64_t cols) {
+  __shared__ __attribute__((aligned(16))) int8_t codes[4096];
   const int64_t row = blockIdx.y;
-  const int64_t c0 = (int64_t)blockIdx.x * 4096 + threadIdx.x * 4;
+  const int64_t base = (int64_t)blockIdx.x * 4096;
   const float sc = scale[row];
-  int32_t w[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) w[i] = *(const int32_t*)(q + row * cols + c0 + 1024 * i);
+  *(u32x4_v*)&codes[threadIdx.x * 16] = *(const u32x4_v*)(q + row * cols + base + threadIdx.x * 16);
+  __syncthreads();
+  T* yr = y + row * cols + base;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int8_t* b = (const int8_t*)&w[i];
+    const int c = threadIdx.x * 4 + 1024 * i;
+    const int32_t w = *(const int32_t*)&codes[c];
+    const int8_t* b = (const int8_t*)&w;
     float v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) v[j] = (float)b[j] * sc;
-    store4<T, true>(y + row * cols, c0 + 1024 * i, cols, true, v);
+    if constexpr (NT && sizeof(T) == 4) {
+      f32x4_v o = {v[0], v[1], v[2], v[3]};
+      __builtin_nontemporal_store(o, (f32x4_v*)(yr + c));
+    } else if constexpr (NT) {
+      T h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[j] = from_f<T>(v[j]);
+      typedef unsigned int u32x2_v __attribute__((ext_vector_type(2)));
+      __builtin_nontemporal_store(*(const u32x2_v*)h, (u32x2_v*)(yr + c));
+    } else {
+      store4<T, true>(yr, c, 4096, true, v);
+    }
   }
 }
+
+// Outputs at least this large are written with nontemporal stores by the
+// quantize / dequantize kernels: they cannot all stay in the 256 MB Infinity
+// Cache for a consumer, and bypassing it measured 4-5 % faster.
+constexpr int64_t kNtStoreBytes = (int64_t)64 << 20;
 
 // Per-row int8 quantize with one wavefront per row for rows of up to 2048
 // columns: the row stays in registers, the absmax is a wave reduction (no
@@ -1053,12 +1079,17 @@ void q_launch(const void* x, int8_t* q, float* scale, int64_t rows, int64_t cols
   dim3 g((unsigned)rows);
   if (vec && cols % 4096 == 0 && cols <= 4096 * 4 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 15) == 0 &&
       (cols * (int64_t)sizeof(T)) % 16 == 0) {
+    const bool nt = rows * cols >= kNtStoreBytes;
+#define AGPU_QV(NG)                                                                                        \
+  if (nt) hipLaunchKernelGGL((quantize_rows_v16<T, NG, true>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); \
+  else hipLaunchKernelGGL((quantize_rows_v16<T, NG, false>), g, dim3(256), 0, s, (const T*)x, q, scale, cols);
     switch (cols / 4096) {
-      case 1: hipLaunchKernelGGL((quantize_rows_v16<T, 1>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
-      case 2: hipLaunchKernelGGL((quantize_rows_v16<T, 2>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
-      case 3: hipLaunchKernelGGL((quantize_rows_v16<T, 3>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
-      default: hipLaunchKernelGGL((quantize_rows_v16<T, 4>), g, dim3(256), 0, s, (const T*)x, q, scale, cols); return;
+      case 1: AGPU_QV(1) return;
+      case 2: AGPU_QV(2) return;
+      case 3: AGPU_QV(3) return;
+      default: AGPU_QV(4) return;
     }
+#undef AGPU_QV
   }
 #define AGPU_Q(NV)                                                                                   \
   if (vec && cols == NV * 1024)                                                                      \
@@ -1238,8 +1269,11 @@ void dequantize_rows(DType out, const int8_t* q, const float* scale, void* y, in
   if (rows == 0 || cols == 0) return;
   AGPU_FLOAT_SWITCH(out, {
     if (cols % 4096 == 0 && rows <= 65535 && ((uintptr_t)q % 16) == 0 && ((uintptr_t)y % 16) == 0) {
-      hipLaunchKernelGGL((dequantize_rows_4x4<T>), dim3((unsigned)(cols / 4096), (unsigned)rows), dim3(256), 0, s, q,
-                         scale, (T*)y, cols);
+      const dim3 g((unsigned)(cols / 4096), (unsigned)rows);
+      if (rows * cols * (int64_t)sizeof(T) >= kNtStoreBytes)
+        hipLaunchKernelGGL((dequantize_rows_lds<T, true>), g, dim3(256), 0, s, q, scale, (T*)y, cols);
+      else
+        hipLaunchKernelGGL((dequantize_rows_lds<T, false>), g, dim3(256), 0, s, q, scale, (T*)y, cols);
       check_launch("dequantize_rows");
       return;
     }

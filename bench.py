@@ -495,14 +495,18 @@ def rows_section(timed, line, randn):
 
 def c5_section(timed, line, randn):
     from applegpu_runtime import eager as E
-    # C5: per-row int8 quantize / dequantize of W [8192, 8192] fp32, three rotating inputs
+    # C5: per-row int8 quantize / dequantize of W [8192, 8192] fp32, three
+    # rotating inputs
     N = 8192
     ws = [randn((N, N), scale=0.02) for _ in range(3)]
     qbytes = 4 * N * N + N * N + 4 * N
     ms, qs = timed(lambda w: E.op("quantize_per_row", [w], nout=2), ws, 12)
     line("quantize_per_row", [N, N], qbytes, ms)
     q, sc = qs
-    ms, _ = timed(lambda qq: E.op("dequantize_per_row", [qq, sc]), [q], 12)
+    # six code copies (6 x 64 MiB), so that dequantize reads them from HBM
+    dq_in = [E.op("quantize_per_row", [ws[i % 3]], nout=2) for i in range(6)]
+    ms, _ = timed(lambda qs_: E.op("dequantize_per_row", list(qs_)), dq_in, 12)
+    del dq_in
     line("dequantize_per_row", [N, N], qbytes, ms)
     deq = E.op("dequantize_per_row", [q, sc])
     del ws
@@ -984,7 +988,11 @@ def c5_pipeline(args):
     q, sc = E.op("quantize_per_row", [ws[0]], nout=2)
     qs = [q] + [E.op("quantize_per_row", [w], nout=2)[0] for w in ws[1:]]
     scs = [sc] + [E.op("quantize_per_row", [w], nout=2)[1] for w in ws[1:]]
-    d_ms, _ = timed(lambda i: E.op("dequantize_per_row", [qs[i], scs[i]]), [0, 1, 2])
+    # dequantize rotates over six code copies (6 x 64 MiB, more than the
+    # 256 MB Infinity Cache), so that its reads come from HBM too
+    dq_in = [(qs[i], scs[i]) for i in range(3)] + [E.op("quantize_per_row", [w], nout=2) for w in ws]
+    d_ms, _ = timed(lambda i: E.op("dequantize_per_row", list(dq_in[i])), list(range(6)))
+    del dq_in
     deq = E.op("dequantize_per_row", [q, sc])
     gemm_ms, y = timed(lambda w: E.matmul_ex(X, w, False, True), [deq])
     fused_ms, yf = timed(lambda i: E.op("linear_int8", [X, qs[i], scs[i]]), [0])
@@ -1023,7 +1031,7 @@ def c5_pipeline(args):
         "data": "synthetic",
         "config": {
             "workload": "C5 W [8192,8192] fp32 N(0,0.02), X [64,8192] N(0,1); per-row absmax/127 int8 "
-                        "quantize (RNE), dequantize, X @ deq^T; three rotating W copies",
+                        "quantize (RNE), dequantize, X @ deq^T; three rotating W copies (six code copies for dequantize)",
             "quantize_us": round(q_ms * 1e3, 2),
             "quantize_hbm_frac": round(q_gbs / HBM_PEAK_GBS, 4),
             "dequantize_us": round(d_ms * 1e3, 2),

@@ -66,6 +66,8 @@ def test_int8_linear_config5_shape(gpu):
     tx = gpu.from_numpy(x)
     y = (tx @ gpu.transpose(deq)).to_numpy()
     deq_np = O.dequantize_per_row(qr, sr)
+    # codes and values at this size take the nontemporal-store kernels
+    np.testing.assert_array_equal(deq.to_numpy(), deq_np)
     ref = O.matmul(x, deq_np.T)
     assert rel_err(y, ref) < 1e-3
     y8 = gpu.linear_int8(tx, q, s).to_numpy()
@@ -208,14 +210,15 @@ def test_mlp_config3_step_vs_oracle(gpu):
 
 
 @pytest.mark.parametrize("rows,cols", [(4, 4096), (3, 12288), (2, 16384), (5, 1040), (6, 8192), (7, 768),
-                                       (4, 1024), (3, 2048), (2, 1284)])
+                                       (4, 1024), (3, 2048), (2, 1284), (4096, 8192)])
 @pytest.mark.parametrize("dt", ["float32", "float16", "bfloat16"])
 def test_quantize_dequantize_wide_rows_bit_exact(gpu, rows, cols, dt):
     """The 16-values-per-thread paths (rows of 4096 k values for quantize,
     16-aligned rows of >= 1024 for dequantize) and the one-wavefront-per-row
     quantize (rows of <= 2048, 16-bit rows read 16 bytes per lane; 1284
     columns are not 16-byte aligned rows), from fp32 and 16-bit input and
-    into each float output: codes and scales bit-exact against the oracle on
+    into each float output ([4096, 8192]: outputs of 64 MiB and more, written
+    with nontemporal stores): codes and scales bit-exact against the oracle on
     the input as stored, dequantized values equal to the oracle's rounded to
     the output dtype."""
     w32 = (RNG.standard_normal((rows, cols)) * 0.02).astype(np.float32)
