@@ -501,6 +501,11 @@ TensorP layer_norm(const TensorP& x, const TensorP& g, const TensorP& b, float e
   return out;
 }
 
+// Rows at least this long, when there are at most kLongRowsMax of them,
+// reduce (sum, mean) over many blocks.
+constexpr int64_t kLongRowCols = (int64_t)1 << 20;
+constexpr int64_t kLongRowsMax = 16;
+
 TensorP row_reduce(int op, const TensorP& x, int correction) {
   const char* name = op == k::kRSum ? "sum" : op == k::kRMean ? "mean" : op == k::kRAmax ? "amax"
                      : op == k::kRArgmax ? "argmax" : "var";
@@ -518,8 +523,21 @@ TensorP row_reduce(int op, const TensorP& x, int correction) {
   }
   DType odt = op == k::kRArgmax ? DType::I32 : x->dtype;
   TensorP out = alloc_out(odt, od);
-  LAUNCH k::row_reduce(op, x->dtype, odt, src->data(), ld, out->data(), rows, x->shape[x->ndim - 1], correction,
-                rt().stream());
+  const int64_t cols = x->shape[x->ndim - 1];
+  if ((op == k::kRSum || op == k::kRMean) && dtype_is_float(x->dtype) && x->dtype != DType::F64 &&
+      rows <= kLongRowsMax && cols >= kLongRowCols) {
+    // A few very long rows: one wavefront per row would read each at a few
+    // GB/s; each row takes the two-stage all-element reduction instead (512
+    // blocks of fp32 partials, then one block).
+    BufferP ws = scratch(k::reduce_all_ws_bytes());
+    const size_t es = dtype_size(x->dtype);
+    for (int64_t r = 0; r < rows; ++r)
+      LAUNCH k::reduce_all(0, x->dtype, (const char*)src->data() + r * ld * (int64_t)es, nullptr, cols,
+                           op == k::kRMean ? 1.f / (float)cols : 1.f, (char*)out->data() + r * (int64_t)es, ws->ptr,
+                           rt().stream());
+    return out;
+  }
+  LAUNCH k::row_reduce(op, x->dtype, odt, src->data(), ld, out->data(), rows, cols, correction, rt().stream());
   return out;
 }
 

@@ -281,6 +281,26 @@ def test_reductions(gpu):
     np.testing.assert_array_equal(gpu.sum(gpu.from_numpy(ints)).to_numpy(), ints.sum(-1))
 
 
+@pytest.mark.parametrize("shape", [(1 << 21,), (3, (1 << 20) + 5)])
+@pytest.mark.parametrize("dt", ["float32", "float16"])
+def test_sum_mean_of_few_long_rows(gpu, shape, dt):
+    """At most 16 rows of >= 2^20 values reduce over many blocks (two-stage
+    fp32 partials): sum and mean of each row against a float64 sum of the
+    values as stored; a plain positive offset keeps the sums well away from
+    zero so that a relative bar applies (fp16: small values, so that the
+    sums of 2^21 of them stay inside the fp16 range)."""
+    x = (RNG.standard_normal(shape) + 2.0).astype(np.float32)
+    if dt == "float16":
+        x *= np.float32(0.005)
+    t = gpu.from_numpy(x)
+    if dt != "float32":
+        t = gpu.cast(t, dt)
+    xs = t.to_numpy().astype(np.float64)
+    tol = 1e-5 if dt == "float32" else 2e-3
+    np.testing.assert_allclose(gpu.sum(t).to_numpy().astype(np.float64), xs.sum(-1), rtol=tol)
+    np.testing.assert_allclose(gpu.mean(t).to_numpy().astype(np.float64), xs.mean(-1), rtol=tol)
+
+
 def test_mse_vs_golden(gpu, fixtures):
     a, b = gpu.from_numpy(fixtures["mse_a"]), gpu.from_numpy(fixtures["mse_b"])
     np.testing.assert_allclose(gpu.mse_loss(a, b).to_numpy(), fixtures["mse_loss"], rtol=1e-5)
