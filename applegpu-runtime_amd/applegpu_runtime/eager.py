@@ -157,10 +157,14 @@ def op(name: str, tensors, f=(), i=(), nout=1):
     return res[0] if nout == 1 else tuple(res)
 
 
-def sgd_matmul_(w, a, b, ta=False, tb=False, alpha=1.0):
+def sgd_matmul_(w, a, b, ta=False, tb=False, alpha=1.0, bias=None):
     """w += alpha * op(a) @ op(b) in place: an SGD weight step fused with its
-    gradient GEMM (the update runs in the GEMM's epilogue)."""
-    op("sgd_matmul_", [w, a, b], f=(float(alpha),), i=(int(ta), int(tb)))
+    gradient GEMM (the update runs in the GEMM's epilogue).  With `bias`
+    (fp32, [rows of op(a)]) also bias += alpha * op(a).sum(1): for a Linear
+    layer's step, op(a) = g^T and this is the bias step bias += alpha *
+    g.sum(0); the outer-product plan computes it while packing g."""
+    ins = [w, a, b] if bias is None else [w, a, b, bias]
+    op("sgd_matmul_", ins, f=(float(alpha),), i=(int(ta), int(tb)))
 
 
 def sgd_sum_rows_(bias, g, alpha=1.0):

@@ -67,8 +67,8 @@ class EagerMLP:
             # dL/d(input of layer i) masked by relu' of the previous layer's
             # output, from W_i before its update
             g_in = E.matmul_masked(g, w, False, False, acts[i]) if i > 0 else None
-            E.sgd_matmul_(w, g, acts[i], True, False, -lr)   # W_i -= lr * g^T a_i
-            E.sgd_sum_rows_(b, g, -lr)                        # b_i -= lr * sum(g, 0)
+            # W_i -= lr * g^T a_i and b_i -= lr * sum(g, 0)
+            E.sgd_matmul_(w, g, acts[i], True, False, -lr, bias=b)
             g = g_in
         return loss
 

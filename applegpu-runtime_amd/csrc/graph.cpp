@@ -230,8 +230,10 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       return {matmul_pp_norm(in[0], in[1], ip(iv, 0, code), in[2], in[3], ip(iv, 1, code),
                              f.empty() ? 1e-5f : (float)f[0])};
     case OP_SGD_MATMUL:
-      need(in, 3, code);
-      return {sgd_matmul_(in[0], in[1], in[2], iv.size() > 0 && iv[0], iv.size() > 1 && iv[1], (float)fp(f, 0, code))};
+      // (w, a, b) or (w, a, b, bias): the bias step rides with the weight step
+      if (in.size() != 4) need(in, 3, code);
+      return {sgd_matmul_(in[0], in[1], in[2], iv.size() > 0 && iv[0], iv.size() > 1 && iv[1], (float)fp(f, 0, code),
+                          in.size() == 4 ? in[3] : nullptr)};
     case OP_SGD_SUM_ROWS: need(in, 2, code); return {sgd_sum_rows_(in[0], in[1], (float)fp(f, 0, code))};
     case OP_QKV_ATTENTION:
       need(in, 3, code);

@@ -191,6 +191,10 @@ struct Gemm {
   // split-K launches leave the partial sums in the workspace (the caller
   // consumes them) instead of reducing them into C
   bool no_reduce = false;
+  // fp32 A only: acc[m] += alpha * sum_k A(m, k) (an SGD bias step beside a
+  // weight-gradient product), computed by the outer-product plan's operand
+  // packing; other plans leave it to the caller (gemm_a_rowsum_fused)
+  void* a_rowsum_acc = nullptr;
   // Y = layer_norm(C) over N (gamma, beta [N]) computed by the split-K
   // reduction while it writes C (gemm_post_ln_fused); Y is [M, N] contiguous
   const void* pln_gamma = nullptr;
@@ -272,6 +276,9 @@ bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K);
 // Whether the launch ends in a split-K reduction that can also produce
 // layer_norm(C) (one batch, N <= 2048); otherwise the caller runs layer_norm.
 bool gemm_post_ln_fused(const Gemm& g);
+// True when the plan for g computes a_rowsum_acc itself (the outer-product
+// plan); otherwise the caller leaves it null and sums A on its own.
+bool gemm_a_rowsum_fused(const Gemm& g);
 // K splits of the launch's plan (1 when it has no split-K reduction).
 int gemm_splits(const Gemm& g);
 // Whether the skinny decode kernel takes this problem, and whether it can

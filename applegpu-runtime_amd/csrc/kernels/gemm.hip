@@ -806,6 +806,8 @@ int gemm_splits(const Gemm& g) {
   return pl.kind == kMf ? pl.splits : 1;
 }
 
+bool gemm_a_rowsum_fused(const Gemm& g) { return g.dt == DType::F32 && use_outer(g); }
+
 bool gemm_post_ln_fused(const Gemm& g) {
   if (!g.b_x3 && (skinny_plan(g, cu_count()).use || thin_kind(g))) return false;
   if (g.batch != 1 || g.N > 2048 || g.N % 4 != 0 || g.c_sm != g.N) return false;
@@ -885,6 +887,7 @@ size_t gemm_workspace_bytes(const Gemm& g) {
 static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s);
 
 void gemm(const Gemm& g, void* workspace, hipStream_t s) {
+  if (g.a_rowsum_acc && !gemm_a_rowsum_fused(g)) fail("internal: A's row sums are fused only into the outer-product plan");
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;
   if (g.b_x3) {
     if (!gemm_x3_ok(g))

@@ -76,6 +76,56 @@ __global__ void __launch_bounds__(256) pack_x3_pair_kernel(PackSrc a, PackSrc b,
   else pack_x3_one(b, ((int64_t)blockIdx.x - nb0) * 256 + threadIdx.x);
 }
 
+// As pack_x3_pair_kernel, and acc[n] += alpha * sum_k a(k, n) for a's
+// columns (an SGD bias step folded into the packing of the gradient).
+// Blocks [0, nb0) take one 32-column strip of a each: wave w packs k steps
+// t = w, w + 4, ... (the fragments pack_x3_one writes for them) while
+// summing its lanes' values; the four waves' and two half-waves' sums are
+// then added in a fixed order, so results repeat exactly.
+__global__ void __launch_bounds__(256) pack_x3_pair_sum_kernel(PackSrc a, PackSrc b, int64_t nb0,
+                                                               float* __restrict__ acc, float alpha) {
+  if ((int64_t)blockIdx.x >= nb0) {
+    pack_x3_one(b, ((int64_t)blockIdx.x - nb0) * 256 + threadIdx.x);
+    return;
+  }
+  __shared__ float red[4][64];
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t s = blockIdx.x;
+  const int64_t n = 32 * s + (l & 31);
+  const bool nin = n < a.N;
+  const int64_t nc = nin ? n : a.N - 1;
+  float sum = 0.f;
+  for (int64_t t = w; t < a.T; t += 4) {
+    const int64_t k0 = 16 * t + 8 * (l >> 5);
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t k = k0 + j;
+      x[j] = nin && k < a.K ? a.B[k * a.b_sk + nc * a.b_sn] : 0.f;
+    }
+    bf16x8_t h, lo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      bf16_t hj, lj;
+      split_bf16(x[j], hj, lj);
+      h[j] = hj;
+      lo[j] = lj;
+      sum += x[j];
+    }
+    bf16_t* dst = a.out + ((s * a.T + t) * 2) * 512 + l * 8;
+    *(bf16x8_t*)dst = h;
+    *(bf16x8_t*)(dst + 512) = lo;
+  }
+  red[w][l] = sum;
+  __syncthreads();
+  if (threadIdx.x < 32 && nin) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) t += red[q][threadIdx.x] + red[q][threadIdx.x + 32];
+    acc[n] += alpha * t;
+  }
+}
+
 template <int FR, int FC, int WR, int WC, int KT, bool APK>
 __global__ void __launch_bounds__(256) gemm_x3p(GArgs p, int64_t T) {
   static_assert(WR * WC == 4, "four wavefronts per block");
@@ -919,8 +969,16 @@ void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s) {
   const int64_t T = g.K / 16;
   const PackSrc pa{(const float*)g.A, g.a_sk, g.a_sm, g.K, g.M, T, apk};
   const PackSrc pb{(const float*)g.B, g.b_sk, g.b_sn, g.K, g.N, T, bpk};
-  const int64_t nba = ((g.M / 32) * T * 64 + 255) / 256, nbb = ((g.N / 32) * T * 64 + 255) / 256;
-  hipLaunchKernelGGL(pack_x3_pair_kernel, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, pa, pb, nba);
+  const int64_t nbb = ((g.N / 32) * T * 64 + 255) / 256;
+  if (g.a_rowsum_acc) {
+    // one block per 32-row strip of A, which also sums the strip's rows
+    const int64_t nba = g.M / 32;
+    hipLaunchKernelGGL(pack_x3_pair_sum_kernel, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, pa, pb, nba,
+                       (float*)g.a_rowsum_acc, g.alpha);
+  } else {
+    const int64_t nba = ((g.M / 32) * T * 64 + 255) / 256;
+    hipLaunchKernelGGL(pack_x3_pair_kernel, dim3((unsigned)(nba + nbb)), dim3(256), 0, s, pa, pb, nba);
+  }
   check_launch("pack_x3_pair");
   const int64_t tiles = (g.M / 128) * (g.N / 128);
   const dim3 grid((unsigned)tiles);

@@ -32,7 +32,9 @@ static BufferP scratch(size_t bytes) {
   if (meta_mode()) return nullptr;
   return rt().pool().acquire(bytes);
 }
-#define LAUNCH if (!meta_mode())
+// Kernel launches are skipped while ops only infer shapes.  Written as
+// if-else so that an `else` after `if (c) LAUNCH f();` binds to `if (c)`.
+#define LAUNCH if (meta_mode()) {} else
 
 // ── dtype rules ────────────────────────────────────────────────────────────
 enum Cls { kFloatOnly, kNumeric, kAny, kNotBool, kOrdered, kEquality, kIntOrBool, kIntOnly };
@@ -728,11 +730,13 @@ std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b) {
   return {loss, grad};
 }
 
-TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha) {
+TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha,
+                    const TensorP& bias) {
   if (w->ndim != 2) fail("sgd_matmul_: the parameter must be 2-D");
   Epilogue e;
   e.alpha = alpha;
   e.residual = w;
+  e.a_rowsum_acc = bias;
   return matmul(a, b, ta, tb, &e, w);
 }
 
@@ -944,7 +948,7 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
     if (meta_mode()) fail("matmul: the allocation-free form runs eagerly only");
     if (!into) fail("matmul: the allocation-free form writes into a caller-provided output");
     if (post_ln) fail("matmul: the allocation-free form takes no layer_norm");
-    if (epi && (epi->ln_gamma || epi->residual || epi->mask))
+    if (epi && (epi->ln_gamma || epi->residual || epi->mask || epi->a_rowsum_acc))
       fail("matmul: the allocation-free form takes a bias and an activation only");
     if (epi && epi->bias && !epi->bias->is_contiguous())
       fail("matmul: the allocation-free form needs a contiguous bias (a copy would allocate)");
@@ -1030,6 +1034,20 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
   }
   EpiKeep keep;
   set_epilogue(g, epi, od, bdims, &keep);
+  bool rowsum_fused = false;
+  if (epi && epi->a_rowsum_acc) {
+    const TensorP& acc = epi->a_rowsum_acc;
+    if (acc->dtype != DType::F32 || g.dt != DType::F32 || a_in->ndim != 2 || b_in->ndim != 2 ||
+        acc->numel() != M || !acc->is_contiguous())
+      fail("matmul: the row-sum accumulator must be a contiguous fp32 [%lld] tensor beside a 2-D fp32 product",
+           (long long)M);
+    if (!meta_mode()) {
+      k::Gemm probe = g;
+      probe.a_rowsum_acc = acc->data();
+      rowsum_fused = k::gemm_a_rowsum_fused(probe);
+      if (rowsum_fused) g = probe;
+    }
+  }
   TensorP pl_g, pl_b;
   bool pln_fused = false;
   if (post_ln) {
@@ -1065,6 +1083,16 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
   if (wsb) ws = scratch(wsb);
   LAUNCH k::gemm(g, ws ? ws->ptr : nullptr, rt().stream());
   if (post_ln && !pln_fused) post_ln->y = layer_norm(out, pl_g, pl_b, post_ln->eps);
+  if (epi && epi->a_rowsum_acc && !rowsum_fused) {
+    // the row sums of op(a) on their own: op(a) = a_in^T with a_in a
+    // contiguous [K, M] gradient is the column-sum kernel of sgd_sum_rows_
+    const TensorP& acc = epi->a_rowsum_acc;
+    if (ta && a_in->is_contiguous()) {
+      LAUNCH k::sum_rows_axpy(DType::F32, a_in->data(), acc->data(), K, M, epi->alpha, rt().stream());
+    } else {
+      axpy_inplace(acc, sum_dim(a, 1, false, 1.f), epi->alpha);
+    }
+  }
   return out;
 }
 

@@ -87,6 +87,8 @@ struct Epilogue {
   // the folded weights' column sums (matmul_pp_norm)
   TensorP norm_stats, norm_cs;
   float norm_eps = 1e-5f;
+  // fp32, 2-D products: a_rowsum_acc[m] += alpha * sum_k op(a)(m, k)
+  TensorP a_rowsum_acc;
 };
 // Also y = layer_norm(out, gamma, beta, eps) over the last dim; computed by
 // the GEMM's split-K reduction when its plan has one, else by layer_norm.
@@ -125,9 +127,13 @@ TensorP matmul(const TensorP& a, const TensorP& b, bool ta = false, bool tb = fa
 bool embedding_add_fusable(const TensorP& w1, const TensorP& i1, const TensorP& w2, const TensorP& i2);
 TensorP embedding_add(const TensorP& w1, const TensorP& i1, const TensorP& w2, const TensorP& i2, PostLn* ln);
 // SGD steps fused with their gradients, in place:
-//   w += alpha * op(a) op(b)   (the weight gradient GEMM; w contiguous 2-D)
+//   w += alpha * op(a) op(b)   (the weight gradient GEMM; w contiguous 2-D),
+//     and with bias also bias += alpha * (row sums of op(a)) (a Linear
+//     layer's bias step: op(a) = g^T, so its row sums are sum(g, 0));
+//     the outer-product plan folds that sum into its operand packing
 //   bias += alpha * sum(g, 0)  (g contiguous [rows, N])
-TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha);
+TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha,
+                    const TensorP& bias = nullptr);
 TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha);
 // MSE loss and its gradient (upstream gradient 1): {loss [1], grad like a}.
 std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b);

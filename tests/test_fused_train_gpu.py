@@ -4,7 +4,8 @@ against the oracle and against the unfused sequence they replace:
   - GEMMs with N == 1, M == 1 or K == 1 (matrix-vector, vector-matrix, outer
     product) with the fused epilogue (bias, relu, residual, mask), fp32 and
     16-bit, batched;
-  - w += alpha * op(a) op(b) in the GEMM epilogue (sgd_matmul_), also with
+  - w += alpha * op(a) op(b) in the GEMM epilogue (sgd_matmul_; with a bias
+    also bias += alpha * sum(g, 0), in the operand packing), also with
     split-K and in the MLP's transposed-A layout;
   - bias += alpha * sum(g, 0) (sgd_sum_rows_);
   - MSE loss and gradient in one launch (mse_loss_grad);
@@ -136,6 +137,44 @@ def test_outer_plan_products(gpu, K, ta, tb, M, N):
         out = gpu.relu(gpu.add_bias(gpu.from_numpy(a) @ gpu.from_numpy(b), gpu.from_numpy(bias))).to_numpy()
         want = np.maximum(ref + bias, 0)
         assert rel_err(out, want) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K,ta,plan", [(4096, 4096, 256, True, "x3 outer"), (2048, 2304, 128, True, "x3 outer"),
+                                            (300, 70, 1000, True, ""), (1, 4096, 256, True, ""),
+                                            (64, 96, 48, False, "")])
+def test_sgd_matmul_with_bias_step(gpu, M, N, K, ta, plan):
+    """sgd_matmul_(w, a, b, bias=...) also takes the bias step bias +=
+    alpha * (row sums of op(a)): for op(a) = g^T that is alpha * g.sum(0), the
+    Linear layer's bias gradient.  The outer-product plan sums g while
+    packing it (one block per 32-row strip, a fixed order, so two runs agree
+    bit for bit); other plans sum on their own (the column-sum kernel for a
+    contiguous g, else a row sum).  Weights and bias against float64."""
+    from applegpu_runtime import eager as E
+    if plan:
+        assert _plan(M, N, K, a_kcontig=not ta).startswith(plan)
+    a = f32(K, M, scale=0.1) if ta else f32(M, K, scale=0.1)
+    b = f32(K, N)
+    w0, b0 = f32(M, N), f32(M)
+    a64 = (a.T if ta else a).astype(np.float64)
+    lr = 0.01
+    outs = []
+    for _ in range(2):
+        wt, bt = E.from_numpy(w0), E.from_numpy(b0)
+        E.sgd_matmul_(wt, E.from_numpy(a), E.from_numpy(b), ta, False, -lr, bias=bt)
+        outs.append((wt.numpy(), bt.numpy()))
+    (w1, b1), (w2, b2) = outs
+    np.testing.assert_array_equal(b1, b2)
+    np.testing.assert_array_equal(w1, w2)
+    assert rel_err(w1 - w0, -lr * (a64 @ b.astype(np.float64))) < 1e-5
+    np.testing.assert_allclose(b1, b0 - lr * a64.sum(1), rtol=1e-5, atol=1e-6)
+
+
+def test_sgd_matmul_bias_step_rejects_bad_bias(gpu):
+    from applegpu_runtime import eager as E
+    w = E.from_numpy(f32(8, 8))
+    with pytest.raises(RuntimeError):
+        E.sgd_matmul_(w, E.from_numpy(f32(4, 8)), E.from_numpy(f32(4, 8)), True, False, -0.1,
+                      bias=E.from_numpy(f32(7)))
 
 
 def test_outer_plan_declines_other_shapes():
