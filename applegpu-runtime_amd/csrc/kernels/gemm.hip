@@ -707,6 +707,7 @@ GArgs make_args(const Gemm& g, const Plan& pl) {
   p.rs_tiles = g.rs_tiles;
   p.rs_n = g.rs_n;
   p.rs_eps = g.rs_eps;
+  p.rowsum_acc = (float*)g.a_rowsum_acc;
   const size_t esz = dtype_size(g.dt);
   const int vw = (int)(16 / esz);  // elements per 16-byte vector
   // Vector loads need 16-byte aligned runs along the contiguous axis.
@@ -806,7 +807,14 @@ int gemm_splits(const Gemm& g) {
   return pl.kind == kMf ? pl.splits : 1;
 }
 
-bool gemm_a_rowsum_fused(const Gemm& g) { return g.dt == DType::F32 && use_outer(g); }
+// The plans that fold A's row sums in: the outer-product plan (while packing
+// A) and the vector-matrix kernel (M == 1: one block also sums A's K values).
+bool gemm_a_rowsum_fused(const Gemm& g) {
+  if (g.dt != DType::F32 || g.b_x3) return false;
+  if (skinny_plan(g, cu_count()).use) return false;
+  if (const int tk = thin_kind(g)) return tk == kThinM1 && g.batch == 1;
+  return use_outer(g);
+}
 
 bool gemm_post_ln_fused(const Gemm& g) {
   if (!g.b_x3 && (skinny_plan(g, cu_count()).use || thin_kind(g))) return false;

@@ -53,6 +53,8 @@ struct GArgs {
   int rs_tiles;
   int64_t rs_n;
   float rs_eps;
+  // rowsum_acc[m] += alpha * sum_k A(m, k) (gemm_a_rowsum_fused plans)
+  float* rowsum_acc;
 };
 
 // Epilogue operands of one output, loadable ahead of the product (they do

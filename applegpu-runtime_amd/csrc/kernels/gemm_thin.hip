@@ -3,7 +3,8 @@
 //           per output row, a shuffle reduction);
 //   M == 1: vector-matrix with B rows contiguous along n, C[b, n] =
 //           sum_k A[b, k] B[b, k, n]  (a 1024-thread block per 64 columns,
-//           16 k slices reduced through LDS in slice order);
+//           16 k slices reduced through LDS in slice order; optionally also
+//           an SGD bias step from A's sum, GArgs::rowsum_acc);
 //   K == 1: outer product, C[b, m, n] = A[b, m] B[b, n]  (elementwise).
 // Same arithmetic as the reference's matmul/linear (fp32 accumulation,
 // crates/core/src/kernel_templates.rs:987-1072) and the same fused epilogue
@@ -53,6 +54,22 @@ __global__ void __launch_bounds__(1024) gevm_m1(GArgs p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) t += sh[i][lane];
     epilogue_store<T>(p, b, 0, n, t);
+  }
+  // rowsum_acc[0] += alpha * sum_k A[k] (one batch): block 0 alone, its 16
+  // wavefront sums added in order
+  if (p.rowsum_acc && blockIdx.x == 0 && blockIdx.y == 0) {
+    __syncthreads();  // slice 0 is done reading sh
+    float r = 0.f;
+    for (int64_t k = threadIdx.x; k < p.K; k += 1024) r += to_f(A[k * p.a_sk]);
+    r = wave_sum(r);
+    if (lane == 0) sh[0][slice] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t += sh[0][i];
+      p.rowsum_acc[0] += p.alpha * t;
+    }
   }
 }
 

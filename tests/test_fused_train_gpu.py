@@ -147,8 +147,10 @@ def test_sgd_matmul_with_bias_step(gpu, M, N, K, ta, plan):
     alpha * (row sums of op(a)): for op(a) = g^T that is alpha * g.sum(0), the
     Linear layer's bias gradient.  The outer-product plan sums g while
     packing it (one block per 32-row strip, a fixed order, so two runs agree
-    bit for bit); other plans sum on their own (the column-sum kernel for a
-    contiguous g, else a row sum).  Weights and bias against float64."""
+    bit for bit), and so does the vector-matrix kernel (M = 1, the MLP's
+    output layer: its first block sums g); other plans sum on their own (the
+    column-sum kernel for a contiguous g, else a row sum).  Weights and bias
+    against float64."""
     from applegpu_runtime import eager as E
     if plan:
         assert _plan(M, N, K, a_kcontig=not ta).startswith(plan)
