@@ -169,6 +169,33 @@ def c2_replays(n):
     g.destroy()
 
 
+def c3_replays(n):
+    """The headline's C3 MLP train step graph alone, replayed n times; prints
+    the mean replay time (each replay updates the parameters in place, as in
+    the headline).  Under rocprofv3 --kernel-trace every dispatch after the
+    parameter uploads is one of the step's kernels."""
+    import applegpu_runtime as gpu
+    from applegpu_runtime import eager as E
+    from applegpu_runtime._native import lib
+    from applegpu_runtime.models.mlp import EagerMLP, torch_default_init
+    gpu.init_backend()
+    params = torch_default_init(MLP_SIZES, seed=42)
+    rng = np.random.default_rng(42)
+    x = E.from_numpy(rng.standard_normal((MLP_BATCH, MLP_SIZES[0]), dtype=np.float32))
+    y = E.from_numpy(rng.standard_normal((MLP_BATCH, MLP_SIZES[-1]), dtype=np.float32))
+    mlp = EagerMLP(params)
+    g = gpu.capture(lambda: mlp.train_step(x, y, lr=0.01))
+    g.replay()
+    lib.applegpu_ffi_synchronize()
+    lib.applegpu_ffi_event_record(0)
+    for _ in range(n):
+        g.replay()
+    lib.applegpu_ffi_event_record(1)
+    lib.applegpu_ffi_synchronize()
+    print(json.dumps({"c3_replays": n, "ms_per_replay": round(lib.applegpu_ffi_event_elapsed_ms(0, 1) / n, 4)}))
+    g.destroy()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -198,9 +225,15 @@ def main():
     ap.add_argument("--c2-replays", type=int, default=0,
                     help="instead of the headline line, capture the C2 forward and replay it this many times "
                          "(nothing else runs: a per-forward kernel trace of exactly the timed graph)")
+    ap.add_argument("--c3-replays", type=int, default=0,
+                    help="instead of the headline line, capture the C3 MLP train step and replay it this many "
+                         "times (a per-step kernel trace of exactly the timed graph)")
     args = ap.parse_args()
     if args.c2_replays > 0:
         c2_replays(args.c2_replays)
+        return
+    if args.c3_replays > 0:
+        c3_replays(args.c3_replays)
         return
     if args.suite:
         kernel_suite(args.only)
