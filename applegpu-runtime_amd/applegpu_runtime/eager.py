@@ -167,6 +167,18 @@ def sgd_matmul_(w, a, b, ta=False, tb=False, alpha=1.0, bias=None):
     op("sgd_matmul_", ins, f=(float(alpha),), i=(int(ta), int(tb)))
 
 
+def linear_backward_sgd_(w, b, g, a, mask=None, alpha=1.0):
+    """A Linear layer's backward and SGD step, in place (y = a @ w^T + b,
+    upstream gradient g): w += alpha * g^T @ a, b += alpha * g.sum(0).  With
+    `mask` also returns (g @ w) where mask > 0, else 0 -- the gradient of the
+    layer input through the previous ReLU, from w before the update; without
+    it returns None.  A one-output layer (w [1, N], mask the input a itself)
+    is one launch."""
+    ins = [w, b, g, a] if mask is None else [w, b, g, a, mask]
+    r = op("linear_backward_sgd_", ins, f=(float(alpha),))
+    return r if mask is not None else None
+
+
 def sgd_sum_rows_(bias, g, alpha=1.0):
     """bias += alpha * g.sum(0) in place: an SGD bias step fused with its
     gradient reduction."""

@@ -65,11 +65,9 @@ class EagerMLP:
         for i in range(len(self.params) - 1, -1, -1):
             w, b = self.params[i]
             # dL/d(input of layer i) masked by relu' of the previous layer's
-            # output, from W_i before its update
-            g_in = E.matmul_masked(g, w, False, False, acts[i]) if i > 0 else None
-            # W_i -= lr * g^T a_i and b_i -= lr * sum(g, 0)
-            E.sgd_matmul_(w, g, acts[i], True, False, -lr, bias=b)
-            g = g_in
+            # output (from W_i before its update), then W_i -= lr * g^T a_i
+            # and b_i -= lr * sum(g, 0)
+            g = E.linear_backward_sgd_(w, b, g, acts[i], acts[i] if i > 0 else None, -lr)
         return loss
 
     def train_step_unfused(self, x, y, lr=0.01):

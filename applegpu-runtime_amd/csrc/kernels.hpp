@@ -276,6 +276,19 @@ bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K);
 // Whether the launch ends in a split-K reduction that can also produce
 // layer_norm(C) (one batch, N <= 2048); otherwise the caller runs layer_norm.
 bool gemm_post_ln_fused(const Gemm& g);
+// Backward and SGD step of a Linear layer with one output, one launch:
+// gin[r, j] = h[r, j] > 0 ? dz[r] * w[j] : 0 (gin may be null), then
+// w[j] += alpha * sum_r dz[r] h[r, j] and (b non-null) b[0] += alpha *
+// sum_r dz[r].  h [R, N] with row stride h_sm and unit column stride, dz
+// [R] with stride dz_s, w [N] and gin [R, N] contiguous.
+struct Lin1Bwd {
+  const void* h; int64_t h_sm;
+  const void* dz; int64_t dz_s;
+  void* w; void* b; void* gin;
+  int64_t R, N;
+  float alpha;
+};
+void linear1_backward_sgd(DType dt, const Lin1Bwd& a, hipStream_t s);
 // True when the plan for g computes a_rowsum_acc itself (the outer-product
 // plan); otherwise the caller leaves it null and sums A on its own.
 bool gemm_a_rowsum_fused(const Gemm& g);

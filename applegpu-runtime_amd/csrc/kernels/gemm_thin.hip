@@ -73,6 +73,60 @@ __global__ void __launch_bounds__(1024) gevm_m1(GArgs p) {
   }
 }
 
+// The backward of a Linear layer with one output (w [1, N]) and its SGD
+// step, in one pass over the layer input h [R, N]: for each column j
+//   g_in[r, j] = h[r, j] > 0 ? dz[r] * w[j] : 0   (with w before the update)
+//   w[j]      += alpha * sum_r dz[r] * h[r, j]
+// and b[0] += alpha * sum_r dz[r] (block 0).  It replaces outer_k1 (with
+// the mask) followed by gevm_m1 (with the residual and rowsum_acc).  A block
+// owns 16 columns over all rows (64 row slices of 16 lanes, so every CU
+// gets a block at N = 4096); a column's 64 slice sums meet in LDS in slice
+// order, so results repeat exactly.
+template <typename T>
+__global__ void __launch_bounds__(1024) linear1_bwd_sgd(Lin1Bwd p) {
+  __shared__ float sh[64][17];
+  const int c = threadIdx.x & 15, slice = threadIdx.x >> 4;
+  const int64_t j = (int64_t)blockIdx.x * 16 + c;
+  const T* h = (const T*)p.h;
+  const T* dz = (const T*)p.dz;
+  T* w = (T*)p.w;
+  float s = 0.f;
+  if (j < p.N) {
+    const float wj = to_f(w[j]);
+#pragma unroll 4
+    for (int64_t r = slice; r < p.R; r += 64) {
+      const float hv = to_f(h[r * p.h_sm + j]);
+      const float d = to_f(dz[r * p.dz_s]);
+      if (p.gin) ((T*)p.gin)[r * p.N + j] = from_f<T>(hv > 0.f ? d * wj : 0.f);
+      s += d * hv;
+    }
+  }
+  sh[slice][c] = s;
+  __syncthreads();
+  if (slice == 0 && j < p.N) {
+    float t = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < 64; ++i) t += sh[i][c];
+    w[j] = from_f<T>(p.alpha * t + to_f(w[j]));
+  }
+  if (p.b && blockIdx.x == 0) {
+    __syncthreads();  // slice 0 is done reading sh
+    float r = 0.f;
+    for (int64_t k = threadIdx.x; k < p.R; k += 1024) r += to_f(dz[k * p.dz_s]);
+    r = wave_sum(r);
+    const int wv = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[0][wv] = r;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) t += sh[0][i];
+      T* b = (T*)p.b;
+      b[0] = from_f<T>(to_f(b[0]) + p.alpha * t);
+    }
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) outer_k1(GArgs p) {
   const int64_t b = blockIdx.y;
@@ -86,6 +140,13 @@ __global__ void __launch_bounds__(256) outer_k1(GArgs p) {
 }
 
 }  // namespace
+
+void linear1_backward_sgd(DType dt, const Lin1Bwd& a, hipStream_t s) {
+  if (a.N == 0) return;
+  if (dt != DType::F32) fail("linear1_backward_sgd: fp32 only");
+  hipLaunchKernelGGL((linear1_bwd_sgd<float>), dim3((unsigned)((a.N + 15) / 16)), dim3(1024), 0, s, a);
+  check_launch("linear1_backward_sgd");
+}
 
 int thin_kind(const Gemm& g) {
   const bool fl = g.dt == DType::F32 || g.dt == DType::F16 || g.dt == DType::BF16;

@@ -740,6 +740,36 @@ TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool t
   return matmul(a, b, ta, tb, &e, w);
 }
 
+TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& g, const TensorP& a,
+                             const TensorP& mask, float alpha) {
+  if (w->ndim != 2 || g->ndim != 2 || a->ndim != 2)
+    fail("linear_backward_sgd_: w, g and a must be 2-D");
+  const int64_t R = g->shape[0], O = w->shape[0], N = w->shape[1];
+  if (g->shape[1] != O || a->shape[0] != R || a->shape[1] != N)
+    fail("linear_backward_sgd_: g %s and a %s do not fit w %s", shape_str(g->dims()).c_str(),
+         shape_str(a->dims()).c_str(), shape_str(w->dims()).c_str());
+  if (b->numel() != O) fail("linear_backward_sgd_: bias must have %lld elements", (long long)O);
+  if (mask && mask->dims() != a->dims()) fail("linear_backward_sgd_: the mask must have a's shape");
+  const bool f32 = w->dtype == DType::F32 && b->dtype == DType::F32 && g->dtype == DType::F32 &&
+                   a->dtype == DType::F32;
+  if (O == 1 && f32 && w->is_contiguous() && b->is_contiguous() && a->strides[1] == 1 &&
+      (!mask || mask.get() == a.get())) {
+    TensorP gin = mask ? alloc_out(DType::F32, {R, N}) : nullptr;
+    k::Lin1Bwd p{a->data(), a->strides[0], g->data(), g->strides[0], w->data(), b->data(),
+                 gin ? gin->data() : nullptr, R, N, alpha};
+    LAUNCH k::linear1_backward_sgd(DType::F32, p, rt().stream());
+    return gin ? gin : w;
+  }
+  TensorP gin;
+  if (mask) {
+    Epilogue e;
+    e.mask = mask;
+    gin = matmul(g, w, false, false, &e);
+  }
+  sgd_matmul_(w, g, a, true, false, alpha, b);
+  return mask ? gin : w;
+}
+
 TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha) {
   check_dtype("sgd_sum_rows_", kFloatOnly, g->dtype);
   if (g->ndim != 2 || bias->dtype != g->dtype || bias->numel() != g->shape[1] || !bias->is_contiguous())

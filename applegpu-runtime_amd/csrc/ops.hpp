@@ -135,6 +135,15 @@ TensorP embedding_add(const TensorP& w1, const TensorP& i1, const TensorP& w2, c
 TensorP sgd_matmul_(const TensorP& w, const TensorP& a, const TensorP& b, bool ta, bool tb, float alpha,
                     const TensorP& bias = nullptr);
 TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha);
+// A Linear layer's backward and SGD step (y = a w^T + b, upstream gradient
+// g [R, out]): with mask, returns g_in = (g w) where mask > 0, else 0 (the
+// gradient of the layer input through the previous ReLU, from w before its
+// update); then w += alpha g^T a and b += alpha sum(g, 0).  Without mask,
+// returns w.  A layer with one output (w [1, N], fp32, mask == a) runs as one
+// launch (linear1_backward_sgd); otherwise matmul with the mask and
+// sgd_matmul_ with the bias.
+TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& g, const TensorP& a,
+                             const TensorP& mask, float alpha);
 // MSE loss and its gradient (upstream gradient 1): {loss [1], grad like a}.
 std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b);
 // Decode-step weights: wt [out N, in K] (fp16/bf16) rearranged for the skinny

@@ -171,6 +171,44 @@ def test_sgd_matmul_with_bias_step(gpu, M, N, K, ta, plan):
     np.testing.assert_allclose(b1, b0 - lr * a64.sum(1), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("R,O,N,with_mask", [(256, 1, 4096, True), (256, 1, 4096, False), (33, 1, 70, True),
+                                              (32, 10, 128, True), (1000, 1, 64, False)])
+def test_linear_backward_sgd(gpu, R, O, N, with_mask):
+    """linear_backward_sgd_: g_in = (g @ w) masked by the ReLU'(a) of the
+    layer input, from w before its update, then w -= lr g^T a and b -= lr
+    sum(g, 0).  A one-output layer (the MLP's output layer) is one launch
+    (16 columns per block, 64 row slices): the masked gradient equals the
+    two-launch sequence it replaces (matmul with the mask, then sgd_matmul_
+    with the bias) exactly, the updated parameters to float rounding (the
+    sums run in another order); two runs agree bit for bit; both against
+    float64."""
+    from applegpu_runtime import eager as E
+    a = np.maximum(f32(R, N), 0).astype(np.float32) * (RNG.random((R, N)) > 0.3).astype(np.float32)
+    g, w0, b0 = f32(R, O, scale=0.1), f32(O, N), f32(O)
+    lr = 0.01
+    wt, bt = E.from_numpy(w0), E.from_numpy(b0)
+    at, gt = E.from_numpy(a), E.from_numpy(g)
+    gin = E.linear_backward_sgd_(wt, bt, gt, at, at if with_mask else None, -lr)
+    assert (gin is None) == (not with_mask)
+    w2, b2 = E.from_numpy(w0), E.from_numpy(b0)
+    E.linear_backward_sgd_(w2, b2, gt, at, None, -lr)
+    np.testing.assert_array_equal(w2.numpy(), wt.numpy())
+    np.testing.assert_array_equal(b2.numpy(), bt.numpy())
+    # the two-launch sequence
+    wu, bu = E.from_numpy(w0), E.from_numpy(b0)
+    ginu = E.matmul_masked(gt, wu, False, False, at) if with_mask else None
+    E.sgd_matmul_(wu, gt, at, True, False, -lr, bias=bu)
+    np.testing.assert_allclose(wt.numpy(), wu.numpy(), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(bt.numpy(), bu.numpy(), rtol=1e-6, atol=1e-7)
+    g64, a64 = g.astype(np.float64), a.astype(np.float64)
+    assert rel_err(wt.numpy() - w0, -lr * (g64.T @ a64)) < 1e-5
+    np.testing.assert_allclose(bt.numpy(), b0 - lr * g64.sum(0), rtol=1e-5, atol=1e-6)
+    if with_mask:
+        np.testing.assert_array_equal(gin.numpy(), ginu.numpy())
+        want = np.where(a > 0, g64 @ w0.astype(np.float64), 0.0)
+        assert rel_err(gin.numpy(), want) < 1e-5
+
+
 def test_sgd_matmul_bias_step_rejects_bad_bias(gpu):
     from applegpu_runtime import eager as E
     w = E.from_numpy(f32(8, 8))
