@@ -179,6 +179,16 @@ def linear_backward_sgd_(w, b, g, a, mask=None, alpha=1.0):
     return r if mask is not None else None
 
 
+def linear_mse_backward_sgd_(h, w, b, y, alpha=1.0, grad_in=True):
+    """The last Linear layer of an MSE regression through its SGD step, in
+    place: z = h @ w^T + b, loss = mean((z - y)^2), then w += alpha * g^T @ h
+    and b += alpha * g.sum(0) for g = dloss/dz.  Returns (loss, g_in), g_in
+    the gradient of h through the previous ReLU (from w before the update),
+    or (loss, None) with grad_in=False.  A one-output layer is two launches."""
+    loss, gi = op("linear_mse_backward_sgd_", [h, w, b, y], f=(float(alpha),), i=(int(bool(grad_in)),), nout=2)
+    return loss, (gi if grad_in else None)
+
+
 def sgd_sum_rows_(bias, g, alpha=1.0):
     """bias += alpha * g.sum(0) in place: an SGD bias step fused with its
     gradient reduction."""

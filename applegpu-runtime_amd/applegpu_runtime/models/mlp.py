@@ -60,9 +60,17 @@ class EagerMLP:
 
     def train_step(self, x, y, lr=0.01):
         """One forward + MSE + backward + SGD step; returns the loss tensor (on device)."""
-        out, acts = self.forward(x)
-        loss, g = E.mse_loss_grad(out, y)
-        for i in range(len(self.params) - 1, -1, -1):
+        n = len(self.params)
+        acts = [x]
+        h = x
+        for w, b in self.params[:-1]:
+            h = E.linear(h, w, b, act=1)
+            acts.append(h)
+        # the output layer (no activation) with the loss, its gradient and
+        # its SGD step
+        w, b = self.params[-1]
+        loss, g = E.linear_mse_backward_sgd_(h, w, b, y, -lr, grad_in=n > 1)
+        for i in range(n - 2, -1, -1):
             w, b = self.params[i]
             # dL/d(input of layer i) masked by relu' of the previous layer's
             # output (from W_i before its update), then W_i -= lr * g^T a_i

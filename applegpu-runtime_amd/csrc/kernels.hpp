@@ -287,8 +287,24 @@ struct Lin1Bwd {
   void* w; void* b; void* gin;
   int64_t R, N;
   float alpha;
+  // optional (loss non-null): loss[0] = inv_n * sum_r (z[r] - y[r])^2, the
+  // MSE of the layer's forward output z against y (contiguous [R]), by
+  // block 0 before it updates b
+  const void* z; const void* y; void* loss; float inv_n;
 };
 void linear1_backward_sgd(DType dt, const Lin1Bwd& a, hipStream_t s);
+// Forward of a Linear layer with one output and the MSE gradient, one
+// launch (one block per row): z[r] = h[r, :] . w + b[0], dz[r] = (z[r] -
+// y[r]) * two_over_n.  h [R, N] with row stride h_sm and unit column
+// stride; w [N], b [1], y, z and dz [R] contiguous.
+struct Lin1Fwd {
+  const void* h; int64_t h_sm;
+  const void* w; const void* b; const void* y;
+  void* z; void* dz;
+  int64_t R, N;
+  float two_over_n;
+};
+void linear1_forward_mse(DType dt, const Lin1Fwd& a, hipStream_t s);
 // True when the plan for g computes a_rowsum_acc itself (the outer-product
 // plan); otherwise the caller leaves it null and sums A on its own.
 bool gemm_a_rowsum_fused(const Gemm& g);

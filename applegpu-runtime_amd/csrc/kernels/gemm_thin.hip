@@ -111,19 +111,61 @@ __global__ void __launch_bounds__(1024) linear1_bwd_sgd(Lin1Bwd p) {
   }
   if (p.b && blockIdx.x == 0) {
     __syncthreads();  // slice 0 is done reading sh
-    float r = 0.f;
-    for (int64_t k = threadIdx.x; k < p.R; k += 1024) r += to_f(dz[k * p.dz_s]);
+    float r = 0.f, q = 0.f;
+    for (int64_t k = threadIdx.x; k < p.R; k += 1024) {
+      r += to_f(dz[k * p.dz_s]);
+      if (p.loss) {
+        const float d = to_f(((const T*)p.z)[k]) - to_f(((const T*)p.y)[k]);
+        q += d * d;
+      }
+    }
     r = wave_sum(r);
+    q = wave_sum(q);
     const int wv = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) sh[0][wv] = r;
+    if ((threadIdx.x & 63) == 0) { sh[0][wv] = r; sh[1][wv] = q; }
     __syncthreads();
     if (threadIdx.x == 0) {
-      float t = 0.f;
+      float t = 0.f, u = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) t += sh[0][i];
+      for (int i = 0; i < 16; ++i) { t += sh[0][i]; u += sh[1][i]; }
       T* b = (T*)p.b;
       b[0] = from_f<T>(to_f(b[0]) + p.alpha * t);
+      if (p.loss) ((T*)p.loss)[0] = from_f<T>(u * p.inv_n);
     }
+  }
+}
+
+// z[r] = h[r, :] . w + b[0] and the MSE gradient dz[r] = (z[r] - y[r]) *
+// 2/n, one 256-thread block per row (16-byte loads when the rows allow);
+// the wavefront sums meet in LDS in order.
+template <typename T>
+__global__ void __launch_bounds__(256) linear1_fwd_mse(Lin1Fwd p) {
+  __shared__ float sh[4];
+  const int64_t r = blockIdx.x;
+  const T* h = (const T*)p.h + r * p.h_sm;
+  const T* w = (const T*)p.w;
+  float s = 0.f;
+  const bool vec = sizeof(T) == 4 && (p.N & 3) == 0 && (((uintptr_t)h | (uintptr_t)w) & 15) == 0;
+  if (vec) {
+    for (int64_t k = threadIdx.x; k < p.N / 4; k += 256) {
+      const float4 a = ((const float4*)h)[k], c = ((const float4*)w)[k];
+      s += a.x * c.x;
+      s += a.y * c.y;
+      s += a.z * c.z;
+      s += a.w * c.w;
+    }
+  } else {
+    for (int64_t k = threadIdx.x; k < p.N; k += 256) s += to_f(h[k]) * to_f(w[k]);
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float z = ((sh[0] + sh[1]) + (sh[2] + sh[3])) + to_f(((const T*)p.b)[0]);
+    const T zt = from_f<T>(z);
+    ((T*)p.z)[r] = zt;
+    const float d = to_f(zt) - to_f(((const T*)p.y)[r]);
+    ((T*)p.dz)[r] = from_f<T>(d * p.two_over_n);
   }
 }
 
@@ -146,6 +188,14 @@ void linear1_backward_sgd(DType dt, const Lin1Bwd& a, hipStream_t s) {
   if (dt != DType::F32) fail("linear1_backward_sgd: fp32 only");
   hipLaunchKernelGGL((linear1_bwd_sgd<float>), dim3((unsigned)((a.N + 15) / 16)), dim3(1024), 0, s, a);
   check_launch("linear1_backward_sgd");
+}
+
+void linear1_forward_mse(DType dt, const Lin1Fwd& a, hipStream_t s) {
+  if (a.R == 0) return;
+  if (dt != DType::F32) fail("linear1_forward_mse: fp32 only");
+  if (a.R > 0x7fffffffLL) fail("linear1_forward_mse: too many rows");
+  hipLaunchKernelGGL((linear1_fwd_mse<float>), dim3((unsigned)a.R), dim3(256), 0, s, a);
+  check_launch("linear1_forward_mse");
 }
 
 int thin_kind(const Gemm& g) {

@@ -770,6 +770,38 @@ TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& 
   return mask ? gin : w;
 }
 
+std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const TensorP& w, const TensorP& b,
+                                                     const TensorP& y, float alpha, bool grad_in) {
+  if (h->ndim != 2 || w->ndim != 2) fail("linear_mse_backward_sgd_: h and w must be 2-D");
+  const int64_t R = h->shape[0], N = h->shape[1], O = w->shape[0];
+  if (w->shape[1] != N) fail("linear_mse_backward_sgd_: w %s does not fit h %s", shape_str(w->dims()).c_str(),
+                             shape_str(h->dims()).c_str());
+  if (b->numel() != O) fail("linear_mse_backward_sgd_: bias must have %lld elements", (long long)O);
+  if (y->dims() != std::vector<int64_t>{R, O})
+    fail("linear_mse_backward_sgd_: y must be [%lld, %lld]", (long long)R, (long long)O);
+  const bool f32 = h->dtype == DType::F32 && w->dtype == DType::F32 && b->dtype == DType::F32 &&
+                   y->dtype == DType::F32;
+  if (O == 1 && R > 0 && f32 && h->strides[1] == 1 && w->is_contiguous() && b->is_contiguous() &&
+      y->is_contiguous()) {
+    TensorP z = alloc_out(DType::F32, {R, 1}), dz = alloc_out(DType::F32, {R, 1});
+    TensorP loss = alloc_out(DType::F32, {1});
+    TensorP gin = grad_in ? alloc_out(DType::F32, {R, N}) : nullptr;
+    const float n = (float)R;
+    k::Lin1Fwd f{h->data(), h->strides[0], w->data(), b->data(), y->data(), z->data(), dz->data(), R, N, 2.f / n};
+    LAUNCH k::linear1_forward_mse(DType::F32, f, rt().stream());
+    k::Lin1Bwd p{h->data(), h->strides[0], dz->data(), 1, w->data(), b->data(), gin ? gin->data() : nullptr,
+                 R, N, alpha, z->data(), y->data(), loss->data(), 1.f / n};
+    LAUNCH k::linear1_backward_sgd(DType::F32, p, rt().stream());
+    return {loss, gin ? gin : w};
+  }
+  Epilogue e;
+  e.bias = b;
+  TensorP out = matmul(h, w, false, true, &e);
+  auto lg = mse_loss_grad(out, y);
+  TensorP gi = linear_backward_sgd_(w, b, lg.second, h, grad_in ? h : nullptr, alpha);
+  return {lg.first, gi};
+}
+
 TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha) {
   check_dtype("sgd_sum_rows_", kFloatOnly, g->dtype);
   if (g->ndim != 2 || bias->dtype != g->dtype || bias->numel() != g->shape[1] || !bias->is_contiguous())

@@ -144,6 +144,16 @@ TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha);
 // sgd_matmul_ with the bias.
 TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& g, const TensorP& a,
                              const TensorP& mask, float alpha);
+// The last Linear layer of an MSE regression (no activation) through its
+// SGD step: z = h w^T + b, loss = mean((z - y)^2), g = dloss/dz, then
+// linear_backward_sgd_(w, b, g, h, grad_in ? h : none, alpha).  Returns
+// {loss, g_in} (g_in: the gradient of h through the previous ReLU, from w
+// before its update; w itself when grad_in is false).  A one-output layer
+// (w [1, N], fp32) is two launches (linear1_forward_mse, then
+// linear1_backward_sgd, which also forms the loss); otherwise linear,
+// mse_loss_grad and linear_backward_sgd_.
+std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const TensorP& w, const TensorP& b,
+                                                     const TensorP& y, float alpha, bool grad_in);
 // MSE loss and its gradient (upstream gradient 1): {loss [1], grad like a}.
 std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b);
 // Decode-step weights: wt [out N, in K] (fp16/bf16) rearranged for the skinny

@@ -209,6 +209,45 @@ def test_linear_backward_sgd(gpu, R, O, N, with_mask):
         assert rel_err(gin.numpy(), want) < 1e-5
 
 
+@pytest.mark.parametrize("R,O,N,grad_in", [(256, 1, 4096, True), (256, 1, 4096, False), (37, 1, 70, True),
+                                            (32, 3, 128, True)])
+def test_linear_mse_backward_sgd(gpu, R, O, N, grad_in):
+    """linear_mse_backward_sgd_: the output layer of an MSE regression with
+    its loss, gradient and SGD step.  A one-output layer is two launches
+    (forward with the MSE gradient, then the fused backward, which also forms
+    the loss); other shapes take linear, mse_loss_grad and
+    linear_backward_sgd_.  Loss, input gradient, weights and bias against
+    float64 at the fp32 bars, and against the op-by-op sequence."""
+    from applegpu_runtime import eager as E
+    h = np.maximum(f32(R, N), 0).astype(np.float32)
+    w0, b0, y = f32(O, N, scale=0.02), f32(O), f32(R, O)
+    lr = 0.01
+    wt, bt = E.from_numpy(w0), E.from_numpy(b0)
+    ht, yt = E.from_numpy(h), E.from_numpy(y)
+    loss, gin = E.linear_mse_backward_sgd_(ht, wt, bt, yt, -lr, grad_in=grad_in)
+    assert (gin is None) == (not grad_in)
+    # float64 reference
+    h64, w64 = h.astype(np.float64), w0.astype(np.float64)
+    z = h64 @ w64.T + b0.astype(np.float64)
+    d = z - y.astype(np.float64)
+    g = 2.0 * d / d.size
+    np.testing.assert_allclose(loss.numpy(), [np.mean(d * d)], rtol=1e-4)
+    assert rel_err(wt.numpy() - w0, -lr * (g.T @ h64)) < 1e-4
+    np.testing.assert_allclose(bt.numpy(), b0 - lr * g.sum(0), rtol=1e-5, atol=1e-6)
+    if grad_in:
+        assert rel_err(gin.numpy(), np.where(h > 0, g @ w64, 0.0)) < 1e-4
+    # the op-by-op sequence
+    wu, bu = E.from_numpy(w0), E.from_numpy(b0)
+    out = E.linear(ht, wu, bu, act=0)
+    lu, gu = E.mse_loss_grad(out, yt)
+    giu = E.linear_backward_sgd_(wu, bu, gu, ht, ht if grad_in else None, -lr)
+    np.testing.assert_allclose(loss.numpy(), lu.numpy(), rtol=1e-5)
+    np.testing.assert_allclose(wt.numpy(), wu.numpy(), rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(bt.numpy(), bu.numpy(), rtol=1e-5, atol=1e-7)
+    if grad_in:
+        np.testing.assert_allclose(gin.numpy(), giu.numpy(), rtol=1e-4, atol=1e-8)
+
+
 def test_sgd_matmul_bias_step_rejects_bad_bias(gpu):
     from applegpu_runtime import eager as E
     w = E.from_numpy(f32(8, 8))
