@@ -631,9 +631,21 @@ __device__ __forceinline__ void argmax_take(float& best, int64_t& bi, float ob, 
   if (take) { best = ob; bi = oi; }
 }
 
+// One thread's scan over its own elements, whose indices arrive in
+// increasing order: a later value wins only if strictly larger, a NaN
+// replaces only a non-NaN (so the first NaN wins), and -inf is never taken
+// (bi stays -1, an empty candidate, which argmax_take ranks last).  Float
+// compares and 32-bit indices: argmax_take's int64 branches per element had
+// made the [8, 50257] argmax 24 us.
+__device__ __forceinline__ void argmax_scan(float& best, int& bi, float v, int idx) {
+  const bool take = v > best || (v != v && best == best);
+  best = take ? v : best;
+  bi = take ? idx : bi;
+}
+
 // Argmax of long rows (e.g. [batch, vocab] logits): one 1024-thread block per
 // row, 16-byte loads over the aligned body of the row (rows of an odd length
-// start unaligned: a scalar head and tail cover the rest).
+// start unaligned: a scalar head and tail cover the rest); cols < 2^31.
 template <typename TI>
 __global__ void __launch_bounds__(1024) argmax_row_block(const TI* __restrict__ x, int64_t ldx,
                                                          int32_t* __restrict__ y, int64_t cols) {
@@ -648,17 +660,19 @@ __global__ void __launch_bounds__(1024) argmax_row_block(const TI* __restrict__ 
   const int64_t nvec = (cols - head) / VE;
   const int64_t tail0 = head + nvec * VE;
   float best = -INFINITY;
-  int64_t bi = -1;
-  if (tid < head) argmax_take(best, bi, to_f(xr[tid]), tid);
+  int b32 = -1;
+  if (tid < head) argmax_scan(best, b32, to_f(xr[tid]), tid);
   const uint4* xv = (const uint4*)(xr + head);
-  for (int64_t v = tid; v < nvec; v += 1024) {
+  const int nv = (int)nvec, hd = (int)head;
+  for (int v = tid; v < nv; v += 1024) {
     const uint4 u = xv[v];
     TI e[VE];
     __builtin_memcpy(e, &u, 16);
 #pragma unroll
-    for (int k = 0; k < VE; ++k) argmax_take(best, bi, to_f(e[k]), head + v * VE + k);
+    for (int k = 0; k < VE; ++k) argmax_scan(best, b32, to_f(e[k]), hd + v * VE + k);
   }
-  if (tail0 + tid < cols) argmax_take(best, bi, to_f(xr[tail0 + tid]), tail0 + tid);
+  if (tail0 + tid < cols) argmax_scan(best, b32, to_f(xr[tail0 + tid]), (int)(tail0 + tid));
+  int64_t bi = b32;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     const float ob = __shfl_xor(best, m, 64);
@@ -1130,7 +1144,7 @@ void row_reduce(int op, DType in, DType out, const void* x, int64_t ldx, void* y
     AGPU_ALL_SWITCH(in, {
       if constexpr (std::is_same<T, int64_t>::value)
         fail("argmax over int64 is not supported");
-      else if (cols >= 4096)
+      else if (cols >= 4096 && cols < 0x7fffffffLL)
         hipLaunchKernelGGL((argmax_row_block<T>), dim3((unsigned)rows), dim3(1024), 0, s, (const T*)x, ldx,
                            (int32_t*)y, cols);
       else
