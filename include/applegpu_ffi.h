@@ -272,7 +272,12 @@ int32_t applegpu_ffi_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t batch, i
  * returns their number (or -1).  Replaces the aten kernels of the
  * PrivateUse1 shim that the reference runs through CPU fallback or several
  * eager calls (backend_cpp/applegpu_backend.cpp:753-764 masked ops,
- * :801-867 mse_loss, :943-951 softmax, :1055-1096 registrations). */
+ * :801-867 mse_loss, :943-951 softmax, :1055-1096 registrations).  The
+ * training-step ops sgd_matmul_ (w, a, b[, bias]), sgd_sum_rows_ (bias, g),
+ * linear_backward_sgd_ (w, b, g, a[, mask]) and linear_mse_backward_sgd_
+ * (h, w, b, y; iparams[0]: return the input gradient) update their
+ * parameters in place; fparams[0] is the step's alpha (-lr).  They run
+ * eagerly only (applegpu_graph_op refuses them). */
 int32_t applegpu_eager_op(const char* op, const uint64_t* inputs, uint32_t n_inputs,
                           const double* fparams, uint32_t n_f, const int64_t* iparams, uint32_t n_i,
                           uint64_t* out_ids, uint32_t max_out);
