@@ -246,6 +246,22 @@ struct GLoad {
       constexpr int TPR = BK / EPT;
       r = t / TPR;
       kk = (t % TPR) * EPT;
+      if constexpr (TPR == 2 && ROWS % 16 == 0 && BK % 16 == 0 && EPT <= 32) {
+        // Rows are permuted within groups of 16 so that a store phase of 16
+        // lanes (8 rows, two lanes each) hits every LDS bank once.  The LDS
+        // tiles hold 2-byte elements with a pitch of BK + 8, i.e. u = BK/8 + 1
+        // (odd) 16-byte chunks, and the two lanes of a row start c = EPT/8
+        // chunks apart.  With g = u*r mod 16, the 8 rows of a phase take the
+        // g whose bit log2(c) equals the phase, so their chunks g and g + c
+        // are 16 distinct ones.  Each lane pair still reads one whole row
+        // segment from global memory.
+        constexpr int u = BK / 8 + 1, c = EPT / 8;
+        constexpr int lc = c == 1 ? 0 : c == 2 ? 1 : 2;
+        constexpr int uinv = (u * u * u) & 15;  // u^4 = 1 mod 16 for odd u
+        const int q = r & 15;
+        const int g = (q & (c - 1)) | (((q >> 3) & 1) << lc) | ((q & 7 & ~(c - 1)) << 1);
+        r = (r & ~15) | ((uinv * g) & 15);
+      }
     } else {
       r = (t / KQ) * VW;
       kk = (t % KQ) * KP;
