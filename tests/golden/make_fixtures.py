@@ -113,6 +113,20 @@ def main():
     qv = torch.round(w / scale[:, None]).clamp(-128, 127)
     qv[3] = 0  # zero row: 0/0 in the fp32 expression; codes are 0 by convention
     fx["quant_w"], fx["quant_scale"], fx["quant_q"] = w.numpy(), scale.numpy(), qv.to(torch.int8).numpy()
+    # dequantize, two independent torch routes: fp32 arithmetic on the codes,
+    # and torch's own per-channel quantized tensor (axis 0, zero points 0)
+    q8 = qv.to(torch.int8)
+    fx["quant_deq"] = (q8.to(torch.float32) * scale[:, None]).numpy()
+    fx["quant_deq_qtensor"] = torch._make_per_channel_quantized_tensor(
+        q8, scale.double(), torch.zeros(q8.shape[0], dtype=torch.long), 0).dequantize().numpy()
+    # per-tensor dequantize (q - zp) * scale with nonzero zero points, int8 and
+    # uint8 codes (torch's per-tensor quantized tensor; no RNG drawn here)
+    codes8 = torch.arange(-128, 128, dtype=torch.int16).to(torch.int8)
+    codes_u8 = torch.arange(0, 256, dtype=torch.int16).to(torch.uint8)
+    fx["dq_pt_i8_q"] = codes8.numpy()
+    fx["dq_pt_i8_y"] = torch._make_per_tensor_quantized_tensor(codes8, 0.1, -3).dequantize().numpy()
+    fx["dq_pt_u8_q"] = codes_u8.numpy()
+    fx["dq_pt_u8_y"] = torch._make_per_tensor_quantized_tensor(codes_u8, 0.05, 7).dequantize().numpy()
     # embedding
     ew = torch.randn(50, 16)
     ei = torch.randint(0, 50, (11,), dtype=torch.int32)

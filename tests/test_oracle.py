@@ -134,9 +134,22 @@ def test_quantize_per_row_vs_torch(fixtures):
     # ties round half to even: codes of the planted .5 multiples
     assert s[5] == np.float32(2.0 ** -10)
     assert q[5, :5].tolist() == [127, 0, 0, 2, -2]
-    # dequantize: q * scale, exact products
-    d = O.dequantize_per_row(q, s)
-    np.testing.assert_array_equal(d, q.astype(np.float32) * s[:, None])
+    # dequantize against torch, two routes: fp32 arithmetic on torch's codes
+    # and torch's per-channel quantized tensor (bit-exact; the products are
+    # exact in fp32 up to one rounding)
+    d = O.dequantize_per_row(fixtures["quant_q"], fixtures["quant_scale"])
+    np.testing.assert_array_equal(d, fixtures["quant_deq"])
+    np.testing.assert_array_equal(d, fixtures["quant_deq_qtensor"])
+    # round trip: every value within half a step of its row's scale
+    w = fixtures["quant_w"]
+    assert np.all(np.abs(O.dequantize_per_row(q, s) - w) <= s[:, None] * 0.5000001)
+
+
+def test_dequantize_per_tensor_vs_torch(fixtures):
+    # (q - zp) * scale (kernel_templates.rs:2222-2240) against torch's
+    # per-tensor quantized tensors, every int8 and uint8 code
+    np.testing.assert_array_equal(O.dequantize_per_tensor(fixtures["dq_pt_i8_q"], 0.1, -3), fixtures["dq_pt_i8_y"])
+    np.testing.assert_array_equal(O.dequantize_per_tensor(fixtures["dq_pt_u8_q"], 0.05, 7), fixtures["dq_pt_u8_y"])
 
 
 def test_quantize_per_tensor_half_away():
@@ -311,7 +324,7 @@ def test_backward_ops_vs_torch_autograd():
     assert (O.embedding_backward(dy, idx, 60)[50:] == 0).all()
 
 
-def test_oracle_catches_planted_mistakes():
+def test_oracle_catches_planted_mistakes(fixtures):
     """The checks above fail on the typical slips (planted in copies, on the CPU)."""
     x = np.random.default_rng(0).standard_normal((4, 9)).astype(np.float32)
     # causal mask off by one (j < i instead of j <= i) breaks row 0
@@ -326,3 +339,13 @@ def test_oracle_catches_planted_mistakes():
     # round-half-away instead of half-even changes the planted ties
     assert O.quantize_per_tensor(np.array([2.5], np.float32), 1.0).tolist() == [3]
     assert np.rint(np.float32(2.5)) == 2.0
+    # dequantize slips: the zero point added instead of subtracted, or the
+    # scale taken per column, differ from torch's per-tensor / per-channel
+    # dequantized values
+    fx = fixtures
+    q8 = fx["dq_pt_i8_q"]
+    wrong_zp = ((q8.astype(np.int32) + (-3)).astype(np.float32) * np.float32(0.1))
+    assert not np.array_equal(wrong_zp, fx["dq_pt_i8_y"])
+    qr, sr = fx["quant_q"], fx["quant_scale"]
+    wrong_axis = qr.astype(np.float32) * np.resize(sr, qr.shape[1])[None, :]
+    assert not np.array_equal(wrong_axis, fx["quant_deq"])
