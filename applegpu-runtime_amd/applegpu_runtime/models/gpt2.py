@@ -449,3 +449,104 @@ def generate_greedy(model: dict, prompt_ids, n_steps: int, cache: KVCache = None
     if keep_logits:
         return toks, np.stack(kept)
     return toks
+
+
+class Generation:
+    """Greedy generation for B prompts of T ids as config C4 runs it: the
+    prefill and one decode step are each captured once as a HIP graph
+    (capture=True) over device-resident ids, positions, cache lengths and
+    tokens, so a generation is one prefill replay and `n_steps` decode
+    replays with no host work between them.  The picked tokens land in
+    `out` [n_steps + 1, B] on the device.  With capture=False the same calls
+    run op by op (the same kernels, launched one at a time).
+
+    The steps follow the reference's generate loop
+    (python/applegpu_runtime/models/generate.py:110-119: gpt2_forward over the
+    prompt, argmax of the last position, then one token per step against the
+    KV cache, python/applegpu_runtime/models/gpt2.py:84-178) for B sequences
+    at once."""
+
+    def __init__(self, model: dict, prompt_ids, n_steps: int, capture: bool = True):
+        prompt = np.asarray(prompt_ids, dtype=np.int32)
+        if prompt.ndim != 2:
+            raise ValueError("prompt_ids must be [batch, length]")
+        B, T = prompt.shape
+        self.model, self.B, self.T, self.n_steps = model, B, T, n_steps
+        self.cache = KVCache(model["config"], B, T + n_steps, model.get("dtype", "float16"))
+        self.ids = gpu.from_numpy(prompt)
+        self.positions = gpu.from_numpy(np.tile(np.arange(T, dtype=np.int32), B))
+        self._zeros = gpu.from_numpy(np.zeros(B, np.int32))
+        self._prompt_len = gpu.from_numpy(np.full(B, T, np.int32))
+        self.tokens = gpu.zeros([B], "int32")
+        self.out = gpu.zeros([n_steps + 1, B], "int32")
+        self._slots = [gpu.slice(self.out, 0, s, s + 1) for s in range(n_steps + 1)]
+        self.graphs = None
+        if capture:
+            self.graphs = (gpu.capture(self._prefill), gpu.capture(self._step) if n_steps > 0 else None)
+
+    def _prefill(self):
+        gpu.blit_copy(self._zeros, self.cache.pos)
+        logits, nxt = gpt2_prefill(self.model, self.ids, self.cache, positions=self.positions)
+        gpu.blit_copy(nxt, self.tokens)
+        gpu.blit_copy(self._prompt_len, self.cache.pos)
+        return logits
+
+    def _step(self):
+        logits, nxt, lens = gpt2_decode_step(self.model, self.tokens, self.cache)
+        gpu.blit_copy(nxt, self.tokens)
+        gpu.blit_copy(lens, self.cache.pos)
+        return logits
+
+    def prefill(self):
+        """Runs the prefill; returns its logits [B*T, vocab] (device) and
+        stores the first pick in out[0]."""
+        if self.graphs is not None:
+            self.graphs[0].replay()
+            logits = self.graphs[0].outputs
+        else:
+            logits = self._prefill()
+            logits.eval()
+        gpu.blit_copy(self.tokens, self._slots[0])
+        return logits
+
+    def step(self, s: int):
+        """Runs decode step s (0-based; input token out[s]); returns its
+        logits [B, vocab] (device) and stores the pick in out[s + 1]."""
+        if not 0 <= s < self.n_steps:
+            raise ValueError(f"decode step {s} outside 0..{self.n_steps - 1}")
+        if self.graphs is not None:
+            self.graphs[1].replay()
+            logits = self.graphs[1].outputs
+        else:
+            logits = self._step()
+            logits.eval()
+        gpu.blit_copy(self.tokens, self._slots[s + 1])
+        return logits
+
+    def last_logits(self, prefill_logits):
+        """The prefill logits at each prompt's last position, [B, vocab]."""
+        V = prefill_logits.shape[-1]
+        return gpu.reshape(gpu.slice(gpu.reshape(prefill_logits, [self.B, self.T, V]), 1, self.T - 1, self.T),
+                           [self.B, V])
+
+    def run(self, keep_logits: bool = False):
+        """One whole generation.  Returns the tokens [B, n_steps + 1] (numpy),
+        and with keep_logits the logits of every pick, [n_steps + 1, B, vocab]
+        (numpy; copying them out synchronises after every step)."""
+        kept = []
+        lg = self.prefill()
+        if keep_logits:
+            kept.append(self.last_logits(lg).to_numpy())
+        for s in range(self.n_steps):
+            lg = self.step(s)
+            if keep_logits:
+                kept.append(lg.to_numpy())
+        toks = self.out.to_numpy().T.copy()
+        return (toks, np.stack(kept)) if keep_logits else toks
+
+    def destroy(self):
+        if self.graphs is not None:
+            for g in self.graphs:
+                if g is not None:
+                    g.destroy()
+            self.graphs = None

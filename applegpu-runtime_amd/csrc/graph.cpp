@@ -760,6 +760,12 @@ void eval_all(const std::vector<TensorP>& roots) {
     }
   }
 
+  // The read-ahead ranges are raw pointers into this walk's weights: clear
+  // them when the walk ends, also when an op throws part way, so that no
+  // later launch reads ahead from memory that may have been freed since.
+  struct PrefetchClear {
+    ~PrefetchClear() { k::set_prefetch(k::Prefetch{}); }
+  } clear_prefetch;
   for (size_t i = 0; i < order.size(); ++i) {
     TensorP t = order[i];
     // Absorbed into a fused GEMM, or already filled by its multi-output
@@ -919,7 +925,6 @@ void eval_all(const std::vector<TensorP>& roots) {
     assign(t, res[0]);
     order[i].reset();
   }
-  k::set_prefetch(k::Prefetch{});
 }
 
 }  // namespace agpu

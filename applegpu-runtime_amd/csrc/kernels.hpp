@@ -216,6 +216,9 @@ struct Gemm {
   int rs_tiles = 0;
   int64_t rs_n = 0;
   float rs_eps = 1e-5f;
+  // the most workspace the caller can provide: a plan that would need more
+  // (the outer-product plan's packed operands) is not taken
+  size_t max_ws = SIZE_MAX;
 };
 // fp32 weights packed for the bf16x3 MFMA GEMM of few-row activations
 // (gemm_x3p.hip): B(k, n) read through strides (b_sk, b_sn) is split into

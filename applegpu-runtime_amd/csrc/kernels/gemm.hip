@@ -786,10 +786,12 @@ bool gemm_x3_panel_ok(int64_t M, int64_t N, int64_t K, bool apk) {
 }
 
 // The outer-product plan (gemm_x3p.hip) for fp32 products it fits, unless a
-// tile configuration, a split count or the native fp32 kernels are forced.
+// tile configuration, a split count or the native fp32 kernels are forced,
+// or its packed operands need more workspace than the caller can give.
 static bool use_outer(const Gemm& g) {
   const GemmTune& tu = gemm_tune();
-  return tu.cfg < 0 && tu.splits == 0 && tu.f32_mode != kF32Native && gemm_x3_outer_ok(g);
+  return tu.cfg < 0 && tu.splits == 0 && tu.f32_mode != kF32Native && gemm_x3_outer_ok(g) &&
+         gemm_x3_outer_workspace(g) <= g.max_ws;
 }
 
 // The 16-bit large-tile plan (gemm_h16.hip), unless a configuration or a

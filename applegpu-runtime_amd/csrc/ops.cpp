@@ -1132,6 +1132,9 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
       }
     }
   }
+  // the allocation-free form: plans whose workspace would not fit the
+  // static scratch (the outer-product plan's packed operands) are skipped
+  if (no_alloc) g.max_ws = no_alloc->cap;
   size_t wsb = meta_mode() ? 0 : k::gemm_workspace_bytes(g);
   if (no_alloc) {
     if (wsb > no_alloc->cap)

@@ -202,7 +202,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-s", type=float, default=15.0)
+    ap.add_argument("--cpu-sample-s", type=float, default=15.0,
+                    help="time budget of the bounded C4 CPU-baseline sample")
     ap.add_argument("--suite", action="store_true",
                     help="instead of the headline line, print one JSON line per hot-path kernel "
                          "(cache-busting working sets, roofline fractions)")
@@ -225,10 +226,16 @@ def main():
     ap.add_argument("--c2-replays", type=int, default=0,
                     help="instead of the headline line, capture the C2 forward and replay it this many times "
                          "(nothing else runs: a per-forward kernel trace of exactly the timed graph)")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="print the C2 + C3 headline line without the c1, c4 and c5 sub-records")
     ap.add_argument("--c3-replays", type=int, default=0,
                     help="instead of the headline line, capture the C3 MLP train step and replay it this many "
                          "times (a per-step kernel trace of exactly the timed graph)")
     args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is designed, not built).", file=sys.stderr)
+        sys.exit(2)
     if args.c2_replays > 0:
         c2_replays(args.c2_replays)
         return
@@ -239,18 +246,14 @@ def main():
         kernel_suite(args.only)
         return
     if args.c4:
-        c4_generate(args)
+        print(json.dumps(c4_generate(args)), flush=True)
         return
     if args.c1:
-        c1_train(args)
+        print(json.dumps(c1_train(args)), flush=True)
         return
     if args.c5:
-        c5_pipeline(args)
+        print(json.dumps(c5_pipeline(args)), flush=True)
         return
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is designed, not built).", file=sys.stderr)
-        sys.exit(2)
 
     import applegpu_runtime as gpu
     from applegpu_runtime import eager as E
@@ -260,6 +263,12 @@ def main():
 
     gpu.init_backend()
     dev = gpu.device_name()
+    if not args.headline_only:
+        # the c1 sub-record runs torch autograd on the PrivateUse1 device, whose
+        # engine sizes its device queues the first time autograd runs: register
+        # the device before the CPU baselines use autograd
+        from applegpu_runtime.cpp_backend import load_cpp_backend
+        load_cpp_backend()
 
     # ── inputs resident in HBM ──────────────────────────────────────────────
     wnp = G.random_weights(GPT2_CFG, seed=42)
@@ -435,9 +444,17 @@ def main():
         },
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wnp, params, ids, xnp, ynp, args.cpu_sample_s)
+        print("bench: headline CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(wnp, params, ids, xnp, ynp)
     g_fwd.destroy()
     g_train.destroy()
+    if not args.headline_only:
+        # the other configs of BASELINE.json, each with its own roofline and
+        # CPU baseline, as sub-records of the one line
+        del model, mlp
+        for name, fn in (("c5", c5_pipeline), ("c4", c4_generate), ("c1", c1_train)):
+            print(f"bench: {name}", file=sys.stderr, flush=True)
+            result[name] = fn(args)
     print(json.dumps(result), flush=True)
 
 
@@ -651,61 +668,30 @@ def c4_generate(args):
     gpu.init_backend()
     cfg = G.GPT2_CONFIGS["gpt2-large"]
     B, T, n = C4_B, C4_T, args.c4_steps
+    print("c4: drawing and loading GPT-2 large fp16 weights", file=sys.stderr, flush=True)
     wnp = G.random_weights(cfg, seed=42)
     model = G.load_model(wnp, cfg, dtype="float16")
     ids = np.random.default_rng(42).integers(0, cfg["vocab_size"], (B, T)).astype(np.int32)
-    ids_dev = gpu.from_numpy(ids)
-    pos_dev = gpu.from_numpy(np.tile(np.arange(T, dtype=np.int32), B))
-    cache = G.KVCache(cfg, B, T + n, "float16")
-    zeros_b = gpu.from_numpy(np.zeros(B, np.int32))
-    t_b = gpu.from_numpy(np.full(B, T, np.int32))
-    tokens = gpu.zeros([B], "int32")
-    out = gpu.zeros([n + 1, B], "int32")
-    print(f"c4: model and cache resident ({cache.nbytes() / 1e9:.2f} GB cache)", file=sys.stderr, flush=True)
-
-    def prefill():
-        gpu.blit_copy(zeros_b, cache.pos)
-        lg, nxt = G.gpt2_prefill(model, ids_dev, cache, positions=pos_dev)
-        gpu.blit_copy(nxt, tokens)
-        gpu.blit_copy(t_b, cache.pos)
-        return lg
-
-    def step():
-        lg, nx, lens = G.gpt2_decode_step(model, tokens, cache)
-        gpu.blit_copy(nx, tokens)
-        gpu.blit_copy(lens, cache.pos)
-        return lg
+    gen = G.Generation(model, ids, n, capture=not args.c4_eager)
+    print(f"c4: model and cache resident ({gen.cache.nbytes() / 1e9:.2f} GB cache)", file=sys.stderr, flush=True)
 
     # eager (op-by-op) timings for comparison: one prefill, a few steps
     lib.applegpu_ffi_synchronize()
     t0 = time.perf_counter()
-    prefill().eval()
+    gen._prefill().eval()
     lib.applegpu_ffi_synchronize()
     prefill_eager_ms = 1e3 * (time.perf_counter() - t0)
     n_eager = min(8, n)
     t0 = time.perf_counter()
     for _ in range(n_eager):
-        step().eval()
+        gen._step().eval()
     lib.applegpu_ffi_synchronize()
     step_eager_ms = 1e3 * (time.perf_counter() - t0) / n_eager
 
-    if args.c4_eager:
-        # the same kernels issued op by op (for kernel traces of the step)
-        g_pre = g_step = None
-        run_pre = lambda: prefill().eval()  # noqa: E731
-        run_step = lambda: step().eval()  # noqa: E731
-    else:
-        g_pre = gpu.capture(prefill)
-        g_step = gpu.capture(step)
-        run_pre, run_step = g_pre.replay, g_step.replay
-    slots = [gpu.slice(out, 0, s, s + 1) for s in range(n + 1)]
-
     def generation():
-        run_pre()
-        gpu.blit_copy(tokens, slots[0])
+        gen.prefill()
         for s in range(n):
-            run_step()
-            gpu.blit_copy(tokens, slots[s + 1])
+            gen.step(s)
 
     for _ in range(args.warmup if args.warmup > 0 else 1):
         generation()
@@ -715,12 +701,10 @@ def c4_generate(args):
     t0 = time.perf_counter()
     for _ in range(reps):
         lib.applegpu_ffi_event_record(0)
-        run_pre()
-        gpu.blit_copy(tokens, slots[0])
+        gen.prefill()
         lib.applegpu_ffi_event_record(1)
         for s in range(n):
-            run_step()
-            gpu.blit_copy(tokens, slots[s + 1])
+            gen.step(s)
         lib.applegpu_ffi_event_record(2)
         pre_ms += lib.applegpu_ffi_event_elapsed_ms(0, 1)
         dec_ms += lib.applegpu_ffi_event_elapsed_ms(1, 2)
@@ -728,7 +712,7 @@ def c4_generate(args):
     wall_ms = 1e3 * (time.perf_counter() - t0) / reps
     pre_ms /= reps
     dec_ms /= reps
-    toks = out.to_numpy().T
+    toks = gen.out.to_numpy().T
     if not ((toks >= 0) & (toks < cfg["vocab_size"])).all():
         raise RuntimeError("generated ids out of range")
 
@@ -764,7 +748,7 @@ def c4_generate(args):
             "prefill_mfma_frac": round(pre_flop / (pre_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
             "prefill_eager_ms": round(prefill_eager_ms, 3),
             "decode_step_eager_ms": round(step_eager_ms, 4),
-            "kv_cache_gb": round(cache.nbytes() / 1e9, 3),
+            "kv_cache_gb": round(gen.cache.nbytes() / 1e9, 3),
             "launch_mode": "op-by-op" if args.c4_eager else "graph replay",
             "reps": reps,
         },
@@ -781,11 +765,10 @@ def c4_generate(args):
         },
     }
     if not args.no_cpu_baseline:
+        print("c4: CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = c4_cpu_baseline(wnp, cfg, ids, args.cpu_sample_s)
-    if g_pre is not None:
-        g_pre.destroy()
-        g_step.destroy()
-    print(json.dumps(result), flush=True)
+    gen.destroy()
+    return result
 
 
 def c4_cpu_baseline(wnp, cfg, ids, budget_s):
@@ -972,15 +955,15 @@ def c1_train(args):
             cpu_step()
             times.append(time.perf_counter() - t0)
         result["cpu_baseline"] = {
-            "value": round(1e3 * float(np.mean(times)), 5),
+            "value": round(1e3 * float(np.median(times)), 5),
             "unit": "ms",
             "cores": torch.get_num_threads(),
             "kind": "port",
             "host": host_info(),
             "sample": f"torch {torch.__version__} CPU eager, 5 warm-up + 50 timed steps (python/tests/"
-                      f"bench_comparison.py:23-38); median {1e3 * float(np.median(times)):.4f} ms",
+                      f"bench_comparison.py:23-38), median; mean {1e3 * float(np.mean(times)):.4f} ms",
         }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def c5_pipeline(args):
@@ -1113,7 +1096,7 @@ def c5_pipeline(args):
                       f"stage after one warm-up: scale {sc_ms:.1f} ms, quantize {qc_ms:.1f} ms, dequantize "
                       f"{dc_ms:.1f} ms, GEMM {gc_ms:.1f} ms",
         }
-    print(json.dumps(result), flush=True)
+    return result
 
 
 def host_info():
@@ -1140,36 +1123,41 @@ def host_info():
     return info
 
 
-def cpu_baseline(wnp, params, ids, xnp, ynp, budget_s):
-    """The reference's CPU path (PyTorch CPU eager) on a bounded sample of the
-    same workload: GPT-2 forwards and MLP steps alternate until ~budget_s."""
+def cpu_baseline(wnp, params, ids, xnp, ynp):
+    """The reference's CPU path (PyTorch CPU eager) on the same workload, as
+    its benchmarks time it: GPT-2 forward under no_grad, 3 warm-up + 20
+    timed forwards, median; MLP train step, 5 warm-up + 50 timed steps
+    (python/tests/bench_comparison.py:23-38), median (the mean is reported
+    beside it).  value = the two medians' sum."""
     import torch
     from oracle.torch_cpu import TorchGPT2, TorchMLP
     g = TorchGPT2(wnp, GPT2_CFG)
     m = TorchMLP(params, lr=0.01)
     tx, ty = torch.from_numpy(xnp), torch.from_numpy(ynp)
-    g.forward(ids)
-    m.step(tx, ty)
-    tg = tm = 0.0
-    n = 0
-    start = time.perf_counter()
-    while n < 2 or (time.perf_counter() - start < budget_s and n < 50):
-        t0 = time.perf_counter()
-        g.forward(ids)
-        t1 = time.perf_counter()
-        m.step(tx, ty)
-        t2 = time.perf_counter()
-        tg += t1 - t0
-        tm += t2 - t1
-        n += 1
+
+    def times(fn, warm, n):
+        for _ in range(warm):
+            fn()
+        out = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            out.append(time.perf_counter() - t0)
+        return np.array(out) * 1e3
+
+    tg = times(lambda: g.forward(ids), 3, 20)
+    tm = times(lambda: m.step(tx, ty), 5, 50)
     return {
-        "value": round(1e3 * (tg + tm) / n, 3),
+        "value": round(float(np.median(tg) + np.median(tm)), 3),
         "unit": "ms",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "host": host_info(),
-        "sample": f"{n} x (GPT-2 small fwd seq128 + MLP 4096 train step), torch {torch.__version__} CPU eager; "
-                  f"gpt2 {1e3 * tg / n:.1f} ms, mlp {1e3 * tm / n:.1f} ms; host cpus {os.cpu_count()}",
+        "gpt2_fwd_ms_median": round(float(np.median(tg)), 3),
+        "mlp_train_ms_median": round(float(np.median(tm)), 3),
+        "sample": f"torch {torch.__version__} CPU eager: GPT-2 small fwd seq128 under no_grad, 3 warm-up + 20 "
+                  f"timed, median {np.median(tg):.1f} ms (mean {tg.mean():.1f}); MLP 4096 train step, 5 warm-up + "
+                  f"50 timed, median {np.median(tm):.1f} ms (mean {tm.mean():.1f}); host cpus {os.cpu_count()}",
     }
 
 

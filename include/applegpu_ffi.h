@@ -313,15 +313,20 @@ uint8_t* applegpu_eager_linear(uint64_t x_id, uint64_t w_id, uint64_t bias_id, i
 /* Allocation-free linear: no counterpart in the reference.  For callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc): out = act(x W^T + b) as
- * applegpu_eager_linear computes it (same kernels, same results), written
+ * applegpu_eager_linear computes it (the same kernels and results wherever
+ * the same plan fits, see below), written
  * into the caller's contiguous [M, N] tensor `out_id` of x's dtype.  x [M, K],
  * weight [N, K] and the optional contiguous bias [N] (bias_id 0 = none) must
  * already hold values, and out may not share storage with them.  The GEMM's
  * split-K partial sums go to a static 64 MiB device array that each GPU the
- * library runs on holds until the process ends; a product whose partials
- * would exceed it (only reachable through a forced applegpu_ffi_gemm_tune
- * split count: the planner's own choices stay below it) is rejected with an
- * error.  Every call on one GPU shares
+ * library runs on holds until the process ends.  A product whose default
+ * plan packs its operands into more workspace than that (the fp32
+ * outer-product plan, (M + N) K 4 bytes) takes a plan that fits instead
+ * (results then agree with applegpu_eager_linear to the fp32 GEMM bar, not
+ * bit for bit); one whose split-K partials would exceed it (only reachable
+ * through a forced applegpu_ffi_gemm_tune split count: the planner's own
+ * split choices stay below it) is rejected with an error.  Every call on one
+ * GPU shares
  * that array and it keeps the last call's partials; calls are ordered on
  * the library's one stream, but work that overlaps them on one GPU from
  * another stream would race on it.  Nothing in it needs to start at zero:

@@ -26,14 +26,31 @@ GPT2_SMALL = dict(n_layer=12, n_head=12, n_embd=768, vocab_size=50257, n_positio
 GPT2_LARGE = dict(n_layer=36, n_head=20, n_embd=1280, vocab_size=50257, n_positions=1024)
 
 
+def _perturb_norms_and_biases(w, seed=7):
+    """Non-identity layer norms and nonzero biases (gamma = 1 + N(0, 0.1),
+    beta and every bias N(0, 0.02)), so that the folds of ln_1 / ln_2 into the
+    GEMMs (gamma into the weights, beta @ W into the bias, column sums) are
+    exercised with every term nonzero."""
+    rng = np.random.default_rng(seed)
+    for k, v in w.items():
+        if ".ln_" in k or k.startswith("transformer.ln_f"):
+            if k.endswith(".weight"):
+                w[k] = (1.0 + 0.1 * rng.standard_normal(v.shape)).astype(np.float32)
+            else:
+                w[k] = (0.02 * rng.standard_normal(v.shape)).astype(np.float32)
+        elif k.endswith(".bias"):
+            w[k] = (0.02 * rng.standard_normal(v.shape)).astype(np.float32)
+    return w
+
+
 def test_captured_c2_forward_full_size_vs_oracle(gpu):
     """The C2 graph with unpacked fp32 weights (the tiled split-K GEMMs and
     qkv_attention): every replay at the fp32 matmul/attention bar (1e-3
     normwise, checked at 1e-4), replays bitwise identical to each other with
     eager work between them, greedy picks equal to the oracle's."""
     from applegpu_runtime.models import gpt2 as G
-    print("C2 captured forward: 12x768, seq 128, unpacked weights", flush=True)
-    wnp = G.random_weights(GPT2_SMALL, seed=42)
+    print("C2 captured forward: 12x768, seq 128, unpacked weights, perturbed norms and biases", flush=True)
+    wnp = _perturb_norms_and_biases(G.random_weights(GPT2_SMALL, seed=42))
     model = G.load_model(wnp, GPT2_SMALL, x3=False)
     ids = np.random.default_rng(42).integers(0, GPT2_SMALL["vocab_size"], 128).astype(np.int32)
     _check_c2_graph(gpu, G, model, wnp, ids)
@@ -43,10 +60,11 @@ def test_captured_c2_forward_packed_weights_vs_oracle(gpu):
     """bench.py's C2 graph: the fp32 projection weights packed as bf16 hi/lo
     fragments (load_model's default), activations passed as packed rows
     written by the embedding, the layer_norm reductions and the fc epilogue,
-    the packed-A row panels and split GEMMs."""
+    the packed-A row panels and split GEMMs, ln_2 folded into c_fc; layer
+    norms and biases perturbed away from identity and zero."""
     from applegpu_runtime.models import gpt2 as G
-    print("C2 captured forward, packed fp32 weights and rows", flush=True)
-    wnp = G.random_weights(GPT2_SMALL, seed=42)
+    print("C2 captured forward, packed fp32 weights and rows, perturbed norms and biases", flush=True)
+    wnp = _perturb_norms_and_biases(G.random_weights(GPT2_SMALL, seed=42))
     model = G.load_model(wnp, GPT2_SMALL)
     assert model["x3"]
     ids = np.random.default_rng(42).integers(0, GPT2_SMALL["vocab_size"], 128).astype(np.int32)
@@ -170,3 +188,59 @@ def test_gpt2_large_full_dims_generation_teacher_forced(gpu):
             top2 = np.sort(ref_steps[s])[-2:]
             if top2[1] - top2[0] > tol * np.abs(ref_steps[s]).max():
                 assert toks[b, s] == int(np.argmax(ref_steps[s])), (b, s)
+
+
+def test_c4_generation_full_size_captured_vs_eager_and_teacher_forced(gpu):
+    """Config C4 exactly as bench.py times it (models.gpt2.Generation):
+    GPT-2 large fp16, 8 prompts of 512 random ids, the prefill and the decode
+    step captured as HIP graphs, 128 greedy steps over the preallocated cache
+    (contexts 513..640).  The captured generation's tokens and logits equal an
+    op-by-op run of the same calls bit for bit; for two sequences every pick's
+    logits (the prompt's last position, then decode steps 0..127) are checked,
+    teacher-forced, against the reference's CPU path (torch CPU eager fp32 on
+    the fp16-rounded weights, oracle/torch_cpu.py, itself pinned against the
+    numpy oracle) at the fp16 bar (1e-2)."""
+    import torch
+    from applegpu_runtime.models import gpt2 as G
+    from oracle.torch_cpu import TorchGPT2
+    B, T, n = 8, 512, 128
+    print(f"C4 full size: GPT-2 large fp16, B={B}, T={T}, {n} captured decode steps", flush=True)
+    w = G.random_weights(GPT2_LARGE, seed=42)
+    model = G.load_model(w, GPT2_LARGE, dtype="float16")
+    ids = np.random.default_rng(42).integers(0, GPT2_LARGE["vocab_size"], (B, T)).astype(np.int32)
+    gen = G.Generation(model, ids, n, capture=True)
+    try:
+        toks, logits = gen.run(keep_logits=True)
+    finally:
+        gen.destroy()
+    del gen
+    print("  captured generation done", flush=True)
+    gen_e = G.Generation(model, ids, n, capture=False)
+    toks_e, logits_e = gen_e.run(keep_logits=True)
+    del gen_e, model
+    print("  op-by-op generation done", flush=True)
+    assert toks.shape == (B, n + 1) and logits.shape == (n + 1, B, GPT2_LARGE["vocab_size"])
+    np.testing.assert_array_equal(toks, toks_e)
+    np.testing.assert_array_equal(logits, logits_e)
+    # every pick is the first maximum of its own logits
+    np.testing.assert_array_equal(toks, logits.astype(np.float32).argmax(-1).T)
+
+    for k in list(w):
+        w[k] = w[k].astype(np.float16).astype(np.float32)
+    ref_model = TorchGPT2(w, GPT2_LARGE)
+    tol = 1e-2
+    with torch.no_grad():
+        for b in (0, 5):
+            seq = np.concatenate([ids[b], toks[b, :-1]])            # 640 ids
+            ref = ref_model.forward(seq).numpy()[T - 1:T + n]     # the 129 picks' positions
+            got = logits[:, b].astype(np.float32)
+            errs = [rel_err(got[s], ref[s]) for s in range(n + 1)]
+            print(f"  sequence {b}: rel err prompt-last {errs[0]:.2e}, step 0 {errs[1]:.2e}, "
+                  f"step 63 {errs[64]:.2e}, step 127 {errs[128]:.2e}, max {max(errs):.2e}", flush=True)
+            for s in (0, 1, 64, 128):
+                assert errs[s] < tol, (b, s, errs[s])
+            assert max(errs) < tol, (b, int(np.argmax(errs)), max(errs))
+            for s in range(n + 1):
+                top2 = np.sort(ref[s])[-2:]
+                if top2[1] - top2[0] > tol * np.abs(ref[s]).max():
+                    assert toks[b, s] == int(np.argmax(ref[s])), (b, s)

@@ -1,7 +1,8 @@
 """The allocation-free linear entry point against the allocating one, through
 the C ABI: the same kernels on the same inputs give the same bits.  Two
 calls in a row (the second smaller) share the static scratch array; a
-product whose split-K partials would not fit in it is rejected."""
+product whose split-K partials would not fit in it is rejected, and one whose
+default plan's packed operands would not fit takes a plan that does."""
 import ctypes
 from ctypes import c_uint64
 
@@ -71,6 +72,34 @@ def test_noalloc_matches_linear_two_calls(lib, first, second):
         got, want = _case(lib, M, K, N, act, bias)
         np.testing.assert_array_equal(got, want)
         assert np.isfinite(got).all()
+
+
+def test_noalloc_outer_shaped_product_takes_a_plan_that_fits(lib):
+    """x [32768, 512] @ w [1024, 512]^T: the allocating linear takes the
+    outer-product plan, whose packed operands ((M + N) K fp32 = 69 MB) would
+    not fit the 64 MiB scratch; the allocation-free call takes a plan that
+    fits and agrees with it (and with float64) at the fp32 GEMM bar.  Run
+    twice, the second call smaller, as the other cases."""
+    assert _plan(lib, 32768, 1024, 512).startswith("x3 outer")
+    for M, K, N in ((32768, 512, 1024), (4096, 512, 512)):
+        print(f"noalloc linear, outer-shaped: M={M} K={K} N={N}", flush=True)
+        xa = RNG.standard_normal((M, K)).astype(np.float32)
+        wa = (RNG.standard_normal((N, K)) * 0.05).astype(np.float32)
+        ba = RNG.standard_normal(N).astype(np.float32)
+        x, w, b = _alloc(lib, (M, K), xa), _alloc(lib, (N, K), wa), _alloc(lib, (N,), ba)
+        want_id = c_uint64()
+        assert lib.applegpu_eager_linear(x, w, b, 1, ctypes.byref(want_id)), lib.applegpu_eager_last_error()
+        out = _alloc(lib, (M, N))
+        rc = lib.applegpu_eager_linear_noalloc(x, w, b, 1, out)
+        assert rc == 0, lib.applegpu_eager_last_error()
+        lib.applegpu_eager_flush_and_wait()
+        got, want = _read(lib, out, (M, N)), _read(lib, want_id.value, (M, N))
+        ref = np.maximum(xa.astype(np.float64) @ wa.astype(np.float64).T + ba, 0)
+        scale = np.abs(ref).max()
+        assert np.abs(got - ref).max() / scale < 1e-4
+        assert np.abs(got - want).max() / scale < 1e-4
+        for t in (x, w, b, out, want_id.value):
+            lib.applegpu_eager_free(t)
 
 
 def test_noalloc_rejects_oversized_workspace_and_bad_operands(lib):
