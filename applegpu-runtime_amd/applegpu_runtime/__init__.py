@@ -601,6 +601,18 @@ def row_stats_x3(x):
     return _op(b"row_stats_x3", [_t(x)])
 
 
+def x3_rows_out_ok(rows, out_features, in_features) -> bool:
+    """Whether packed rows [rows, in_features] times packed fp32 weights
+    [in_features, out_features] run a plan whose one launch writes the
+    output, its packed rows and its row statistics (an unsplit row panel,
+    or a split one whose tiles are finished in the launch)."""
+    _check_init()
+    r = lib.applegpu_ffi_x3_rows_out(int(rows), int(out_features), int(in_features))
+    if r < 0:
+        raise ValueError(ffi_error())
+    return r == 1
+
+
 def matmul_pp_norm(packed_rows, stats, rows, packed, cs, out_features, eps=1e-5):
     """layer_norm(x) @ W without normalising x first: packed_rows =
     pack_rows_x3(x), stats = row_stats_x3(x), packed = pack_weight_x3(gamma[:,

@@ -112,6 +112,8 @@ _SIGS = {
     "applegpu_graph_bytes": (c_uint64, [c_int64]),
     "applegpu_ffi_gemm_tune": (c_int32, [c_int32, c_int32, c_int32]),
     "applegpu_ffi_gemm_skinny": (c_int32, [c_int32]),
+    "applegpu_ffi_split_inkernel": (c_int32, [c_int32]),
+    "applegpu_ffi_x3_rows_out": (c_int32, [c_int64, c_int64, c_int64]),
     "applegpu_ffi_gemm_plan": (c_int32, [c_int64, c_int64, c_int64, c_int64, c_int8, c_bool, c_bool, c_char_p,
                                          c_uint32]),
     "applegpu_ffi_event_record": (c_int32, [c_uint32]),

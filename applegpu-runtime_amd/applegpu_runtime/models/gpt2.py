@@ -112,7 +112,7 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
                 p = gpu.pack_weight(t)
                 p.eval()
                 pk[k] = (p, t.shape[0], "rows16")
-    fold = {}
+    fold, fold1 = {}, {}
     if x3:
         for k, t in w.items():
             if k.endswith(CONV1D):
@@ -126,27 +126,40 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
         pk["transformer.wte.weight"] = (p, wte.shape[0], "x3")
         if cfg["n_embd"] in _FOLD_WIDTHS:
             for i in range(cfg["n_layer"]):
-                fold[i] = _fold_ln2(np_weights, f"transformer.h.{i}")
+                fold[i] = _fold_ln(np_weights, f"transformer.h.{i}", "ln_2", "mlp.c_fc")
+            # ln_1 of layers after the first: the previous layer's MLP c_proj
+            # writes x with its packed rows and row statistics when its plan
+            # finishes its output in one launch (a row panel, split or not)
+            d = cfg["n_embd"]
+            if gpu.x3_rows_out_ok(_ROWS_HINT, d, 4 * d):
+                for i in range(1, cfg["n_layer"]):
+                    fold1[i] = _fold_ln(np_weights, f"transformer.h.{i}", "ln_1", "attn.c_attn")
     return {"weights": w, "config": dict(cfg), "dtype": dtype, "kmajor": bool(kmajor), "packed": pk,
-            "x3": bool(x3), "fold_ln2": fold}
+            "x3": bool(x3), "fold_ln2": fold, "fold_ln1": fold1}
 
 
 # Widths whose c_proj and c_fc run unsplit packed-row panel GEMMs (K a
-# multiple of 256 up to 1536), the condition for folding ln_2 into c_fc.
+# multiple of 256 up to 1536), the condition for folding ln_2 into c_fc (and
+# ln_1 into c_attn).
 _FOLD_WIDTHS = (256, 512, 768, 1024, 1280, 1536)
+# The row count the ln_1 fold is planned for (C2's sequence length): the
+# MLP c_proj of that many rows must write its output, packed rows and row
+# statistics in one launch.
+_ROWS_HINT = 128
 
 
-def _fold_ln2(np_weights: dict, p: str):
-    """ln_2 folded into c_fc: layer_norm(x, g, b) @ W + c = inv * (x @ (g W)
-    - mean * colsum(g W)) + (b @ W + c) per row, so that c_fc can read the
-    residual stream x itself (as packed rows with the row statistics the
-    producing GEMM writes) instead of a normalised copy.  g W is rounded to
-    fp32 once, and colsum is taken over those fp32 values so that the mean
-    term cancels against the product of the same weights."""
-    g = np.asarray(np_weights[f"{p}.ln_2.weight"], np.float64)
-    b = np.asarray(np_weights[f"{p}.ln_2.bias"], np.float64)
-    W = np.asarray(np_weights[f"{p}.mlp.c_fc.weight"], np.float64)
-    c = np.asarray(np_weights[f"{p}.mlp.c_fc.bias"], np.float64)
+def _fold_ln(np_weights: dict, p: str, ln: str, proj: str):
+    """A layer_norm folded into the projection that reads it (ln_2 into c_fc,
+    ln_1 into c_attn): layer_norm(x, g, b) @ W + c = inv * (x @ (g W) -
+    mean * colsum(g W)) + (b @ W + c) per row, so that the projection can
+    read the residual stream x itself (as packed rows with the row
+    statistics the producing GEMM writes) instead of a normalised copy.  g W
+    is rounded to fp32 once, and colsum is taken over those fp32 values so
+    that the mean term cancels against the product of the same weights."""
+    g = np.asarray(np_weights[f"{p}.{ln}.weight"], np.float64)
+    b = np.asarray(np_weights[f"{p}.{ln}.bias"], np.float64)
+    W = np.asarray(np_weights[f"{p}.{proj}.weight"], np.float64)
+    c = np.asarray(np_weights[f"{p}.{proj}.bias"], np.float64)
     gw = (g[:, None] * W).astype(np.float32)
     cs = gw.astype(np.float64).sum(0).astype(np.float32)
     bb = (b @ W + c).astype(np.float32)
@@ -219,12 +232,20 @@ def gpt2_forward(model: dict, input_ids, kv_cache=None, positions=None, need_cac
     new_cache = []
     for i in range(L):
         p = f"transformer.h.{i}"
-        h = gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
+        fold1 = model.get("fold_ln1", {}).get(i) if rows else None
+        h = None if fold1 is not None else gpu.layer_norm(x, w[f"{p}.ln_1.weight"], w[f"{p}.ln_1.bias"])
         if not cached and not need_cache and not model.get("kmajor") and not model.get("x3"):
             # projection + head split + causal attention in one op
             a = gpu.qkv_attention(h, w[f"{p}.attn.c_attn.weight"], w[f"{p}.attn.c_attn.bias"], H, causal=True)
         else:
-            qkv = gpu.add_bias(mm_in(h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
+            if fold1 is not None:
+                # ln_1 folded into c_attn: the previous layer's MLP c_proj
+                # wrote x as packed rows with row statistics
+                packed1, cs1, bb1, n_qkv = fold1
+                qkv = gpu.add_bias(gpu.matmul_pp_norm(gpu.pack_rows_x3(x), gpu.row_stats_x3(x), T, packed1, cs1,
+                                                      n_qkv), bb1)
+            else:
+                qkv = gpu.add_bias(mm_in(h, f"{p}.attn.c_attn.weight"), w[f"{p}.attn.c_attn.bias"])
 
             def heads(lo):
                 part = gpu.slice(qkv, 1, lo, lo + d)

@@ -565,6 +565,20 @@ int32_t applegpu_ffi_gemm_skinny(int32_t enable) {
   return prev;
 }
 
+int32_t applegpu_ffi_split_inkernel(int32_t enable) {
+  k::GemmTune& t = k::gemm_tune();
+  const int32_t prev = t.inkernel_splits ? 1 : 0;
+  t.inkernel_splits = enable != 0;
+  return prev;
+}
+
+int32_t applegpu_ffi_x3_rows_out(int64_t M, int64_t N, int64_t K) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (M < 1 || N < 1 || K < 1) fail("x3_rows_out: extents must be positive");
+    return k::gemm_x3_rows_out_ok(M, N, K, true) ? 1 : 0;
+  });
+}
+
 int32_t applegpu_ffi_gemm_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int8_t dtype_i8, bool a_kcontig,
                                bool b_kcontig, char* out, uint32_t cap) {
   return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {

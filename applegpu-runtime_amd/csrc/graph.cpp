@@ -739,7 +739,17 @@ void eval_all(const std::vector<TensorP>& roots) {
     auto reads_ahead = [&](size_t j) {
       Tensor* t = order[j].get();
       if (absorbed.count(t)) return false;
-      if (groups.count(t)) return post_ln.count(t) > 0;
+      auto git = groups.find(t);
+      if (git != groups.end()) {
+        if (post_ln.count(t)) return true;
+        // a split packed-row panel that finishes its tiles in its own launch
+        // leaves CUs idle too
+        const Group& g = git->second;
+        if (g.a_rows < 1 || g.packed_n <= 0 || !ops::is_x3_packed(g.b) || g.norm_stats) return false;
+        const int64_t K = g.b->shape[1] * 16;
+        return k::gemm_x3_rows_out_ok(g.a_rows, g.packed_n, K, true) &&
+               !k::gemm_x3_panel_ok(g.a_rows, g.packed_n, K, true);
+      }
       return emb_adds.count(t) > 0;
     };
     for (size_t i = 0; i < order.size(); ++i) {

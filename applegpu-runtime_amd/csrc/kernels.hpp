@@ -264,6 +264,13 @@ void row_tile_stats(const float* x, int64_t x_sm, int64_t M, int64_t N, float* o
 // Whether the packed-weight GEMM of this shape runs an unsplit row-panel
 // plan (packed outputs and row statistics come from its epilogue).
 bool gemm_x3_panel_ok(int64_t M, int64_t N, int64_t K, bool apk);
+// Whether its plan is a row panel whose epilogue writes the output (and its
+// packed rows and row statistics) in the same launch: unsplit, or split
+// with every tile finished in the kernel by its last-arriving split.
+bool gemm_x3_rows_out_ok(int64_t M, int64_t N, int64_t K, bool apk);
+// Device address of the split row-panel tiles' arrival counters (looked up
+// once at init on the runtime's device; false with the error set on failure).
+bool split_counters_setup(std::string* err);
 // Packed x3 rows of an fp32 matrix X [M, K] read through strides (x_sm,
 // x_sk), K % 16 == 0: the A-operand counterpart of pack_weights_x3
 // (packed_x3_elems(K, M) bf16 elements).
@@ -338,6 +345,9 @@ struct GemmTune {
   int cfg = -1;
   int splits = 0;
   bool no_skinny = false;  // route M <= 16 through gemm_mf too
+  // split row panels finish their tiles in the kernel (no reduction launch);
+  // APPLEGPU_SPLIT_INKERNEL=0 sends their sums to the reduction launch
+  bool inkernel_splits = true;
 };
 GemmTune& gemm_tune();
 // Name of the configuration the heuristic (or a forced tune) picks.

@@ -756,6 +756,16 @@ static X3Plan x3_plan_of(const Gemm& g) {
   return x3_plan(g.M, g.N, g.K, cu_count(), g.a_x3, g.pln_y != nullptr || g.pln_ypk != nullptr);
 }
 
+// Whether a split packed-A row-panel launch finishes its tiles in the kernel
+// (each tile's last-arriving split sums the splits and runs the epilogue)
+// instead of leaving them to a reduction launch: not when the caller wants
+// the partial sums, nor when the reduction must compute a layer_norm over
+// whole rows.
+static bool x3_split_inkernel(const Gemm& g, const X3Plan& pl) {
+  return pl.rows && pl.apk && pl.splits > 1 && !g.no_reduce && !g.pln_y && !g.pln_ypk &&
+         split_tile_counters(pl.tiles_m * pl.tiles_n) != nullptr;
+}
+
 bool gemm_x3_ok(const Gemm& g) {
   if (!g.b_x3 || g.dt != DType::F32 || g.batch != 1 || g.K % 16 != 0 || g.K <= 0 || !al16(g.A) || !al16(g.B) ||
       g.b_scale)
@@ -768,7 +778,8 @@ bool gemm_x3_ok(const Gemm& g) {
   }
   if (g.c_pk || g.rs_out || g.rs_in) {
     const X3Plan pl = x3_plan_of(g);
-    if (!(pl.rows && pl.splits == 1)) return false;
+    if (!pl.rows) return false;
+    if (pl.splits > 1 && (g.rs_in || !x3_split_inkernel(g, pl))) return false;
     if (g.c_pk && (g.N % 16 != 0 || !al16(g.c_pk))) return false;
     if (g.rs_out && (g.N % 32 != 0 || ((uintptr_t)g.rs_out & 7))) return false;
     if (g.rs_in && (!g.a_x3 || !g.rs_cs || g.rs_tiles < 1 || g.rs_tiles > 48 || g.rs_n < 1 || ((uintptr_t)g.rs_in & 7)))
@@ -783,6 +794,16 @@ bool gemm_x3_pk_out_ok(int64_t M, int64_t N, int64_t K) { return gemm_x3_panel_o
 bool gemm_x3_panel_ok(int64_t M, int64_t N, int64_t K, bool apk) {
   const X3Plan pl = x3_plan(M, N, K, cu_count(), apk, false);
   return pl.rows && pl.splits == 1;
+}
+
+bool gemm_x3_rows_out_ok(int64_t M, int64_t N, int64_t K, bool apk) {
+  const X3Plan pl = x3_plan(M, N, K, cu_count(), apk, false);
+  if (!pl.rows) return false;
+  if (pl.splits == 1) return true;
+  Gemm g;
+  g.M = M; g.N = N; g.K = K;
+  g.a_x3 = apk;
+  return x3_split_inkernel(g, pl);
 }
 
 // The outer-product plan (gemm_x3p.hip) for fp32 products it fits, unless a
@@ -849,6 +870,8 @@ GemmTune& gemm_tune() {
     if (m && (!strcmp(m, "native") || !strcmp(m, "f32"))) d.f32_mode = kF32Native;
     const char* sk = getenv("APPLEGPU_GEMM_SKINNY");
     if (sk && *sk == '0') d.no_skinny = true;
+    const char* ik = getenv("APPLEGPU_SPLIT_INKERNEL");
+    if (ik && *ik == '0') d.inkernel_splits = false;
     return d;
   }();
   return t;
@@ -915,6 +938,7 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     GArgs p = make_args(g, one);
     p.ws = (float*)workspace;
     if (xp.splits > 1 && !workspace) fail("gemm: split-K workspace missing");
+    if (x3_split_inkernel(g, xp)) p.tile_cnt = split_tile_counters(xp.tiles_m * xp.tiles_n);
     gemm_x3p_launch(xp, p, s);
     reduce_splits(g, p, s);
     return;
@@ -1042,7 +1066,7 @@ PfArgs make_prefetch(int main, int threads) {
 // order) into C with the epilogue, and layer_norm(C) into Y when asked.
 static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s) {
   if (p.splits > 1) {
-    if (g.no_reduce) return;
+    if (g.no_reduce || p.tile_cnt) return;  // (tiles finished in the GEMM launch)
     if (g.pln_y || g.pln_ypk) {
       if (!gemm_post_ln_fused(g)) fail("gemm: this launch cannot fuse layer_norm into its reduction");
       AGPU_FLOAT_SWITCH(g.dt, launch_reduce_ln<T>(p, s));

@@ -55,6 +55,10 @@ struct GArgs {
   float rs_eps;
   // rowsum_acc[m] += alpha * sum_k A(m, k) (gemm_a_rowsum_fused plans)
   float* rowsum_acc;
+  // split row-panel launches that finish each output tile in the kernel:
+  // one arrival counter per tile (zero before the launch, zero after it);
+  // null = the splits' sums go to the workspace for a reduction launch
+  unsigned* tile_cnt;
 };
 
 // Epilogue operands of one output, loadable ahead of the product (they do
@@ -883,6 +887,9 @@ void gemm_thin(int kind, DType dt, const GArgs& p, hipStream_t s);
 // The packed-weight bf16x3 GEMM (gemm_x3p.hip): partial sums into p.ws when
 // the plan splits K, else the epilogue into C.
 void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s);
+// Arrival counters for a split packed-A row-panel launch of `tiles` tiles
+// that finishes its tiles in the kernel, or null (reduction launch instead).
+unsigned* split_tile_counters(int64_t tiles);
 
 // Outer-shaped fp32 products (M, N multiples of 128 with at least 256 tiles
 // of 128 x 128, K = 128, 256 or 512; one batch, no mask): both operands

@@ -529,8 +529,8 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
 }
 
 // Row panel over packed A: the block (8 wavefronts) owns 32 rows x 32
-// columns over a K range of 8 KPW k steps (split blockIdx.y; the whole K when
-// splits == 1); wave w multiplies k steps [w KPW, (w + 1) KPW) of the range
+// columns over a K range of 8 KPW k steps (block id = split x tiles + tile;
+// the whole K when splits == 1); wave w multiplies k steps [w KPW, (w + 1) KPW) of the range
 // with its A and B fragments loaded straight from global memory into
 // registers (both operands are stored in MFMA order), so the product needs
 // no LDS, no barrier and no conversion.  The eight partial 32 x 32 blocks
@@ -539,20 +539,34 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
 // bits).  Without a split they apply the epilogue, whose operands they load
 // while the products run, and write C (fp32) and/or, as packed x3 rows,
 // c_pk (N % 16 == 0) for the next packed-A GEMM; with one, the split's sums
-// go to the workspace for the split-K reduction.  Block ids run along the
-// columns (tm = id / tiles_n): with cold weights this measured faster than
-// dealing the row tiles of one column strip to one XCD back to back (qkv's
-// weight loads 8.7 vs 10.5 us), whose simultaneous misses on the same lines
-// are not merged.
+// go to the workspace, and either a split-K reduction launch follows
+// (tile_cnt null) or the tile is finished in this launch by whichever of its
+// splits arrives last (tile_cnt: one counter per tile).  Then every split
+// writes its sums with agent-scope (L2-bypassing) stores, waits until they
+// have completed and counts itself in with an atomic add on the tile's
+// counter; the block that brings the count to `splits` resets the counter
+// for the next launch, reads the other splits' sums with agent-scope loads,
+// adds all of them in split order (0 + s0 + s1 + ..., the reduction
+// launch's order, so the bits are the same) and runs the epilogue.  No
+// block waits for another (a split-owner that waited for its tile's other
+// splits measured 20 us slower per GPT-2 forward: the polls add latency).
+// Blocks past tiles x splits read ahead the next GEMMs' weights
+// (prefetch_block).  Tile ids run along the columns (tm = tile / tiles_n):
+// with cold weights this measured faster than dealing the row tiles of one
+// column strip to one XCD back to back (qkv's weight loads 8.7 vs 10.5 us),
+// whose simultaneous misses on the same lines are not merged.
 template <int KPW>
 __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
   constexpr int W = 8;
+  if (prefetch_block(p.pf)) return;
   const int64_t T = p.K >> 4;
   __shared__ __attribute__((aligned(16))) float red[W * 16 * 64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x % p.tiles_n;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int tile = (int)blockIdx.x % tiles, split = (int)blockIdx.x / tiles;
+  const int tm = tile / p.tiles_n, tn = tile % p.tiles_n;
   const int64_t m0 = (int64_t)tm * 32, n0 = (int64_t)tn * 32;
-  const int64_t t0 = (int64_t)blockIdx.y * (W * KPW) + (int64_t)wave * KPW;
+  const int64_t t0 = (int64_t)split * (W * KPW) + (int64_t)wave * KPW;
 
   // 1. Fragments: tiles_m and tiles_n equal the strip counts, so tm and tn
   //    name existing strips.
@@ -574,7 +588,7 @@ __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
   const int64_t row = m0 + r, rc = row < p.M ? row : p.M - 1;
   RowEpi ep;
   RowStats rs;
-  if (wave < 4 && p.splits == 1) {
+  if (wave < 4 && (p.splits == 1 || p.tile_cnt)) {
     row_epi_load(p, row, n0 + 4 * q, ep);
     if (p.rs_in) row_norm_load(p, rc, q, rs);
   }
@@ -593,28 +607,63 @@ __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
 #pragma unroll
   for (int e = 0; e < 16; ++e) red[(wave * 16 + e) * 64 + lane] = acc[e];
   __syncthreads();
-  if (wave >= 4 || row >= p.M) return;
+  const bool fin = wave < 4 && row < p.M;  // this thread finishes row r, columns 4q..4q+3
+  if (!fin && !(p.splits > 1 && p.tile_cnt)) return;
   // 5. Row r, columns 4q..4q+3: register 4 (r / 8) + r % 4 of lanes
   //    32 ((r / 4) % 2) + 4q + 0..3 in every wave.
   const int e = 4 * (r >> 3) + (r & 3);
   const int lb = 32 * ((r >> 2) & 1) + 4 * q;
-  float v[4];
-  {
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (fin) {
     const float4 w0 = *(const float4*)&red[e * 64 + lb];
     v[0] = w0.x; v[1] = w0.y; v[2] = w0.z; v[3] = w0.w;
-  }
 #pragma unroll
-  for (int x = 1; x < W; ++x) {
-    const float4 w = *(const float4*)&red[(x * 16 + e) * 64 + lb];
-    v[0] += w.x; v[1] += w.y; v[2] += w.z; v[3] += w.w;
+    for (int x = 1; x < W; ++x) {
+      const float4 w = *(const float4*)&red[(x * 16 + e) * 64 + lb];
+      v[0] += w.x; v[1] += w.y; v[2] += w.z; v[3] += w.w;
+    }
   }
   const int64_t col = n0 + 4 * q;
   if (p.splits > 1) {
-    float* ws = p.ws + (int64_t)blockIdx.y * p.M * p.N + row * p.N;
+    const int64_t plane = p.M * p.N;
+    float* ws = p.ws + (int64_t)split * plane + row * p.N;
+    if (!p.tile_cnt) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (col + j < p.N) ws[col + j] = v[j];
-    return;
+      for (int j = 0; j < 4; ++j)
+        if (col + j < p.N) ws[col + j] = v[j];
+      return;
+    }
+    // the tile is finished by whichever split arrives last: sums out, wait
+    // until they have completed, count in (all 512 threads reach both
+    // barriers)
+    if (fin) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (col + j < p.N) __hip_atomic_store(ws + col + j, v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+    __shared__ unsigned last;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned before =
+          __hip_atomic_fetch_add(p.tile_cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = before == (unsigned)(p.splits - 1);
+      if (last) __hip_atomic_store(p.tile_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last || !fin) return;
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+    const float* wr = p.ws + row * p.N;
+    for (int sp = 0; sp < p.splits; ++sp) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t cj = col + j < p.N ? col + j : p.N - 1;
+        sum[j] += sp == split ? v[j]
+                              : __hip_atomic_load(wr + sp * plane + cj, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = sum[j];
   }
   float mean = 0.f, inv = 1.f;
   if (p.rs_in) row_norm_stats(p, q, rs, mean, inv);
@@ -997,6 +1046,35 @@ void row_tile_stats(const float* x, int64_t x_sm, int64_t M, int64_t N, float* o
   check_launch("row_tile_stats");
 }
 
+// Arrival counters of the split row-panel tiles finished in the kernel
+// (gemm_x3_rows_pk with tile_cnt): zero when the code object loads, and
+// every launch leaves the counters it used at zero.  One array per device;
+// the runtime drives device 0 only, whose address split_counters_setup
+// looks up (the array's name is a host stand-in, never a kernel argument).
+constexpr int64_t kTileCounters = 1 << 16;
+static __device__ __align__(256) unsigned tile_counters[kTileCounters];
+static unsigned* g_tile_counters = nullptr;
+
+bool split_counters_setup(std::string* err) {
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(tile_counters));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    if (err)
+      *err = std::string("split-tile counters: hipGetSymbolAddress failed: ") +
+             (e != hipSuccess ? hipGetErrorString(e) : "null address");
+    return false;
+  }
+  g_tile_counters = (unsigned*)ptr;
+  return true;
+}
+
+// The counters for a split row-panel launch of `tiles` output tiles, or null
+// when its tiles go to the reduction launch instead.
+unsigned* split_tile_counters(int64_t tiles) {
+  return gemm_tune().inkernel_splits && g_tile_counters && tiles <= kTileCounters ? g_tile_counters : nullptr;
+}
+
 void pack_rows_x3(const void* x, int64_t x_sm, int64_t x_sk, int64_t M, int64_t K, void* out, hipStream_t s) {
   // X(m, k) = B(k, n = m): the weights' kernel with rows as columns
   pack_weights_x3(x, x_sk, x_sm, K, M, out, s);
@@ -1094,9 +1172,14 @@ X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus, bool apk, bool split) {
 
 bool gemm_x3_ln_ok(int64_t M, int64_t N, int64_t K) { return x3_plan(M, N, K, 256).rows; }
 
-static void launch_rows_pk(const X3Plan& pl, const GArgs& p, hipStream_t s) {
-  if (p.K != 128LL * pl.kpw * pl.splits) fail("internal: gemm_x3_rows_pk plan does not cover K");
-  const dim3 grid((unsigned)(pl.tiles_m * pl.tiles_n), (unsigned)pl.splits);
+static void launch_rows_pk(const X3Plan& pl, const GArgs& p0, hipStream_t s) {
+  if (p0.K != 128LL * pl.kpw * pl.splits) fail("internal: gemm_x3_rows_pk plan does not cover K");
+  GArgs p = p0;
+  const int64_t main = pl.tiles_m * pl.tiles_n * pl.splits;
+  if (main > 0x7fffff00) fail("gemm_x3_rows_pk: grid too large");
+  // a split finished in the launch leaves CUs idle: read ahead there
+  if (p.tile_cnt) p.pf = make_prefetch((int)main, 512);
+  const dim3 grid((unsigned)(main + (p.tile_cnt ? p.pf.blocks : 0)));
   switch (pl.kpw) {
     case 1: hipLaunchKernelGGL((gemm_x3_rows_pk<1>), grid, dim3(512), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gemm_x3_rows_pk<2>), grid, dim3(512), 0, s, p); break;
@@ -1125,10 +1208,15 @@ static void launch_rows(const X3Plan& pl, const GArgs& p, hipStream_t s) {
 void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s) {
   if (pl.apk != p.a_x3) fail("internal: gemm_x3p plan and A operand disagree");
   const bool panel = pl.rows && pl.splits == 1;
-  if (p.c_pk && !(panel && p.N % 16 == 0))
-    fail("gemm_x3p: packed output needs an unsplit row-panel plan and N %% 16 == 0");
-  if (p.rs_out && !(panel && p.N % 32 == 0))
-    fail("gemm_x3p: row statistics need an unsplit row-panel plan and N %% 32 == 0");
+  // the epilogue runs in this launch: unsplit, or packed-A split tiles
+  // finished in the kernel
+  const bool epi_here = panel || (pl.rows && pl.apk && p.tile_cnt);
+  if (p.tile_cnt && !(pl.rows && pl.apk && pl.splits > 1))
+    fail("internal: in-kernel split completion needs a split packed-A row-panel plan");
+  if (p.c_pk && !(epi_here && p.N % 16 == 0))
+    fail("gemm_x3p: packed output needs a row-panel plan that runs its epilogue and N %% 16 == 0");
+  if (p.rs_out && !(epi_here && p.N % 32 == 0))
+    fail("gemm_x3p: row statistics need a row-panel plan that runs its epilogue and N %% 32 == 0");
   if (p.rs_in && !(panel && pl.apk)) fail("gemm_x3p: a folded layer_norm needs the unsplit packed-A row-panel plan");
   if (pl.stream) {
     if (p.ln_g || !pl.apk) fail("internal: the weight-streaming panel takes packed A only");

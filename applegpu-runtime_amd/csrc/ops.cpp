@@ -1235,9 +1235,9 @@ static TensorP matmul_x3(const TensorP& a_in, int64_t a_rows, const TensorP& pw,
   TensorP pc = contiguous(pw);
   const std::vector<int64_t> od{M, N};
   const std::vector<int64_t> pkd{(M + 31) / 32, N / 16, 2, 64, 8};
-  // packed rows and row statistics straight from an unsplit row-panel
-  // epilogue when the plan has one
-  const bool panel = !post_ln && k::gemm_x3_panel_ok(M, N, K, apk);
+  // packed rows and row statistics straight from a row-panel epilogue when
+  // the plan has one (unsplit, or split with its tiles finished in the launch)
+  const bool panel = !post_ln && k::gemm_x3_rows_out_ok(M, N, K, apk);
   const bool pk_direct = po && po->want_pk && panel && N % 16 == 0;
   const bool st_direct = po && po->want_stats && panel && N % 32 == 0;
   const bool norm = epi && epi->norm_stats;

@@ -1,6 +1,7 @@
 // Runtime: device init, the single stream, the buffer pool and the id registry.
 #include <atomic>
 #include "core.hpp"
+#include "kernels.hpp"
 
 #include <cstdarg>
 #include <cstdio>
@@ -395,7 +396,7 @@ bool Runtime::init(std::string* err) {
       delete rt;
       return;
     }
-    if (!noalloc_setup(&g_init_err)) {
+    if (!noalloc_setup(&g_init_err) || !k::split_counters_setup(&g_init_err)) {
       delete rt;
       return;
     }

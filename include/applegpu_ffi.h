@@ -261,6 +261,19 @@ int32_t applegpu_ffi_gemm_tune(int32_t f32_mode, int32_t cfg, int32_t splits);
  * also APPLEGPU_GEMM_SKINNY=0) or a cfg/splits tune is forced.  Returns the
  * previous setting (1 = on).  No reference counterpart (tuning). */
 int32_t applegpu_ffi_gemm_skinny(int32_t enable);
+/* Split-K packed-A row panels (fp32 GPT-2 projections) finish each output
+ * tile in the GEMM launch itself, by whichever split of the tile arrives
+ * last, instead of in a separate reduction launch, unless this is switched
+ * off (enable = 0; also APPLEGPU_SPLIT_INKERNEL=0).  Both give the same bits.
+ * Returns the previous setting (1 = on).  No reference counterpart (tuning;
+ * it replaces nothing the reference has). */
+int32_t applegpu_ffi_split_inkernel(int32_t enable);
+/* 1 when an M x K (packed rows) by K x N (packed fp32 weights) product runs
+ * a row-panel plan that writes its output, packed rows and row statistics
+ * in one launch (so a layer_norm of its output can fold into the next
+ * projection), 0 when not, -1 on bad extents.  No reference counterpart
+ * (plan introspection). */
+int32_t applegpu_ffi_x3_rows_out(int64_t M, int64_t N, int64_t K);
 /* The plan the GEMM heuristic picks for an M x N x K (batch) problem of the
  * given dtype and operand layouts (a_kcontig: A(m,k) has unit k stride;
  * b_kcontig: B(k,n) has unit k stride), written as text into out. */

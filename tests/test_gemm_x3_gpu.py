@@ -475,3 +475,67 @@ def test_weight_streaming_panel_matches_oracle(gpu, M, K, N, forced):
         lib.applegpu_ffi_gemm_tune(0, -1, 0)
     assert rel_err(got, O.matmul(a, b)) < 1e-4
     np.testing.assert_array_equal(exact, ai @ bi)
+
+
+@pytest.mark.parametrize("M,K,N,N2", [(128, 3072, 768, 2304), (70, 2048, 256, 512), (33, 4096, 256, 96)])
+def test_split_panel_finishes_tiles_in_the_launch(gpu, M, K, N, N2):
+    """A split packed-A row panel (2, 8 and 16 K splits at these shapes)
+    whose tiles are finished in the GEMM launch by their last-arriving split:
+    one launch writes x1 = r + (a @ W + b), its packed rows and its row
+    statistics, and the folded layer_norm product reading them is one more;
+    x1, the statistics, the packed rows and the product have the same bits
+    as with the split-K reduction launch (switched back on for comparison),
+    are identical over repeated launches and graph replays (the arrival
+    counters return to zero), and meet the fp32 bar against the oracle."""
+    from applegpu_runtime._native import lib
+    a, W, b, r = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1), f32(M, N)
+    g, be = f32(N, scale=0.5) + 1.0, f32(N, scale=0.1)
+    W2, c2 = f32(N, N2, scale=0.05), f32(N2, scale=0.1)
+    gw, cs, bb = _fold(g, be, W2, c2)
+    ad, bd, rd, csd, bbd = (gpu.from_numpy(v) for v in (a, b, r, cs, bb))
+    apk, pk_w, pk_g = gpu.pack_rows_x3(ad), gpu.pack_weight_x3(gpu.from_numpy(W)), gpu.pack_weight_x3(gpu.from_numpy(gw))
+    for t in (ad, bd, rd, csd, bbd, apk, pk_w, pk_g):
+        t.eval()
+
+    def forward():
+        x1 = rd + gpu.add_bias(gpu.matmul_pp(apk, M, pk_w, N), bd)
+        st, xp = gpu.row_stats_x3(x1), gpu.pack_rows_x3(x1)
+        return x1, st, xp, gpu.add_bias(gpu.matmul_pp_norm(xp, st, M, pk_g, csd, N2), bbd)
+
+    def run():
+        x1, st, xp, y = forward()
+        before = gpu.graph_stats()["launcher_calls"]
+        y.eval()
+        calls = gpu.graph_stats()["launcher_calls"] - before
+        return x1.to_numpy(), st.to_numpy(), _valid_rows(_bits_of(xp), M), y.to_numpy(), calls
+
+    prev = lib.applegpu_ffi_split_inkernel(1)
+    try:
+        got = [run() for _ in range(2)]
+        graph = gpu.capture(lambda: forward()[3])
+        try:
+            reps = []
+            for _ in range(3):
+                graph.replay()
+                reps.append(graph.outputs.to_numpy())
+                t = gpu.from_numpy(np.ones(64, np.float32))
+                (t + t).to_numpy()
+        finally:
+            graph.destroy()
+        lib.applegpu_ffi_split_inkernel(0)
+        want = run()
+    finally:
+        lib.applegpu_ffi_split_inkernel(prev)
+    x1, st, xp, y, calls = got[0]
+    assert calls == 2, calls
+    assert want[4] > 2, want[4]
+    for u, v in zip(got[1][:4], got[0][:4]):
+        np.testing.assert_array_equal(u, v)
+    for u, v in zip(got[0][:4], want[:4]):
+        np.testing.assert_array_equal(u, v)
+    for rep in reps:
+        np.testing.assert_array_equal(rep, y)
+    np.testing.assert_array_equal(st, gpu.row_stats_x3(gpu.from_numpy(x1)).to_numpy())
+    x1_ref = r + O.add_bias(O.matmul(a, W), b)
+    assert rel_err(x1, x1_ref) < 1e-4
+    assert rel_err(y, O.add_bias(O.matmul(O.layer_norm(x1_ref, g, be), W2), c2)) < 1e-4
