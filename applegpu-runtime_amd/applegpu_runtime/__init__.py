@@ -291,6 +291,16 @@ def eval(t):
     _t(t).eval()
 
 
+def eval_many(tensors):
+    """Evaluates several lazy tensors in one walk, so that a producer several
+    of them read (a GEMM writing its output, packed rows and row
+    statistics) runs once with all of its outputs."""
+    ts = [_t(t) for t in tensors]
+    ids = (ctypes.c_uint64 * len(ts))(*[t._id for t in ts])
+    if lib.applegpu_ffi_eval_many(ids, len(ts)) != 0:
+        raise ValueError(ffi_error())
+
+
 def to_list(t):
     return _t(t).to_list()
 

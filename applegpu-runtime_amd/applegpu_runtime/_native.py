@@ -51,6 +51,7 @@ _SIGS = {
     "applegpu_ffi_scalar_mul_out": (c_void_p, [c_uint64, c_float, u64p]),
     "applegpu_ffi_mean_all_out": (c_void_p, [c_uint64, u64p]),
     "applegpu_ffi_eval": (c_int32, [c_uint64]),
+    "applegpu_ffi_eval_many": (c_int32, [POINTER(c_uint64), c_uint32]),
     "applegpu_ffi_synchronize": (None, []),
     "applegpu_ffi_read_f32": (c_int32, [c_uint64, POINTER(c_float), c_uint64]),
     # eager path (reference surface)

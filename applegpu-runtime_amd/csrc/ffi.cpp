@@ -315,6 +315,17 @@ int32_t applegpu_ffi_eval(uint64_t tensor_id) {
   });
 }
 
+int32_t applegpu_ffi_eval_many(const uint64_t* tensor_ids, uint32_t n) {
+  return guarded<int32_t>(kFfi, -1, [&]() -> int32_t {
+    if (n > 0 && !tensor_ids) fail("eval_many: null id array");
+    std::vector<TensorP> roots;
+    roots.reserve(n);
+    for (uint32_t i = 0; i < n; ++i) roots.push_back(rt().lookup(tensor_ids[i]));
+    eval_all(roots);
+    return 0;
+  });
+}
+
 void applegpu_ffi_synchronize(void) {
   guarded<int>(kFfi, 0, [&]() {
     if (Runtime::initialized()) rt().sync();

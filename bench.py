@@ -15,15 +15,19 @@ timed region.  value = gpt2_fwd_ms + mlp_train_ms, each the mean over
 --steps replays bracketed by stream synchronisations.
 
 Roofline (`roofline`): the kernel with the largest time per step, the
-packed-A row-panel GEMM gemm_x3_rows_pk<6> of GPT-2's qkv (128 x 768 x 2304,
-bias) and fc (128 x 768 x 3072, bias + gelu, output written as packed rows)
-projections, 24 launches per forward.  Both operands are pre-split bf16 hi/lo
-MFMA fragments (three bf16 MFMAs per product) and the weights are read once
-per launch, so the kernel is bound by HBM: algorithmic bytes per launch =
-packed A + packed weights + bias + output.  Its launch duration is timed with
-HIP events on the library stream over a captured graph of back-to-back
-launches that rotate through 40 weight sets per shape (more than the 256 MB
-Infinity Cache holds, so the weights stream from HBM as in the forward).
+packed-A row-panel GEMM gemm_x3_rows_pk<6>, at each of the three shapes it
+runs at in the forward, 12 launches each: qkv (128 x 768 x 2304, ln_1 folded
+in, bias), the attention projection (128 x 768 x 768, bias + residual, x also
+written as packed rows and row statistics) and fc (128 x 768 x 3072, ln_2
+folded in, bias + gelu, packed rows out).  Both operands are pre-split bf16
+hi/lo MFMA fragments (three bf16 MFMAs per product) and the weights are read
+once per launch, so the kernel is bound by HBM: algorithmic bytes per launch
+= packed A + packed weights + bias (+ the folded norm's statistics and column
+sums, the residual) + every output.  Each shape's launch duration is timed
+with HIP events on the library stream over a captured graph of back-to-back
+launches that rotate through 40 weight sets (more than the 256 MB Infinity
+Cache holds, so the weights stream from HBM as in the forward); the
+aggregate is the bytes of one launch of each shape over their summed time.
 The same launches in MFMA terms are reported beside it (against the fp32
 MFMA peak and against the bf16x3 ceiling, one third of the bf16 MFMA peak).
 `roofline_mlp_dw` is the MLP weight-gradient GEMM with its SGD step
@@ -35,8 +39,10 @@ the rocprofv3 --pmc summaries committed under profiles/ (FETCH_SIZE,
 WRITE_SIZE of each kernel, scaled by the same counters read for the 256 MiB
 calibration copy this script runs), when present.
 
-Prints ONE JSON line.  `python bench.py --gpus N` with N > 1 exits: this
-build runs on one GPU.
+Prints ONE JSON line: the headline, with the other configs of BASELINE.json
+as sub-records (`c1`, `c4`, `c5`), each with its own roofline and CPU
+baseline (`--headline-only` leaves them out).  `python bench.py --gpus N`
+with N > 1 exits: this build runs on one GPU.
 """
 from __future__ import annotations
 
@@ -93,35 +99,57 @@ def load_traffic(path=TRAFFIC_FILE):
         return None, None
 
 
-PROJ_SHAPES = (("qkv", 2304, False), ("fc", 3072, True))
+PANEL_SHAPES = (("qkv", 2304), ("proj", 768), ("fc", 3072))
 
 
-def proj_gemm_roofline(gpu, lib, rng, reps=4, nw=40):
-    """The dominant kernel, as the forward runs it: packed rows [128, 768]
-    times packed weights of each shape, bias (qkv) or bias + gelu with the
-    output written as packed rows (fc).  Each shape: one captured graph of
-    `nw` launches over `nw` weight sets, replayed `reps` times between HIP
-    events on the library stream."""
+def panel_roofline(gpu, lib, rng, reps=4, nw=40):
+    """The dominant kernel, gemm_x3_rows_pk<6>, at each shape and with each
+    epilogue it runs with in the forward (12 launches of each per forward):
+
+    - qkv   128 x 768 -> 2304: ln_1 folded in (the previous layer's x as packed
+            rows with its row statistics), bias; fp32 output;
+    - proj  128 x 768 -> 768: packed attention rows in, bias + residual; x
+            written as fp32, packed rows and row statistics;
+    - fc    128 x 768 -> 3072: ln_2 folded in, bias + gelu; packed rows out.
+
+    Each shape: one captured graph of `nw` launches over `nw` weight sets
+    (more than the 256 MB Infinity Cache holds, so the weights stream from
+    HBM as in the forward), replayed `reps` times between HIP events on the
+    library stream.  Algorithmic bytes per launch: packed A, packed weights,
+    bias (and folded-norm column sums, statistics, residual) read once,
+    every output written once."""
     M, K = SEQ, GPT2_CFG["n_embd"]
-    a = gpu.from_numpy(rng.standard_normal((M, K), dtype=np.float32))
-    apk = gpu.pack_rows_x3(a)
-    apk.eval()
+    x = gpu.from_numpy(rng.standard_normal((M, K), dtype=np.float32))
+    apk, ast = gpu.pack_rows_x3(x), gpu.row_stats_x3(x)
+    res = gpu.from_numpy(rng.standard_normal((M, K), dtype=np.float32))
+    for t in (apk, ast, res):
+        t.eval()
     out = {}
-    for name, N, gelu in PROJ_SHAPES:
+    for name, N in PANEL_SHAPES:
         ws = [gpu.pack_weight_x3(gpu.from_numpy(rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)))
               for _ in range(nw)]
         bias = gpu.from_numpy(np.zeros(N, np.float32))
-        for t in ws + [bias]:
+        cs = gpu.from_numpy(rng.standard_normal(N, dtype=np.float32) * np.float32(0.1))
+        for t in ws + [bias, cs]:
             t.eval()
 
         def launches():
-            outs = []
+            last = None
             for w in ws:
-                y = gpu.add_bias(gpu.matmul_pp(apk, M, w, N), bias)
-                y = gpu.pack_rows_x3(gpu.gelu(y)) if gelu else y
-                y.eval()
-                outs.append(y)
-            return outs[-1]
+                if name == "qkv":
+                    y = gpu.add_bias(gpu.matmul_pp_norm(apk, ast, M, w, cs, N), bias)
+                    y.eval()
+                    last = y
+                elif name == "fc":
+                    y = gpu.pack_rows_x3(gpu.gelu(gpu.add_bias(gpu.matmul_pp_norm(apk, ast, M, w, cs, N), bias)))
+                    y.eval()
+                    last = y
+                else:
+                    y = res + gpu.add_bias(gpu.matmul_pp(apk, M, w, N), bias)
+                    pk, st = gpu.pack_rows_x3(y), gpu.row_stats_x3(y)
+                    gpu.eval_many([y, pk, st])
+                    last = y
+            return last
 
         before = gpu.graph_stats()["launcher_calls"]
         g = gpu.capture(launches)
@@ -136,10 +164,17 @@ def proj_gemm_roofline(gpu, lib, rng, reps=4, nw=40):
         lib.applegpu_ffi_event_record(1)
         ms = lib.applegpu_ffi_event_elapsed_ms(0, 1) / (reps * nw)
         g.destroy()
-        # packed A, packed weights (hi + lo), bias, output (fp32 or packed hi + lo)
-        nbytes = 4 * M * K + 4 * K * N + 4 * N + 4 * M * N
-        out[name] = {"M": M, "N": N, "K": K, "avg_launch_ms": round(ms, 5), "algorithmic_bytes": nbytes,
-                     "flop": 2 * M * N * K, "epilogue": "bias + gelu, packed-row output" if gelu else "bias"}
+        # packed A and weights (hi + lo: 4 bytes per element), bias
+        nbytes = 4 * M * K + 4 * K * N + 4 * N
+        if name in ("qkv", "fc"):
+            nbytes += 4 * N + 8 * M * (K // 32) + 4 * M * N   # column sums, A's statistics, output
+        else:
+            nbytes += 4 * M * N + 4 * M * N + 4 * M * N + 8 * M * (N // 32)  # residual, C, packed C, statistics
+        out[name] = {"M": M, "N": N, "K": K, "launches_per_fwd": GPT2_CFG["n_layer"], "avg_launch_ms": round(ms, 5),
+                     "algorithmic_bytes": nbytes, "flop": 2 * M * N * K,
+                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "epilogue": {"qkv": "folded ln_1, bias", "fc": "folded ln_2, bias + gelu, packed rows out",
+                                  "proj": "bias + residual; fp32, packed rows and row statistics out"}[name]}
         del ws
     return out
 
@@ -366,8 +401,10 @@ def main():
     lib.applegpu_ffi_gemm_plan(M_, N_, K_, 1, 0, False, False, plan, 96)
     traffic, tinfo = load_traffic()
 
-    # ── roofline: the dominant kernel (GPT-2's packed qkv / fc projections) ──
-    shapes = proj_gemm_roofline(gpu, lib, rng)
+    # ── roofline: the dominant kernel, every shape it runs at in the forward ─
+    shapes = panel_roofline(gpu, lib, rng)
+    # each shape runs 12 times per forward: the aggregate is total bytes over
+    # total time of one launch of each
     p_ms = sum(v["avg_launch_ms"] for v in shapes.values())
     p_bytes = sum(v["algorithmic_bytes"] for v in shapes.values())
     p_flop = sum(v["flop"] for v in shapes.values())
@@ -402,9 +439,9 @@ def main():
             "device": dev,
         },
         "roofline": {
-            "kernel": "gemm_x3_rows_pk<6>: packed-A row-panel GEMM of GPT-2's qkv and fc projections "
-                      "(bf16 hi/lo fragments of both operands, 8 wavefronts x 6 k-steps, whole K per block); "
-                      "one qkv + one fc launch",
+            "kernel": "gemm_x3_rows_pk<6>: packed-A row-panel GEMM of GPT-2's qkv, attention-projection and fc "
+                      "projections (bf16 hi/lo fragments of both operands, 8 wavefronts x 6 k-steps, whole K per "
+                      "block), 36 launches per forward; all three shapes with their forward epilogues",
             "bound": "hbm",
             "achieved": round(p_gbs, 1),
             "peak": HBM_PEAK_GBS,
@@ -419,8 +456,9 @@ def main():
                 "bf16x3_ceiling_tflops": round(BF16X3_CEILING_TFLOPS, 1),
                 "frac_bf16x3_ceiling": round(p_tflops / BF16X3_CEILING_TFLOPS, 4),
             },
-            "timing": "captured graph of 40 back-to-back launches per shape over 40 weight sets (cold, as in "
-                      "the forward), HIP events on the library stream",
+            "timing": "per shape, a captured graph of 40 back-to-back launches over 40 weight sets (cold, as in "
+                      "the forward), HIP events on the library stream; aggregate = bytes / time of one launch of "
+                      "each shape (each runs 12 times per forward)",
             "traffic_source": os.path.relpath(PROJ_TRAFFIC_FILE, ROOT) if p_tinfo else None,
         },
         "roofline_mlp_dw": {

@@ -274,6 +274,14 @@ int32_t applegpu_ffi_split_inkernel(int32_t enable);
  * projection), 0 when not, -1 on bad extents.  No reference counterpart
  * (plan introspection). */
 int32_t applegpu_ffi_x3_rows_out(int64_t M, int64_t N, int64_t K);
+/* Evaluates several lazy tensors in one fusion-planned walk (a producer
+ * whose outputs are read by more than one of them, such as a GEMM writing
+ * its output, its packed rows and its row statistics, then runs once).  No
+ * reference counterpart: the reference's lazy eval takes one root
+ * (crates/core/src/lazy.rs:208-474); this is the multi-root walk that
+ * applegpu_eager_execute_graph runs for a graph's outputs.  Returns 0, or -1
+ * with the error set. */
+int32_t applegpu_ffi_eval_many(const uint64_t* tensor_ids, uint32_t n);
 /* The plan the GEMM heuristic picks for an M x N x K (batch) problem of the
  * given dtype and operand layouts (a_kcontig: A(m,k) has unit k stride;
  * b_kcontig: B(k,n) has unit k stride), written as text into out. */

@@ -539,3 +539,33 @@ def test_split_panel_finishes_tiles_in_the_launch(gpu, M, K, N, N2):
     x1_ref = r + O.add_bias(O.matmul(a, W), b)
     assert rel_err(x1, x1_ref) < 1e-4
     assert rel_err(y, O.add_bias(O.matmul(O.layer_norm(x1_ref, g, be), W2), c2)) < 1e-4
+
+
+def test_eval_many_runs_a_shared_producer_once(gpu):
+    """eval_many over a GEMM's output, its packed rows and its row statistics:
+    one launch (the row panel writes all three), the same bits as evaluating
+    them one after another (three launches)."""
+    M, K, N = 128, 768, 768
+    a, W, b, r = f32(M, K), f32(K, N, scale=0.05), f32(N, scale=0.1), f32(M, N)
+    ad, bd, rd = gpu.from_numpy(a), gpu.from_numpy(b), gpu.from_numpy(r)
+    apk, pk_w = gpu.pack_rows_x3(ad), gpu.pack_weight_x3(gpu.from_numpy(W))
+    for t in (ad, bd, rd, apk, pk_w):
+        t.eval()
+
+    def build():
+        y = rd + gpu.add_bias(gpu.matmul_pp(apk, M, pk_w, N), bd)
+        return y, gpu.pack_rows_x3(y), gpu.row_stats_x3(y)
+
+    y, pk, st = build()
+    before = gpu.graph_stats()["launcher_calls"]
+    gpu.eval_many([y, pk, st])
+    assert gpu.graph_stats()["launcher_calls"] - before == 1
+    y2, pk2, st2 = build()
+    for t in (y2, pk2, st2):
+        t.eval()
+    np.testing.assert_array_equal(y.to_numpy(), y2.to_numpy())
+    np.testing.assert_array_equal(st.to_numpy(), st2.to_numpy())
+    np.testing.assert_array_equal(_valid_rows(_bits_of(pk), M), _valid_rows(_bits_of(pk2), M))
+    assert rel_err(y.to_numpy(), r + O.add_bias(O.matmul(a, W), b)) < 1e-4
+    with pytest.raises(ValueError):
+        gpu.eval_many([y, 123456789])
