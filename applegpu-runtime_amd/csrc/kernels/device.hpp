@@ -34,12 +34,16 @@ __device__ __forceinline__ float wave_max(float v) {
 // GELU, tanh approximation (crates/core/src/kernel_templates.rs:272-307):
 // 0.5 x (1 + tanh(u)), u = clamp(0.7978845608 (x + 0.044715 x^3), -10, 10).
 // Evaluated through the identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)): one
-// exp and one division instead of tanh, the same function to within fp32
-// rounding (no cancellation: the 1 + tanh sum is formed exactly).
+// exp2 and one reciprocal instead of tanh, the same function to within a few
+// fp32 ulp (no cancellation: the 1 + tanh sum is formed exactly).
 __device__ __forceinline__ float gelu_tanh(float x) {
   float u = 0.7978845608f * (x + 0.044715f * x * x * x);
   u = fminf(fmaxf(u, -10.f), 10.f);
-  return x / (1.f + expf(-2.f * u));
+  // exp(-2u) as the hardware exp2 of -2u log2(e) and the division as the
+  // hardware reciprocal (about 1 ulp each): with u clamped to +-10 the
+  // exponent stays within +-28.9, so neither underflows nor overflows, and
+  // the result stays within a few ulp of x / (1 + exp(-2u))
+  return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(u * -2.8853900817779268f));
 }
 
 // Read-ahead blocks: a launch may carry extra blocks that read one dword of
