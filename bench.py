@@ -69,6 +69,8 @@ SEQ = 128
 CALIB_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "mlp_dw_gemm_traffic.json")
 PROJ_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gpt2_proj_gemm_traffic.json")
+C5_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c5_quantize_traffic.json")
+C4_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c4_decode_step_traffic.json")
 BF16X3_CEILING_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 3
 
 
@@ -96,6 +98,17 @@ def load_traffic(path=TRAFFIC_FILE):
             t = json.load(f)
         return float(t["bytes_per_launch"]), t
     except (OSError, KeyError, ValueError):
+        return None, None
+
+
+def load_step_traffic(path=C4_TRAFFIC_FILE):
+    """HBM bytes per C4 decode step (median over the profiled steps) from a
+    committed PMC summary."""
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return float(np.median([s["bytes"] for s in t["steps"]])), t
+    except (OSError, KeyError, ValueError, TypeError):
         return None, None
 
 
@@ -755,6 +768,7 @@ def c4_generate(args):
         raise RuntimeError("generated ids out of range")
 
     pre_flop, dec_flop, dec_bytes = c4_work(cfg, B, T, n)
+    step_traffic, _ = load_step_traffic()
     step_ms = dec_ms / n
     total_ms = pre_ms + dec_ms
     tok_s = B * (n + 1) / (total_ms * 1e-3)
@@ -797,7 +811,12 @@ def c4_generate(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": step_traffic,
+            "traffic_note": "HBM bytes per decode step measured at contexts 513-516 (op-by-op launches of the "
+                            "same kernels); the decode attention loads every cache row up to the cache length "
+                            "(640) and masks the rows past the context, so the per-step traffic does not grow "
+                            "with the context" if step_traffic else None,
+            "traffic_source": os.path.relpath(C4_TRAFFIC_FILE, ROOT) if step_traffic else None,
             "bytes_per_step_avg": int(dec_bytes / n),
             "flop_per_step_avg": int(dec_flop / n),
         },
@@ -1070,6 +1089,7 @@ def c5_pipeline(args):
     gemm_flop = 2.0 * Mx * N * N
     total_ms = q_ms + d_ms + gemm_ms
     q_gbs = qbytes / (q_ms * 1e-3) / 1e9
+    q_traffic, _ = load_traffic(C5_TRAFFIC_FILE)
     result = {
         "metric": "C5 int8 per-row quantize + dequantize + [64,8192]x[8192,8192]^T GEMM, ms, 1 MI355X",
         "value": round(total_ms, 5),
@@ -1105,7 +1125,8 @@ def c5_pipeline(args):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(q_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": q_traffic,
+            "traffic_source": os.path.relpath(C5_TRAFFIC_FILE, ROOT) if q_traffic else None,
             "bytes_per_launch": qbytes,
         },
     }
