@@ -554,9 +554,13 @@ __global__ void __launch_bounds__(256) gemm_x3_rows(GArgs p) {
 // (prefetch_block).  Tile ids run along the columns (tm = tile / tiles_n):
 // with cold weights this measured faster than dealing the row tiles of one
 // column strip to one XCD back to back (qkv's weight loads 8.7 vs 10.5 us),
-// whose simultaneous misses on the same lines are not merged.
+// whose simultaneous misses on the same lines are not merged.  Up to 6 k
+// steps per wave the kernel is held to 128 VGPRs (the epilogue operands are
+// loaded after the products), so two blocks share a CU and a 288- or
+// 384-block grid runs in one round (GPT-2 forward 0.6305 -> 0.6215 ms
+// against 144 VGPRs, one block per CU).
 template <int KPW>
-__global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
+__global__ void __launch_bounds__(512, KPW <= 6 ? 2 : 1) gemm_x3_rows_pk(GArgs p) {
   constexpr int W = 8;
   if (prefetch_block(p.pf)) return;
   const int64_t T = p.K >> 4;
@@ -582,17 +586,8 @@ __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
       al[i] = *(const bf16x8_t*)(as + i * 1024 + 512);
     }
   }
-  // 2. Epilogue operands of this thread's four outputs (waves 0..3), and
-  //    with a folded layer_norm the statistics of its row of A.
-  const int r = (threadIdx.x >> 3) & 31, q = threadIdx.x & 7;
-  const int64_t row = m0 + r, rc = row < p.M ? row : p.M - 1;
-  RowEpi ep;
-  RowStats rs;
-  if (wave < 4 && (p.splits == 1 || p.tile_cnt)) {
-    row_epi_load(p, row, n0 + 4 * q, ep);
-    if (p.rs_in) row_norm_load(p, rc, q, rs);
-  }
-  // 3. This wave's k steps.
+  __builtin_amdgcn_sched_barrier(0);  // every fragment load goes out before the first product
+  // 2. This wave's k steps.
   f32x16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.f;
@@ -601,6 +596,18 @@ __global__ void __launch_bounds__(512) gemm_x3_rows_pk(GArgs p) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[i], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[i], acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[i], acc, 0, 0, 0);
+  }
+  // 3. Epilogue operands of this thread's four outputs (waves 0..3), and
+  //    with a folded layer_norm the statistics of its row of A, loaded once
+  //    the fragments' registers are free (their latency then overlaps the
+  //    partial tiles' meeting in LDS), so that two blocks fit on a CU.
+  const int r = (threadIdx.x >> 3) & 31, q = threadIdx.x & 7;
+  const int64_t row = m0 + r, rc = row < p.M ? row : p.M - 1;
+  RowEpi ep;
+  RowStats rs;
+  if (wave < 4 && (p.splits == 1 || p.tile_cnt)) {
+    row_epi_load(p, row, n0 + 4 * q, ep);
+    if (p.rs_in) row_norm_load(p, rc, q, rs);
   }
   // 4. Partials to LDS: register e of lane l is row 8 (e / 4) + 4 (l / 32) +
   //    e % 4, column l % 32.
