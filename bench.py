@@ -102,13 +102,16 @@ def load_traffic(path=TRAFFIC_FILE):
 
 
 def load_step_traffic(path=C4_TRAFFIC_FILE):
-    """HBM bytes per C4 decode step (median over the profiled steps) from a
-    committed PMC summary."""
+    """HBM bytes of one C4 decode step from a committed PMC summary: the
+    profiled step at the median context, with that context and its ratio to
+    the step's algorithmic bytes."""
     try:
         with open(path) as f:
             t = json.load(f)
-        return float(np.median([s["bytes"] for s in t["steps"]])), t
-    except (OSError, KeyError, ValueError, TypeError):
+        steps = sorted(t["steps"], key=lambda s: s["context"])
+        s = steps[len(steps) // 2]
+        return float(s["bytes"]), {"context": s["context"], "ratio": s["ratio"]}
+    except (OSError, KeyError, ValueError, TypeError, IndexError):
         return None, None
 
 
@@ -768,7 +771,7 @@ def c4_generate(args):
         raise RuntimeError("generated ids out of range")
 
     pre_flop, dec_flop, dec_bytes = c4_work(cfg, B, T, n)
-    step_traffic, _ = load_step_traffic()
+    step_traffic, step_tinfo = load_step_traffic()
     step_ms = dec_ms / n
     total_ms = pre_ms + dec_ms
     tok_s = B * (n + 1) / (total_ms * 1e-3)
@@ -812,10 +815,11 @@ def c4_generate(args):
             "unit": "GB/s",
             "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
             "traffic": step_traffic,
-            "traffic_note": "HBM bytes per decode step measured at contexts 513-516 (op-by-op launches of the "
-                            "same kernels); the decode attention loads every cache row up to the cache length "
-                            "(640) and masks the rows past the context, so the per-step traffic does not grow "
-                            "with the context" if step_traffic else None,
+            "traffic_context": step_tinfo["context"] if step_traffic else None,
+            "traffic_ratio": step_tinfo["ratio"] if step_traffic else None,
+            "traffic_note": "HBM bytes of one decode step at the context given (op-by-op launches of the same "
+                            "kernels); it grows with the context at the K/V rows' rate, and traffic_ratio is its "
+                            "ratio to that step's algorithmic bytes" if step_traffic else None,
             "traffic_source": os.path.relpath(C4_TRAFFIC_FILE, ROOT) if step_traffic else None,
             "bytes_per_step_avg": int(dec_bytes / n),
             "flop_per_step_avg": int(dec_flop / n),
