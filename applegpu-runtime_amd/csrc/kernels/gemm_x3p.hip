@@ -889,12 +889,15 @@ namespace {
 // halves the L2 -> CU traffic, which bounds this kernel (measured on MI355X,
 // M = N = 4096, K = 256 with the SGD epilogue: 54 us per-wavefront, 41 us
 // shared; 256 x 128 and 256 x 256 tiles were not faster).  The residual and
-// bias are loaded after the products and each output is written once by the
-// lane whose accumulator holds it.
+// bias are loaded after the products, one 32-row half at a time, and each
+// output is written once by the lane whose accumulator holds it.  One k step
+// per LDS stage (32 KB) and 120 VGPRs let four blocks share a CU, so the
+// 1024-tile MLP update runs in one round: C3 step 0.2537 -> 0.2477 ms against
+// two k steps per stage (64 KB) at two blocks per CU.
 template <int T>
-__global__ void __launch_bounds__(256) gemm_x3_outer_kernel(GArgs p, const bf16_t* __restrict__ apk,
+__global__ void __launch_bounds__(256, 3) gemm_x3_outer_kernel(GArgs p, const bf16_t* __restrict__ apk,
                                                            const bf16_t* __restrict__ bpk) {
-  constexpr int S = 2;                  // k steps per stage
+  constexpr int S = 1;                  // k steps per stage
   constexpr int STAGE = S * 16 * 512;   // bf16 elements per stage
   constexpr int NST = T / S;
   static_assert(T % S == 0, "whole stages");
@@ -976,33 +979,33 @@ __global__ void __launch_bounds__(256) gemm_x3_outer_kernel(GArgs p, const bf16_
   // register e of subtile (i, j): row 32 i + 8 (e / 4) + 4 (lane / 32) + e % 4,
   // column 32 j + lane % 32 of the wavefront's 64 x 64 quarter
   const int64_t rbase = tm * 128 + wm * 64 + 4 * (lane >> 5), cbase = tn * 128 + wn * 64 + (lane & 31);
-  float res[2][2][16];
-  if (p.res) {
-    const float* R = (const float*)p.res;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          res[i][j][e] = R[(rbase + 32 * i + 8 * (e >> 2) + (e & 3)) * p.r_sm + cbase + 32 * j];
-  }
   float bias[2] = {0.f, 0.f};
   if (p.bias) {
     bias[0] = ((const float*)p.bias)[cbase];
     bias[1] = ((const float*)p.bias)[cbase + 32];
   }
+  // one 32-row half of the quarter at a time (half the residual registers)
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i) {
+    float res[2][16];
+    if (p.res) {
+      const float* R = (const float*)p.res;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          res[j][e] = R[(rbase + 32 * i + 8 * (e >> 2) + (e & 3)) * p.r_sm + cbase + 32 * j];
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         EpiIn<float> in;
         in.bias = bias[j];
-        in.res = p.res ? res[i][j][e] : 0.f;
+        in.res = p.res ? res[j][e] : 0.f;
         epilogue_finish<float>(p, 0, rbase + 32 * i + 8 * (e >> 2) + (e & 3), cbase + 32 * j, acc[i][j][e], in);
       }
+  }
 }
 
 }  // namespace
