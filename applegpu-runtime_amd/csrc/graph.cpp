@@ -721,12 +721,12 @@ void eval_all(const std::vector<TensorP>& roots) {
   }
 
   // Read-ahead of packed weights: a launch that leaves most CUs idle (a
-  // split-K layer_norm reduction, the fused embedding) gets
+  // split-K layer_norm reduction, the fused embedding, a row panel) gets
   // extra blocks that read the packed weights of the GEMMs after it, up to
   // and including the next such launch, so that those GEMMs find their
   // weights in the Infinity Cache instead of HBM (GPT-2 small forward
-  // 0.695 -> 0.681 ms; spreading the reads more evenly over the launches
-  // measured slower).  Results are unchanged.
+  // 0.695 -> 0.681 ms with the reduction and embedding launches carrying).
+  // Results are unchanged.
   std::vector<k::Prefetch> pf_for(order.size());
   {
     auto x3_weights = [&](size_t j) -> const Tensor* {
@@ -742,10 +742,15 @@ void eval_all(const std::vector<TensorP>& roots) {
       auto git = groups.find(t);
       if (git != groups.end()) {
         if (post_ln.count(t)) return true;
-        // a split packed-row panel that finishes its tiles in its own launch
-        // leaves CUs idle too
+        // A packed-row panel with a layer_norm folded in, and a split panel
+        // that finishes its tiles in its own launch, leave CUs idle too.
+        // GPT-2 small forward 0.6124 -> 0.5885 ms with the folded panels
+        // (c_attn, c_fc) carrying; the unfolded c_proj panel carrying as
+        // well measured 0.598 ms, the attention launch carrying in place of
+        // c_attn 0.613 ms.
         const Group& g = git->second;
-        if (g.a_rows < 1 || g.packed_n <= 0 || !ops::is_x3_packed(g.b) || g.norm_stats) return false;
+        if (g.a_rows < 1 || g.packed_n <= 0 || !ops::is_x3_packed(g.b)) return false;
+        if (g.norm_stats) return true;
         const int64_t K = g.b->shape[1] * 16;
         return k::gemm_x3_rows_out_ok(g.a_rows, g.packed_n, K, true) &&
                !k::gemm_x3_panel_ok(g.a_rows, g.packed_n, K, true);

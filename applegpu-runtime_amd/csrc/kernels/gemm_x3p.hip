@@ -1203,9 +1203,10 @@ static void launch_rows_pk(const X3Plan& pl, const GArgs& p0, hipStream_t s) {
   GArgs p = p0;
   const int64_t main = pl.tiles_m * pl.tiles_n * pl.splits;
   if (main > 0x7fffff00) fail("gemm_x3_rows_pk: grid too large");
-  // a split finished in the launch leaves CUs idle: read ahead there
-  if (p.tile_cnt) p.pf = make_prefetch((int)main, 512);
-  const dim3 grid((unsigned)(main + (p.tile_cnt ? p.pf.blocks : 0)));
+  // blocks beyond the tiles read ahead what the graph walk asked this launch
+  // to (none when it asked nothing)
+  p.pf = make_prefetch((int)main, 512);
+  const dim3 grid((unsigned)(main + p.pf.blocks));
   switch (pl.kpw) {
     case 1: hipLaunchKernelGGL((gemm_x3_rows_pk<1>), grid, dim3(512), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gemm_x3_rows_pk<2>), grid, dim3(512), 0, s, p); break;
