@@ -527,11 +527,91 @@ struct FaTile32 {
   }
 };
 
+// The end of the key-split kernels: wavefronts 1..3 hand their running
+// maximum, sum and output to wavefront 0 through LDS (`red`: 3 * 64 *
+// (D/4 + 2) floats), which rescales and adds them in wavefront order.
+// Returns false on the wavefronts that handed theirs over.
+template <int D>
+__device__ __forceinline__ bool fa32_merge(float* red, int w, int lane, float m, float& l, f32x4v (&acc)[D / 16]) {
+  constexpr int DT = D / 16;
+  constexpr int PER = DT * 4 + 2;
+  if (w > 0) {
+    float* dst = red + ((w - 1) * 64 + lane) * PER;
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[u * 4 + r] = acc[u][r];
+    dst[DT * 4] = m;
+    dst[DT * 4 + 1] = l;
+  }
+  __syncthreads();
+  if (w > 0) return false;
+  float mw[kFaWaves], lw[kFaWaves];
+  mw[0] = m;
+  lw[0] = l;
+#pragma unroll
+  for (int v = 1; v < kFaWaves; ++v) {
+    const float* src = red + ((v - 1) * 64 + lane) * PER;
+    mw[v] = src[DT * 4];
+    lw[v] = src[DT * 4 + 1];
+  }
+  float M = mw[0];
+#pragma unroll
+  for (int v = 1; v < kFaWaves; ++v) M = fmaxf(M, mw[v]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float sc[kFaWaves];
+  l = 0.f;
+#pragma unroll
+  for (int v = 0; v < kFaWaves; ++v) {
+    sc[v] = __builtin_amdgcn_exp2f(mw[v] - Mu);
+    l += lw[v] * sc[v];
+  }
+#pragma unroll
+  for (int u = 0; u < DT; ++u) acc[u] *= sc[0];
+#pragma unroll
+  for (int v = 1; v < kFaWaves; ++v) {
+    const float* src = red + ((v - 1) * 64 + lane) * PER;
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[u][r] += src[u * 4 + r] * sc[v];
+  }
+  return true;
+}
+
+// Query row qi's output from the lane's O^T registers (register r of tile u:
+// dimension (D/16)*(4g + r) + u), divided by the softmax sum l: fp32, or
+// packed x3 rows when p.o_pk is set.
+template <int D>
+__device__ __forceinline__ void fa32_store(const AArgs& p, int64_t b, int64_t h, int64_t qi, int g, float l,
+                                           const f32x4v (&acc)[D / 16]) {
+  constexpr int DT = D / 16;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qi >= p.Tq) return;
+  float* O = (float*)p.o + b * p.o_sb + h * p.o_sh + qi * p.o_st;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float o[DT];
+#pragma unroll
+    for (int u = 0; u < DT; ++u) o[u] = acc[u][r] * inv;
+#pragma unroll
+    for (int u = 0; u < DT; u += 4) {
+      if (p.o_pk) {
+        const float o4[4] = {o[u], o[u + 1], o[u + 2], o[u + 3]};
+        x3_store4(p.o_pk, p.H * D / 16, b * p.Tq + qi, h * D + DT * (4 * g + r) + u, o4);
+      } else {
+        *(float4*)(O + DT * (4 * g + r) + u) = make_float4(o[u], o[u + 1], o[u + 2], o[u + 3]);
+      }
+    }
+  }
+}
+
 // KSPLIT: the block's 4 wavefronts share one group of 16 queries and split
 // every key tile four ways (wavefront w takes its keys 16w..16w+15), then
 // merge their running maxima, sums and outputs through LDS.  Used when there
 // are too few 64-query blocks to fill the GPU (GPT-2 at 128 tokens: 24):
-// each wavefront then does a quarter of the serial work.
+// each wavefront then does a quarter of the serial work.  At D = 64 that
+// case runs flash_attn_f32_kr below instead, with its operands in registers.
 // NSP > 0: Q, K and V are read as split-K partials plus bias (ld_part4).
 template <int D, bool KSPLIT, int NSP>
 __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
@@ -699,71 +779,149 @@ __global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32(AArgs p) {
   float l = ls + __shfl_xor(ls, 16, 64);
   l += __shfl_xor(l, 32, 64);
   if constexpr (KSPLIT) {
-    // merge the four wavefronts' states (the tile buffers are free after the
-    // loop's last barrier): wave w > 0 hands (m, l, acc) to wave 0
-    float* red = &Ks[0][0];
-    constexpr int PER = DT * 4 + 2;
-    if (w > 0) {
-      float* dst = red + ((w - 1) * 64 + lane) * PER;
-#pragma unroll
-      for (int u = 0; u < DT; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[u * 4 + r] = acc[u][r];
-      dst[DT * 4] = m;
-      dst[DT * 4 + 1] = l;
-    }
-    __syncthreads();
-    if (w > 0) return;
-    float mw[kFaWaves], lw[kFaWaves];
-    mw[0] = m;
-    lw[0] = l;
-#pragma unroll
-    for (int v = 1; v < kFaWaves; ++v) {
-      const float* src = red + ((v - 1) * 64 + lane) * PER;
-      mw[v] = src[DT * 4];
-      lw[v] = src[DT * 4 + 1];
-    }
-    float M = mw[0];
-#pragma unroll
-    for (int v = 1; v < kFaWaves; ++v) M = fmaxf(M, mw[v]);
-    const float Mu = M == -INFINITY ? 0.f : M;
-    float sc[kFaWaves];
-    l = 0.f;
-#pragma unroll
-    for (int v = 0; v < kFaWaves; ++v) {
-      sc[v] = __builtin_amdgcn_exp2f(mw[v] - Mu);
-      l += lw[v] * sc[v];
-    }
-#pragma unroll
-    for (int u = 0; u < DT; ++u) acc[u] *= sc[0];
-#pragma unroll
-    for (int v = 1; v < kFaWaves; ++v) {
-      const float* src = red + ((v - 1) * 64 + lane) * PER;
-#pragma unroll
-      for (int u = 0; u < DT; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[u][r] += src[u * 4 + r] * sc[v];
-    }
+    // the tile buffers are free after the loop's last barrier
+    if (!fa32_merge<D>(&Ks[0][0], w, lane, m, l, acc)) return;
   }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  if (qi >= p.Tq) return;
-  float* O = (float*)p.o + b * p.o_sb + h * p.o_sh + qi * p.o_st;
-  // register r of O^T tile u: dimension DT*(4g + r) + u
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float o[DT];
-#pragma unroll
-    for (int u = 0; u < DT; ++u) o[u] = acc[u][r] * inv;
-#pragma unroll
-    for (int u = 0; u < DT; u += 4) {
-      if (p.o_pk) {
-        const float o4[4] = {o[u], o[u + 1], o[u + 2], o[u + 3]};
-        x3_store4(p.o_pk, p.H * D / 16, b * p.Tq + qi, h * D + DT * (4 * g + r) + u, o4);
-      } else {
-        *(float4*)(O + DT * (4 * g + r) + u) = make_float4(o[u], o[u + 1], o[u + 2], o[u + 3]);
-      }
-    }
+  fa32_store<D>(p, b, h, qi, g, l, acc);
+}
+
+// Key-split fp32 attention with register operands (D = 64): the case of
+// flash_attn_f32<64, true, NSP> without its LDS tiles.  Wavefront w of the
+// block takes the 16-key sub-tiles w, w+4, w+8, ... of the block's 16
+// queries, which is the share of every 64-key tile it takes there, so no
+// sub-tile is read by two wavefronts: each loads its K and V operands from
+// global memory straight into registers, the next sub-tile's loads in
+// flight while the current one's products run, and the block meets only
+// for the merge.  The products, masks and online-softmax updates are the
+// LDS kernel's, in the same order.
+template <int NSP>
+__global__ void __launch_bounds__(64 * kFaWaves) flash_attn_f32_kr(AArgs p) {
+  if (prefetch_block(p.pf)) return;
+  constexpr int D = 64, DS = D / 4, DT = D / 16;
+  __shared__ __attribute__((aligned(16))) float red[(kFaWaves - 1) * 64 * (DT * 4 + 2)];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int64_t BH = p.B * p.H;
+  const int64_t bh = blockIdx.x % BH;
+  const int64_t tq = blockIdx.x / BH;
+  const int64_t qt = p.causal ? p.q_tiles - 1 - tq : tq;
+  const int64_t b = bh / p.H, h = bh % p.H;
+  const int64_t q0 = qt * 16;
+
+  const float* Q = (const float*)p.q + b * p.q_sb + h * p.q_sh;
+  const float* K = (const float*)p.k + b * p.k_sb + h * p.k_sh;
+  const float* V = (const float*)p.v + b * p.v_sb + h * p.v_sh;
+  const float* QB = NSP > 0 ? p.qb + h * p.b_sh : Q;
+  const float* KB = NSP > 0 ? p.kb + h * p.b_sh : K;
+  const float* VB = NSP > 0 ? p.vb + h * p.b_sh : V;
+
+  int64_t kv_end = p.Tk;
+  if (p.causal) {
+    const int64_t qe = q0 + 16 < p.Tq ? q0 + 16 : p.Tq;
+    kv_end = qe < p.Tk ? qe : p.Tk;
   }
+  const int nsub = (int)((kv_end + 15) / 16);
+
+  // sub-tile t's operands of this lane: K row 16t + l16, dims 16g .. 16g+15;
+  // V rows 16t + 4g + r (r = 0..3), dims 4*l16 .. 4*l16+3 (rows past Tk
+  // repeat row Tk-1 and are masked)
+  float4 ka0, ka1, ka2, ka3, va0, va1, va2, va3;
+  float4 kb0, kb1, kb2, kb3, vb0, vb1, vb2, vb3;
+#define AGPU_FA32R_LD(S, t)                                                                 \
+  {                                                                                         \
+    const int64_t jk = 16 * (int64_t)(t) + l16 < p.Tk ? 16 * (int64_t)(t) + l16 : p.Tk - 1; \
+    const float* kr = K + jk * p.k_st + DS * g;                                             \
+    k##S##0 = ld_part4<NSP>(kr, p.plane, KB + DS * g);                                      \
+    k##S##1 = ld_part4<NSP>(kr + 4, p.plane, KB + DS * g + 4);                              \
+    k##S##2 = ld_part4<NSP>(kr + 8, p.plane, KB + DS * g + 8);                              \
+    k##S##3 = ld_part4<NSP>(kr + 12, p.plane, KB + DS * g + 12);                            \
+    const int64_t jv = 16 * (int64_t)(t) + 4 * g;                                           \
+    const float* vr = V + DT * l16;                                                         \
+    v##S##0 = ld_part4<NSP>(vr + (jv < p.Tk ? jv : p.Tk - 1) * p.v_st, p.plane, VB + DT * l16);         \
+    v##S##1 = ld_part4<NSP>(vr + (jv + 1 < p.Tk ? jv + 1 : p.Tk - 1) * p.v_st, p.plane, VB + DT * l16); \
+    v##S##2 = ld_part4<NSP>(vr + (jv + 2 < p.Tk ? jv + 2 : p.Tk - 1) * p.v_st, p.plane, VB + DT * l16); \
+    v##S##3 = ld_part4<NSP>(vr + (jv + 3 < p.Tk ? jv + 3 : p.Tk - 1) * p.v_st, p.plane, VB + DT * l16); \
+  }
+  if (w < nsub) AGPU_FA32R_LD(a, w)
+
+  // query row l16, dims 16g .. 16g+15
+  const int64_t qi = q0 + l16;
+  const int64_t qr = qi < p.Tq ? qi : p.Tq - 1;
+  float qf[DS];
+#pragma unroll
+  for (int s = 0; s < DS; s += 4) {
+    const float4 x = ld_part4<NSP>(Q + qr * p.q_st + g * DS + s, p.plane, QB + g * DS + s);
+    qf[s] = x.x; qf[s + 1] = x.y; qf[s + 2] = x.z; qf[s + 3] = x.w;
+  }
+  const int lim = (int)(p.causal ? (qi + 1 < p.Tk ? qi + 1 : p.Tk) : p.Tk);
+
+  f32x4v acc[DT];
+#pragma unroll
+  for (int u = 0; u < DT; ++u) acc[u] = f32x4v{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, ls = 0.f;
+  const float c2 = p.scale * 1.4426950408889634f;
+
+  auto sub = [&](int t, const float4& k0, const float4& k1, const float4& k2, const float4& k3, const float4& v0,
+                 const float4& v1, const float4& v2, const float4& v3) {
+    f32x4v st = f32x4v{0.f, 0.f, 0.f, 0.f};
+    const float4 kk[4] = {k0, k1, k2, k3};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[i].x, qf[4 * i], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[i].y, qf[4 * i + 1], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[i].z, qf[4 * i + 2], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[i].w, qf[4 * i + 3], st, 0, 0, 0);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = st[r] * c2;
+      v = 16 * t + 4 * g + r < lim ? v : -INFINITY;
+      st[r] = v;
+      mx = fmaxf(mx, v);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - mu);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pv = __builtin_amdgcn_exp2f(st[r] - mu);
+      ps += pv;
+      st[r] = pv;
+    }
+    ls = ls * alpha + ps;
+#pragma unroll
+    for (int u = 0; u < DT; ++u) acc[u] *= alpha;
+    const float4 vv[4] = {v0, v1, v2, v3};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r].x, st[r], acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r].y, st[r], acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r].z, st[r], acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[r].w, st[r], acc[3], 0, 0, 0);
+    }
+  };
+
+  for (int t = w; t < nsub; t += 2 * kFaWaves) {
+    if (t + kFaWaves < nsub) AGPU_FA32R_LD(b, t + kFaWaves)
+    __builtin_amdgcn_sched_barrier(0);
+    sub(t, ka0, ka1, ka2, ka3, va0, va1, va2, va3);
+    if (t + kFaWaves >= nsub) break;
+    if (t + 2 * kFaWaves < nsub) AGPU_FA32R_LD(a, t + 2 * kFaWaves)
+    __builtin_amdgcn_sched_barrier(0);
+    sub(t + kFaWaves, kb0, kb1, kb2, kb3, vb0, vb1, vb2, vb3);
+  }
+#undef AGPU_FA32R_LD
+
+  float l = ls + __shfl_xor(ls, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  if (!fa32_merge<D>(red, w, lane, m, l, acc)) return;
+  fa32_store<D>(p, b, h, qi, g, l, acc);
 }
 }  // namespace
 
@@ -804,13 +962,27 @@ static void launch_fa32_d(const AArgs& p, int nsp, unsigned blocks, hipStream_t 
   }
 }
 
+static void launch_fa32_kr(const AArgs& p, int nsp, unsigned blocks, hipStream_t s) {
+  const dim3 grid(blocks), block(64 * kFaWaves);
+  switch (nsp) {
+    case 0: hipLaunchKernelGGL((flash_attn_f32_kr<0>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((flash_attn_f32_kr<2>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((flash_attn_f32_kr<4>), grid, block, 0, s, p); break;
+    case 8: hipLaunchKernelGGL((flash_attn_f32_kr<8>), grid, block, 0, s, p); break;
+    default: fail("fused attention: %d projection partials (2, 4 or 8 supported)", nsp);
+  }
+}
+
 template <bool KS>
 static void launch_fa32(const AArgs& p0, const Attn& a, unsigned blocks, hipStream_t s) {
   AArgs p = p0;
   p.pf = make_prefetch((int)blocks, 64 * kFaWaves);
   blocks += (unsigned)p.pf.blocks;
-  if (a.D == 64) launch_fa32_d<KS, 64>(p, a.nsplit, blocks, s);
-  else launch_fa32_d<KS, 128>(p, a.nsplit, blocks, s);
+  // key split at D = 64: operands in registers (GPT-2 small forward
+  // 0.6129 -> 0.6039 ms against the LDS-tiled kernel, A/B on one box)
+  if (a.D != 64) launch_fa32_d<KS, 128>(p, a.nsplit, blocks, s);
+  else if constexpr (KS) launch_fa32_kr(p, a.nsplit, blocks, s);
+  else launch_fa32_d<false, 64>(p, a.nsplit, blocks, s);
 }
 
 bool attention_partials_ok(const Attn& a) { return a.dt == DType::F32 && attention_mfma_ok(a); }
