@@ -721,7 +721,8 @@ void eval_all(const std::vector<TensorP>& roots) {
   }
 
   // Read-ahead of packed weights: a launch that leaves most CUs idle (a
-  // split-K layer_norm reduction, the fused embedding, a row panel) gets
+  // split-K layer_norm reduction, the fused embedding, a row panel, the
+  // decode attention) gets
   // extra blocks that read the packed weights of the GEMMs after it, up to
   // and including the next such launch, so that those GEMMs find their
   // weights in the Infinity Cache instead of HBM (GPT-2 small forward
@@ -733,7 +734,9 @@ void eval_all(const std::vector<TensorP>& roots) {
       auto it = groups.find(order[j].get());
       if (it == groups.end() || absorbed.count(order[j].get())) return nullptr;
       const Group& g = it->second;
-      if (g.packed_n <= 0 || !ops::is_x3_packed(g.b) || g.b->pending() || !g.b->buf) return nullptr;
+      // packed weights of either layout: fp32 hi/lo (row panels) or 16-bit
+      // decode-packed (skinny GEMMs)
+      if (g.packed_n <= 0 || g.b->pending() || !g.b->buf) return nullptr;
       return g.b.get();
     };
     auto reads_ahead = [&](size_t j) {
@@ -755,6 +758,12 @@ void eval_all(const std::vector<TensorP>& roots) {
         return k::gemm_x3_rows_out_ok(g.a_rows, g.packed_n, K, true) &&
                !k::gemm_x3_panel_ok(g.a_rows, g.packed_n, K, true);
       }
+      // the whole-row decode attention runs 160 blocks for GPT-2 large's
+      // 8 x 20 heads: it reads ahead the projection's weights (C4 decode
+      // step 1.2746 -> 1.2660 and 1.3291 -> 1.3261 ms, alternating runs on
+      // two boxes; reading c_fc's as well measured 1.2977, and the 80-block
+      // projection and fc2 skinny launches as carriers 1.3793)
+      if (t->node && t->node->code == OP_DECODE_ATTENTION) return true;
       return emb_adds.count(t) > 0;
     };
     for (size_t i = 0; i < order.size(); ++i) {

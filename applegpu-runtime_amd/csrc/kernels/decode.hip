@@ -53,6 +53,8 @@ struct DArgs {
   // and head); they become cache row lens[b] - 1
   const void* kn; const void* vn;
   int64_t kn_sb, kn_sh, vn_sb, vn_sh;
+  // read-ahead blocks (whole-row launches): rows pf.first .. of the grid's y
+  PfArgs pf;
 };
 
 // 8 consecutive elements, raw: one 16-byte load (two for fp32) when VEC.
@@ -190,6 +192,10 @@ __global__ void __launch_bounds__(64 * NW) decode_attn(DArgs p) {
   __shared__ float sm_acc[NW][D];
   __shared__ float sm_m[NW], sm_l[NW];
 
+  if ((int)blockIdx.y >= p.pf.first) {
+    prefetch_lines(p.pf, (int64_t)blockIdx.y - p.pf.first);
+    return;
+  }
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int g = lane / LPK, sub = lane % LPK;
   const int s = blockIdx.x;
@@ -402,8 +408,13 @@ __global__ void __launch_bounds__(256) kv_write_kernel(KvArgs<E> a) {
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <typename T, int D, bool NEW>
-void launch_decode_n(const DArgs& p, bool vec, int64_t rows, bool whole, hipStream_t s) {
-  const dim3 grid((unsigned)p.splits, (unsigned)rows);
+void launch_decode_n(const DArgs& p0, bool vec, int64_t rows, bool whole, hipStream_t s) {
+  DArgs p = p0;
+  p.pf.first = 0x7fffffff;
+  // a whole-row launch leaves CUs idle: blocks past the rows read ahead
+  // what the graph walk asked this launch to
+  if (whole && p.splits == 1) p.pf = make_prefetch((int)rows, 64 * kDWavesWhole);
+  const dim3 grid((unsigned)p.splits, (unsigned)(rows + (whole && p.splits == 1 ? p.pf.blocks : 0)));
   constexpr int NWW = kDWavesWhole, UW = kDUnrollWhole, NWS = kDWavesSplit, US = kDUnrollSplit;
   // 6 key steps per wave when that covers the whole cache in one iteration
   constexpr int UW6 = kDUnrollWhole6;

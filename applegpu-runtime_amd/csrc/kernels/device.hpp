@@ -59,6 +59,17 @@ struct PfArgs {
   int first;   // first read-ahead block (gridDim.x when there are none)
   int blocks;  // read-ahead blocks
 };
+// The reads of read-ahead block `b` (0 .. pf.blocks - 1).
+__device__ __forceinline__ void prefetch_lines(const PfArgs& pf, int64_t b) {
+  const int64_t stride = (int64_t)pf.blocks * blockDim.x;
+  const int64_t t0 = b * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  for (int r = 0; r < pf.n; ++r) {
+#pragma unroll 4
+    for (int64_t l = t0; l < pf.lines[r]; l += stride) acc ^= *(const uint32_t*)(pf.p[r] + (l << 6));
+  }
+  asm volatile("" ::"v"(acc));
+}
 __device__ __forceinline__ bool prefetch_block(const PfArgs& pf) {
   if ((int)blockIdx.x < pf.first) return false;
   const int64_t stride = (int64_t)pf.blocks * blockDim.x;
