@@ -189,6 +189,14 @@ def linear_mse_backward_sgd_(h, w, b, y, alpha=1.0, grad_in=True):
     return loss, (gi if grad_in else None)
 
 
+def mlp2_sgd_step_(x, y, w1, b1, w2, b2, alpha=1.0):
+    """One SGD step of Linear(w1, b1) -> ReLU -> Linear(w2, b2) with MSE
+    loss against y, in place (w += alpha * grad, every gradient from the
+    step's starting parameters); returns the loss [1].  Small fp32 shapes
+    (activations within 64 KB) run as one launch."""
+    return op("mlp2_sgd_step_", [x, y, w1, b1, w2, b2], f=(float(alpha),))
+
+
 def sgd_sum_rows_(bias, g, alpha=1.0):
     """bias += alpha * g.sum(0) in place: an SGD bias step fused with its
     gradient reduction."""

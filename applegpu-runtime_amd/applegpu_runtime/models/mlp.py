@@ -15,6 +15,8 @@ through the eager C ABI, with the fusions the MI355X backend offers:
   + SGD     W += -lr * g^T h            one GEMM, the update in its epilogue
             b += -lr * sum(g, 0)        one column reduction
 (the output layer's 4096 -> 1 products run on the unit-extent GEMM kernels).
+A two-layer net is one op, mlp2_sgd_step_: at small sizes (config C1,
+64 -> 128 -> 10 at batch 32) the whole step runs in one workgroup, one launch.
 Every gradient is formed from the step's starting parameters, as autograd
 does: layer i's input gradient (which reads W_i) is computed before W_i is
 updated in place.
@@ -61,6 +63,10 @@ class EagerMLP:
     def train_step(self, x, y, lr=0.01):
         """One forward + MSE + backward + SGD step; returns the loss tensor (on device)."""
         n = len(self.params)
+        if n == 2:
+            # Linear -> ReLU -> Linear: one op (one launch at small sizes)
+            (w1, b1), (w2, b2) = self.params
+            return E.mlp2_sgd_step_(x, y, w1, b1, w2, b2, -lr)
         acts = [x]
         h = x
         for w, b in self.params[:-1]:

@@ -307,6 +307,20 @@ void linear1_backward_sgd(DType dt, const Lin1Bwd& a, hipStream_t s);
 // launch (one block per row): z[r] = h[r, :] . w + b[0], dz[r] = (z[r] -
 // y[r]) * two_over_n.  h [R, N] with row stride h_sm and unit column
 // stride; w [N], b [1], y, z and dz [R] contiguous.
+// One SGD step of Linear(N0 -> N1) -> ReLU -> Linear(N1 -> N2) with MSE
+// loss over all R x N2 outputs, in one workgroup (mlp_step.hip): x [R, N0],
+// y [R, N2], W1 [N1, N0], b1 [N1], W2 [N2, N1], b2 [N2] contiguous fp32, the
+// parameters updated in place (w += alpha * grad), loss [1] written.
+struct Mlp2Step {
+  const float* x; const float* y;
+  float* w1; float* b1; float* w2; float* b2;
+  float* loss;
+  int R, N0, N1, N2;
+  float alpha;
+};
+// Whether the shape fits the one-workgroup step (activations in 64 KB of LDS).
+bool mlp2_step_ok(int64_t R, int64_t N0, int64_t N1, int64_t N2);
+void mlp2_step(const Mlp2Step& a, hipStream_t s);
 struct Lin1Fwd {
   const void* h; int64_t h_sm;
   const void* w; const void* b; const void* y;

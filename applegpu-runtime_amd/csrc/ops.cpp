@@ -770,6 +770,38 @@ TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& 
   return mask ? gin : w;
 }
 
+TensorP mlp2_sgd_step_(const TensorP& x, const TensorP& y, const TensorP& w1, const TensorP& b1, const TensorP& w2,
+                       const TensorP& b2, float alpha) {
+  const char* name = "mlp2_sgd_step_";
+  if (x->ndim != 2 || w1->ndim != 2 || w2->ndim != 2 || y->ndim != 2) fail("%s: x, y, w1 and w2 must be 2-D", name);
+  const int64_t R = x->shape[0], N0 = x->shape[1], N1 = w1->shape[0], N2 = w2->shape[0];
+  if (w1->shape[1] != N0 || w2->shape[1] != N1 || b1->numel() != N1 || b2->numel() != N2 ||
+      y->dims() != std::vector<int64_t>{R, N2})
+    fail("%s: x %s, w1 %s, b1 %s, w2 %s, b2 %s and y %s do not form Linear -> ReLU -> Linear", name,
+         shape_str(x->dims()).c_str(), shape_str(w1->dims()).c_str(), shape_str(b1->dims()).c_str(),
+         shape_str(w2->dims()).c_str(), shape_str(b2->dims()).c_str(), shape_str(y->dims()).c_str());
+  const bool f32 = x->dtype == DType::F32 && y->dtype == DType::F32 && w1->dtype == DType::F32 &&
+                   b1->dtype == DType::F32 && w2->dtype == DType::F32 && b2->dtype == DType::F32;
+  const bool contig = x->is_contiguous() && y->is_contiguous() && w1->is_contiguous() && b1->is_contiguous() &&
+                      w2->is_contiguous() && b2->is_contiguous();
+  const bool al16 = (((uintptr_t)x->data() | (uintptr_t)w1->data() | (uintptr_t)w2->data()) & 15) == 0;
+  if (f32 && contig && al16 && k::mlp2_step_ok(R, N0, N1, N2)) {
+    TensorP loss = alloc_out(DType::F32, {1});
+    k::Mlp2Step a{(const float*)x->data(), (const float*)y->data(), (float*)w1->data(), (float*)b1->data(),
+                  (float*)w2->data(), (float*)b2->data(), (float*)loss->data(),
+                  (int)R, (int)N0, (int)N1, (int)N2, alpha};
+    LAUNCH k::mlp2_step(a, rt().stream());
+    return loss;
+  }
+  Epilogue e;
+  e.bias = b1;
+  e.act = k::kActRelu;
+  TensorP h = matmul(x, w1, false, true, &e);
+  auto r = linear_mse_backward_sgd_(h, w2, b2, y, alpha, true);
+  linear_backward_sgd_(w1, b1, r.second, x, nullptr, alpha);
+  return r.first;
+}
+
 std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const TensorP& w, const TensorP& b,
                                                      const TensorP& y, float alpha, bool grad_in) {
   if (h->ndim != 2 || w->ndim != 2) fail("linear_mse_backward_sgd_: h and w must be 2-D");

@@ -154,6 +154,12 @@ TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& 
 // mse_loss_grad and linear_backward_sgd_.
 std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const TensorP& w, const TensorP& b,
                                                      const TensorP& y, float alpha, bool grad_in);
+// One SGD step of Linear(w1, b1) -> ReLU -> Linear(w2, b2) with MSE loss
+// against y, in place (w += alpha * grad, every gradient from the step's
+// starting parameters); returns the loss [1].  Small fp32 shapes run as one
+// launch (k::mlp2_step_ok), others as the layer ops above.
+TensorP mlp2_sgd_step_(const TensorP& x, const TensorP& y, const TensorP& w1, const TensorP& b1, const TensorP& w2,
+                       const TensorP& b2, float alpha);
 // MSE loss and its gradient (upstream gradient 1): {loss [1], grad like a}.
 std::pair<TensorP, TensorP> mse_loss_grad(const TensorP& a, const TensorP& b);
 // Decode-step weights: wt [out N, in K] (fp16/bf16) rearranged for the skinny
