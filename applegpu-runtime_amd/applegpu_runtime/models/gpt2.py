@@ -119,7 +119,7 @@ def load_model(np_weights: dict, cfg: dict, dtype: str = "float32", kmajor=None,
                 p = gpu.pack_weight_x3(t)
                 p.eval()
                 pk[k] = (p, t.shape[1], "x3")
-        # the tied LM head as B = wte^T, for the weight-streaming GEMM
+        # the tied LM head as B = wte^T, for the vocabulary-head GEMM
         wte = w["transformer.wte.weight"]
         p = gpu.pack_weight_x3(gpu.transpose(wte))
         p.eval()

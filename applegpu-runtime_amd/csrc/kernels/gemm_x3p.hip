@@ -726,141 +726,160 @@ __global__ void __launch_bounds__(256) row_tile_stats_kernel(const float* __rest
   *(float2*)(out + gid * 2) = make_float2(sm_, d2);
 }
 
-// Weight-streaming panel for packed A and many columns (a vocabulary head:
-// 128 x 768 x 50257).  A row panel reads each weight strip once per 32-row
-// tile, so at four row tiles the weights would come from HBM four times; here
-// one block (four wavefronts) owns up to 128 rows (wave w: A strip w) and
-// NC column strips over the whole K, so each weight byte is read once.  K is
-// walked in chunks of KC k steps: chunk c's weight fragments are loaded into
-// registers S chunks ahead (256 threads share the loads), written to one of
-// two LDS buffers when chunk c comes up, and read from there by every wave;
-// each wave loads its own A fragments (small, L2-resident) S chunks ahead too.
-// One barrier per chunk.  Epilogue per element as gemm_x3p's unsplit path.
-// Launched as NC = 4 strips, KC = 1 step, S = 8 chunks ahead: for GPT-2's
-// head (cold weights) 50 us against 52-78 us for deeper chunks, fewer or more
-// strips, and 67 us for the fp32 tiled GEMM.
-template <int NC, int KC, int S>
-__global__ void __launch_bounds__(256, 2) gemm_x3_stream(GArgs p) {
-  constexpr int NV = NC * KC * 2 * 64;  // 16-byte fragment pieces per chunk
-  static_assert(NV % 256 == 0, "chunk split over 256 threads");
-  constexpr int PER = NV / 256;
-  __shared__ __attribute__((aligned(16))) bf16x8_t sB[2][NV];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Vocabulary head, one column strip per wavefront: 128 rows of packed A times
+// many 32-column weight strips (GPT-2's head: 128 x 768 x 50257, 1571
+// strips).  The grid has one 8-wavefront block per CU (256 per row tile);
+// block b owns the strips [b Sn / G, (b + 1) Sn / G) (6 or 7 for the head),
+// so every CU streams the same share of the weights, and wavefront w takes
+// strip w of the block's range, loading its weight fragments straight into
+// registers P k steps ahead: no LDS and no barrier on the weight stream.  The
+// 128 rows of A (393 KB for the head, more than LDS holds) go through LDS in
+// phases of P k steps (64 KB, two buffers): the next phase is loaded into
+// registers while the current one is read, and written to LDS at the phase's
+// end, one barrier per phase.  Each k step a wavefront reads the 8 A
+// fragments of its 4 row strips from LDS and runs 12 MFMAs, per element in
+// the row panels' order (lo.hi, hi.lo, hi.hi, k ascending).  Wavefronts past
+// the block's range only load A and meet the barriers.
+// Measured on MI355X in the GPT-2 forward (alternating runs on one box):
+// 0.5926 -> 0.5841 ms against 128 x 128 blocks sharing their weight
+// fragments through LDS (393 blocks, so 137 CUs ran two and set the time;
+// that kernel took 35 us at 256 blocks and 54 us at 393).  Pinning each
+// step's weight loads in place with scheduling barriers made it slower
+// (0.593 ms).
+template <int P, bool TAIL>
+__global__ void __launch_bounds__(512) gemm_x3_head(GArgs p, int64_t G) {
+  constexpr int PHASE = 4 * P * 1024;        // bf16 elements of A per phase: 4 strips x P steps x hi, lo
+  constexpr int PER = PHASE / (8 * 512);     // 16-byte pieces per thread per phase
+  __shared__ __attribute__((aligned(16))) bf16_t sA[2 * PHASE];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t T = p.K >> 4;
-  const int nch = (int)(T / KC);
+  const int nph = (int)((T + P - 1) / P);
   const int64_t Sm = (p.M + 31) / 32, Sn = (p.N + 31) / 32;
-  const int64_t tn = blockIdx.x, tm = blockIdx.y;
-  int64_t sa = tm * 4 + wave;
-  sa = sa < Sm ? sa : Sm - 1;
-  const bf16_t* Ap = (const bf16_t*)p.A + (sa * T * 2) * 512 + lane * 8;
-  const bf16_t* Bp = (const bf16_t*)p.B;
-  // this thread's pieces of a chunk: piece i -> (strip j, step kk, part h, lane l)
-  int64_t boff[PER];
+  const int64_t tm = blockIdx.y;
+  const int64_t s0 = (int64_t)blockIdx.x * Sn / G, s1 = ((int64_t)blockIdx.x + 1) * Sn / G;
+  const bf16_t* A = (const bf16_t*)p.A;
+  const bf16_t* B = (const bf16_t*)p.B;
+  // piece q = tid + 512 r of a phase lands at q * 8 in the phase buffer, so
+  // fragment (strip i, step t, part h) is the 1 KB at ((i P + t) 2 + h) 512:
+  // piece r of this thread is strip r / 2, step tid / 128 + 4 (r % 2), part
+  // (tid / 64) % 2, lane tid % 64
+  static_assert(P == 8 && PER == 8, "piece mapping assumes 8 steps per phase");
+  const int t0 = threadIdx.x >> 7;
+  int64_t abase[4];
 #pragma unroll
-  for (int r = 0; r < PER; ++r) {
-    const int i = threadIdx.x + 256 * r;
-    const int l = i & 63, h = (i >> 6) & 1, kk = (i >> 7) % KC, j = i / (128 * KC);
-    int64_t st = tn * NC + j;
-    st = st < Sn ? st : Sn - 1;
-    boff[r] = ((st * T + kk) * 2 + h) * 512 + l * 8;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t sa = tm * 4 + i < Sm ? tm * 4 + i : Sm - 1;
+    abase[i] = (sa * T * 2 + ((threadIdx.x >> 6) & 1)) * 512 + lane * 8;
   }
-  bf16x8_t bst[S][PER], ah[S][KC], al[S][KC];
-  f32x16 acc[NC];
-#pragma unroll
-  for (int j = 0; j < NC; ++j)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
-
-#define AGPU_STREAM_ISSUE(c, u)                                                                   \
-  {                                                                                               \
-    _Pragma("unroll") for (int r = 0; r < PER; ++r) bst[u][r] =                                    \
-        *(const bf16x8_t*)(Bp + boff[r] + (int64_t)(c) * KC * 1024);                               \
-    _Pragma("unroll") for (int kk = 0; kk < KC; ++kk) {                                            \
-      ah[u][kk] = *(const bf16x8_t*)(Ap + ((int64_t)(c) * KC + kk) * 1024);                         \
-      al[u][kk] = *(const bf16x8_t*)(Ap + ((int64_t)(c) * KC + kk) * 1024 + 512);                   \
-    }                                                                                             \
+  bf16x8_t ast[PER];
+#define AGPU_HEAD_ISSUE_A(ph)                                                              \
+  _Pragma("unroll") for (int r = 0; r < PER; ++r) {                                        \
+    const int64_t kk_ = (int64_t)(ph) * P + t0 + 4 * (r & 1);                              \
+    ast[r] = *(const bf16x8_t*)(A + abase[r >> 1] + (kk_ < T ? kk_ : T - 1) * 1024);       \
   }
-  // Chunk c's weight fragments go into LDS buffer c & 1 (the other buffer
-  // may still be read by a wave finishing chunk c - 1), then one barrier.
-  auto consume = [&](int c, int u) __attribute__((always_inline)) {
-    const int buf = c & 1;
+  // (with TAIL, steps past K are written as zeros)
+#define AGPU_HEAD_WRITE_A(ph)                                                              \
+  _Pragma("unroll") for (int r = 0; r < PER; ++r) {                                        \
+    bf16x8_t v_ = ast[r];                                                                  \
+    if (TAIL && (int64_t)(ph) * P + t0 + 4 * (r & 1) >= T) v_ = bf16x8_t{};                \
+    ((bf16x8_t*)(sA + ((ph) & 1) * PHASE))[threadIdx.x + 512 * r] = v_;                    \
+  }
+  // (at most 8 strips per block: the launch sizes the grid for that)
+  const int64_t want = s0 + w;
+  const bool mine = want < s1;
+  const int64_t s = mine ? want : s0;
+  const bf16_t* Bs = B + s * T * 1024 + lane * 8;
+  bf16x8_t bh[P], bl[P];
+  if (mine) {
 #pragma unroll
-    for (int r = 0; r < PER; ++r) sB[buf][threadIdx.x + 256 * r] = bst[u][r];
-    __syncthreads();
+    for (int t = 0; t < P; ++t) {
+      const int64_t kk = t < T ? t : T - 1;
+      bh[t] = *(const bf16x8_t*)(Bs + kk * 1024);
+      bl[t] = *(const bf16x8_t*)(Bs + kk * 1024 + 512);
+    }
+  }
+  AGPU_HEAD_ISSUE_A(0)
+  AGPU_HEAD_WRITE_A(0)
+  __syncthreads();
+  f32x16 acc[4];
 #pragma unroll
-    for (int kk = 0; kk < KC; ++kk) {
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < NC; ++j) {
-        const bf16x8_t bh = sB[buf][((j * KC + kk) * 2 + 0) * 64 + lane];
-        const bf16x8_t bl = sB[buf][((j * KC + kk) * 2 + 1) * 64 + lane];
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[u][kk], bh, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[u][kk], bl, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[u][kk], bh, acc[j], 0, 0, 0);
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
+  // Every phase loads the next one (the one past the end re-reads the last
+  // step and lands in the buffer no phase reads): no branch in the loop, so
+  // the LDS reads of a step issue together ahead of its MFMAs.  With TAIL
+  // (K not a multiple of 16 P), steps past K multiply zeros: their A pieces
+  // are written as zeros and their weight fragments replaced by zeros.
+  for (int ph = 0; ph < nph; ++ph) {
+    AGPU_HEAD_ISSUE_A(ph + 1)
+    const bf16_t* a = sA + (ph & 1) * PHASE + lane * 8;
+    if (mine) {
+#pragma unroll
+      for (int t = 0; t < P; ++t) {
+        const int64_t kk = (int64_t)ph * P + t;
+        bf16x8_t ah[4], al[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ah[i] = *(const bf16x8_t*)(a + ((i * P + t) * 2) * 512);
+          al[i] = *(const bf16x8_t*)(a + ((i * P + t) * 2 + 1) * 512);
+        }
+        bf16x8_t bhv = bh[t], blv = bl[t];
+        if (TAIL && kk >= T) {
+          bhv = bf16x8_t{};
+          blv = bf16x8_t{};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bhv, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], blv, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bhv, acc[i], 0, 0, 0);
+        }
+        // step kk + P into the registers just used (past the end: the last
+        // step again, never used)
+        const int64_t nx = kk + P < T ? kk + P : T - 1;
+        bh[t] = *(const bf16x8_t*)(Bs + nx * 1024);
+        bl[t] = *(const bf16x8_t*)(Bs + nx * 1024 + 512);
       }
     }
-  };
-  // Every load is issued unconditionally (chunk indices past the end are
-  // clamped to the last chunk, whose copy is never consumed): a load under a
-  // condition makes the compiler wait for every load in flight where the
-  // branches join, which had held the S-chunk read-ahead to one chunk.
-#pragma unroll
-  for (int u = 0; u < S; ++u) AGPU_STREAM_ISSUE(u < nch ? u : nch - 1, u)
-  const int full = nch / S * S;
-  for (int cb = 0; cb < full; cb += S) {
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int c = cb + u;
-      consume(c, u);
-      const int nx = c + S < nch ? c + S : nch - 1;
-      AGPU_STREAM_ISSUE(nx, u)
-    }
+    AGPU_HEAD_WRITE_A(ph + 1)
+    __syncthreads();
   }
-  // the last nch % S chunks, already in flight
-#pragma unroll
-  for (int u = 0; u < S; ++u)
-    if (full + u < nch) consume(full + u, u);
-#undef AGPU_STREAM_ISSUE
-  // output block (wave, j): lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32
-  const int64_t r0 = (tm * 4 + wave) * 32 + 4 * (lane >> 5);
+  if (!mine) return;
+  // acc[i], lane l, register r -> row (4 tm + i) 32 + 8 (r / 4) + 4 (l / 32) + r % 4, column 32 s + l % 32
+  const int64_t col = s * 32 + (lane & 31);
+  const int64_t cc = col < p.N ? col : p.N - 1;
+  const float bias = p.bias ? ((const float*)p.bias)[cc] : 0.f;
+  const bool cok = col < p.N;
+  float* C = (float*)p.C;
   if (p.act == kActNone && !p.res && !p.mask) {
-    // Plain (and biased) outputs, the vocabulary head's case: straight-line
-    // stores.  The general loop below keeps every epilogue branch per
-    // element; with 8 strips per block it had made the head 82 us instead
-    // of 56 (in the GPT-2 forward).
-    float* C = (float*)p.C;
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const int64_t col = (tn * NC + j) * 32 + (lane & 31);
-      const int64_t cc = col < p.N ? col : p.N - 1;
-      const float bias = p.bias ? ((const float*)p.bias)[cc] : 0.f;
-      const bool cok = col < p.N;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = r0 + 8 * (r >> 2) + (r & 3);
-        if (cok && row < p.M) C[row * p.c_sm + col] = p.alpha * acc[j][r] + bias;
+        const int64_t row = (tm * 4 + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (cok && row < p.M) C[row * p.c_sm + col] = p.alpha * acc[i][r] + bias;
       }
-    }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < NC; ++j) {
-    const int64_t col = (tn * NC + j) * 32 + (lane & 31);
-    const int64_t cc = col < p.N ? col : p.N - 1;
-    const float bias = p.bias ? ((const float*)p.bias)[cc] : 0.f;
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int64_t row = r0 + 8 * (r >> 2) + (r & 3);
-      if (row >= p.M || col >= p.N) continue;
-      float v = p.alpha * acc[j][r] + bias;
+      const int64_t row = (tm * 4 + i) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (!cok || row >= p.M) continue;
+      float v = p.alpha * acc[i][r] + bias;
       if (p.act == kActRelu) v = fmaxf(v, 0.f);
       else if (p.act == kActGelu) v = gelu_tanh(v);
       else if (p.act == kActGeluExact) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
       if (p.res) v += ((const float*)p.res)[row * p.r_sm + col];
       if (p.mask) v = ((const float*)p.mask)[row * p.k_sm + col] > 0.f ? v : 0.f;
-      ((float*)p.C)[row * p.c_sm + col] = v;
+      C[row * p.c_sm + col] = v;
     }
-  }
 }
+
+#undef AGPU_HEAD_ISSUE_A
+#undef AGPU_HEAD_WRITE_A
 
 template <int FR, int FC, int WR, int WC, bool APK>
 void launch_x3p_kt(const GArgs& p, int kt, int64_t T, dim3 grid, hipStream_t s) {
@@ -1115,7 +1134,8 @@ X3Plan x3_plan(int64_t M, int64_t N, int64_t K, int cus, bool apk, bool split) {
   // 0 wide split tiles, 1 narrow split tiles, 2 the packed-A row panel.
   const int fcfg = gemm_tune().cfg;
   // Packed A with many columns (each weight strip would be read by several
-  // row panels): the weight-streaming panel, 128 x 128 per block, whole K.
+  // row panels): the vocabulary-head panel, one weight strip per wavefront,
+  // whole K.
   if (apk && !split && forced == 0 && (fcfg == -1 || fcfg == 3) && K % 32 == 0 &&
       (fcfg == 3 || (N >= 8192 && ((M + 31) / 32) * ((N + 31) / 32) >= 2048))) {
     pl.stream = true;
@@ -1246,10 +1266,16 @@ void gemm_x3p_launch(const X3Plan& pl, const GArgs& p, hipStream_t s) {
     fail("gemm_x3p: row statistics need a row-panel plan that runs its epilogue and N %% 32 == 0");
   if (p.rs_in && !(panel && pl.apk)) fail("gemm_x3p: a folded layer_norm needs the unsplit packed-A row-panel plan");
   if (pl.stream) {
-    if (p.ln_g || !pl.apk) fail("internal: the weight-streaming panel takes packed A only");
-    if (pl.tiles_n > 0x7fffffff || pl.tiles_m > 65535) fail("gemm_x3_stream: grid too large");
-    hipLaunchKernelGGL((gemm_x3_stream<4, 1, 8>), dim3((unsigned)pl.tiles_n, (unsigned)pl.tiles_m), dim3(256), 0, s, p);
-    check_launch("gemm_x3_stream");
+    if (p.ln_g || !pl.apk) fail("internal: the vocabulary-head panel takes packed A only");
+    if (pl.tiles_m > 65535) fail("gemm_x3_head: grid too large");
+    // one block per CU, or more blocks when a CU's share passes 8 strips
+    const int64_t Sn = (p.N + 31) / 32;
+    const int64_t G = std::max((Sn + 7) / 8, std::min<int64_t>(Sn, 256));
+    if (G > 0x7fffffff) fail("gemm_x3_head: grid too large");
+    const dim3 grid((unsigned)G, (unsigned)pl.tiles_m);
+    if ((p.K >> 4) % 8 == 0) hipLaunchKernelGGL((gemm_x3_head<8, false>), grid, dim3(512), 0, s, p, G);
+    else hipLaunchKernelGGL((gemm_x3_head<8, true>), grid, dim3(512), 0, s, p, G);
+    check_launch("gemm_x3_head");
     return;
   }
   if (pl.rows && pl.apk) {

@@ -457,7 +457,8 @@ def test_attention_writes_packed_rows(gpu, H, T, D, causal):
                                           (33, 512, 1000, True), (130, 96, 260, True)])
 def test_weight_streaming_panel_matches_oracle(gpu, M, K, N, forced):
     """Packed rows times many columns (a vocabulary head) runs the
-    weight-streaming panel (every weight byte read once, LDS-staged); forced
+    vocabulary-head panel (one weight strip per wavefront, every weight byte
+    read once; K = 96 leaves a partial phase of k steps); forced
     through gemm_tune's cfg 3 for small and ragged shapes and more than 128
     rows; at the fp32 bar, and exact on small integers."""
     from applegpu_runtime._native import lib
