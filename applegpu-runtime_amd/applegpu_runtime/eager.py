@@ -189,6 +189,16 @@ def linear_mse_backward_sgd_(h, w, b, y, alpha=1.0, grad_in=True):
     return loss, (gi if grad_in else None)
 
 
+def linear_backward_sgd_pair_(w1, b1, g, h, w0, b0, x, alpha=1.0):
+    """The backward and SGD steps of the first two Linear layers of a net,
+    in place: h = relu(x @ w0^T + b0) feeds the layer (w1, b1), whose output
+    gradient is g.  g0 = (g @ w1) * (h > 0) from w1 before its step; then
+    w1 += alpha * g^T @ h, b1 += alpha * g.sum(0), w0 += alpha * g0^T @ x and
+    b0 += alpha * g0.sum(0).  Large fp32 layers update both weights in one
+    pack launch and one GEMM launch."""
+    op("linear_backward_sgd_pair_", [w1, b1, g, h, w0, b0, x], f=(float(alpha),))
+
+
 def mlp2_sgd_step_(x, y, w1, b1, w2, b2, alpha=1.0):
     """One SGD step of Linear(w1, b1) -> ReLU -> Linear(w2, b2) with MSE
     loss against y, in place (w += alpha * grad, every gradient from the

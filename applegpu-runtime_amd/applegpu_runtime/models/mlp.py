@@ -13,8 +13,10 @@ through the eager C ABI, with the fusions the MI355X backend offers:
   loss      mse and dL/dout             one launch
   backward  dh = (g W) * (h > 0)        one GEMM, relu' mask in the epilogue
   + SGD     W += -lr * g^T h            one GEMM, the update in its epilogue
-            b += -lr * sum(g, 0)        one column reduction
-(the output layer's 4096 -> 1 products run on the unit-extent GEMM kernels).
+            b += -lr * sum(g, 0)        folded into the packing of g
+(the first two layers' weight updates share one pack launch and one GEMM
+launch; the output layer's 4096 -> 1 products run on the unit-extent GEMM
+kernels).
 A two-layer net is one op, mlp2_sgd_step_: at small sizes (config C1,
 64 -> 128 -> 10 at batch 32) the whole step runs in one workgroup, one launch.
 Every gradient is formed from the step's starting parameters, as autograd
@@ -76,12 +78,17 @@ class EagerMLP:
         # its SGD step
         w, b = self.params[-1]
         loss, g = E.linear_mse_backward_sgd_(h, w, b, y, -lr, grad_in=n > 1)
-        for i in range(n - 2, -1, -1):
+        for i in range(n - 2, 1, -1):
             w, b = self.params[i]
             # dL/d(input of layer i) masked by relu' of the previous layer's
             # output (from W_i before its update), then W_i -= lr * g^T a_i
             # and b_i -= lr * sum(g, 0)
-            g = E.linear_backward_sgd_(w, b, g, acts[i], acts[i] if i > 0 else None, -lr)
+            g = E.linear_backward_sgd_(w, b, g, acts[i], acts[i], -lr)
+        if n > 2:
+            # the first two layers together: both weight updates in one
+            # launch pair
+            (w0, b0), (w1, b1) = self.params[0], self.params[1]
+            E.linear_backward_sgd_pair_(w1, b1, g, acts[1], w0, b0, x, -lr)
         return loss
 
     def train_step_unfused(self, x, y, lr=0.01):

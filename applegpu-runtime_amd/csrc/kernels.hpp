@@ -347,6 +347,11 @@ void pack_weights(DType dt, const void* w, int64_t s_n, int64_t s_k, int64_t N, 
 // Workspace bytes the launch needs (split-K partials); 0 when none.
 size_t gemm_workspace_bytes(const Gemm& g);
 void gemm(const Gemm& g, void* workspace, hipStream_t s);
+// Two fp32 SGD weight updates (W += alpha A^T B with a bias row-sum
+// accumulator each, same K) in one pack and one GEMM launch, when both take
+// the outer-product plan; workspaces as gemm_workspace_bytes gives for each.
+bool gemm_outer_pair_ok(const Gemm& g0, const Gemm& g1);
+void gemm_outer_pair(const Gemm& g0, void* ws0, const Gemm& g1, void* ws1, hipStream_t s);
 
 // How fp32 GEMMs compute: kF32Split3 splits each operand into bf16 hi + lo
 // and accumulates hi*hi + hi*lo + lo*hi on bf16 MFMA in fp32 (default);

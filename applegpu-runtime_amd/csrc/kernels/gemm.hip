@@ -919,6 +919,19 @@ size_t gemm_workspace_bytes(const Gemm& g) {
 
 static void reduce_splits(const Gemm& g, const GArgs& p, hipStream_t s);
 
+bool gemm_outer_pair_ok(const Gemm& g0, const Gemm& g1) {
+  return use_outer(g0) && use_outer(g1) && gemm_x3_outer2_ok(g0, g1);
+}
+
+void gemm_outer_pair(const Gemm& g0, void* ws0, const Gemm& g1, void* ws1, hipStream_t s) {
+  if (!gemm_outer_pair_ok(g0, g1)) fail("gemm: these two products do not take the paired outer-product plan");
+  Plan one{};
+  one.bm = one.bn = 64;
+  one.splits = 1;
+  one.kps = g0.K;
+  gemm_x3_outer2(g0, make_args(g0, one), ws0, g1, make_args(g1, one), ws1, s);
+}
+
 void gemm(const Gemm& g, void* workspace, hipStream_t s) {
   if (g.a_rowsum_acc && !gemm_a_rowsum_fused(g)) fail("internal: A's row sums are fused only into the outer-product plan");
   if (g.M == 0 || g.N == 0 || g.batch == 0) return;

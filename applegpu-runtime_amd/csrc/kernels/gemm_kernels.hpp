@@ -904,6 +904,12 @@ bool gemm_h16_ok(const Gemm& g, int cus);
 void gemm_h16(const Gemm& g, const GArgs& p, int cus, hipStream_t s);
 size_t gemm_x3_outer_workspace(const Gemm& g);
 void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s);
+// Two such products with the same K and a row-sum accumulator each (two SGD
+// weight updates with their bias steps) as one pack launch and one GEMM
+// launch; each product's workspace is its own gemm_x3_outer_workspace.
+bool gemm_x3_outer2_ok(const Gemm& g0, const Gemm& g1);
+void gemm_x3_outer2(const Gemm& g0, const GArgs& p0, void* ws0, const Gemm& g1, const GArgs& p1, void* ws1,
+                    hipStream_t s);
 
 // Defined in gemm_mf_{f32,f16,bf16}_{fast,edge}.hip.
 void launch_mf_f32(const GArgs& p, int cfg, bool ak, bool bk, bool fast, dim3 grid, hipStream_t s);

@@ -82,15 +82,15 @@ __global__ void __launch_bounds__(256) pack_x3_pair_kernel(PackSrc a, PackSrc b,
 // t = w, w + 4, ... (the fragments pack_x3_one writes for them) while
 // summing its lanes' values; the four waves' and two half-waves' sums are
 // then added in a fixed order, so results repeat exactly.
-__global__ void __launch_bounds__(256) pack_x3_pair_sum_kernel(PackSrc a, PackSrc b, int64_t nb0,
-                                                               float* __restrict__ acc, float alpha) {
-  if ((int64_t)blockIdx.x >= nb0) {
-    pack_x3_one(b, ((int64_t)blockIdx.x - nb0) * 256 + threadIdx.x);
+__device__ __forceinline__ void pack_pair_sum_block(const PackSrc& a, const PackSrc& b, int64_t nb0,
+                                                    float* __restrict__ acc, float alpha, int64_t bid,
+                                                    float (&red)[4][64]) {
+  if (bid >= nb0) {
+    pack_x3_one(b, (bid - nb0) * 256 + threadIdx.x);
     return;
   }
-  __shared__ float red[4][64];
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t s = blockIdx.x;
+  const int64_t s = bid;
   const int64_t n = 32 * s + (l & 31);
   const bool nin = n < a.N;
   const int64_t nc = nin ? n : a.N - 1;
@@ -124,6 +124,23 @@ __global__ void __launch_bounds__(256) pack_x3_pair_sum_kernel(PackSrc a, PackSr
     for (int q = 0; q < 4; ++q) t += red[q][threadIdx.x] + red[q][threadIdx.x + 32];
     acc[n] += alpha * t;
   }
+}
+
+__global__ void __launch_bounds__(256) pack_x3_pair_sum_kernel(PackSrc a, PackSrc b, int64_t nb0,
+                                                               float* __restrict__ acc, float alpha) {
+  __shared__ float red[4][64];
+  pack_pair_sum_block(a, b, nb0, acc, alpha, blockIdx.x, red);
+}
+
+// Two products' operands in one launch (two SGD weight updates): blocks
+// [0, n0) are the first product's pack_x3_pair_sum_kernel, the rest the
+// second's.
+__global__ void __launch_bounds__(256) pack_x3_2pair_sum_kernel(PackSrc a0, PackSrc b0, int64_t nb0, int64_t n0,
+                                                                float* __restrict__ acc0, PackSrc a1, PackSrc b1,
+                                                                int64_t nb1, float* __restrict__ acc1, float alpha) {
+  __shared__ float red[4][64];
+  if ((int64_t)blockIdx.x < n0) pack_pair_sum_block(a0, b0, nb0, acc0, alpha, blockIdx.x, red);
+  else pack_pair_sum_block(a1, b1, nb1, acc1, alpha, (int64_t)blockIdx.x - n0, red);
 }
 
 template <int FR, int FC, int WR, int WC, int KT, bool APK>
@@ -929,15 +946,16 @@ namespace {
 // per LDS stage (32 KB) and 120 VGPRs let four blocks share a CU, so the
 // 1024-tile MLP update runs in one round: C3 step 0.2537 -> 0.2477 ms against
 // two k steps per stage (64 KB) at two blocks per CU.
+constexpr int kOuterStage = 16 * 512;  // bf16 elements per LDS stage (one k step)
+
 template <int T>
-__global__ void __launch_bounds__(256, 3) gemm_x3_outer_kernel(GArgs p, const bf16_t* __restrict__ apk,
-                                                           const bf16_t* __restrict__ bpk) {
+__device__ __forceinline__ void outer_tile(const GArgs& p, const bf16_t* __restrict__ apk,
+                                           const bf16_t* __restrict__ bpk, int64_t bid, bf16_t* lds) {
   constexpr int S = 1;                  // k steps per stage
   constexpr int STAGE = S * 16 * 512;   // bf16 elements per stage
   constexpr int NST = T / S;
-  static_assert(T % S == 0, "whole stages");
+  static_assert(T % S == 0 && STAGE == kOuterStage, "whole stages");
   typedef __attribute__((address_space(3))) void* lds_ptr;
-  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * STAGE];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t tiles_m = p.M >> 7, tiles_n = p.N >> 7;
   int64_t tm, tn;
@@ -945,13 +963,13 @@ __global__ void __launch_bounds__(256, 3) gemm_x3_outer_kernel(GArgs p, const bf
     // Workgroups go to the 8 XCDs in turn (block b to XCD b % 8): XCD x
     // takes the tiles of row half x / 4 and column quarter x % 4, so that
     // its L2 holds the half of A and the quarter of B it reads.
-    const int64_t x = blockIdx.x & 7, local = blockIdx.x >> 3;
+    const int64_t x = bid & 7, local = bid >> 3;
     const int64_t qn = tiles_n / 4;
     tm = (x >> 2) * (tiles_m / 2) + local / qn;
     tn = (x & 3) * qn + local % qn;
   } else {
-    tm = (int64_t)blockIdx.x / tiles_n;
-    tn = (int64_t)blockIdx.x % tiles_n;
+    tm = bid / tiles_n;
+    tn = bid % tiles_n;
   }
   // Fragment f of a k step (0..15): f < 8 row strip f / 2 of the tile, else
   // column strip (f - 8) / 2; part f % 2 (hi, lo).  Packed strip s, step t,
@@ -1043,6 +1061,28 @@ __global__ void __launch_bounds__(256, 3) gemm_x3_outer_kernel(GArgs p, const bf
   }
 }
 
+template <int T>
+__global__ void __launch_bounds__(256, 3) gemm_x3_outer_kernel(GArgs p, const bf16_t* __restrict__ apk,
+                                                           const bf16_t* __restrict__ bpk) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * kOuterStage];
+  outer_tile<T>(p, apk, bpk, blockIdx.x, lds);
+}
+
+// Two outer products with the same K in one launch (the two weight updates
+// of an MLP's last backward pair): blocks [0, tiles0) are the first
+// product's tiles, the rest the second's.  As one grid the 2048 tiles of two
+// 4096 x 4096 updates run in two full rounds of four blocks per CU: 75-81 us
+// against 92-98 us as two pack + outer launch pairs (measured on MI355X).
+template <int T>
+__global__ void __launch_bounds__(256, 3) gemm_x3_outer2_kernel(GArgs p0, const bf16_t* __restrict__ apk0,
+                                                            const bf16_t* __restrict__ bpk0, int64_t tiles0,
+                                                            GArgs p1, const bf16_t* __restrict__ apk1,
+                                                            const bf16_t* __restrict__ bpk1) {
+  __shared__ __attribute__((aligned(16))) bf16_t lds[2 * kOuterStage];
+  if ((int64_t)blockIdx.x < tiles0) outer_tile<T>(p0, apk0, bpk0, blockIdx.x, lds);
+  else outer_tile<T>(p1, apk1, bpk1, (int64_t)blockIdx.x - tiles0, lds);
+}
+
 }  // namespace
 
 bool gemm_x3_outer_ok(const Gemm& g) {
@@ -1080,6 +1120,37 @@ void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s) {
   else if (g.K == 256) hipLaunchKernelGGL(gemm_x3_outer_kernel<16>, grid, dim3(256), 0, s, p, apk, bpk);
   else hipLaunchKernelGGL(gemm_x3_outer_kernel<32>, grid, dim3(256), 0, s, p, apk, bpk);
   check_launch("gemm_x3_outer");
+}
+
+bool gemm_x3_outer2_ok(const Gemm& g0, const Gemm& g1) {
+  return gemm_x3_outer_ok(g0) && gemm_x3_outer_ok(g1) && g0.K == g1.K && g0.a_rowsum_acc && g1.a_rowsum_acc &&
+         g0.alpha == g1.alpha;
+}
+
+void gemm_x3_outer2(const Gemm& g0, const GArgs& p0, void* ws0, const Gemm& g1, const GArgs& p1, void* ws1,
+                    hipStream_t s) {
+  if (!gemm_x3_outer2_ok(g0, g1) || !ws0 || !ws1) fail("gemm: the paired outer-product plan does not fit");
+  const int64_t T = g0.K / 16;
+  bf16_t* apk0 = (bf16_t*)ws0;
+  bf16_t* bpk0 = apk0 + g0.M * g0.K * 2;
+  bf16_t* apk1 = (bf16_t*)ws1;
+  bf16_t* bpk1 = apk1 + g1.M * g1.K * 2;
+  const PackSrc pa0{(const float*)g0.A, g0.a_sk, g0.a_sm, g0.K, g0.M, T, apk0};
+  const PackSrc pb0{(const float*)g0.B, g0.b_sk, g0.b_sn, g0.K, g0.N, T, bpk0};
+  const PackSrc pa1{(const float*)g1.A, g1.a_sk, g1.a_sm, g1.K, g1.M, T, apk1};
+  const PackSrc pb1{(const float*)g1.B, g1.b_sk, g1.b_sn, g1.K, g1.N, T, bpk1};
+  const int64_t nba0 = g0.M / 32, nbb0 = ((g0.N / 32) * T * 64 + 255) / 256;
+  const int64_t nba1 = g1.M / 32, nbb1 = ((g1.N / 32) * T * 64 + 255) / 256;
+  hipLaunchKernelGGL(pack_x3_2pair_sum_kernel, dim3((unsigned)(nba0 + nbb0 + nba1 + nbb1)), dim3(256), 0, s, pa0,
+                     pb0, nba0, nba0 + nbb0, (float*)g0.a_rowsum_acc, pa1, pb1, nba1, (float*)g1.a_rowsum_acc,
+                     g0.alpha);
+  check_launch("pack_x3_2pair");
+  const int64_t tiles0 = (g0.M / 128) * (g0.N / 128), tiles1 = (g1.M / 128) * (g1.N / 128);
+  const dim3 grid((unsigned)(tiles0 + tiles1));
+  if (T == 8) hipLaunchKernelGGL(gemm_x3_outer2_kernel<8>, grid, dim3(256), 0, s, p0, apk0, bpk0, tiles0, p1, apk1, bpk1);
+  else if (T == 16) hipLaunchKernelGGL(gemm_x3_outer2_kernel<16>, grid, dim3(256), 0, s, p0, apk0, bpk0, tiles0, p1, apk1, bpk1);
+  else hipLaunchKernelGGL(gemm_x3_outer2_kernel<32>, grid, dim3(256), 0, s, p0, apk0, bpk0, tiles0, p1, apk1, bpk1);
+  check_launch("gemm_x3_outer2");
 }
 
 void row_tile_stats(const float* x, int64_t x_sm, int64_t M, int64_t N, float* out, hipStream_t s) {

@@ -1193,6 +1193,60 @@ TensorP matmul(const TensorP& a_in, const TensorP& b_in, bool ta, bool tb, const
   return out;
 }
 
+// The SGD step w += alpha g^T a with b += alpha sum(g, 0) as the Gemm that
+// sgd_matmul_(w, g, a, true, false, alpha, b) hands to k::gemm (A = g^T read
+// in place, the residual and output w, the bias as A's row-sum
+// accumulator); false when an operand is not plain contiguous fp32.
+static bool sgd_update_gemm(const TensorP& w, const TensorP& b, const TensorP& g, const TensorP& a, float alpha,
+                            k::Gemm& G, EpiKeep& keep) {
+  for (const TensorP* t : {&w, &b, &g, &a})
+    if ((*t)->dtype != DType::F32 || !(*t)->is_contiguous()) return false;
+  const int64_t R = g->shape[0], O = w->shape[0], N = w->shape[1];
+  if (R < 2 || O < 2 || N < 2) return false;
+  G = k::Gemm{};
+  G.dt = G.b_dt = DType::F32;
+  G.M = O; G.N = N; G.K = R; G.batch = 1;
+  G.A = g->data(); G.a_sm = g->strides[1]; G.a_sk = g->strides[0]; G.a_sb = 0;
+  G.B = a->data(); G.b_sk = a->strides[0]; G.b_sn = a->strides[1]; G.b_sb = 0;
+  G.C = w->data(); G.c_sm = N; G.c_sb = O * N;
+  Epilogue e;
+  e.alpha = alpha;
+  e.residual = w;
+  set_epilogue(G, &e, {O, N}, {1}, &keep);
+  G.a_rowsum_acc = b->data();
+  return true;
+}
+
+TensorP linear_backward_sgd_pair_(const TensorP& w1, const TensorP& b1, const TensorP& g, const TensorP& h,
+                                  const TensorP& w0, const TensorP& b0, const TensorP& x, float alpha) {
+  const char* name = "linear_backward_sgd_pair_";
+  if (w1->ndim != 2 || g->ndim != 2 || h->ndim != 2 || w0->ndim != 2 || x->ndim != 2)
+    fail("%s: w1, g, h, w0 and x must be 2-D", name);
+  const int64_t R = g->shape[0], O1 = w1->shape[0], N1 = w1->shape[1], N0 = w0->shape[1];
+  if (g->shape[1] != O1 || h->dims() != std::vector<int64_t>{R, N1} || w0->shape[0] != N1 ||
+      x->dims() != std::vector<int64_t>{R, N0} || b1->numel() != O1 || b0->numel() != N1)
+    fail("%s: g %s, h %s, x %s, w1 %s, b1 %s, w0 %s and b0 %s do not form two stacked Linear layers", name,
+         shape_str(g->dims()).c_str(), shape_str(h->dims()).c_str(), shape_str(x->dims()).c_str(),
+         shape_str(w1->dims()).c_str(), shape_str(b1->dims()).c_str(), shape_str(w0->dims()).c_str(),
+         shape_str(b0->dims()).c_str());
+  // the lower layer's output gradient through its ReLU, from w1 before its step
+  Epilogue e;
+  e.mask = h;
+  TensorP g0 = matmul(g, w1, false, false, &e);
+  k::Gemm G1, G0;
+  EpiKeep k1, k0;
+  if (!meta_mode() && sgd_update_gemm(w1, b1, g, h, alpha, G1, k1) && sgd_update_gemm(w0, b0, g0, x, alpha, G0, k0) &&
+      k::gemm_outer_pair_ok(G1, G0)) {
+    BufferP ws1 = scratch(k::gemm_workspace_bytes(G1)), ws0 = scratch(k::gemm_workspace_bytes(G0));
+    k::gemm_outer_pair(G1, ws1->ptr, G0, ws0->ptr, rt().stream());
+    return w0;
+  }
+  sgd_matmul_(w1, g, h, true, false, alpha, b1);
+  sgd_matmul_(w0, g0, x, true, false, alpha, b0);
+  return w0;
+}
+
+
 TensorP pack_weight(const TensorP& wt) {
   if (wt->ndim != 2) fail("pack_weight: weights must be 2-D [out, in]");
   if (wt->dtype != DType::F16 && wt->dtype != DType::BF16) fail("pack_weight: fp16 or bf16 weights only");

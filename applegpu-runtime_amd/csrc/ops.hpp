@@ -154,6 +154,15 @@ TensorP linear_backward_sgd_(const TensorP& w, const TensorP& b, const TensorP& 
 // mse_loss_grad and linear_backward_sgd_.
 std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const TensorP& w, const TensorP& b,
                                                      const TensorP& y, float alpha, bool grad_in);
+// The backward and SGD steps of two stacked Linear layers, the lower one
+// first in the net (no input gradient): y = relu(x w0^T + b0) = h, then
+// h w1^T + b1 with output gradient g.  g0 = (g w1) * (h > 0) from w1
+// before its step; then w1 += alpha g^T h, b1 += alpha sum(g, 0),
+// w0 += alpha g0^T x, b0 += alpha sum(g0, 0).  Returns w0.  When both
+// updates take the outer-product plan they run as one pack launch and one
+// GEMM launch (k::gemm_outer_pair); otherwise as two sgd_matmul_ calls.
+TensorP linear_backward_sgd_pair_(const TensorP& w1, const TensorP& b1, const TensorP& g, const TensorP& h,
+                                  const TensorP& w0, const TensorP& b0, const TensorP& x, float alpha);
 // One SGD step of Linear(w1, b1) -> ReLU -> Linear(w2, b2) with MSE loss
 // against y, in place (w += alpha * grad, every gradient from the step's
 // starting parameters); returns the loss [1].  Small fp32 shapes run as one

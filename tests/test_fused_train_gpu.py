@@ -210,6 +210,46 @@ def test_linear_backward_sgd(gpu, R, O, N, with_mask):
         assert rel_err(gin.numpy(), want) < 1e-5
 
 
+@pytest.mark.parametrize("R,N0,N1,O1,paired", [(256, 4096, 4096, 4096, True), (128, 2048, 4096, 2048, True),
+                                                (256, 2048, 2048, 1024, False), (33, 70, 50, 20, False)])
+def test_linear_backward_sgd_pair(gpu, R, N0, N1, O1, paired):
+    """linear_backward_sgd_pair_ (the first two layers' backward and SGD
+    steps): g0 = (g @ w1) masked by h > 0 from w1 before its step, then both
+    weight and bias steps.  Where both updates take the outer-product plan
+    (the MLP's 4096-wide layers) they run as one pack launch and one GEMM
+    launch, four launches in all with the masked product's two; else as
+    two sgd_matmul_ calls.  Bit for bit the two linear_backward_sgd_ calls
+    it replaces (the same per-tile products and column sums), twice in a
+    row; against float64 at the fp32 bar."""
+    from applegpu_runtime import eager as E
+    x = f32(R, N0)
+    h = np.maximum(f32(R, N1), 0).astype(np.float32)
+    g = f32(R, O1, scale=0.1)
+    w1, b1, w0, b0 = f32(O1, N1, scale=0.05), f32(O1), f32(N1, N0, scale=0.05), f32(N1)
+    lr = 0.01
+    xt, ht, gt = E.from_numpy(x), E.from_numpy(h), E.from_numpy(g)
+    pw1, pb1, pw0, pb0 = (E.from_numpy(v) for v in (w1, b1, w0, b0))
+    sw1, sb1, sw0, sb0 = (E.from_numpy(v) for v in (w1, b1, w0, b0))
+    for rep in range(2):
+        E.synchronize()
+        before = gpu.graph_stats()["launcher_calls"]
+        E.linear_backward_sgd_pair_(pw1, pb1, gt, ht, pw0, pb0, xt, -lr)
+        calls = gpu.graph_stats()["launcher_calls"] - before
+        if paired:
+            assert calls == 4, calls
+        gin = E.linear_backward_sgd_(sw1, sb1, gt, ht, ht, -lr)
+        E.linear_backward_sgd_(sw0, sb0, gin, xt, None, -lr)
+        for a, b in ((pw1, sw1), (pb1, sb1), (pw0, sw0), (pb0, sb0)):
+            np.testing.assert_array_equal(a.numpy(), b.numpy())
+        if rep == 0:
+            g64, h64, x64 = g.astype(np.float64), h.astype(np.float64), x.astype(np.float64)
+            g0 = np.where(h > 0, g64 @ w1.astype(np.float64), 0.0)
+            assert rel_err(pw1.numpy() - w1, -lr * (g64.T @ h64)) < 1e-5
+            assert rel_err(pw0.numpy() - w0, -lr * (g0.T @ x64)) < 1e-4
+            np.testing.assert_allclose(pb1.numpy(), b1 - lr * g64.sum(0), rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(pb0.numpy(), b0 - lr * g0.sum(0), rtol=1e-4, atol=1e-5)
+
+
 @pytest.mark.parametrize("R,O,N,grad_in", [(256, 1, 4096, True), (256, 1, 4096, False), (37, 1, 70, True),
                                             (32, 3, 128, True)])
 def test_linear_mse_backward_sgd(gpu, R, O, N, grad_in):
