@@ -31,9 +31,10 @@ aggregate is the bytes of one launch of each shape over their summed time.
 The same launches in MFMA terms are reported beside it (against the fp32
 MFMA peak and against the bf16x3 ceiling, one third of the bf16 MFMA peak).
 `roofline_mlp_dw` is the MLP weight-gradient GEMM with its SGD step
-(W += -lr g^T h, M = N = 4096, K = 256): one launch packs g^T and h as bf16
-hi/lo fragments, a second (gemm_x3_outer) multiplies them in 128 x 128 tiles
-and updates W in place; its floor is W's read and write through HBM
+(W += -lr g^T h, M = N = 4096, K = 256), one update alone: one launch packs
+g^T and h as bf16 hi/lo fragments, a second (gemm_x3_outer) multiplies them
+in 128 x 128 tiles and updates W in place (the step pairs its two updates
+in one pack and one GEMM launch with the same tile code); its floor is W's read and write through HBM
 (algorithmic bytes: W twice plus g and h once).  HBM traffic comes from
 the rocprofv3 --pmc summaries committed under profiles/ (FETCH_SIZE,
 WRITE_SIZE of each kernel, scaled by the same counters read for the 256 MiB
@@ -393,8 +394,10 @@ def main():
     if not (np.isfinite(logits).all() and np.isfinite(loss)):
         raise RuntimeError("non-finite results")
 
-    # ── roofline: the MLP weight-gradient GEMM with its SGD update, as the
-    # step runs it: W += -lr * g^T h (bias-free; W a scratch copy) ──────────
+    # ── roofline: the MLP weight-gradient GEMM with its SGD update, one
+    # update alone: W += -lr * g^T h (bias-free; W a scratch copy).  The step
+    # runs its two updates with the same tile code as one paired launch
+    # (linear_backward_sgd_pair_) ──────────────────────────────────────────
     K_, M_, N_ = MLP_BATCH, MLP_SIZES[1], MLP_SIZES[0]
     g_act = E.from_numpy(rng.standard_normal((K_, M_), dtype=np.float32) * np.float32(1e-3))
     h_act = E.from_numpy(np.maximum(rng.standard_normal((K_, N_), dtype=np.float32), 0))
