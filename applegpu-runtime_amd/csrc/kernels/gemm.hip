@@ -815,6 +815,13 @@ static bool use_outer(const Gemm& g) {
          gemm_x3_outer_workspace(g) <= g.max_ws;
 }
 
+// The few-row fp32 weight-streaming plan (gemm_f32s.hip), unless a tile
+// configuration, a split count or the native fp32 kernels are forced.
+static bool use_f32s(const Gemm& g) {
+  const GemmTune& tu = gemm_tune();
+  return tu.cfg < 0 && tu.splits == 0 && tu.f32_mode != kF32Native && gemm_f32_stream_ok(g, cu_count());
+}
+
 // The 16-bit large-tile plan (gemm_h16.hip), unless a configuration or a
 // split count is forced.
 static bool use_h16(const Gemm& g) {
@@ -826,6 +833,7 @@ int gemm_splits(const Gemm& g) {
   if (g.b_x3) return x3_plan_of(g).splits;
   if (use_outer(g) || use_h16(g)) return 1;
   if (skinny_plan(g, cu_count()).use || thin_kind(g)) return 1;
+  if (use_f32s(g)) return gemm_f32_stream_splits(g, cu_count());
   const Plan pl = make_plan(g, cu_count());
   return pl.kind == kMf ? pl.splits : 1;
 }
@@ -896,6 +904,10 @@ const char* gemm_plan_name(const Gemm& g) {
     snprintf(buf, sizeof buf, "h16 256x256 w16");
     return buf;
   }
+  if (use_f32s(g)) {
+    snprintf(buf, sizeof buf, "f32 stream 256 cols splits=%d", gemm_f32_stream_splits(g, cu_count()));
+    return buf;
+  }
   Plan pl = make_plan(g, cu_count());
   const char* kind = pl.kind == kGeneric ? "generic" : pl.kind == kNative32 ? "f32-native" : "mf";
   snprintf(buf, sizeof buf, "%s cfg%d %dx%dx%d splits=%d", kind, pl.kind == kMf ? pl.cfg : -1, pl.bm, pl.bn, pl.bk,
@@ -912,6 +924,7 @@ size_t gemm_workspace_bytes(const Gemm& g) {
   }
   const SkinnyPlan sp = skinny_plan(g, cu_count());
   if (sp.use || thin_kind(g)) return 0;
+  if (use_f32s(g)) return (size_t)gemm_f32_stream_splits(g, cu_count()) * g.M * g.N * sizeof(float);
   Plan pl = make_plan(g, cu_count());
   if (pl.splits <= 1) return 0;
   return (size_t)pl.splits * g.batch * g.M * g.N * sizeof(float);
@@ -984,6 +997,19 @@ void gemm(const Gemm& g, void* workspace, hipStream_t s) {
     one.splits = 1;
     one.kps = g.K;
     gemm_x3_outer(g, make_args(g, one), workspace, s);
+    return;
+  }
+  if (use_f32s(g)) {
+    Plan fs{};
+    fs.bm = 64;
+    fs.bn = 256;
+    fs.splits = gemm_f32_stream_splits(g, cu_count());
+    fs.kps = g.K / fs.splits;
+    GArgs p = make_args(g, fs);
+    p.ws = (float*)workspace;
+    if (!workspace) fail("gemm: split-K workspace missing");
+    gemm_f32_stream(g, p, cu_count(), s);
+    reduce_splits(g, p, s);
     return;
   }
   if (use_h16(g)) {

@@ -907,6 +907,12 @@ void gemm_x3_outer(const Gemm& g, const GArgs& p, void* ws, hipStream_t s);
 // Two such products with the same K and a row-sum accumulator each (two SGD
 // weight updates with their bias steps) as one pack launch and one GEMM
 // launch; each product's workspace is its own gemm_x3_outer_workspace.
+// fp32 products with at most 64 rows and large fp32 weights contiguous along
+// k (gemm_f32s.hip): each weight byte read once into registers and split
+// there, K split into ranges reduced by the split-K reduction.
+bool gemm_f32_stream_ok(const Gemm& g, int cus);
+int gemm_f32_stream_splits(const Gemm& g, int cus);
+void gemm_f32_stream(const Gemm& g, const GArgs& p, int cus, hipStream_t s);
 bool gemm_x3_outer2_ok(const Gemm& g0, const Gemm& g1);
 void gemm_x3_outer2(const Gemm& g0, const GArgs& p0, void* ws0, const Gemm& g1, const GArgs& p1, void* ws1,
                     hipStream_t s);
