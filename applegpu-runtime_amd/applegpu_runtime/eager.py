@@ -189,6 +189,18 @@ def linear_mse_backward_sgd_(h, w, b, y, alpha=1.0, grad_in=True):
     return loss, (gi if grad_in else None)
 
 
+def linear_relu_mse_backward_sgd_(a, wh, bh, w, b, y, alpha=1.0, grad_in=True):
+    """The last hidden layer h = relu(a @ wh^T + bh) and a one-output MSE
+    regression layer (w [1, N], b [1]) through the output layer's SGD step,
+    as linear(a, wh, bh, act=1) then linear_mse_backward_sgd_(h, w, b, y):
+    returns (loss, g_in or None, h).  The hidden GEMM's split-K partial sums
+    are reduced by the output layer's forward (three launches instead of
+    four)."""
+    loss, gi, h = op("linear_relu_mse_backward_sgd_", [a, wh, bh, w, b, y], f=(float(alpha),),
+                     i=(int(bool(grad_in)),), nout=3)
+    return loss, (gi if grad_in else None), h
+
+
 def linear_backward_sgd_pair_(w1, b1, g, h, w0, b0, x, alpha=1.0):
     """The backward and SGD steps of the first two Linear layers of a net,
     in place: h = relu(x @ w0^T + b0) feeds the layer (w1, b1), whose output

@@ -69,15 +69,20 @@ class EagerMLP:
             # Linear -> ReLU -> Linear: one op (one launch at small sizes)
             (w1, b1), (w2, b2) = self.params
             return E.mlp2_sgd_step_(x, y, w1, b1, w2, b2, -lr)
+        if n == 1:
+            w, b = self.params[0]
+            return E.linear_mse_backward_sgd_(x, w, b, y, -lr, grad_in=False)[0]
         acts = [x]
         h = x
-        for w, b in self.params[:-1]:
+        for w, b in self.params[:-2]:
             h = E.linear(h, w, b, act=1)
             acts.append(h)
-        # the output layer (no activation) with the loss, its gradient and
-        # its SGD step
-        w, b = self.params[-1]
-        loss, g = E.linear_mse_backward_sgd_(h, w, b, y, -lr, grad_in=n > 1)
+        # the last hidden layer and the output layer (no activation) with the
+        # loss, its gradient and the output layer's SGD step (the hidden
+        # GEMM's split-K sums are reduced by the output layer's forward)
+        (wh, bh), (w, b) = self.params[-2], self.params[-1]
+        loss, g, h = E.linear_relu_mse_backward_sgd_(h, wh, bh, w, b, y, -lr, grad_in=True)
+        acts.append(h)
         for i in range(n - 2, 1, -1):
             w, b = self.params[i]
             # dL/d(input of layer i) masked by relu' of the previous layer's

@@ -35,6 +35,7 @@ enum Op : int {
   OP_LAYER_NORM_BACKWARD, OP_LAYER_NORM_GRADS, OP_GELU_BACKWARD, OP_GELU_TANH_BACKWARD, OP_GELU_EXACT_BACKWARD,
   OP_EMBEDDING_BACKWARD, OP_PACK_WEIGHT_X3, OP_PACK_ROWS_X3, OP_MATMUL_PP, OP_ROW_STATS_X3, OP_MATMUL_PP_NORM,
   OP_LINEAR_BACKWARD_SGD, OP_LINEAR_MSE_BACKWARD_SGD, OP_MLP2_SGD_STEP, OP_LINEAR_BACKWARD_SGD_PAIR,
+  OP_LINEAR_RELU_MSE_BACKWARD_SGD,
   OP_COUNT
 };
 
@@ -56,6 +57,7 @@ static const char* kNames[OP_COUNT] = {
     "layer_norm_backward", "layer_norm_grads", "gelu_backward", "gelu_tanh_backward", "gelu_exact_backward",
     "embedding_backward", "pack_weight_x3", "pack_rows_x3", "matmul_pp", "row_stats_x3", "matmul_pp_norm",
     "linear_backward_sgd_", "linear_mse_backward_sgd_", "mlp2_sgd_step_", "linear_backward_sgd_pair_",
+    "linear_relu_mse_backward_sgd_",
 };
 
 int op_code(const char* name) {
@@ -247,6 +249,13 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
       // (x, y, w1, b1, w2, b2)
       need(in, 6, code);
       return {mlp2_sgd_step_(in[0], in[1], in[2], in[3], in[4], in[5], (float)fp(f, 0, code))};
+    case OP_LINEAR_RELU_MSE_BACKWARD_SGD: {
+      // (a, wh, bh, w, b, y); iv[0]: also return the input gradient
+      need(in, 6, code);
+      auto r = linear_relu_mse_backward_sgd_(in[0], in[1], in[2], in[3], in[4], in[5], (float)fp(f, 0, code),
+                                             !iv.empty() && iv[0]);
+      return {std::get<0>(r), std::get<1>(r), std::get<2>(r)};
+    }
     case OP_LINEAR_BACKWARD_SGD_PAIR:
       // (w1, b1, g, h, w0, b0, x)
       need(in, 7, code);
@@ -291,7 +300,8 @@ std::vector<TensorP> run_op(int code, const std::vector<TensorP>& in, const std:
 std::vector<TensorP> record_op(int code, const std::vector<TensorP>& in, const std::vector<double>& f,
                                const std::vector<int64_t>& iv) {
   if (code == OP_SGD_MATMUL || code == OP_SGD_SUM_ROWS || code == OP_LINEAR_BACKWARD_SGD ||
-      code == OP_LINEAR_MSE_BACKWARD_SGD || code == OP_MLP2_SGD_STEP || code == OP_LINEAR_BACKWARD_SGD_PAIR)
+      code == OP_LINEAR_MSE_BACKWARD_SGD || code == OP_MLP2_SGD_STEP || code == OP_LINEAR_BACKWARD_SGD_PAIR ||
+      code == OP_LINEAR_RELU_MSE_BACKWARD_SGD)
     fail("%s updates its first operand in place: eager only", op_name(code));
   std::vector<TensorP> metas;
   {

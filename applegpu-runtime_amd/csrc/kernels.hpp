@@ -329,6 +329,18 @@ struct Lin1Fwd {
   float two_over_n;
 };
 void linear1_forward_mse(DType dt, const Lin1Fwd& a, hipStream_t s);
+// The same with the layer's input h formed here from the previous GEMM's
+// split-K partial sums: h = relu(sum of the splits in split order + hb),
+// written to h_out (fp32, rows of N, N % 4 == 0, 16-byte aligned).
+struct Lin1FwdParts {
+  const float* part; int splits; int64_t plane;  // part[s * plane + r * N + k]
+  const float* hb; float* h_out;
+  const float* w; const float* b; const float* y;
+  float* z; float* dz;
+  int64_t R, N;
+  float two_over_n;
+};
+void linear1_forward_mse_parts(const Lin1FwdParts& a, hipStream_t s);
 // True when the plan for g computes a_rowsum_acc itself (the outer-product
 // plan); otherwise the caller leaves it null and sums A on its own.
 bool gemm_a_rowsum_fused(const Gemm& g);

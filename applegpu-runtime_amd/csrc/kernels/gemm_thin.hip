@@ -169,6 +169,51 @@ __global__ void __launch_bounds__(256) linear1_fwd_mse(Lin1Fwd p) {
   }
 }
 
+// linear1_fwd_mse with the input row formed from split-K partials (the
+// previous layer's GEMM left them unreduced): one 1024-thread block per row;
+// each thread sums the splits of its 4-column groups in split order, adds
+// the bias, applies the ReLU (the split-K reduction's arithmetic, so h is
+// the same bits), stores h and accumulates its dot with w.
+__global__ void __launch_bounds__(1024) linear1_fwd_mse_parts(Lin1FwdParts p) {
+  __shared__ float sh[16];
+  const int64_t r = blockIdx.x;
+  const float* pr = p.part + r * p.N;
+  float s = 0.f;
+  for (int64_t k = threadIdx.x; k < p.N / 4; k += 1024) {
+    float4 parts[8];
+#pragma unroll
+    for (int sp = 0; sp < 8; ++sp)
+      if (sp < p.splits) parts[sp] = ((const float4*)(pr + sp * p.plane))[k];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int sp = 0; sp < 8; ++sp)
+      if (sp < p.splits) {
+        acc.x += parts[sp].x; acc.y += parts[sp].y; acc.z += parts[sp].z; acc.w += parts[sp].w;
+      }
+    const float4 bb = ((const float4*)p.hb)[k];
+    float4 h;
+    h.x = fmaxf(acc.x + bb.x, 0.f); h.y = fmaxf(acc.y + bb.y, 0.f);
+    h.z = fmaxf(acc.z + bb.z, 0.f); h.w = fmaxf(acc.w + bb.w, 0.f);
+    ((float4*)(p.h_out + r * p.N))[k] = h;
+    const float4 c = ((const float4*)p.w)[k];
+    s += h.x * c.x;
+    s += h.y * c.y;
+    s += h.z * c.z;
+    s += h.w * c.w;
+  }
+  s = wave_sum(s);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += sh[i];
+    const float z = t + p.b[0];
+    p.z[r] = z;
+    p.dz[r] = (z - p.y[r]) * p.two_over_n;
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256) outer_k1(GArgs p) {
   const int64_t b = blockIdx.y;
@@ -188,6 +233,15 @@ void linear1_backward_sgd(DType dt, const Lin1Bwd& a, hipStream_t s) {
   if (dt != DType::F32) fail("linear1_backward_sgd: fp32 only");
   hipLaunchKernelGGL((linear1_bwd_sgd<float>), dim3((unsigned)((a.N + 15) / 16)), dim3(1024), 0, s, a);
   check_launch("linear1_backward_sgd");
+}
+
+void linear1_forward_mse_parts(const Lin1FwdParts& a, hipStream_t s) {
+  if (a.R == 0) return;
+  if (a.R > 0x7fffffffLL || a.splits < 1 || a.splits > 8 || a.N % 4 != 0 ||
+      (((uintptr_t)a.part | (uintptr_t)a.hb | (uintptr_t)a.h_out | (uintptr_t)a.w) & 15) || a.plane % 4 != 0)
+    fail("linear1_forward_mse_parts: 1-8 splits, N %% 4 == 0 and 16-byte aligned operands needed");
+  hipLaunchKernelGGL(linear1_fwd_mse_parts, dim3((unsigned)a.R), dim3(1024), 0, s, a);
+  check_launch("linear1_forward_mse_parts");
 }
 
 void linear1_forward_mse(DType dt, const Lin1Fwd& a, hipStream_t s) {

@@ -834,6 +834,58 @@ std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const Ten
   return {lg.first, gi};
 }
 
+std::tuple<TensorP, TensorP, TensorP> linear_relu_mse_backward_sgd_(const TensorP& a, const TensorP& wh,
+                                                                    const TensorP& bh, const TensorP& w,
+                                                                    const TensorP& b, const TensorP& y, float alpha,
+                                                                    bool grad_in) {
+  const char* name = "linear_relu_mse_backward_sgd_";
+  if (a->ndim != 2 || wh->ndim != 2) fail("%s: a and wh must be 2-D", name);
+  const int64_t R = a->shape[0], K = a->shape[1], N = wh->shape[0];
+  if (wh->shape[1] != K || bh->numel() != N)
+    fail("%s: wh %s and bh %s do not fit a %s", name, shape_str(wh->dims()).c_str(), shape_str(bh->dims()).c_str(),
+         shape_str(a->dims()).c_str());
+  auto layered = [&]() {
+    Epilogue e;
+    e.bias = bh;
+    e.act = k::kActRelu;
+    TensorP h = matmul(a, wh, false, true, &e);
+    auto r = linear_mse_backward_sgd_(h, w, b, y, alpha, grad_in);
+    return std::make_tuple(r.first, r.second, h);
+  };
+  const bool f32 = a->dtype == DType::F32 && wh->dtype == DType::F32 && bh->dtype == DType::F32 &&
+                   w->dtype == DType::F32 && b->dtype == DType::F32 && y->dtype == DType::F32;
+  if (meta_mode() || !f32 || w->ndim != 2 || w->shape[0] != 1 || w->shape[1] != N || b->numel() != 1 ||
+      y->dims() != std::vector<int64_t>{R, 1} || N % 4 != 0 || !a->is_contiguous() || !wh->is_contiguous() ||
+      !bh->is_contiguous() || !w->is_contiguous() || !b->is_contiguous() || !y->is_contiguous())
+    return layered();
+  // h's GEMM with its split-K partial sums left for the output layer's
+  // forward, which reduces them (bias, ReLU) while it forms z
+  k::Gemm g;
+  g.dt = g.b_dt = DType::F32;
+  g.M = R; g.N = N; g.K = K; g.batch = 1;
+  g.A = a->data(); g.a_sm = K; g.a_sk = 1; g.a_sb = R * K;
+  g.B = wh->data(); g.b_sk = 1; g.b_sn = K; g.b_sb = N * K;
+  g.C = nullptr; g.c_sm = N; g.c_sb = R * N;
+  g.no_reduce = true;
+  const int splits = k::gemm_splits(g);
+  if (splits < 2 || splits > 8) return layered();
+  BufferP ws = scratch(k::gemm_workspace_bytes(g));
+  LAUNCH k::gemm(g, ws->ptr, rt().stream());
+  TensorP h = alloc_out(DType::F32, {R, N});
+  TensorP z = alloc_out(DType::F32, {R, 1}), dz = alloc_out(DType::F32, {R, 1});
+  TensorP loss = alloc_out(DType::F32, {1});
+  TensorP gin = grad_in ? alloc_out(DType::F32, {R, N}) : nullptr;
+  const float n = (float)R;
+  k::Lin1FwdParts f{(const float*)ws->ptr, splits, R * N, (const float*)bh->data(), (float*)h->data(),
+                    (const float*)w->data(), (const float*)b->data(), (const float*)y->data(), (float*)z->data(),
+                    (float*)dz->data(), R, N, 2.f / n};
+  LAUNCH k::linear1_forward_mse_parts(f, rt().stream());
+  k::Lin1Bwd p{h->data(), N, dz->data(), 1, w->data(), b->data(), gin ? gin->data() : nullptr,
+               R, N, alpha, z->data(), y->data(), loss->data(), 1.f / n};
+  LAUNCH k::linear1_backward_sgd(DType::F32, p, rt().stream());
+  return std::make_tuple(loss, gin ? gin : w, h);
+}
+
 TensorP sgd_sum_rows_(const TensorP& bias, const TensorP& g, float alpha) {
   check_dtype("sgd_sum_rows_", kFloatOnly, g->dtype);
   if (g->ndim != 2 || bias->dtype != g->dtype || bias->numel() != g->shape[1] || !bias->is_contiguous())

@@ -3,6 +3,8 @@
 // runtime stream.  Used by both the eager C ABI and the lazy graph executor.
 #pragma once
 
+#include <tuple>
+
 #include "core.hpp"
 #include "kernels.hpp"
 
@@ -163,6 +165,17 @@ std::pair<TensorP, TensorP> linear_mse_backward_sgd_(const TensorP& h, const Ten
 // GEMM launch (k::gemm_outer_pair); otherwise as two sgd_matmul_ calls.
 TensorP linear_backward_sgd_pair_(const TensorP& w1, const TensorP& b1, const TensorP& g, const TensorP& h,
                                   const TensorP& w0, const TensorP& b0, const TensorP& x, float alpha);
+// The last hidden layer and the one-output regression layer of an MLP
+// through their forward, MSE loss, backward and the output layer's SGD
+// step: h = relu(a wh^T + bh), then linear_mse_backward_sgd_(h, w, b, y,
+// alpha, grad_in).  Returns {loss, g_in, h}.  For fp32 with one output the
+// hidden GEMM leaves its split-K partial sums unreduced and the output
+// layer's forward reduces them (bias, ReLU, h written) while it forms z:
+// three launches (GEMM, forward, backward) where the layered form has four.
+std::tuple<TensorP, TensorP, TensorP> linear_relu_mse_backward_sgd_(const TensorP& a, const TensorP& wh,
+                                                                    const TensorP& bh, const TensorP& w,
+                                                                    const TensorP& b, const TensorP& y, float alpha,
+                                                                    bool grad_in);
 // One SGD step of Linear(w1, b1) -> ReLU -> Linear(w2, b2) with MSE loss
 // against y, in place (w += alpha * grad, every gradient from the step's
 // starting parameters); returns the loss [1].  Small fp32 shapes run as one

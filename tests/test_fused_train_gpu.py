@@ -210,6 +210,51 @@ def test_linear_backward_sgd(gpu, R, O, N, with_mask):
         assert rel_err(gin.numpy(), want) < 1e-5
 
 
+@pytest.mark.parametrize("R,K,N,fused", [(256, 4096, 4096, True), (64, 1024, 2048, True), (37, 70, 50, False)])
+def test_linear_relu_mse_backward_sgd(gpu, R, K, N, fused):
+    """linear_relu_mse_backward_sgd_ (the last hidden layer and a one-output
+    MSE layer): h = relu(a @ wh^T + bh), then the output layer's forward,
+    loss, backward and SGD step.  Where the hidden GEMM has a K split its
+    partial sums are reduced by the output layer's forward (3 launches): h
+    then has the same bits as the layered form (linear with bias + ReLU,
+    then linear_mse_backward_sgd_), and the loss, the input gradient and
+    the updated parameters agree to fp32 rounding (z's dot product is summed
+    over 1024 threads instead of 256); all against float64."""
+    from applegpu_runtime import eager as E
+    a = f32(R, K)
+    wh, bh = f32(N, K, scale=0.05), f32(N, scale=0.1)
+    w, b, y = f32(1, N, scale=0.05), f32(1), f32(R, 1)
+    lr = 0.01
+    at, wht, bht, yt = (E.from_numpy(v) for v in (a, wh, bh, y))
+    fw, fb = E.from_numpy(w), E.from_numpy(b)
+    before = gpu.graph_stats()["launcher_calls"]
+    loss, gin, h = E.linear_relu_mse_backward_sgd_(at, wht, bht, fw, fb, yt, -lr)
+    calls = gpu.graph_stats()["launcher_calls"] - before
+    if fused:
+        assert calls == 3, calls
+    lw, lb = E.from_numpy(w), E.from_numpy(b)
+    hl = E.linear(at, wht, bht, act=1)
+    lloss, lgin = E.linear_mse_backward_sgd_(hl, lw, lb, yt, -lr)
+    np.testing.assert_array_equal(h.numpy(), hl.numpy())
+    np.testing.assert_allclose(loss.numpy(), lloss.numpy(), rtol=1e-6)
+    np.testing.assert_allclose(gin.numpy(), lgin.numpy(), rtol=1e-5, atol=1e-8)
+    # (dz differs from the layered form by a rounding, so w moves by a few
+    # ulp of its scale, 0.05)
+    np.testing.assert_allclose(fw.numpy(), lw.numpy(), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(fb.numpy(), lb.numpy(), rtol=1e-6, atol=1e-7)
+    # float64
+    h64 = np.maximum(a.astype(np.float64) @ wh.astype(np.float64).T + bh, 0.0)
+    z = h64 @ w.astype(np.float64).T + b
+    dz = 2.0 * (z - y) / R
+    assert rel_err(h.numpy(), h64) < 1e-4
+    np.testing.assert_allclose(loss.numpy()[0], np.mean((z - y) ** 2), rtol=1e-4)
+    # (masked by the device's h: a hidden unit within rounding of zero can
+    # take the other side of the ReLU than in float64, which moves a whole
+    # gradient entry)
+    assert rel_err(gin.numpy(), np.where(h.numpy() > 0, dz @ w.astype(np.float64), 0.0)) < 1e-4
+    assert rel_err(fw.numpy() - w, -lr * (dz.T @ h64)) < 1e-4
+
+
 @pytest.mark.parametrize("R,N0,N1,O1,paired", [(256, 4096, 4096, 4096, True), (128, 2048, 4096, 2048, True),
                                                 (256, 2048, 2048, 1024, False), (33, 70, 50, 20, False)])
 def test_linear_backward_sgd_pair(gpu, R, N0, N1, O1, paired):
